@@ -1,0 +1,124 @@
+/* imq.h -- C ABI of the gfx950 (MI355X) weight-only quantized Linear library (libimq.so).
+ *
+ * One entry point per kernel family of the reference's quantized-Linear hot path. The
+ * reference has no C ABI: its operators are Python callables returned by lazy builders in
+ * worker_quant.py. Each entry below names the operator it replaces (file:line in the
+ * reference tree); the Python layer (infinitemodel_amd.worker_quant) keeps the reference's
+ * operator signatures and calls these.
+ *
+ * Conventions
+ *   - Pointers are device pointers owned by the caller (torch allocates every buffer).
+ *   - Strides are in elements, except packed-weight row strides which are in BYTES.
+ *   - x / y are bf16 unless stated otherwise.
+ *   - scale / zero dtype codes: IMQ_DT_BF16, IMQ_DT_FP16, IMQ_DT_FP32.
+ *   - `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream).
+ *   - Return 0 on success, IMQ_ERR_* (< 0) for rejected arguments, or a positive hipError_t
+ *     when a launch fails. No call allocates, frees or synchronizes; all are re-entrant and
+ *     keep no state between calls except a per-device immutable attribute cache.
+ */
+#ifndef IMQ_H
+#define IMQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IMQ_ABI_VERSION 1
+
+#define IMQ_DT_BF16 0
+#define IMQ_DT_FP16 1
+#define IMQ_DT_FP32 2
+
+#define IMQ_OK 0
+#define IMQ_ERR_INVALID (-1)     /* bad shape / stride / dtype / null pointer */
+#define IMQ_ERR_UNSUPPORTED (-2) /* valid for the reference but not for this kernel family */
+#define IMQ_ERR_ALIGN (-3)       /* pointer or stride not aligned as the kernel requires */
+
+int imq_abi_version(void);
+const char* imq_strerror(int status);
+
+/* ---- dequant: the reference dequant, bit-exact ----------------------------------------------
+ * out[n, k] = R(R(q[n,k] - R(zero[n, k/G])) * R(scale[n, k/G])) for k < in_features, where R
+ * rounds to out_dtype -- QuantLinear4._dequant (worker_quant.py:638-648).
+ * qweight: u8 [N, K_pad/2], low nibble = even column. */
+int imq_dequant_w4(const void* qweight, int64_t q_row_stride, const void* scale, int64_t s_stride_n,
+                   int64_t s_stride_g, int s_dtype, const void* zero, int64_t z_stride_n,
+                   int64_t z_stride_g, int z_dtype, int64_t N, int64_t in_features, int64_t group_size,
+                   void* out, int64_t out_row_stride, int out_dtype, void* stream);
+
+/* QuantLinear2._dequant (worker_quant.py:1652-1664); qweight u8 [N, K_pad/4], crumb i = col 4j+i. */
+int imq_dequant_w2(const void* qweight, int64_t q_row_stride, const void* scale, int64_t s_stride_n,
+                   int64_t s_stride_g, int s_dtype, const void* zero, int64_t z_stride_n,
+                   int64_t z_stride_g, int z_dtype, int64_t N, int64_t in_features, int64_t group_size,
+                   void* out, int64_t out_row_stride, int out_dtype, void* stream);
+
+/* int8 naive weight `qweight.to(dt) * scale` rounded to out_dtype (worker_quant.py:439); the
+ * scale is rounded to out_dtype first only when out_dtype is the scale's own dtype class
+ * (callers choose out_dtype = torch's promoted dtype). qweight int8 [N, K]. */
+int imq_dequant_w8(const void* qweight, int64_t q_row_stride, const void* scale, int64_t s_stride_n,
+                   int s_dtype, int64_t N, int64_t K, void* out, int64_t out_row_stride, int out_dtype,
+                   void* stream);
+
+/* ---- fused dequant linear: y[M, N] = x[M, K_pad] @ dequant(W)^T, fp32 accumulate, bf16 out ---
+ * Replaces the op returned by _w4a16_triton_op() (worker_quant.py:1079-1225: `_ksk` M==1 split-K
+ * GEMV, `_k` M>1 tl.dot GEMM), called as op(x[M,Kpad] bf16, qweight, group, (scale, zero)).
+ * K_pad = 2 * qweight columns; x must be zero beyond in_features (the module pads, 839-840).
+ * Any M >= 1; the library picks the decode (MFMA skinny GEMV) or prefill (LDS-dequant MFMA
+ * GEMM) kernel. Scale/zero are rounded to bf16 as _dequant(torch.bfloat16) does. */
+int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad, const void* qweight,
+                  int64_t q_row_stride, const void* scale, int64_t s_stride_n, int64_t s_stride_g,
+                  int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
+                  int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* stream);
+
+/* int2 twin: replaces _w2a16_triton_op() (worker_quant.py:1775-1918: `_ksk2`, `_k2`).
+ * K_pad = 4 * qweight columns. */
+int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad, const void* qweight,
+                  int64_t q_row_stride, const void* scale, int64_t s_stride_n, int64_t s_stride_g,
+                  int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
+                  int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* stream);
+
+/* int8 per-row symmetric: y = bf16(scale[n] * sum_k x[m,k] * q[n,k]). Replaces
+ * _w8a16_triton_op() (worker_quant.py:926-1057: `_ksk8`, `_k8`), op(x, qweight, scale). */
+int imq_linear_w8(const void* x, int64_t x_row_stride, int64_t M, int64_t K, const void* qweight,
+                  int64_t q_row_stride, const void* scale, int64_t s_stride_n, int s_dtype, int64_t N,
+                  void* y, int64_t y_row_stride, void* stream);
+
+/* ---- fused MoE experts (int4 g-wise, [E, N, K_pad/2] stacks) ----------------------------------
+ * Per-row grouped GEMV: y[b, :] = x[b, :] @ dequant(W[eid[b]])^T for b < B (fp32 accumulate,
+ * bf16 out). Replaces the op returned by _w4a16_moe_op() (worker_quant.py:1342-1495, `_mk`),
+ * op(x[B,Kin], eid[B], q[E,N,Kpad/2], scale, zero, group, in_features). x is [B, K_pad] bf16
+ * (zero beyond in_features); eid int32 [B]. */
+int imq_moe_rows_w4(const void* x, int64_t x_row_stride, int64_t B, int64_t K_pad, const int32_t* eid,
+                    int64_t E, const void* qweight, int64_t q_stride_e, int64_t q_row_stride,
+                    const void* scale, int64_t s_stride_e, int64_t s_stride_n, int64_t s_stride_g,
+                    const void* zero, int64_t z_stride_e, int64_t z_stride_n, int64_t z_stride_g,
+                    int sz_dtype, int64_t N, int64_t group_size, void* y, int64_t y_row_stride,
+                    void* stream);
+
+/* Whole experts forward of one MoE layer (the patched experts.forward of
+ * _install_fused_moe_forward, worker_quant.py:2131-2248, whose semantics are the transformers
+ * eager experts loop): out[t] = sum_j w[t,j] * down_e( silu(gate) * up ), [gate | up] =
+ * gate_up_e(x[t]), e = topk_idx[t,j].
+ *   hidden bf16 [T, H_pad] (row stride; zero beyond H when H_pad > H), topk_idx int32 [T, k]
+ *   contiguous, topk_w bf16 [T, k] contiguous, gate_up stack [E, 2I, H_pad/2] + s/z [E, 2I, ng1],
+ *   down stack [E, H, I_pad/2] + s/z [E, H, ng2] (scale and zero share strides), out bf16 [T, H].
+ *   workspace: device bytes >= imq_moe_workspace_bytes(T, k, E, H, I, G); contents need not be
+ *   initialised; calls sharing a workspace must be stream-ordered. */
+int64_t imq_moe_workspace_bytes(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                                int64_t group_size);
+int imq_moe_experts_w4(const void* hidden, int64_t h_row_stride, int64_t T, int64_t H, int64_t top_k,
+                       const int32_t* topk_idx, const void* topk_w, int64_t E,
+                       const void* gu_q, int64_t gu_q_stride_e, int64_t gu_q_row_stride,
+                       const void* gu_s, const void* gu_z, int64_t gu_sz_stride_e, int64_t gu_sz_stride_n,
+                       int64_t I, const void* dn_q, int64_t dn_q_stride_e, int64_t dn_q_row_stride,
+                       const void* dn_s, const void* dn_z, int64_t dn_sz_stride_e, int64_t dn_sz_stride_n,
+                       int sz_dtype, int64_t group_size, void* out, int64_t out_row_stride,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IMQ_H */

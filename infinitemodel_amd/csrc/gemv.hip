@@ -1,0 +1,397 @@
+// Decode-regime (M <= 16) fused dequant GEMV kernels for gfx950.
+//
+// w4 skinny kernel (the hot path of the north-star metric)
+// -------------------------------------------------------
+// Tile = 16 output rows (n) x all of K; a workgroup of W waves owns one tile at a time and
+// splits its K range across the waves; the tile loop is grid-strided.
+//
+// Per K-step (128 codes = 64 bytes of a packed row) every lane (j = lane/16, n = lane%16) does
+// ONE 16-byte load of row n (codes 32j..32j+31 of the step), so a wave reads 16 rows x 64
+// contiguous bytes per load instruction. The 32 codes are turned into four MFMA B operands
+// with one v_and_or_b32 per code pair: (code | 0x4300) is exactly the bf16 value 128 + code.
+// Four v_mfma_f32_16x16x32_bf16 accumulate  acc[m][n] = sum_k x[m][k] * (128 + q[n][k])  over
+// the step; the zero point and scale are folded in per step (all 128 codes share one group
+// because G % 128 == 0):
+//     y[m][n] += s * acc[m][n] - s * (128 + z) * xsum[m]
+// with xsum[m] = sum of x[m][k] over the step. That is sum_k x * (q - z) * s exactly in fp32,
+// i.e. the unrounded-weight GEMV of the reference's split-K kernel (worker_quant.py:1176-1177).
+// s and z are first rounded to bf16 like _dequant(torch.bfloat16) (worker_quant.py:646-647).
+//
+// Activations are staged once per workgroup in LDS, pre-permuted into the element order the
+// unpacked weight operands use ([x0,x4,x1,x5,x2,x6,x3,x7] per 8), together with per-step
+// row sums. Rows m >= M are never read (their MFMA A lanes are zero). When M*K does not fit
+// in LDS, K is processed in chunks that are restaged per tile.
+//
+// Partial sums of the W waves are reduced through LDS in a fixed order: deterministic, no
+// atomics, no memset, a single launch per linear.
+#include "imq_common.h"
+
+namespace imq {
+
+struct SkinnyArgs {
+  const uint16_t* x;
+  int64_t sxm;
+  int M;
+  int Kpad;
+  const uint8_t* q;
+  int64_t sqn;
+  const void* sc;
+  int64_t ssn, ssg;
+  const void* zr;
+  int64_t szn, szg;
+  int N;
+  int G;
+  uint16_t* y;
+  int64_t sym;
+  int chunk_steps;   // K-steps (128 codes) staged in LDS at once
+};
+
+constexpr int kStep = 128;          // codes per K-step
+constexpr int kXPad = 8;            // bf16 elements of padding per LDS activation row
+
+template <int W, int MC, int SDT, int ZDT>
+__global__ __launch_bounds__(64 * W) void w4_skinny_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nl = lane & 15;          // row within tile (B/D column), also A row m
+  const int jl = lane >> 4;          // K quarter of the step (A/B), D row group
+  constexpr int RC = (MC < 4) ? MC : 4;   // D registers that can hold a real row
+
+  const int KS = a.Kpad / kStep;
+  const int cs_max = a.chunk_steps;
+  const int nchunks = (KS + cs_max - 1) / cs_max;
+  const int xls = cs_max * kStep + kXPad;           // LDS row stride (elements)
+
+  uint16_t* xl = (uint16_t*)smem;                                    // [M][xls]
+  float* xs = (float*)(smem + (size_t)a.M * xls * 2);                // [cs_max][16]
+  float* red = xs + (size_t)cs_max * 16;                             // [2][W][16][16]
+
+  const int NT = (a.N + 15) / 16;
+  const int gpd = a.G / kStep;       // K-steps per group
+
+  auto stage = [&](int c0, int c1) {
+    const int nblk = (c1 - c0) * (kStep / 8);
+    for (int idx = threadIdx.x; idx < a.M * nblk; idx += 64 * W) {
+      const int m = idx / nblk;
+      const int b = idx - m * nblk;
+      const u32x4_t v = *(const u32x4_t*)(a.x + (int64_t)m * a.sxm + (int64_t)c0 * kStep + 8 * b);
+      *(u32x4_t*)(xl + m * xls + 8 * b) = permute_x8(v);
+    }
+    __syncthreads();
+    const int cs = c1 - c0;
+    for (int idx = threadIdx.x; idx < 16 * cs; idx += 64 * W) {
+      const int st = idx >> 4;
+      const int m = idx & 15;
+      float sum = 0.f;
+      if (m < a.M) {
+        const uint16_t* p = xl + m * xls + st * kStep;
+        for (int e = 0; e < kStep; e += 8) {
+          const u32x4_t v = *(const u32x4_t*)(p + e);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            sum += __uint_as_float(v[d] << 16);
+            sum += __uint_as_float(v[d] & 0xffff0000u);
+          }
+        }
+      }
+      xs[st * 16 + m] = sum;
+    }
+    __syncthreads();
+  };
+
+  if (nchunks == 1) stage(0, KS);
+
+  int buf = 0;
+  for (int tile = blockIdx.x; tile < NT; tile += gridDim.x) {
+    const int n0 = tile * 16;
+    const int row = n0 + nl;
+    const bool row_ok = row < a.N;
+    const uint8_t* qrow = a.q + (int64_t)(row_ok ? row : 0) * a.sqn;
+    float yacc[4] = {0.f, 0.f, 0.f, 0.f};
+
+    for (int c = 0; c < nchunks; ++c) {
+      const int c0 = c * cs_max;
+      const int c1 = (c0 + cs_max < KS) ? c0 + cs_max : KS;
+      if (nchunks > 1) stage(c0, c1);
+      const int spw = (c1 - c0 + W - 1) / W;
+      const int s_beg = c0 + wave * spw;
+      const int s_end = (s_beg + spw < c1) ? s_beg + spw : c1;
+
+      constexpr int U = 4;
+      for (int sb = s_beg; sb < s_end; sb += U) {
+        u32x4_t wv[U];
+        float sv[U], zv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int s = sb + u;
+          if (s < s_end && row_ok) {
+            wv[u] = __builtin_nontemporal_load((const u32x4_t*)(qrow + (int64_t)s * 64 + 16 * jl));
+            const int g = s / gpd;
+            sv[u] = load_as_bf16_f32<SDT>(a.sc, (int64_t)row * a.ssn + (int64_t)g * a.ssg);
+            zv[u] = load_as_bf16_f32<ZDT>(a.zr, (int64_t)row * a.szn + (int64_t)g * a.szg);
+          } else {
+            wv[u] = u32x4_t{0u, 0u, 0u, 0u};
+            sv[u] = 0.f;
+            zv[u] = 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int s = sb + u;
+          if (s < s_end) {
+            const int sl = s - c0;
+            const uint16_t* xa = xl + nl * xls + sl * kStep + 32 * jl;
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              bf16x8_t av;
+              if (nl < a.M) {
+                av = *(const bf16x8_t*)(xa + 8 * i);
+              } else {
+                av = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
+              }
+              acc = mfma16x16x32(av, unpack_nib8_bf16(wv[u][i]), acc);
+            }
+            const f32x4_t xsum = *(const f32x4_t*)(xs + sl * 16 + 4 * jl);
+            const float sc = sv[u];
+            const float cz = -(128.f + zv[u]) * sc;
+#pragma unroll
+            for (int r = 0; r < RC; ++r) {
+              yacc[r] = fmaf(sc, acc[r], yacc[r]);
+              yacc[r] = fmaf(cz, xsum[r], yacc[r]);
+            }
+          }
+        }
+      }
+      if (nchunks > 1) __syncthreads();   // before the next chunk overwrites the staged x
+    }
+
+    // Cross-wave reduction, fixed order.
+    float* rb = red + buf * (W * 256);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rb[wave * 256 + (4 * jl + r) * 16 + nl] = yacc[r];
+    __syncthreads();
+    for (int t = threadIdx.x; t < 16 * a.M; t += 64 * W) {
+      const int m = t >> 4;
+      const int n = t & 15;
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) sum += rb[w * 256 + t];
+      if (n0 + n < a.N) a.y[(int64_t)m * a.sym + n0 + n] = (uint16_t)f32_to_bf16_bits(sum);
+    }
+    buf ^= 1;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Generic fallback: any bit width (2/4/8), any group size, any stride/alignment, M <= 16.
+// One wave per output row; every weight is dequantized to the reference's exact bf16 value
+// bf16(bf16(q - bf16(z)) * bf16(s)) (worker_quant.py:646-647) and accumulated in fp32, i.e.
+// literally dequantize-then-matmul. Slow but faithful; used for shapes the fast kernels reject.
+// ---------------------------------------------------------------------------------------------
+struct GenericArgs {
+  const uint16_t* x;
+  int64_t sxm;
+  int M;
+  int64_t K;       // codes per row to reduce over (K_pad for int2/4, K for int8)
+  const uint8_t* q;
+  int64_t sqn;
+  const void* sc;
+  int64_t ssn, ssg;
+  const void* zr;
+  int64_t szn, szg;
+  int64_t N;
+  int64_t G;
+  uint16_t* y;
+  int64_t sym;
+};
+
+template <int BITS, int SDT, int ZDT>
+__global__ __launch_bounds__(256) void generic_gemv_kernel(GenericArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.N) return;
+  float acc[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) acc[m] = 0.f;
+  const uint8_t* qr = a.q + row * a.sqn;
+  for (int64_t k = lane; k < a.K; k += 64) {
+    float w;
+    if constexpr (BITS == 8) {
+      w = (float)((const int8_t*)qr)[k];
+    } else {
+      constexpr int CPB = 8 / BITS;
+      const uint32_t byte = qr[k / CPB];
+      const float code = (float)((byte >> (BITS * (k % CPB))) & ((1u << BITS) - 1u));
+      const int64_t g = k / a.G;
+      const float z = load_as_bf16_f32<ZDT>(a.zr, row * a.szn + g * a.szg);
+      const float s = load_as_bf16_f32<SDT>(a.sc, row * a.ssn + g * a.ssg);
+      w = round_bf16(round_bf16(code - z) * s);
+    }
+#pragma unroll
+    for (int m = 0; m < 16; ++m)
+      if (m < a.M) acc[m] = fmaf(bf16_bits_to_f32(a.x[m * a.sxm + k]), w, acc[m]);
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    float v = acc[m];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    acc[m] = v;
+  }
+  if (lane < a.M) {
+    float v = 0.f;
+#pragma unroll
+    for (int m = 0; m < 16; ++m)
+      if (m == lane) v = acc[m];
+    if constexpr (BITS == 8) v *= load_as_f32<SDT>(a.sc, row * a.ssn);
+    a.y[lane * a.sym + row] = (uint16_t)f32_to_bf16_bits(v);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// host dispatch
+// ---------------------------------------------------------------------------------------------
+struct DevInfo {
+  int cus;
+  int max_lds;
+};
+
+DevInfo device_info() {
+  static DevInfo cache[64];
+  static int ready[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DevInfo{256, 65536};
+  if (!__atomic_load_n(&ready[dev], __ATOMIC_ACQUIRE)) {
+    DevInfo d{256, 65536};
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      d.cus = v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
+      d.max_lds = v;
+    cache[dev] = d;
+    __atomic_store_n(&ready[dev], 1, __ATOMIC_RELEASE);
+  }
+  return cache[dev];
+}
+
+template <int W, int MC, int SDT, int ZDT>
+int launch_skinny_w4(const SkinnyArgs& a, size_t lds, int grid, hipStream_t st) {
+  auto kern = w4_skinny_kernel<W, MC, SDT, ZDT>;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+  }
+  kern<<<dim3(grid), dim3(64 * W), lds, st>>>(a);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+template <int W, int SDT, int ZDT>
+int skinny_w4_mc(const SkinnyArgs& a, size_t lds, int grid, hipStream_t st) {
+  if (a.M == 1) return launch_skinny_w4<W, 1, SDT, ZDT>(a, lds, grid, st);
+  if (a.M == 2) return launch_skinny_w4<W, 2, SDT, ZDT>(a, lds, grid, st);
+  if (a.M <= 4) return launch_skinny_w4<W, 4, SDT, ZDT>(a, lds, grid, st);
+  return launch_skinny_w4<W, 16, SDT, ZDT>(a, lds, grid, st);
+}
+
+template <int SDT, int ZDT>
+int skinny_w4_w(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
+  if (W == 4) return skinny_w4_mc<4, SDT, ZDT>(a, lds, grid, st);
+  return skinny_w4_mc<8, SDT, ZDT>(a, lds, grid, st);
+}
+
+// Fast path eligibility + launch. Returns IMQ_ERR_UNSUPPORTED when the caller must fall back.
+int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
+              const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st) {
+  if (M < 1 || M > 16 || G % kStep != 0 || Kpad % G != 0 || Kpad <= 0) return IMQ_ERR_UNSUPPORTED;
+  if (((uintptr_t)q & 15) || (sqn & 15) || ((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
+  if (N > (1 << 30) || Kpad > (1 << 28)) return IMQ_ERR_UNSUPPORTED;
+  if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
+  const DevInfo di = device_info();
+  const int KS = (int)(Kpad / kStep);
+  const int W = (KS >= 16) ? 8 : 4;
+  const size_t red_bytes = (size_t)2 * W * 256 * 4;
+  const size_t budget = (size_t)di.max_lds;
+  // chunk so that x [M][cs*128+pad] + xsum [cs][16] + reduction fit
+  int cs = KS;
+  auto need = [&](int c) { return (size_t)M * (c * kStep + kXPad) * 2 + (size_t)c * 64 + red_bytes; };
+  while (cs > 1 && need(cs) > budget) cs = (cs + 1) / 2;
+  if (need(cs) > budget) return IMQ_ERR_UNSUPPORTED;
+  SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, cs};
+  const int NT = (int)imq_cdiv(N, 16);
+  const int per_cu = (need(cs) <= budget / 2) ? 2 : 1;
+  int grid = di.cus * per_cu;
+  if (grid > NT) grid = NT;
+  switch (sdt) {
+    case IMQ_DT_BF16: return skinny_w4_w<IMQ_DT_BF16, IMQ_DT_BF16>(a, need(cs), grid, W, st);
+    case IMQ_DT_FP16: return skinny_w4_w<IMQ_DT_FP16, IMQ_DT_FP16>(a, need(cs), grid, W, st);
+    case IMQ_DT_FP32: return skinny_w4_w<IMQ_DT_FP32, IMQ_DT_FP32>(a, need(cs), grid, W, st);
+  }
+  return IMQ_ERR_INVALID;
+}
+
+template <int BITS, int SDT, int ZDT>
+int launch_generic(const GenericArgs& a, hipStream_t st) {
+  const int64_t blocks = imq_cdiv(a.N, 4);
+  generic_gemv_kernel<BITS, SDT, ZDT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+template <int BITS, int SDT>
+int generic_z(const GenericArgs& a, int zdt, hipStream_t st) {
+  switch (zdt) {
+    case IMQ_DT_BF16: return launch_generic<BITS, SDT, IMQ_DT_BF16>(a, st);
+    case IMQ_DT_FP16: return launch_generic<BITS, SDT, IMQ_DT_FP16>(a, st);
+    case IMQ_DT_FP32: return launch_generic<BITS, SDT, IMQ_DT_FP32>(a, st);
+  }
+  return IMQ_ERR_INVALID;
+}
+
+template <int BITS>
+int generic_gemv(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
+                 const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn,
+                 int64_t szg, int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st) {
+  // rows of x/y beyond 16 are handled by re-launching on 16-row slices
+  for (int64_t m0 = 0; m0 < M; m0 += 16) {
+    const int mm = (int)((M - m0) < 16 ? (M - m0) : 16);
+    GenericArgs a{x + m0 * sxm, sxm, mm, K, q, sqn, sc, ssn, ssg, zr, szn, szg, N, G, y + m0 * sym, sym};
+    int rc;
+    switch (sdt) {
+      case IMQ_DT_BF16: rc = generic_z<BITS, IMQ_DT_BF16>(a, BITS == 8 ? IMQ_DT_BF16 : zdt, st); break;
+      case IMQ_DT_FP16: rc = generic_z<BITS, IMQ_DT_FP16>(a, BITS == 8 ? IMQ_DT_BF16 : zdt, st); break;
+      case IMQ_DT_FP32: rc = generic_z<BITS, IMQ_DT_FP32>(a, BITS == 8 ? IMQ_DT_BF16 : zdt, st); break;
+      default: return IMQ_ERR_INVALID;
+    }
+    if (rc != IMQ_OK) return rc;
+  }
+  return IMQ_OK;
+}
+
+template int generic_gemv<2>(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, int64_t, const void*,
+                             int64_t, int64_t, int, const void*, int64_t, int64_t, int, int64_t, int64_t,
+                             uint16_t*, int64_t, hipStream_t);
+template int generic_gemv<4>(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, int64_t, const void*,
+                             int64_t, int64_t, int, const void*, int64_t, int64_t, int, int64_t, int64_t,
+                             uint16_t*, int64_t, hipStream_t);
+template int generic_gemv<8>(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, int64_t, const void*,
+                             int64_t, int64_t, int, const void*, int64_t, int64_t, int, int64_t, int64_t,
+                             uint16_t*, int64_t, hipStream_t);
+
+}  // namespace imq
+
+namespace imq {
+// int2 / int8 decode fast paths: not specialised yet -> caller falls back to the generic kernel.
+int skinny_w2(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, int64_t, const void*, int64_t,
+              int64_t, int, const void*, int64_t, int64_t, int, int64_t, int64_t, uint16_t*, int64_t,
+              hipStream_t) {
+  return IMQ_ERR_UNSUPPORTED;
+}
+int skinny_w8(const uint16_t*, int64_t, int64_t, int64_t, const int8_t*, int64_t, const void*, int64_t, int,
+              int64_t, uint16_t*, int64_t, hipStream_t) {
+  return IMQ_ERR_UNSUPPORTED;
+}
+}  // namespace imq

@@ -1,0 +1,120 @@
+// Shared device/host helpers for the gfx950 weight-only quantized Linear kernels.
+//
+// Conventions used by every kernel in this library:
+//   * activations x and outputs y are bf16, row-major with an explicit row stride (elements);
+//   * packed weights are byte arrays with an explicit row stride (bytes);
+//   * scale / zero carry (n, g) strides in elements and a dtype code (IMQ_DT_*);
+//   * every launch goes to the caller's stream; no kernel allocates, frees or synchronizes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/imq.h"
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+#define IMQ_DEV __device__ __forceinline__
+
+// ---- bf16 / fp16 <-> fp32 (bit-level, round-to-nearest-even) --------------------------------
+IMQ_DEV float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+IMQ_DEV uint32_t f32_to_bf16_bits(float f) {
+  // RNE; NaN kept quiet. Same rule as torch's float -> bfloat16 conversion.
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+IMQ_DEV float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+
+IMQ_DEV float round_fp16(float f) { return __half2float(__float2half_rn(f)); }
+
+// Load element `idx` of a dtype-coded array as fp32 (exact widening).
+template <int DT>
+IMQ_DEV float load_as_f32(const void* p, int64_t idx) {
+  if constexpr (DT == IMQ_DT_BF16) {
+    return bf16_bits_to_f32(((const uint16_t*)p)[idx]);
+  } else if constexpr (DT == IMQ_DT_FP16) {
+    return __half2float(((const __half*)p)[idx]);
+  } else {
+    return ((const float*)p)[idx];
+  }
+}
+
+// Round an fp32 value to dtype DT (result kept as fp32).
+template <int DT>
+IMQ_DEV float round_to(float f) {
+  if constexpr (DT == IMQ_DT_BF16) return round_bf16(f);
+  else if constexpr (DT == IMQ_DT_FP16) return round_fp16(f);
+  else return f;
+}
+
+// Load a scale/zero element and round it to bf16, i.e. `t.to(torch.bfloat16)` of the stored
+// value -- the operand the reference dequant `_dequant(torch.bfloat16)` multiplies with.
+template <int DT>
+IMQ_DEV float load_as_bf16_f32(const void* p, int64_t idx) {
+  float v = load_as_f32<DT>(p, idx);
+  if constexpr (DT == IMQ_DT_BF16) return v;
+  else return round_bf16(v);
+}
+
+template <int DT>
+IMQ_DEV void store_from_f32(void* p, int64_t idx, float v) {
+  if constexpr (DT == IMQ_DT_BF16) {
+    ((uint16_t*)p)[idx] = (uint16_t)f32_to_bf16_bits(v);
+  } else if constexpr (DT == IMQ_DT_FP16) {
+    ((__half*)p)[idx] = __float2half_rn(v);
+  } else {
+    ((float*)p)[idx] = v;
+  }
+}
+
+// (a & m) | o  -> v_and_or_b32
+IMQ_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) { return (a & m) | o; }
+
+IMQ_DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// 8 int4 codes (one u32, code i at bits 4i..4i+3) -> 8 bf16 values (128 + code), exact.
+// Output element order is [c0, c4, c1, c5, c2, c6, c3, c7]; activations fed against these
+// operands must use the same order (see permute_x8).
+IMQ_DEV bf16x8_t unpack_nib8_bf16(uint32_t w) {
+  u32x4_t r;
+  r[0] = and_or(w, 0x000F000Fu, 0x43004300u);
+  r[1] = and_or(w >> 4, 0x000F000Fu, 0x43004300u);
+  r[2] = and_or(w >> 8, 0x000F000Fu, 0x43004300u);
+  r[3] = and_or(w >> 12, 0x000F000Fu, 0x43004300u);
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+// 8 consecutive bf16 activations (16 bytes as 4 dwords) -> order [x0,x4,x1,x5,x2,x6,x3,x7].
+IMQ_DEV u32x4_t permute_x8(u32x4_t v) {
+  u32x4_t p;
+  p[0] = perm_b32(v[2], v[0], 0x05040100u);
+  p[1] = perm_b32(v[2], v[0], 0x07060302u);
+  p[2] = perm_b32(v[3], v[1], 0x05040100u);
+  p[3] = perm_b32(v[3], v[1], 0x07060302u);
+  return p;
+}
+
+IMQ_DEV f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+static inline int64_t imq_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Host-side launch error check: hipGetLastError after a launch, mapped to an int status.
+#define IMQ_LAUNCH_CHECK()                                   \
+  do {                                                       \
+    hipError_t _e = hipGetLastError();                       \
+    if (_e != hipSuccess) return (int)_e;                    \
+  } while (0)

@@ -1,0 +1,129 @@
+// C-ABI entry points of the fused dequant linear family (imq_linear_w4 / _w2 / _w8) and the
+// ABI metadata calls. Dispatch: decode rows (M <= 16) go to the MFMA skinny GEMV, prefill rows
+// to the LDS-dequant MFMA GEMM; shapes or alignments a fast kernel rejects fall back to the
+// generic dequantize-then-matmul kernel (never wrong, just slower).
+#include "imq_common.h"
+
+namespace imq {
+int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
+              const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st);
+int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
+              const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st);
+int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t* q, int64_t sqn,
+              const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st);
+int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
+            const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
+            int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st);
+template <int BITS>
+int generic_gemv(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
+                 const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn,
+                 int64_t szg, int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st);
+}  // namespace imq
+
+namespace {
+
+bool dt_ok(int d) { return d == IMQ_DT_BF16 || d == IMQ_DT_FP16 || d == IMQ_DT_FP32; }
+
+// Shared argument validation of the group-wise formats (int4 / int2).
+int check_g(int bits, const void* x, int64_t sxm, int64_t M, int64_t Kpad, const void* q, int64_t sqn,
+            const void* sc, int sdt, const void* zr, int zdt, int64_t N, int64_t G, const void* y,
+            int64_t sym) {
+  if (!x || !q || !sc || !zr || !y) return IMQ_ERR_INVALID;
+  if (M < 0 || N < 0 || Kpad <= 0 || G <= 0 || Kpad % G != 0) return IMQ_ERR_INVALID;
+  if ((Kpad * bits) % 8 != 0 || sqn < Kpad * bits / 8) return IMQ_ERR_INVALID;
+  if (sxm < Kpad || sym < N) return IMQ_ERR_INVALID;
+  if (!dt_ok(sdt) || !dt_ok(zdt)) return IMQ_ERR_INVALID;
+  return IMQ_OK;
+}
+
+}  // namespace
+
+extern "C" int imq_abi_version(void) { return IMQ_ABI_VERSION; }
+
+extern "C" const char* imq_strerror(int status) {
+  switch (status) {
+    case IMQ_OK: return "ok";
+    case IMQ_ERR_INVALID: return "invalid argument (shape, stride, dtype or null pointer)";
+    case IMQ_ERR_UNSUPPORTED: return "configuration not supported by this kernel family";
+    case IMQ_ERR_ALIGN: return "pointer or stride misaligned for this kernel";
+  }
+  if (status > 0) return hipGetErrorString((hipError_t)status);
+  return "unknown status";
+}
+
+extern "C" int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
+                             const void* qweight, int64_t q_row_stride, const void* scale,
+                             int64_t s_stride_n, int64_t s_stride_g, int s_dtype, const void* zero,
+                             int64_t z_stride_n, int64_t z_stride_g, int z_dtype, int64_t N,
+                             int64_t group_size, void* y, int64_t y_row_stride, void* stream) {
+  int rc = check_g(4, x, x_row_stride, M, K_pad, qweight, q_row_stride, scale, s_dtype, zero, z_dtype, N,
+                   group_size, y, y_row_stride);
+  if (rc != IMQ_OK) return rc;
+  if (M == 0 || N == 0) return IMQ_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xb = (const uint16_t*)x;
+  uint16_t* yb = (uint16_t*)y;
+  const uint8_t* q = (const uint8_t*)qweight;
+  if (M <= 16) {
+    rc = imq::skinny_w4(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g, s_dtype,
+                        zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
+  } else {
+    rc = imq::gemm_wq(4, xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
+                      s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
+  }
+  if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+  return imq::generic_gemv<4>(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
+                              s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb,
+                              y_row_stride, st);
+}
+
+extern "C" int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
+                             const void* qweight, int64_t q_row_stride, const void* scale,
+                             int64_t s_stride_n, int64_t s_stride_g, int s_dtype, const void* zero,
+                             int64_t z_stride_n, int64_t z_stride_g, int z_dtype, int64_t N,
+                             int64_t group_size, void* y, int64_t y_row_stride, void* stream) {
+  int rc = check_g(2, x, x_row_stride, M, K_pad, qweight, q_row_stride, scale, s_dtype, zero, z_dtype, N,
+                   group_size, y, y_row_stride);
+  if (rc != IMQ_OK) return rc;
+  if (M == 0 || N == 0) return IMQ_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xb = (const uint16_t*)x;
+  uint16_t* yb = (uint16_t*)y;
+  const uint8_t* q = (const uint8_t*)qweight;
+  if (M <= 16) {
+    rc = imq::skinny_w2(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g, s_dtype,
+                        zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
+  } else {
+    rc = imq::gemm_wq(2, xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
+                      s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
+  }
+  if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+  return imq::generic_gemv<2>(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
+                              s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb,
+                              y_row_stride, st);
+}
+
+extern "C" int imq_linear_w8(const void* x, int64_t x_row_stride, int64_t M, int64_t K,
+                             const void* qweight, int64_t q_row_stride, const void* scale,
+                             int64_t s_stride_n, int s_dtype, int64_t N, void* y, int64_t y_row_stride,
+                             void* stream) {
+  if (!x || !qweight || !scale || !y || M < 0 || N < 0 || K <= 0) return IMQ_ERR_INVALID;
+  if (q_row_stride < K || x_row_stride < K || y_row_stride < N || !dt_ok(s_dtype)) return IMQ_ERR_INVALID;
+  if (M == 0 || N == 0) return IMQ_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xb = (const uint16_t*)x;
+  uint16_t* yb = (uint16_t*)y;
+  int rc;
+  if (M <= 16) {
+    rc = imq::skinny_w8(xb, x_row_stride, M, K, (const int8_t*)qweight, q_row_stride, scale, s_stride_n,
+                        s_dtype, N, yb, y_row_stride, st);
+  } else {
+    rc = imq::gemm_wq(8, xb, x_row_stride, M, K, (const uint8_t*)qweight, q_row_stride, scale, s_stride_n,
+                      0, s_dtype, nullptr, 0, 0, s_dtype, N, 0, yb, y_row_stride, st);
+  }
+  if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+  return imq::generic_gemv<8>(xb, x_row_stride, M, K, (const uint8_t*)qweight, q_row_stride, scale,
+                              s_stride_n, 0, s_dtype, nullptr, 0, 0, s_dtype, N, 1, yb, y_row_stride, st);
+}

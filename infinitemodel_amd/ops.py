@@ -1,0 +1,221 @@
+"""torch-facing wrappers of the libimq kernels.
+
+Every function takes/returns torch tensors on a ROCm device, checks shapes/strides on the host,
+and launches on torch's current stream for that device. Outputs are allocated with torch (so
+they come from the caching allocator, and from the graph pool under stream capture); nothing
+here synchronizes, so these calls are capturable into HIP graphs.
+
+These are the product path: they never fall back to a CPU/torch computation. A missing library
+raises ``ImqUnavailable``, a rejected call raises ``ImqError``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import call, dtype_code
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _check_dev(*ts):
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise ValueError("libimq ops need tensors on a ROCm device")
+    for t in ts[1:]:
+        if t is not None and t.device != dev:
+            raise ValueError(f"device mismatch: {t.device} vs {dev}")
+    return dev
+
+
+def _rows2d(x: torch.Tensor) -> torch.Tensor:
+    if x.dim() != 2:
+        x = x.reshape(-1, x.shape[-1])
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    if x.stride(1) != 1 or (x.stride(0) % 8) != 0 or (x.data_ptr() % 16) != 0:
+        x = x.contiguous()
+    return x
+
+
+def _check_packed(q: torch.Tensor, dt=torch.uint8):
+    if q.dtype != dt or q.dim() < 2 or q.stride(-1) != 1:
+        raise ValueError(f"packed weight must be {dt} with a unit last stride, got {q.dtype} {tuple(q.stride())}")
+
+
+# ---------------------------------------------------------------------------------------------
+# dequant (bit-exact reference dequant)
+# ---------------------------------------------------------------------------------------------
+def _dequant_g(fn: str, bits: int, qweight, scale, zero, in_features: int, group_size: int, dtype):
+    dev = _check_dev(qweight, scale, zero)
+    _check_packed(qweight)
+    N = qweight.shape[0]
+    out = torch.empty((N, in_features), dtype=dtype, device=dev)
+    with torch.cuda.device(dev):
+        call(fn, _ptr(qweight), qweight.stride(0), _ptr(scale), scale.stride(0), scale.stride(1),
+             dtype_code(scale.dtype), _ptr(zero), zero.stride(0), zero.stride(1), dtype_code(zero.dtype),
+             N, in_features, group_size, _ptr(out), out.stride(0), dtype_code(dtype), _stream(dev))
+    return out
+
+
+def dequant_w4(qweight, scale, zero, in_features: int, group_size: int, dtype=torch.bfloat16):
+    """QuantLinear4._dequant(dtype) on the GPU (worker_quant.py:638-648), bit-exact."""
+    return _dequant_g("imq_dequant_w4", 4, qweight, scale, zero, in_features, group_size, dtype)
+
+
+def dequant_w2(qweight, scale, zero, in_features: int, group_size: int, dtype=torch.bfloat16):
+    """QuantLinear2._dequant(dtype) on the GPU (worker_quant.py:1652-1664), bit-exact."""
+    return _dequant_g("imq_dequant_w2", 2, qweight, scale, zero, in_features, group_size, dtype)
+
+
+def dequant_w8(qweight, scale, dtype):
+    """``qweight.to(x_dtype) * scale`` (worker_quant.py:439) with torch's dtype promotion: the
+    result dtype is ``torch.promote_types(dtype, scale.dtype)``."""
+    dev = _check_dev(qweight, scale)
+    _check_packed(qweight, torch.int8)
+    res = torch.promote_types(dtype, scale.dtype)
+    N, K = qweight.shape
+    out = torch.empty((N, K), dtype=res, device=dev)
+    with torch.cuda.device(dev):
+        call("imq_dequant_w8", _ptr(qweight), qweight.stride(0), _ptr(scale), scale.stride(0),
+             dtype_code(scale.dtype), N, K, _ptr(out), out.stride(0), dtype_code(res), _stream(dev))
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
+# fused dequant linears
+# ---------------------------------------------------------------------------------------------
+def _linear_g(fn: str, codes_per_byte: int, x, qweight, group_size: int, sz, out=None):
+    scale, zero = sz
+    dev = _check_dev(x, qweight, scale, zero)
+    _check_packed(qweight)
+    x = _rows2d(x)
+    Kpad = qweight.shape[1] * codes_per_byte
+    if x.shape[1] != Kpad:
+        x = torch.nn.functional.pad(x, (0, Kpad - x.shape[1])).contiguous()
+    M = x.shape[0]
+    N = qweight.shape[0]
+    ng = Kpad // group_size
+    if Kpad % group_size or tuple(scale.shape) != (N, ng) or tuple(zero.shape) != (N, ng):
+        raise ValueError(f"scale/zero must be [{N}, {ng}] for K_pad={Kpad}, group={group_size}; "
+                         f"got {tuple(scale.shape)} / {tuple(zero.shape)}")
+    if out is not None and (tuple(out.shape) != (M, N) or out.dtype != torch.bfloat16 or out.stride(1) != 1):
+        raise ValueError("out must be a bf16 [M, N] tensor with unit column stride")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        call(fn, _ptr(x), x.stride(0), M, Kpad, _ptr(qweight), qweight.stride(0), _ptr(scale), scale.stride(0),
+             scale.stride(1), dtype_code(scale.dtype), _ptr(zero), zero.stride(0), zero.stride(1),
+             dtype_code(zero.dtype), N, group_size, _ptr(y), y.stride(0), _stream(dev))
+    return y
+
+
+def linear_w4(x, qweight, group_size: int, sz, out=None):
+    """``op(x[M,Kpad] bf16, qweight u8[N,Kpad/2], group, (scale, zero)) -> y[M,N] bf16``: the
+    signature of the op returned by the reference's _w4a16_triton_op (worker_quant.py:1180-1217)."""
+    return _linear_g("imq_linear_w4", 2, x, qweight, group_size, sz, out)
+
+
+def linear_w2(x, qweight, group_size: int, sz, out=None):
+    """int2 twin (worker_quant.py:1876-1910): qweight u8 [N, Kpad/4]."""
+    return _linear_g("imq_linear_w2", 4, x, qweight, group_size, sz, out)
+
+
+def linear_w8(x, qweight, scale, out=None):
+    """``op(x, qweight int8[N,K], scale[N,1]) -> y bf16 [M,N]`` (worker_quant.py:1022-1048)."""
+    dev = _check_dev(x, qweight, scale)
+    _check_packed(qweight, torch.int8)
+    x = _rows2d(x)
+    M, K = x.shape
+    N = qweight.shape[0]
+    if qweight.shape[1] != K:
+        raise ValueError(f"x has {K} columns, qweight {qweight.shape[1]}")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        call("imq_linear_w8", _ptr(x), x.stride(0), M, K, _ptr(qweight), qweight.stride(0), _ptr(scale),
+             scale.stride(0), dtype_code(scale.dtype), N, _ptr(y), y.stride(0), _stream(dev))
+    return y
+
+
+# ---------------------------------------------------------------------------------------------
+# fused MoE experts
+# ---------------------------------------------------------------------------------------------
+def moe_rows_w4(x, eid, q, scale, zero, group_size: int, in_features: int):
+    """``op(x[B,Kin], eid[B], q[E,N,Kpad/2], scale, zero, group, in_features) -> y[B,N] bf16``:
+    the op returned by the reference's _w4a16_moe_op (worker_quant.py:1452-1487)."""
+    dev = _check_dev(x, eid, q, scale, zero)
+    _check_packed(q)
+    if scale.dtype != zero.dtype:
+        zero = zero.to(scale.dtype)
+    x = _rows2d(x)
+    Kpad = q.shape[2] * 2
+    if x.shape[1] != Kpad:
+        x = torch.nn.functional.pad(x, (0, Kpad - x.shape[1])).contiguous()
+    eid = eid.to(torch.int32).contiguous()
+    B = x.shape[0]
+    E, N = q.shape[0], q.shape[1]
+    ng = Kpad // group_size
+    if tuple(scale.shape) != (E, N, ng) or tuple(zero.shape) != (E, N, ng) or eid.numel() != B:
+        raise ValueError("scale/zero must be [E, N, K_pad/group] and eid [B]")
+    y = torch.empty((B, N), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        call("imq_moe_rows_w4", _ptr(x), x.stride(0), B, Kpad, _ptr(eid), E, _ptr(q), q.stride(0), q.stride(1),
+             _ptr(scale), scale.stride(0), scale.stride(1), scale.stride(2), _ptr(zero), zero.stride(0),
+             zero.stride(1), zero.stride(2), dtype_code(scale.dtype), N, group_size, _ptr(y), y.stride(0),
+             _stream(dev))
+    return y
+
+
+def moe_workspace_bytes(T: int, top_k: int, E: int, H: int, I: int, group_size: int) -> int:
+    return int(_lib.lib().imq_moe_workspace_bytes(T, top_k, E, H, I, group_size))
+
+
+def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=None):
+    """One MoE layer's experts forward: ``out[t] = sum_j w[t,j] * down_e(silu(gate) * up)``.
+
+    ``gu`` / ``dn`` are (qweight, scale, zero, in_features) of the gate_up [E, 2I, H_pad/2] and
+    down [E, H, I_pad/2] Packed4Tensor3D holders. Semantics of the transformers eager experts
+    loop (modeling_olmoe.py:301-325) as fused by worker_quant.py:2167-2191."""
+    gq, gs, gz, H = gu
+    dq, ds, dz, I = dn
+    dev = _check_dev(hidden, topk_idx, topk_w, gq, gs, gz, dq, ds, dz)
+    for t in (gq, dq):
+        _check_packed(t)
+    T = hidden.shape[0]
+    k = topk_idx.shape[1]
+    E = gq.shape[0]
+    if gq.shape[1] != 2 * I or dq.shape[1] != H:
+        raise ValueError("gate_up must be [E, 2I, .] and down [E, H, .]")
+    sdt = gs.dtype
+    gz = gz if gz.dtype == sdt else gz.to(sdt)
+    ds = ds if ds.dtype == sdt else ds.to(sdt)
+    dz = dz if dz.dtype == sdt else dz.to(sdt)
+    for t in (gs, gz, ds, dz):
+        if t.stride(2) != 1:
+            raise ValueError("scale/zero need a unit last stride")
+    if gs.stride() != gz.stride() or ds.stride() != dz.stride():
+        gz = gz.contiguous() if gz.stride() != gs.stride() else gz
+        gs, gz = gs.contiguous(), gz.contiguous()
+        ds, dz = ds.contiguous(), dz.contiguous()
+    x = _rows2d(hidden)
+    H_pad = gq.shape[2] * 2
+    if x.shape[1] != H_pad:
+        x = torch.nn.functional.pad(x, (0, H_pad - x.shape[1])).contiguous()
+    idx = topk_idx.to(torch.int32).contiguous()
+    w = topk_w.to(torch.bfloat16).contiguous()
+    need = moe_workspace_bytes(T, k, E, H, I, group_size)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        call("imq_moe_experts_w4", _ptr(x), x.stride(0), T, H, k, _ptr(idx), _ptr(w), E,
+             _ptr(gq), gq.stride(0), gq.stride(1), _ptr(gs), _ptr(gz), gs.stride(0), gs.stride(1), I,
+             _ptr(dq), dq.stride(0), dq.stride(1), _ptr(ds), _ptr(dz), ds.stride(0), ds.stride(1),
+             dtype_code(sdt), group_size, _ptr(out), out.stride(0), _ptr(workspace),
+             workspace.numel() * workspace.element_size(), _stream(dev))
+    return out

@@ -1,0 +1,192 @@
+"""GPU parity: HIP dequant (bit-exact) and fused dequant linears vs the CPU oracle.
+
+Tolerances for the fused linears:
+  * north star: normwise max relative error <= 1e-2 of the oracle's dequantize-then-matmul
+    (bf16-rounded reference weights), and mean relative error <= 5e-3;
+  * per element, against the exact fp64 product with the un-rounded weights (q - z) * s that the
+    kernels accumulate with: |y - ref| <= 2^-8 |ref| + 1e-5 max|ref| -- i.e. only the final bf16
+    rounding and fp32 accumulation noise; this catches any single wrong output element.
+"""
+import numpy as np
+import pytest
+
+from oracle import quant as oq
+from tests import _cases as C
+
+pytestmark = pytest.mark.gpu
+
+MAX_REL = 1e-2
+MEAN_REL = 5e-3
+
+
+def _bits(t):
+    import torch
+    return t.view(torch.int16).cpu().numpy()
+
+
+@pytest.mark.parametrize("N,K,G", [(4096, 4096, 128), (37, 384, 128), (64, 256, 64), (48, 200, 128)])
+def test_dequant_w4_bitexact(dev, N, K, G):
+    import torch
+    from infinitemodel_amd import ops
+    c = C.int4_case(N, K, G, seed=N + K)
+    q = C.u8(c["q"], dev)
+    s = C.to_torch(c["s"], "bf16", dev)
+    z = C.to_torch(c["z"], "bf16", dev)
+    out = ops.dequant_w4(q, s, z, c["in_f"], G, torch.bfloat16)
+    torch.cuda.synchronize()
+    ref = oq.f32_to_bf16_bits(c["Wd"]).view(np.int16)
+    assert np.array_equal(_bits(out), ref)
+
+
+@pytest.mark.parametrize("odt", ["fp16", "fp32"])
+def test_dequant_w4_other_dtypes(dev, odt):
+    import torch
+    from infinitemodel_amd import ops
+    c = C.int4_case(64, 256, 128, seed=3)
+    q = C.u8(c["q"], dev)
+    s = C.to_torch(c["s"], "bf16", dev)
+    z = C.to_torch(c["z"], "bf16", dev)
+    tdt = {"fp16": torch.float16, "fp32": torch.float32}[odt]
+    out = ops.dequant_w4(q, s, z, c["in_f"], 128, tdt)
+    ref = oq.dequant_int4(c["q"], c["s"], c["z"], c["in_f"], 128, odt)
+    assert np.array_equal(C.t2np(out), ref)
+
+
+def test_dequant_w2_bitexact_nonint_zero(dev):
+    """BASELINE C3 style: fp16 non-integer zeros -> the two-rounding reference rule."""
+    import torch
+    from infinitemodel_amd import ops
+    c = C.int2_random_case(128, 512, 64, seed=2000, dt="fp16")
+    q = C.u8(c["q"], dev)
+    s = C.to_torch(c["s"], "fp16", dev)
+    z = C.to_torch(c["z"], "fp16", dev)
+    out = ops.dequant_w2(q, s, z, c["in_f"], 64, torch.bfloat16)
+    assert np.array_equal(_bits(out), oq.f32_to_bf16_bits(c["Wd"]).view(np.int16))
+
+
+def test_dequant_w8_promotion(dev):
+    import torch
+    from infinitemodel_amd import ops
+    c = C.int8_case(64, 999, seed=5, dt="fp16")
+    q = C.u8(c["q"], dev)
+    s = C.to_torch(c["s"], "fp16", dev)
+    out = ops.dequant_w8(q, s, torch.bfloat16)          # bf16 x fp16 -> fp32 (torch promotion)
+    assert out.dtype == torch.float32
+    ref, res = oq.dequant_int8(c["q"], c["s"], "fp16", "bf16")
+    assert res == "fp32"
+    assert np.array_equal(C.t2np(out), ref)
+
+
+def _linear_check(dev, c, M, seed, bits=4, view_pad=0):
+    import torch
+    from infinitemodel_amd import ops
+    r = C.rng(seed)
+    Kpad = c["q"].shape[1] * (8 // bits)
+    x = np.zeros((M, Kpad), np.float32)
+    x[:, : c["in_f"]] = C.bf16_normal(r, (M, c["in_f"]))
+    q = C.u8(c["q"], dev)
+    if view_pad:
+        buf = torch.zeros((q.shape[0], q.shape[1] + view_pad), dtype=torch.uint8, device=dev)
+        buf[:, : q.shape[1]].copy_(q)
+        q = buf[:, : q.shape[1]]
+    s = C.to_torch(c["s"], c["dt"], dev)
+    z = C.to_torch(c["z"], c["dt"], dev)
+    xt = C.to_torch(x, "bf16", dev)
+    fn = ops.linear_w4 if bits == 4 else ops.linear_w2
+    y = fn(xt, q, c["G"], (s, z))
+    ref = oq.linear_ref(x[:, : c["in_f"]], c["Wd"])
+    yn = C.t2np(y)
+    assert yn.shape == ref.shape
+    assert np.isfinite(yn).all()
+    mr, me = oq.max_rel(yn, ref), oq.mean_rel(yn, ref)
+    assert mr <= MAX_REL and me <= MEAN_REL, (M, mr, me)
+    unpack = oq.unpack_int4 if bits == 4 else oq.unpack_int2
+    exact = oq.linear_ref(x[:, : c["in_f"]], oq.dequant_exact(unpack(c["q"]), c["s"], c["z"], c["G"], c["in_f"]))
+    tol = 2.0 ** -8 * np.abs(exact) + 1e-5 * np.abs(exact).max()
+    bad = np.abs(yn - exact) > tol
+    assert not bad.any(), (M, int(bad.sum()), np.argwhere(bad)[:5].tolist())
+    return y
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 16])
+def test_linear_w4_c1_shape(dev, M):
+    """BASELINE C1 shape 1x4096 -> 4096 (and the C2 M values)."""
+    c = C.int4_case(4096, 4096, 128, seed=0)
+    _linear_check(dev, c, M, seed=100 + M)
+
+
+@pytest.mark.parametrize("N,K", [(37, 384), (1000, 256), (16, 128), (17, 1152), (6144, 4096)])
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_linear_w4_ragged(dev, N, K, M):
+    c = C.int4_case(N, K, 128, seed=N * 7 + K)
+    _linear_check(dev, c, M, seed=M)
+
+
+def test_linear_w4_in_features_not_multiple_of_group(dev):
+    c = C.int4_case(80, 300, 128, seed=11)     # K_pad = 384, x zero-padded past 300
+    for M in (1, 3, 16):
+        _linear_check(dev, c, M, seed=M)
+
+
+def test_linear_w4_dealias_view(dev):
+    """The reference's #dram-dealias padded row view (worker_quant.py:685-690) must read the same."""
+    c = C.int4_case(512, 1024, 128, seed=21)
+    for M in (1, 4, 16):
+        _linear_check(dev, c, M, seed=M, view_pad=64)
+
+
+@pytest.mark.parametrize("G", [64, 256])
+def test_linear_w4_other_groups(dev, G):
+    c = C.int4_case(96, 1024, G, seed=G)
+    for M in (1, 5):
+        _linear_check(dev, c, M, seed=M)
+
+
+@pytest.mark.parametrize("M", [17, 33, 64])
+def test_linear_w4_midrange_rows(dev, M):
+    c = C.int4_case(256, 512, 128, seed=31)
+    _linear_check(dev, c, M, seed=M)
+
+
+def test_linear_w4_repeat_calls_identical(dev):
+    """Repeated M=1 calls are bit-identical (no stale accumulator, deterministic reduction)."""
+    import torch
+    from infinitemodel_amd import ops
+    c = C.int4_case(2048, 2048, 128, seed=9)
+    q = C.u8(c["q"], dev)
+    s = C.to_torch(c["s"], "bf16", dev)
+    z = C.to_torch(c["z"], "bf16", dev)
+    x = C.to_torch(C.bf16_normal(C.rng(1), (1, 2048)), "bf16", dev)
+    ys = [ops.linear_w4(x, q, 128, (s, z)) for _ in range(4)]
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+
+
+def test_linear_w4_one_hot_column_extraction(dev):
+    """x = e_k picks column k of the dequantized weight (pins the K index mapping end to end)."""
+    import torch
+    from infinitemodel_amd import ops
+    c = C.int4_case(64, 512, 128, seed=4)
+    q = C.u8(c["q"], dev)
+    s = C.to_torch(c["s"], "bf16", dev)
+    z = C.to_torch(c["z"], "bf16", dev)
+    ks = [0, 1, 7, 8, 31, 32, 127, 128, 300, 511]
+    x = np.zeros((len(ks), 512), np.float32)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    y = C.t2np(ops.linear_w4(C.to_torch(x, "bf16", dev), q, 128, (s, z)))
+    for i, k in enumerate(ks):
+        np.testing.assert_allclose(y[i], oq.round_to(c["Wd"][:, k], "bf16"), rtol=0, atol=1e-6 + 4e-3 * np.abs(c["Wd"][:, k]))
+
+
+@pytest.mark.parametrize("sdt", ["fp16", "fp32"])
+def test_linear_w4_scale_dtypes(dev, sdt):
+    """fp16 / fp32 scale-zero storage (GPTQ-style caches keep fp32 s/z)."""
+    c = C.int4_case(128, 512, 128, seed=12, dt="bf16")
+    c = dict(c)
+    c["s"] = oq.round_to(c["s"], sdt)
+    c["z"] = oq.round_to(c["z"], sdt)
+    c["dt"] = sdt
+    c["Wd"] = oq.dequant_int4(c["q"], c["s"], c["z"], c["in_f"], 128, "bf16")
+    for M in (1, 16):
+        _linear_check(dev, c, M, seed=M)
