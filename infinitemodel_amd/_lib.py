@@ -16,7 +16,7 @@ import os
 import threading
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "_lib", "libimq.so")
+LIB_PATH = os.environ.get("IMQ_LIB_PATH") or os.path.join(HERE, "_lib", "libimq.so")
 
 IMQ_DT_BF16, IMQ_DT_FP16, IMQ_DT_FP32 = 0, 1, 2
 IMQ_OK, IMQ_ERR_INVALID, IMQ_ERR_UNSUPPORTED, IMQ_ERR_ALIGN = 0, -1, -2, -3

@@ -49,8 +49,208 @@ struct SkinnyArgs {
 constexpr int kStep = 128;          // codes per K-step
 constexpr int kXPad = 8;            // bf16 elements of padding per LDS activation row
 
+// Raw 16/32-bit scale/zero word -> fp32 value rounded to bf16 (conversion deferred to use, so the
+// loads of a whole unit can be issued back to back).
+template <int DT>
+IMQ_DEV uint32_t load_raw(const void* p, int64_t idx) {
+  if constexpr (DT == IMQ_DT_FP32) return ((const uint32_t*)p)[idx];
+  else return ((const uint16_t*)p)[idx];
+}
+template <int DT>
+IMQ_DEV float raw_to_bf16_f32(uint32_t r) {
+  if constexpr (DT == IMQ_DT_BF16) return __uint_as_float(r << 16);
+  else if constexpr (DT == IMQ_DT_FP16) return round_bf16(__half2float(__ushort_as_half((unsigned short)r)));
+  else return round_bf16(__uint_as_float(r));
+}
+
+// x resident in LDS (M * K_pad fits). One workgroup = one 16-row tile; its W waves split K,
+// wave w owning steps [(r*W + w)*S, +S) of round r. Each wave issues all S loads of a round
+// back to back (S*1 KB per wave in flight), then consumes them; latency is hidden by the many
+// resident waves/workgroups, not by in-wave double buffering. Steps past K and rows past N are
+// clamped to valid addresses (zero scale / never stored), so every load is unconditional.
+//
+// STRIP: with one group per step (G == 128), contiguous per-row scale/zero storage and K-steps a
+// multiple of S, a wave's S scales of a row are S adjacent values: they are fetched with one
+// vector load per row (all four lanes of a row load the same strip) instead of S scattered
+// 2-byte loads, which would cost a cache-line lookup per row per step in the texture path.
+template <int S, int MC, int SDT, int ZDT, bool STRIP>
+__global__ __launch_bounds__(1024) void w4_skinny_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform -> SGPR
+  const int W = blockDim.x >> 6;
+  const int nl = lane & 15;
+  const int jl = lane >> 4;
+  constexpr int RC = (MC < 4) ? MC : 4;
+  constexpr int SZB = (SDT == IMQ_DT_FP32) ? 4 : 2;
+  constexpr int ZZB = (ZDT == IMQ_DT_FP32) ? 4 : 2;
+
+  const int KS = a.Kpad / kStep;
+  const int R = (KS + W * S - 1) / (W * S);
+  const int xls = KS * kStep + kXPad;
+  uint16_t* xl = (uint16_t*)smem;                                    // [M][xls]
+  float* xs = (float*)(smem + (size_t)a.M * xls * 2);                // [KS][16]
+  float* red = xs + (size_t)KS * 16;                                 // [W][256]
+  const int gsh = 31 - __builtin_clz(a.G / kStep);                   // steps per group = 2^gsh
+  const int tile = blockIdx.x;
+
+  int row = tile * 16 + nl;
+  row = row < a.N ? row : a.N - 1;
+  const uint8_t* qrow = a.q + (int64_t)row * a.sqn + 16 * jl;
+  const unsigned char* srow = (const unsigned char*)a.sc + (int64_t)row * a.ssn * SZB;
+  const unsigned char* zrow = (const unsigned char*)a.zr + (int64_t)row * a.szn * ZZB;
+  const int64_t ssg_b = a.ssg * SZB, szg_b = a.szg * ZZB;
+
+  u32x4_t wv[S];
+  uint32_t sr[S], zr[S];
+  // strip words: S values of SZB bytes = S*SZB/4 dwords
+  constexpr int SW = STRIP ? (S * SZB + 3) / 4 : 1;
+  constexpr int ZW = STRIP ? (S * ZZB + 3) / 4 : 1;
+  uint32_t sst[SW], zst[ZW];
+  auto load_round = [&](int rnd) {
+    const int sbase = (rnd * W + wave) * S;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      int s = sbase + i;
+      s = s < KS ? s : KS - 1;
+      wv[i] = __builtin_nontemporal_load((const u32x4_t*)(qrow + (int64_t)s * 64));
+      if constexpr (!STRIP) {
+        const int64_t g = s >> gsh;
+        sr[i] = load_raw<SDT>(srow + g * ssg_b, 0);
+        zr[i] = load_raw<ZDT>(zrow + g * szg_b, 0);
+      }
+    }
+    if constexpr (STRIP) {
+      const int64_t g0 = sbase < KS ? sbase : 0;     // whole strip past K: any valid strip
+#pragma unroll
+      for (int v = 0; v < SW; v += 4) {
+        const u32x4_t t = *(const u32x4_t*)(srow + g0 * SZB + 4 * v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) if (v + e < SW) sst[v + e] = t[e];
+      }
+#pragma unroll
+      for (int v = 0; v < ZW; v += 4) {
+        const u32x4_t t = *(const u32x4_t*)(zrow + g0 * ZZB + 4 * v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) if (v + e < ZW) zst[v + e] = t[e];
+      }
+    }
+  };
+  // raw 16/32-bit scale and zero word of step i of the current round
+  auto s_raw = [&](int i) -> uint32_t {
+    if constexpr (!STRIP) return sr[i];
+    else if constexpr (SZB == 4) return sst[i];
+    else return (i & 1) ? (sst[i >> 1] >> 16) : (sst[i >> 1] & 0xffffu);
+  };
+  auto z_raw = [&](int i) -> uint32_t {
+    if constexpr (!STRIP) return zr[i];
+    else if constexpr (ZZB == 4) return zst[i];
+    else return (i & 1) ? (zst[i >> 1] >> 16) : (zst[i >> 1] & 0xffffu);
+  };
+
+  // first round's weights are independent of x: issue them before staging
+  load_round(0);
+
+  // ---- stage x (permuted) and per-step row sums --------------------------------------------
+  {
+    const int nblk = KS * (kStep / 8);
+    const int total = a.M * nblk;
+    for (int idx = threadIdx.x; idx < 16 * KS; idx += blockDim.x) xs[idx] = 0.f;
+    lds_barrier();
+    for (int base = threadIdx.x; base < total; base += 4 * blockDim.x) {
+      u32x4_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        int idx = base + u * blockDim.x;
+        idx = idx < total ? idx : total - 1;
+        const int m = idx / nblk;
+        const int b = idx - m * nblk;
+        v[u] = *(const u32x4_t*)(a.x + (int64_t)m * a.sxm + 8 * b);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int idx = base + u * blockDim.x;
+        if (idx < total) {
+          const int m = idx / nblk;
+          const int b = idx - m * nblk;
+          *(u32x4_t*)(xl + m * xls + 8 * b) = permute_x8(v[u]);
+          float sum = 0.f;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[u][d] << 16) + __uint_as_float(v[u][d] & 0xffff0000u);
+          // the 16 blocks of one step are 16 consecutive idx (nblk is a multiple of 16, and
+          // idx groups of 16 lie entirely inside or outside [0, total))
+#pragma unroll
+          for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+          if ((b & 15) == 0) xs[(b >> 4) * 16 + m] = sum;
+        }
+      }
+    }
+    lds_barrier();
+  }
+
+  // A rows m >= M read row M-1: they only feed D rows that are never stored.
+  const uint16_t* xlane = xl + (nl < a.M ? nl : a.M - 1) * xls + 32 * jl;
+  const float* xslane = xs + 4 * jl;
+  const uint32_t magic = magic_bf16_128x2();
+  float yacc[4] = {0.f, 0.f, 0.f, 0.f};
+
+  for (int rnd = 0; rnd < R; ++rnd) {
+    if (rnd > 0) load_round(rnd);
+    // steps in pairs: two independent MFMA chains interleaved (ILP across the MFMA latency).
+    // Everything the corrections need (row sums from LDS, scale terms) is read *before* the
+    // MFMAs are issued, so no LDS return can land in a register an in-flight MFMA still reads.
+#pragma unroll
+    for (int i = 0; i < S; i += 2) {
+      const int s0a = (rnd * W + wave) * S + i;
+      const int s0b = s0a + 1;
+      const bool va = s0a < KS, vb = s0b < KS;
+      const int sa = va ? s0a : KS - 1;
+      const int sb = vb ? s0b : KS - 1;
+      const f32x4_t xsa = *(const f32x4_t*)(xslane + sa * 16);
+      const f32x4_t xsb = *(const f32x4_t*)(xslane + sb * 16);
+      bf16x8_t aa[4], ab[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        aa[k] = *(const bf16x8_t*)(xlane + sa * kStep + 8 * k);
+        ab[k] = *(const bf16x8_t*)(xlane + sb * kStep + 8 * k);
+      }
+      const float sca = va ? raw_to_bf16_f32<SDT>(s_raw(i)) : 0.f;
+      const float scb = vb ? raw_to_bf16_f32<SDT>(s_raw(i + 1)) : 0.f;
+      const float cza = -(128.f + raw_to_bf16_f32<ZDT>(z_raw(i))) * sca;
+      const float czb = -(128.f + raw_to_bf16_f32<ZDT>(z_raw(i + 1))) * scb;
+      f32x4_t acca = {0.f, 0.f, 0.f, 0.f}, accb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acca = mfma16x16x32(aa[k], unpack_nib8_bf16(wv[i][k], magic), acca);
+        accb = mfma16x16x32(ab[k], unpack_nib8_bf16(wv[i + 1][k], magic), accb);
+      }
+#pragma unroll
+      for (int q = 0; q < RC; ++q) {
+        yacc[q] = fmaf(cza, xsa[q], yacc[q]);
+        yacc[q] = fmaf(czb, xsb[q], yacc[q]);
+        yacc[q] = fmaf(sca, acca[q], yacc[q]);
+        yacc[q] = fmaf(scb, accb[q], yacc[q]);
+      }
+    }
+  }
+
+  // cross-wave reduction in a fixed order
+#pragma unroll
+  for (int q = 0; q < 4; ++q) red[wave * 256 + (4 * jl + q) * 16 + nl] = yacc[q];
+  lds_barrier();
+  const int n0 = tile * 16;
+  for (int e = threadIdx.x; e < 16 * a.M; e += blockDim.x) {
+    const int m = e >> 4;
+    const int n = e & 15;
+    float sum = 0.f;
+    for (int w = 0; w < W; ++w) sum += red[w * 256 + e];
+    if (n0 + n < a.N) a.y[(int64_t)m * a.sym + n0 + n] = (uint16_t)f32_to_bf16_bits(sum);
+  }
+}
+
+// x too large for LDS (large M * K_pad): K is staged in chunks, restaged per tile.
 template <int W, int MC, int SDT, int ZDT>
-__global__ __launch_bounds__(64 * W) void w4_skinny_kernel(SkinnyArgs a) {
+__global__ __launch_bounds__(64 * W) void w4_skinny_chunked_kernel(SkinnyArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -151,7 +351,7 @@ __global__ __launch_bounds__(64 * W) void w4_skinny_kernel(SkinnyArgs a) {
               } else {
                 av = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
               }
-              acc = mfma16x16x32(av, unpack_nib8_bf16(wv[u][i]), acc);
+              acc = mfma16x16x32(av, unpack_nib8_bf16(wv[u][i], magic_bf16_128x2()), acc);
             }
             const f32x4_t xsum = *(const f32x4_t*)(xs + sl * 16 + 4 * jl);
             const float sc = sv[u];
@@ -186,9 +386,9 @@ __global__ __launch_bounds__(64 * W) void w4_skinny_kernel(SkinnyArgs a) {
 
 // ---------------------------------------------------------------------------------------------
 // Generic fallback: any bit width (2/4/8), any group size, any stride/alignment, M <= 16.
-// One wave per output row; every weight is dequantized to the reference's exact bf16 value
-// bf16(bf16(q - bf16(z)) * bf16(s)) (worker_quant.py:646-647) and accumulated in fp32, i.e.
-// literally dequantize-then-matmul. Slow but faithful; used for shapes the fast kernels reject.
+// One wave per output row; every weight is dequantized in fp32 as (q - bf16(z)) * bf16(s), the
+// same un-rounded weight the fast kernels accumulate with, and accumulated in fp32. Slow but
+// simple; used for shapes the fast kernels reject.
 // ---------------------------------------------------------------------------------------------
 struct GenericArgs {
   const uint16_t* x;
@@ -227,7 +427,7 @@ __global__ __launch_bounds__(256) void generic_gemv_kernel(GenericArgs a) {
       const int64_t g = k / a.G;
       const float z = load_as_bf16_f32<ZDT>(a.zr, row * a.szn + g * a.szg);
       const float s = load_as_bf16_f32<SDT>(a.sc, row * a.ssn + g * a.ssg);
-      w = round_bf16(round_bf16(code - z) * s);
+      w = (code - z) * s;
     }
 #pragma unroll
     for (int m = 0; m < 16; ++m)
@@ -276,30 +476,73 @@ DevInfo device_info() {
   return cache[dev];
 }
 
-template <int W, int MC, int SDT, int ZDT>
-int launch_skinny_w4(const SkinnyArgs& a, size_t lds, int grid, hipStream_t st) {
-  auto kern = w4_skinny_kernel<W, MC, SDT, ZDT>;
+template <typename K>
+int launch_with_lds(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t st, const SkinnyArgs& a) {
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
   }
-  kern<<<dim3(grid), dim3(64 * W), lds, st>>>(a);
+  kern<<<grid, block, lds, st>>>(a);
   IMQ_LAUNCH_CHECK();
   return IMQ_OK;
 }
 
+template <int S, int SDT, int ZDT, bool STRIP>
+int skinny_resident_m(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
+  const dim3 g(grid), b(64 * W);
+  if (a.M == 1) return launch_with_lds(w4_skinny_kernel<S, 1, SDT, ZDT, STRIP>, g, b, lds, st, a);
+  if (a.M == 2) return launch_with_lds(w4_skinny_kernel<S, 2, SDT, ZDT, STRIP>, g, b, lds, st, a);
+  if (a.M <= 4) return launch_with_lds(w4_skinny_kernel<S, 4, SDT, ZDT, STRIP>, g, b, lds, st, a);
+  return launch_with_lds(w4_skinny_kernel<S, 16, SDT, ZDT, STRIP>, g, b, lds, st, a);
+}
+
+template <int S, int SDT, int ZDT>
+int skinny_resident(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
+  constexpr int SZB = (SDT == IMQ_DT_FP32) ? 4 : 2;
+  constexpr int ZZB = (ZDT == IMQ_DT_FP32) ? 4 : 2;
+  const int KS = a.Kpad / kStep;
+  const bool strip = a.G == kStep && (KS % S) == 0 && a.ssg == 1 && a.szg == 1 &&
+                     ((uintptr_t)a.sc % 16) == 0 && ((uintptr_t)a.zr % 16) == 0 &&
+                     ((a.ssn * SZB) % 16) == 0 && ((a.szn * ZZB) % 16) == 0;
+  if (strip) return skinny_resident_m<S, SDT, ZDT, true>(a, lds, grid, W, st);
+  return skinny_resident_m<S, SDT, ZDT, false>(a, lds, grid, W, st);
+}
+
 template <int W, int SDT, int ZDT>
-int skinny_w4_mc(const SkinnyArgs& a, size_t lds, int grid, hipStream_t st) {
-  if (a.M == 1) return launch_skinny_w4<W, 1, SDT, ZDT>(a, lds, grid, st);
-  if (a.M == 2) return launch_skinny_w4<W, 2, SDT, ZDT>(a, lds, grid, st);
-  if (a.M <= 4) return launch_skinny_w4<W, 4, SDT, ZDT>(a, lds, grid, st);
-  return launch_skinny_w4<W, 16, SDT, ZDT>(a, lds, grid, st);
+int skinny_chunked(const SkinnyArgs& a, size_t lds, int grid, hipStream_t st) {
+  const dim3 g(grid), b(64 * W);
+  if (a.M == 1) return launch_with_lds(w4_skinny_chunked_kernel<W, 1, SDT, ZDT>, g, b, lds, st, a);
+  if (a.M == 2) return launch_with_lds(w4_skinny_chunked_kernel<W, 2, SDT, ZDT>, g, b, lds, st, a);
+  if (a.M <= 4) return launch_with_lds(w4_skinny_chunked_kernel<W, 4, SDT, ZDT>, g, b, lds, st, a);
+  return launch_with_lds(w4_skinny_chunked_kernel<W, 16, SDT, ZDT>, g, b, lds, st, a);
 }
 
 template <int SDT, int ZDT>
-int skinny_w4_w(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
-  if (W == 4) return skinny_w4_mc<4, SDT, ZDT>(a, lds, grid, st);
-  return skinny_w4_mc<8, SDT, ZDT>(a, lds, grid, st);
+int skinny_dispatch(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
+  SkinnyArgs a = a0;
+  const int KS = a.Kpad / kStep;
+  const int NT = (a.N + 15) / 16;
+  // S steps (S KB of packed weights) per wave per round; W = waves per tile (<= 16).
+  const int S = (KS >= 16) ? 8 : 4;
+  int W = (KS + S - 1) / S;
+  if (W > 16) W = 16;
+  const size_t resident = (size_t)a.M * (KS * kStep + kXPad) * 2 + (size_t)KS * 64 + (size_t)W * 256 * 4;
+  if (resident <= (size_t)di.max_lds) {
+    a.chunk_steps = KS;
+    if (S == 8) return skinny_resident<8, SDT, ZDT>(a, resident, NT, W, st);
+    return skinny_resident<4, SDT, ZDT>(a, resident, NT, W, st);
+  }
+  // chunked fallback
+  const int Wc = 8;
+  const size_t redc = (size_t)2 * Wc * 256 * 4;
+  int cs = KS;
+  auto need = [&](int c) { return (size_t)a.M * (c * kStep + kXPad) * 2 + (size_t)c * 64 + redc; };
+  while (cs > 1 && need(cs) > (size_t)di.max_lds) cs = (cs + 1) / 2;
+  if (need(cs) > (size_t)di.max_lds) return IMQ_ERR_UNSUPPORTED;
+  a.chunk_steps = cs;
+  int grid = di.cus;
+  if (grid > NT) grid = NT;
+  return skinny_chunked<8, SDT, ZDT>(a, need(cs), grid, st);
 }
 
 // Fast path eligibility + launch. Returns IMQ_ERR_UNSUPPORTED when the caller must fall back.
@@ -307,28 +550,16 @@ int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
               int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st) {
   if (M < 1 || M > 16 || G % kStep != 0 || Kpad % G != 0 || Kpad <= 0) return IMQ_ERR_UNSUPPORTED;
+  if (((G / kStep) & (G / kStep - 1)) != 0) return IMQ_ERR_UNSUPPORTED;   // groups of 2^k steps
   if (((uintptr_t)q & 15) || (sqn & 15) || ((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
   if (N > (1 << 30) || Kpad > (1 << 28)) return IMQ_ERR_UNSUPPORTED;
   if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
   const DevInfo di = device_info();
-  const int KS = (int)(Kpad / kStep);
-  const int W = (KS >= 16) ? 8 : 4;
-  const size_t red_bytes = (size_t)2 * W * 256 * 4;
-  const size_t budget = (size_t)di.max_lds;
-  // chunk so that x [M][cs*128+pad] + xsum [cs][16] + reduction fit
-  int cs = KS;
-  auto need = [&](int c) { return (size_t)M * (c * kStep + kXPad) * 2 + (size_t)c * 64 + red_bytes; };
-  while (cs > 1 && need(cs) > budget) cs = (cs + 1) / 2;
-  if (need(cs) > budget) return IMQ_ERR_UNSUPPORTED;
-  SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, cs};
-  const int NT = (int)imq_cdiv(N, 16);
-  const int per_cu = (need(cs) <= budget / 2) ? 2 : 1;
-  int grid = di.cus * per_cu;
-  if (grid > NT) grid = NT;
+  SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, 0};
   switch (sdt) {
-    case IMQ_DT_BF16: return skinny_w4_w<IMQ_DT_BF16, IMQ_DT_BF16>(a, need(cs), grid, W, st);
-    case IMQ_DT_FP16: return skinny_w4_w<IMQ_DT_FP16, IMQ_DT_FP16>(a, need(cs), grid, W, st);
-    case IMQ_DT_FP32: return skinny_w4_w<IMQ_DT_FP32, IMQ_DT_FP32>(a, need(cs), grid, W, st);
+    case IMQ_DT_BF16: return skinny_dispatch<IMQ_DT_BF16, IMQ_DT_BF16>(a, di, st);
+    case IMQ_DT_FP16: return skinny_dispatch<IMQ_DT_FP16, IMQ_DT_FP16>(a, di, st);
+    case IMQ_DT_FP32: return skinny_dispatch<IMQ_DT_FP32, IMQ_DT_FP32>(a, di, st);
   }
   return IMQ_ERR_INVALID;
 }

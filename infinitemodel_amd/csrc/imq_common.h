@@ -84,15 +84,27 @@ IMQ_DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// 8 int4 codes (one u32, code i at bits 4i..4i+3) -> 8 bf16 values (128 + code), exact.
+// The bf16 bit pattern 0x4300 (= 128.0) in both halves, produced in a VGPR the compiler cannot
+// constant-fold: `(x & mask) | magic` then selects one v_and_or_b32 (mask in an SGPR, magic in
+// a VGPR), since a gfx9-family VOP3 cannot encode the two literals. The unpack itself stays
+// plain C so the compiler sees every VALU write that feeds an MFMA operand and inserts the
+// required wait states (an inline-asm VALU op is invisible to its hazard recognizer).
+IMQ_DEV uint32_t magic_bf16_128x2() {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(r));
+  return r;
+}
+
+// 8 int4 codes (one u32, code i at bits 4i..4i+3) -> 8 bf16 values (128 + code), exact:
+// (code | 0x4300) is the bf16 128 + code. Seven VALU ops for eight weights.
 // Output element order is [c0, c4, c1, c5, c2, c6, c3, c7]; activations fed against these
 // operands must use the same order (see permute_x8).
-IMQ_DEV bf16x8_t unpack_nib8_bf16(uint32_t w) {
+IMQ_DEV bf16x8_t unpack_nib8_bf16(uint32_t w, uint32_t magic) {
   u32x4_t r;
-  r[0] = and_or(w, 0x000F000Fu, 0x43004300u);
-  r[1] = and_or(w >> 4, 0x000F000Fu, 0x43004300u);
-  r[2] = and_or(w >> 8, 0x000F000Fu, 0x43004300u);
-  r[3] = and_or(w >> 12, 0x000F000Fu, 0x43004300u);
+  r[0] = (w & 0x000F000Fu) | magic;
+  r[1] = ((w >> 4) & 0x000F000Fu) | magic;
+  r[2] = ((w >> 8) & 0x000F000Fu) | magic;
+  r[3] = ((w >> 12) & 0x000F000Fu) | magic;
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
@@ -109,6 +121,10 @@ IMQ_DEV u32x4_t permute_x8(u32x4_t v) {
 IMQ_DEV f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+
+// Workgroup barrier that orders LDS only. __syncthreads() also waits for every outstanding
+// global load (vmcnt(0)), which would drain the prefetched weight stream at each barrier.
+IMQ_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 static inline int64_t imq_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

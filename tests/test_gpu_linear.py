@@ -176,7 +176,8 @@ def test_linear_w4_one_hot_column_extraction(dev):
         x[i, k] = 1.0
     y = C.t2np(ops.linear_w4(C.to_torch(x, "bf16", dev), q, 128, (s, z)))
     for i, k in enumerate(ks):
-        np.testing.assert_allclose(y[i], oq.round_to(c["Wd"][:, k], "bf16"), rtol=0, atol=1e-6 + 4e-3 * np.abs(c["Wd"][:, k]))
+        col = c["Wd"][:, k]
+        assert np.all(np.abs(y[i] - col) <= 1e-6 + 8e-3 * np.abs(col)), k
 
 
 @pytest.mark.parametrize("sdt", ["fp16", "fp32"])
