@@ -63,6 +63,24 @@ IMQ_DEV float raw_to_bf16_f32(uint32_t r) {
   else return round_bf16(__uint_as_float(r));
 }
 
+// Load exactly NW dwords (NW in {2, 4, 8}) from a 4*NW-byte aligned address.
+template <int NW>
+IMQ_DEV void load_strip(const unsigned char* p, uint32_t* out) {
+  static_assert(NW == 2 || NW == 4 || NW == 8, "strip of 8, 16 or 32 bytes");
+  if constexpr (NW == 2) {
+    const u32x2_t t = *(const u32x2_t*)p;
+    out[0] = t[0];
+    out[1] = t[1];
+  } else {
+#pragma unroll
+    for (int v = 0; v < NW; v += 4) {
+      const u32x4_t t = *(const u32x4_t*)(p + 4 * v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[v + e] = t[e];
+    }
+  }
+}
+
 // x resident in LDS (M * K_pad fits). One workgroup = one 16-row tile; its W waves split K,
 // wave w owning steps [(r*W + w)*S, +S) of round r. Each wave issues all S loads of a round
 // back to back (S*1 KB per wave in flight), then consumes them; latency is hidden by the many
@@ -90,15 +108,22 @@ __global__ __launch_bounds__(1024) void w4_skinny_kernel(SkinnyArgs a) {
   const int xls = KS * kStep + kXPad;
   uint16_t* xl = (uint16_t*)smem;                                    // [M][xls]
   float* xs = (float*)(smem + (size_t)a.M * xls * 2);                // [KS][16]
-  float* red = xs + (size_t)KS * 16;                                 // [W][256]
+  float* red = xs + (size_t)KS * 16;                                 // [2][W][256]
   const int gsh = 31 - __builtin_clz(a.G / kStep);                   // steps per group = 2^gsh
-  const int tile = blockIdx.x;
+  const int NT = (a.N + 15) / 16;
+  int tile = blockIdx.x;          // the grid never exceeds the tile count
 
-  int row = tile * 16 + nl;
-  row = row < a.N ? row : a.N - 1;
-  const uint8_t* qrow = a.q + (int64_t)row * a.sqn + 16 * jl;
-  const unsigned char* srow = (const unsigned char*)a.sc + (int64_t)row * a.ssn * SZB;
-  const unsigned char* zrow = (const unsigned char*)a.zr + (int64_t)row * a.szn * ZZB;
+  const uint8_t* qrow;
+  const unsigned char* srow;
+  const unsigned char* zrow;
+  auto set_tile = [&](int t) {
+    int row = t * 16 + nl;
+    row = row < a.N ? row : a.N - 1;
+    qrow = a.q + (int64_t)row * a.sqn + 16 * jl;
+    srow = (const unsigned char*)a.sc + (int64_t)row * a.ssn * SZB;
+    zrow = (const unsigned char*)a.zr + (int64_t)row * a.szn * ZZB;
+  };
+  set_tile(tile);
   const int64_t ssg_b = a.ssg * SZB, szg_b = a.szg * ZZB;
 
   u32x4_t wv[S];
@@ -121,19 +146,11 @@ __global__ __launch_bounds__(1024) void w4_skinny_kernel(SkinnyArgs a) {
       }
     }
     if constexpr (STRIP) {
+      // exactly S values (S*SZB bytes, naturally aligned: the host checks 16-byte row and
+      // base alignment and S*SZB is 8, 16 or 32) -- never past the row end
       const int64_t g0 = sbase < KS ? sbase : 0;     // whole strip past K: any valid strip
-#pragma unroll
-      for (int v = 0; v < SW; v += 4) {
-        const u32x4_t t = *(const u32x4_t*)(srow + g0 * SZB + 4 * v);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) if (v + e < SW) sst[v + e] = t[e];
-      }
-#pragma unroll
-      for (int v = 0; v < ZW; v += 4) {
-        const u32x4_t t = *(const u32x4_t*)(zrow + g0 * ZZB + 4 * v);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) if (v + e < ZW) zst[v + e] = t[e];
-      }
+      load_strip<SW>(srow + g0 * SZB, sst);
+      load_strip<ZW>(zrow + g0 * ZZB, zst);
     }
   };
   // raw 16/32-bit scale and zero word of step i of the current round
@@ -148,52 +165,56 @@ __global__ __launch_bounds__(1024) void w4_skinny_kernel(SkinnyArgs a) {
     else return (i & 1) ? (zst[i >> 1] >> 16) : (zst[i >> 1] & 0xffffu);
   };
 
-  // first round's weights are independent of x: issue them before staging
-  load_round(0);
-
   // ---- stage x (permuted) and per-step row sums --------------------------------------------
-  {
-    const int nblk = KS * (kStep / 8);
-    const int total = a.M * nblk;
-    for (int idx = threadIdx.x; idx < 16 * KS; idx += blockDim.x) xs[idx] = 0.f;
-    lds_barrier();
-    for (int base = threadIdx.x; base < total; base += 4 * blockDim.x) {
-      u32x4_t v[4];
+  // Loads complete in issue order, so the x loads are issued *before* the first weight round:
+  // the staging then finishes under the weight latency and compute consumes the weights as
+  // they arrive. Up to XB 16-byte blocks per thread are held in registers across the weight
+  // issue; any remainder (large M) is staged afterwards.
+  constexpr int XB = 4;
+  const int nblk = KS * (kStep / 8);
+  const int xtotal = a.M * nblk;
+  u32x4_t xv[XB];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        int idx = base + u * blockDim.x;
-        idx = idx < total ? idx : total - 1;
-        const int m = idx / nblk;
-        const int b = idx - m * nblk;
-        v[u] = *(const u32x4_t*)(a.x + (int64_t)m * a.sxm + 8 * b);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int idx = base + u * blockDim.x;
-        if (idx < total) {
-          const int m = idx / nblk;
-          const int b = idx - m * nblk;
-          *(u32x4_t*)(xl + m * xls + 8 * b) = permute_x8(v[u]);
-          float sum = 0.f;
-#pragma unroll
-          for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[u][d] << 16) + __uint_as_float(v[u][d] & 0xffff0000u);
-          // the 16 blocks of one step are 16 consecutive idx (nblk is a multiple of 16, and
-          // idx groups of 16 lie entirely inside or outside [0, total))
-#pragma unroll
-          for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
-          if ((b & 15) == 0) xs[(b >> 4) * 16 + m] = sum;
-        }
-      }
-    }
-    lds_barrier();
+  for (int u = 0; u < XB; ++u) {
+    int idx = threadIdx.x + u * blockDim.x;
+    idx = idx < xtotal ? idx : xtotal - 1;
+    const int m = idx / nblk;
+    const int b = idx - m * nblk;
+    xv[u] = *(const u32x4_t*)(a.x + (int64_t)m * a.sxm + 8 * b);
   }
+  load_round(0);
+  for (int idx = threadIdx.x; idx < 16 * KS; idx += blockDim.x) xs[idx] = 0.f;
+  lds_barrier();
+  auto stage_block = [&](int idx, const u32x4_t& v) {
+    const int m = idx / nblk;
+    const int b = idx - m * nblk;
+    *(u32x4_t*)(xl + m * xls + 8 * b) = permute_x8(v);
+    float sum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
+    // the 16 blocks of one step are 16 consecutive idx (nblk is a multiple of 16, and idx
+    // groups of 16 lie entirely inside or outside [0, xtotal))
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    if ((b & 15) == 0) xs[(b >> 4) * 16 + m] = sum;
+  };
+#pragma unroll
+  for (int u = 0; u < XB; ++u) {
+    const int idx = threadIdx.x + u * blockDim.x;
+    if (idx < xtotal) stage_block(idx, xv[u]);
+  }
+  for (int idx = threadIdx.x + XB * blockDim.x; idx < xtotal; idx += blockDim.x)
+    stage_block(idx, *(const u32x4_t*)(a.x + (int64_t)(idx / nblk) * a.sxm + 8 * (idx % nblk)));
+  lds_barrier();
 
   // A rows m >= M read row M-1: they only feed D rows that are never stored.
   const uint16_t* xlane = xl + (nl < a.M ? nl : a.M - 1) * xls + 32 * jl;
   const float* xslane = xs + 4 * jl;
   const uint32_t magic = magic_bf16_128x2();
   float yacc[4] = {0.f, 0.f, 0.f, 0.f};
+  int buf = 0;
 
+  for (;;) {
   for (int rnd = 0; rnd < R; ++rnd) {
     if (rnd > 0) load_round(rnd);
     // steps in pairs: two independent MFMA chains interleaved (ILP across the MFMA latency).
@@ -234,17 +255,31 @@ __global__ __launch_bounds__(1024) void w4_skinny_kernel(SkinnyArgs a) {
     }
   }
 
-  // cross-wave reduction in a fixed order
+  // cross-wave reduction in a fixed order; the buffer alternates between tiles, so one barrier
+  // per tile suffices (a buffer is rewritten only after the next tile's barrier)
+  float* rb = red + buf * (W * 256);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) red[wave * 256 + (4 * jl + q) * 16 + nl] = yacc[q];
+  for (int q = 0; q < 4; ++q) rb[wave * 256 + (4 * jl + q) * 16 + nl] = yacc[q];
   lds_barrier();
   const int n0 = tile * 16;
+  // next tile's first round before the reduction, to overlap its latency
+  const int next = tile + gridDim.x;
+  if (next < NT) {
+    set_tile(next);
+    load_round(0);
+  }
   for (int e = threadIdx.x; e < 16 * a.M; e += blockDim.x) {
     const int m = e >> 4;
     const int n = e & 15;
     float sum = 0.f;
-    for (int w = 0; w < W; ++w) sum += red[w * 256 + e];
+    for (int w = 0; w < W; ++w) sum += rb[w * 256 + e];
     if (n0 + n < a.N) a.y[(int64_t)m * a.sym + n0 + n] = (uint16_t)f32_to_bf16_bits(sum);
+  }
+  if (next >= NT) break;
+  tile = next;
+  buf ^= 1;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) yacc[q] = 0.f;
   }
 }
 
@@ -517,20 +552,40 @@ int skinny_chunked(const SkinnyArgs& a, size_t lds, int grid, hipStream_t st) {
   return launch_with_lds(w4_skinny_chunked_kernel<W, 16, SDT, ZDT>, g, b, lds, st, a);
 }
 
+// Workgroups of the resident kernel: enough to fill every CU several times over, each looping
+// over ceil(NT / grid) tiles so the x staging is amortized over several tiles.
+int skinny_grid(int NT, int W, size_t lds, const DevInfo& di) {
+  int by_lds = lds > 0 ? (int)((size_t)di.max_lds / lds) : 8;
+  int by_waves = 32 / W;                    // ~32 resident waves per CU
+  int per_cu = by_lds < by_waves ? by_lds : by_waves;
+  if (per_cu < 1) per_cu = 1;
+  long g = (long)di.cus * per_cu;
+  return (int)(g < NT ? g : NT);
+}
+
 template <int SDT, int ZDT>
 int skinny_dispatch(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
   SkinnyArgs a = a0;
   const int KS = a.Kpad / kStep;
   const int NT = (a.N + 15) / 16;
-  // S steps (S KB of packed weights) per wave per round; W = waves per tile (<= 16).
-  const int S = (KS >= 16) ? 8 : 4;
-  int W = (KS + S - 1) / S;
+  // S steps (S KB of packed weights) per wave per round, W waves per tile (<= 16). Measured on
+  // MI355X at Llama-8B shapes: many tiles (N >= 16K) prefer deep batches (S=8) in persistent
+  // workgroups; fewer tiles prefer splitting K over more waves (S=4), one tile per workgroup
+  // while x is small.
+  const bool wide = NT >= 1024 && KS >= 16;
+  int S, W;
+  if (wide) { S = 8; W = (KS + 7) / 8; }
+  else { S = 4; W = (KS + 3) / 4; }
   if (W > 16) W = 16;
-  const size_t resident = (size_t)a.M * (KS * kStep + kXPad) * 2 + (size_t)KS * 64 + (size_t)W * 256 * 4;
+  if (W < 1) W = 1;
+  const size_t resident = (size_t)a.M * (KS * kStep + kXPad) * 2 + (size_t)KS * 64 + (size_t)2 * W * 256 * 4;
   if (resident <= (size_t)di.max_lds) {
     a.chunk_steps = KS;
-    if (S == 8) return skinny_resident<8, SDT, ZDT>(a, resident, NT, W, st);
-    return skinny_resident<4, SDT, ZDT>(a, resident, NT, W, st);
+    // one tile per workgroup while staging x is cheap (M <= 4); otherwise persistent
+    // workgroups that stage x once and loop over tiles
+    const int grid = (a.M <= 4 && !wide) ? NT : skinny_grid(NT, W, resident, di);
+    if (S == 8) return skinny_resident<8, SDT, ZDT>(a, resident, grid, W, st);
+    return skinny_resident<4, SDT, ZDT>(a, resident, grid, W, st);
   }
   // chunked fallback
   const int Wc = 8;

@@ -1,0 +1,115 @@
+"""CPU model of the global-memory address ranges of the int4 skinny GEMV kernel.
+
+The model restates the host dispatch in csrc/gemv.hip (skinny_dispatch / skinny_resident) and
+the kernel's per-lane address arithmetic (load_round, the strip loads and the x staging), then
+checks that every byte a launch can touch lies inside its buffer, for a matrix of shapes,
+scale dtypes, the de-alias padded row view and the exact-fit (no slack) allocation. It guards
+against out-of-bounds reads that a generous allocator would hide on the GPU.
+"""
+import math
+
+import pytest
+
+STEP = 128
+
+
+def _dispatch(Kpad, N=16):
+    """skinny_dispatch in csrc/gemv.hip."""
+    KS = Kpad // STEP
+    NT = -(-N // 16)
+    if NT >= 1024 and KS >= 16:
+        S, W = 8, -(-KS // 8)
+    else:
+        S, W = 4, -(-KS // 4)
+    return KS, S, max(1, min(16, W))
+
+
+def _strip_ok(G, KS, S, ssg, szb, ssn_elems, base_align=256):
+    return G == STEP and KS % S == 0 and ssg == 1 and (ssn_elems * szb) % 16 == 0 and base_align % 16 == 0
+
+
+def skinny_ranges(N, Kpad, M, G, szb, sqn, ssn, strip_bytes=None):
+    """Max exclusive byte offset touched in (qweight, scale, x) for one launch."""
+    KS, S, W = _dispatch(Kpad, N)
+    R = -(-KS // (W * S))
+    gsh = int(math.log2(G // STEP))
+    strip = _strip_ok(G, KS, S, 1, szb, ssn)
+    q_hi = s_hi = 0
+    for row in range(N):
+        for rnd in range(R):
+            for wave in range(W):
+                sbase = (rnd * W + wave) * S
+                for i in range(S):
+                    s = min(sbase + i, KS - 1)
+                    for jl in range(4):
+                        q_hi = max(q_hi, row * sqn + 16 * jl + s * 64 + 16)
+                    if not strip:
+                        s_hi = max(s_hi, (row * ssn + (s >> gsh)) * szb + szb)
+                if strip:
+                    g0 = sbase if sbase < KS else 0
+                    s_hi = max(s_hi, row * ssn * szb + g0 * szb + (strip_bytes or S * szb))
+        if row > 2:      # rows are independent and affine: first rows + last row suffice
+            break
+    # last row (clamped rows read row N-1)
+    row = N - 1
+    for rnd in range(R):
+        for wave in range(W):
+            sbase = (rnd * W + wave) * S
+            for i in range(S):
+                s = min(sbase + i, KS - 1)
+                q_hi = max(q_hi, row * sqn + 48 + s * 64 + 16)
+                if not strip:
+                    s_hi = max(s_hi, (row * ssn + (s >> gsh)) * szb + szb)
+            if strip:
+                g0 = sbase if sbase < KS else 0
+                s_hi = max(s_hi, row * ssn * szb + g0 * szb + (strip_bytes or S * szb))
+    nblk = KS * (STEP // 8)
+    x_hi = (M - 1) * Kpad * 2 + (nblk - 1) * 16 + 16
+    return q_hi, s_hi, x_hi, strip
+
+
+SHAPES = [(4096, 4096), (28672, 4096), (28672, 8192), (16384, 4224), (4096, 14336), (6144, 4096), (37, 384), (1000, 256),
+          (16, 128), (17, 1152), (2048, 1024), (2048, 2048), (80, 384), (96, 1024), (33, 512)]
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("szb", [2, 4])
+@pytest.mark.parametrize("pad", [0, 64])
+def test_skinny_reads_in_bounds(N, K, szb, pad):
+    G = 128
+    Kpad = -(-K // G) * G
+    ng = Kpad // G
+    row_bytes = Kpad // 2
+    sqn = row_bytes + pad
+    q_bytes = (N - 1) * sqn + row_bytes          # exact fit: the last row has no padding after it
+    s_bytes = N * ng * szb
+    for M in (1, 4, 16):
+        q_hi, s_hi, x_hi, _ = skinny_ranges(N, Kpad, M, G, szb, sqn, ng)
+        assert q_hi <= q_bytes, (N, K, M, q_hi, q_bytes)
+        assert s_hi <= s_bytes, (N, K, M, s_hi, s_bytes)
+        assert x_hi <= M * Kpad * 2
+
+
+@pytest.mark.parametrize("G", [256, 512])
+def test_skinny_reads_in_bounds_wide_groups(G):
+    for (N, K) in [(64, 1024), (96, 4096)]:
+        Kpad = -(-K // G) * G
+        ng = Kpad // G
+        q_hi, s_hi, _, strip = skinny_ranges(N, Kpad, 1, G, 2, Kpad // 2, ng)
+        assert not strip
+        assert q_hi <= (N - 1) * (Kpad // 2) + Kpad // 2
+        assert s_hi <= N * ng * 2
+
+
+def test_strip_size_is_exact():
+    """The strip load reads exactly S values: S=4 bf16 is an 8-byte load, not 16."""
+    for KS, szb in [(4, 2), (8, 2), (16, 2), (32, 4)]:
+        _, S, _ = _dispatch(KS * STEP)
+        assert S * szb in (8, 16, 32)
+
+
+def test_model_catches_oversized_strip_load():
+    """Negative control: a 16-byte load of an 8-byte strip (S=4, bf16) reads past the last row."""
+    N, K = 33, 1024          # 8 groups: 16-byte scale rows, S=4 strips of 8 bytes
+    _, s_hi, _, strip = skinny_ranges(N, K, 1, 128, 2, K // 2, K // 128, strip_bytes=16)
+    assert strip and s_hi > N * (K // 128) * 2
