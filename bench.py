@@ -1,19 +1,24 @@
 #!/usr/bin/env python3
 """Benchmark of the weight-only quantized Linear hot path on one MI355X.
 
-Default (the driver's line): BASELINE config C2 -- the Llama-3-8B-shaped int4 g128 decode
-layer stack, 32 layers x {qkv 4096->6144, o 4096->4096, gate_up 4096->28672, down
-14336->4096}, M=1, 32 distinct weight sets (3.7 GB, far past the 256 MB MALL). One "step" is
-one pass over the 128 linears, launched back to back on one stream and captured in a HIP graph.
+Default line (the driver's): BASELINE config C2 -- the Llama-3-8B-shaped int4 g128 decode layer
+stack, 32 layers x {qkv 4096->6144, o 4096->4096, gate_up 4096->28672, down 14336->4096}, M=1,
+32 distinct weight sets (3.7 GB, far past the 256 MB MALL). One step is one pass over the 128
+linears, launched back to back on one stream and replayed as a HIP graph.
 
-value   = whole-pass algorithmic bytes (int4 codes + bf16 scale/zero + x + y) / step time (GB/s)
-roofline= the dominant kernel (the w4 skinny GEMV: all 128 launches) -- algorithmic bytes per
-          launch / average launch duration from HIP events bracketing each launch on torch's
-          stream, vs the 8 TB/s HBM peak
-cpu_baseline = the reference's CPU int4 path (torch tinygemm, oracle/cpu_path.py) on a bounded
-          sample (C2 layer 0..L-1 at M=1) on this host's cores
+  value        whole-pass algorithmic bytes (int4 codes + bf16 scale/zero + x + y) / step time
+  roofline     the dominant (here: only) kernel family, imq's w4 skinny GEMV: algorithmic bytes
+               per launch / average launch duration, both over the timed region (HIP events on
+               the stream the graph replays on); ``traffic`` = HBM bytes per launch from the
+               committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, scaled by a copy-kernel
+               calibration (profiles/), null when no summary matches the workload
+  cpu_baseline the reference's CPU int4 path (torch tinygemm, as worker_quant.py:732-759 binds
+               it) on a bounded sample: 8 layers of the same shapes (0.93 GB, beyond host cache),
+               median pass time on this host's cores
 
-Other configs (--config c1|c3|c4|c5, --m) print lines of the same shape for measurement work.
+Other configs print lines of the same shape: --config c1 (single 1x4096->4096 linear), c3 (int2
+g64 70B shapes), c4 (prefill, --quant int4|int8, --m 512|2048), c5 (OLMoE fused MoE, --m = T),
+and ``copy`` (the plain device copy used to calibrate the PMC byte counters).
 """
 from __future__ import annotations
 
@@ -24,8 +29,10 @@ import statistics
 import sys
 import time
 
+HERE = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK = 8.0e12       # B/s, MI355X HBM3E
 BF16_PEAK = 2.5e15      # dense bf16 MFMA FLOP/s
+METRIC = "w4a16 decode GEMV GB/s & % HBM peak at 8B shapes; prefill TFLOP/s % MFMA"
 
 
 def _parse():
@@ -33,14 +40,18 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
-    ap.add_argument("--m", type=int, default=None, help="rows (C2 M / C4 M / C5 T)")
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy"])
+    ap.add_argument("--m", type=int, default=None, help="rows: C2/C3/C4 M, C5 tokens T")
+    ap.add_argument("--quant", default="int4", choices=["int4", "int8"], help="C4 weight format")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
 
 
+# ---------------------------------------------------------------------------------------------
+# timing helpers
+# ---------------------------------------------------------------------------------------------
 def _graph_or_eager(fn, use_graph: bool):
     import torch
     fn()
@@ -60,7 +71,9 @@ def _graph_or_eager(fn, use_graph: bool):
     return g.replay
 
 
-def _time_steps(step, steps: int, warmup: int):
+def _time_steps(step, steps: int, warmup: int) -> float:
+    """ms per step: warmup, then EXACTLY ``steps`` steps bracketed by a device synchronize and
+    HIP events on the current stream (the stream the graph replays on)."""
     import torch
     for _ in range(warmup):
         step()
@@ -75,27 +88,63 @@ def _time_steps(step, steps: int, warmup: int):
     return t0.elapsed_time(t1) / steps
 
 
-def _per_launch_ms(launches, reps: int = 3):
-    """Average device duration of each launch, from events recorded on torch's current stream
-    immediately before and after it (eager, the same kernels as the timed region)."""
-    import torch
-    evs = []
-    for _ in range(reps):
-        for fn in launches:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record()
-            fn()
-            b.record()
-            evs.append((a, b))
-    torch.cuda.synchronize()
-    return [a.elapsed_time(b) for a, b in evs]
+def _cpu_time(fn, seconds: float, min_runs: int = 3) -> tuple:
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+def _traffic(key: str):
+    """HBM bytes per launch of the dominant kernel for workload ``key`` from the committed PMC
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, copy-calibrated), or None."""
+    path = os.path.join(HERE, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        v = d.get(key)
+        return None if v is None else float(v["bytes_per_launch"])
+    except Exception:
+        return None
+
+
+def _line(value, unit, ms, args, config, roofline, cpu, hib=True, dtype="bf16",
+          data="synthetic: random weights of the named shapes, RTN-packed; x ~ N(0,1) bf16"):
+    return {"metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": hib,
+            "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": data, "config": config,
+            "roofline": roofline, "cpu_baseline": cpu}
+
+
+def _hbm_roofline(kernel: str, bytes_per_launch: float, us_per_launch: float, traffic):
+    ach = bytes_per_launch / (us_per_launch * 1e-6)
+    return {"bound": "hbm", "achieved": round(ach / 1e9, 2), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK, 4), "traffic": traffic, "kernel": kernel,
+            "avg_launch_us": round(us_per_launch, 3), "algorithmic_bytes_per_launch": int(bytes_per_launch)}
 
 
 # ---------------------------------------------------------------------------------------------
-def bench_c2(args, dev, M: int):
+# C2: Llama-3-8B int4 decode stack (the default line)
+# ---------------------------------------------------------------------------------------------
+def bench_c2(args, dev):
     import torch
     from infinitemodel_amd import ops, workloads as wl
+    M = args.m or 1
     lins = wl.llama8b_stack(dev)
     x_in = wl.activations(M, 4096, 1, dev)
     x_dn = wl.activations(M, 14336, 2, dev)
@@ -110,100 +159,277 @@ def bench_c2(args, dev, M: int):
         for fn in launches:
             fn()
 
-    run = _graph_or_eager(step, not args.no_graph)
-    ms = _time_steps(run, args.steps, args.warmup)
-    total_bytes = sum(L.algorithmic_bytes(M) for L in lins)
-    per = _per_launch_ms(launches)
-    avg_ms = sum(per) / len(per)
-    avg_bytes = total_bytes / len(lins)
-    ach = avg_bytes / (avg_ms * 1e-3)
-    line = {
-        "metric": "w4a16 decode GEMV GB/s & % HBM peak at 8B shapes; prefill TFLOP/s % MFMA",
-        "value": round(total_bytes / (ms * 1e-3) / 1e9, 2),
-        "unit": "GB/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int4-w/bf16-a (fp32 acc)",
-        "data": "synthetic (random N(0,0.02) weights RTN-packed int4 g128; x ~ N(0,1))",
-        "config": {"workload": f"C2 llama-3-8b int4 g128 decode stack, 32 layers x 4 linears, M={M}",
-                   "layers": 32, "M": M, "graph": not args.no_graph,
-                   "bytes_per_step": total_bytes, "hbm_frac_whole_step": round(total_bytes / (ms * 1e-3) / HBM_PEAK, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(ach / 1e9, 2), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK, 4), "traffic": None,
-                     "kernel": "imq w4_skinny_kernel", "avg_launch_us": round(avg_ms * 1e3, 3),
-                     "avg_algorithmic_bytes_per_launch": int(avg_bytes)},
-    }
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_c2(args, M)
-    line["cpu_baseline"] = cpu
-    return line
+    ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
+    total = sum(L.algorithmic_bytes(M) for L in lins)
+    per_launch_us = ms * 1e3 / len(lins)
+    roof = _hbm_roofline("w4_skinny_kernel (imq_linear_w4, M<=16)", total / len(lins), per_launch_us,
+                         _traffic(f"c2_m{M}"))
+    cfg = {"workload": f"C2 llama-3-8b int4 g128 decode stack, 32 layers x (qkv, o, gate_up, down), M={M}",
+           "layers": 32, "M": M, "launches_per_step": len(lins), "graph": not args.no_graph,
+           "bytes_per_step": total, "weights": "int4 g128 asymmetric, bf16 scale/zero"}
+    del lins
+    torch.cuda.empty_cache()
+    cpu = None if args.no_cpu else cpu_c2(args, M)
+    return _line(round(total / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
 
 
-def cpu_c2(args, M: int):
-    """Reference CPU int4 path (tinygemm) on C2 layers 0..L-1 at the same M, bounded by time."""
+def _cpu_int4_random(N, K, seed, G=128):
+    """CPU int4 linear with random codes and scale/zero (timing sample; values do not change the
+    work of the tinygemm kernel)."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    ng = K // G
+    q = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8)
+    s = (torch.rand(N, ng, generator=g) * 0.01 + 0.001).to(torch.bfloat16)
+    z = torch.randint(0, 16, (N, ng), generator=g).to(torch.bfloat16)
+    return q, s, z
+
+
+def cpu_c2(args, M: int, layers: int = 8):
     import torch
     from oracle import cpu_path
     from infinitemodel_amd import workloads as wl
     n = cpu_path.tune_cpu_threads()
-    cpu = torch.device("cpu")
-    layers = []
+    packs = []
     nbytes = 0
-    for p, (name, K, N) in enumerate(wl.LLAMA8B_PROJ):
-        L = wl.rtn_int4_linear(N, K, 1000 + p, cpu, name=name)
-        mat2, sz = cpu_path.tinygemm_prepare(L.q, L.s, L.z, 128)
-        layers.append((name, K, mat2, sz))
-        nbytes += L.algorithmic_bytes(M)
+    for l in range(layers):
+        for p, (name, K, N) in enumerate(wl.LLAMA8B_PROJ):
+            q, s, z = _cpu_int4_random(N, K, 1000 + 4 * l + p)
+            mat2, sz = cpu_path.tinygemm_prepare(q, s, z, 128)
+            packs.append((name, mat2, sz))
+            nbytes += N * K // 2 + N * (K // 128) * 4 + M * K * 2 + M * N * 2
+            del q, s, z
     x_in = torch.randn(M, 4096).to(torch.bfloat16)
     x_dn = torch.randn(M, 14336).to(torch.bfloat16)
 
-    def one_layer():
-        for name, K, mat2, sz in layers:
+    def one_pass():
+        for name, mat2, sz in packs:
             cpu_path.tinygemm_linear(x_dn if name == "down" else x_in, mat2, 128, sz)
 
-    one_layer()
-    times = []
-    t_end = time.perf_counter() + args.cpu_seconds
-    while time.perf_counter() < t_end or len(times) < 5:
-        t0 = time.perf_counter()
-        one_layer()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    med, runs = _cpu_time(one_pass, args.cpu_seconds)
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
-            "sample": f"C2 layer 0 (qkv, o, gate_up, down) int4 g128, M={M}, torch tinygemm "
-                      f"_weight_int4pack_mm_for_cpu, median of {len(times)} passes over {args.cpu_seconds:.0f}s",
-            "ms_per_layer": round(med * 1e3, 3), "cpu": _cpu_model()}
+            "sample": f"C2 shapes, {layers} layers x 4 linears (0.93 GB of int4 weights, beyond host cache), "
+                      f"M={M}, torch tinygemm _weight_int4pack_mm_for_cpu, median of {runs} passes",
+            "ms_per_layer": round(med * 1e3 / layers, 3), "cpu": _cpu_model()}
 
 
-def _cpu_model() -> str:
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except Exception:
-        pass
-    return "unknown"
+# ---------------------------------------------------------------------------------------------
+# C1: one int4 linear 1 x 4096 -> 4096 (rotated over 32 distinct copies)
+# ---------------------------------------------------------------------------------------------
+def bench_c1(args, dev):
+    import torch
+    from infinitemodel_amd import ops, workloads as wl
+    M = args.m or 1
+    lins = [wl.rtn_int4_linear(4096, 4096, i, dev, name=f"c1.{i}") for i in range(32)]
+    x = wl.activations(M, 4096, 0, dev)
+    y = torch.empty((M, 4096), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        for L in lins:
+            ops.linear_w4(x, L.q, 128, (L.s, L.z), out=y)
+
+    ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
+    b = lins[0].algorithmic_bytes(M)
+    us = ms * 1e3 / len(lins)
+    roof = _hbm_roofline("w4_skinny_kernel (imq_linear_w4, M<=16)", b, us, _traffic(f"c1_m{M}"))
+    cfg = {"workload": f"C1 single int4 g128 linear {M}x4096->4096, 32 distinct copies per step", "M": M,
+           "launches_per_step": len(lins)}
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cpu_path
+        n = cpu_path.tune_cpu_threads()
+        packs = [cpu_path.tinygemm_prepare(*_cpu_int4_random(4096, 4096, i), 128) for i in range(48)]
+        xc = torch.randn(M, 4096).to(torch.bfloat16)
+
+        def one():
+            for mat2, sz in packs:
+                cpu_path.tinygemm_linear(xc, mat2, 128, sz)
+
+        med, runs = _cpu_time(one, args.cpu_seconds)
+        cpu = {"value": round(b * len(packs) / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
+               "sample": f"C1 shape, 48 distinct weights (0.43 GB), torch tinygemm, median of {runs} passes",
+               "cpu": _cpu_model()}
+    return _line(round(b * len(lins) / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
+
+
+# ---------------------------------------------------------------------------------------------
+# C3: int2 g64 at 70B shapes (fp16 s/z, non-integer zeros), 8 copies of each shape
+# ---------------------------------------------------------------------------------------------
+def bench_c3(args, dev):
+    import torch
+    from infinitemodel_amd import ops, workloads as wl
+    M = args.m or 1
+    shapes = [(28672, 8192), (8192, 28672)]
+    sets = []
+    for i in range(8):
+        for j, (N, K) in enumerate(shapes):
+            q, s, z = wl.int2_random_linear(N, K, 2000 + 2 * i + j, dev)
+            sets.append((N, K, q, s, z))
+    xs = {K: wl.activations(M, K, 7, dev) for _, K in shapes}
+    ys = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for N, _ in shapes}
+
+    def step():
+        for N, K, q, s, z in sets:
+            ops.linear_w2(xs[K], q, 64, (s, z), out=ys[N])
+
+    ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
+    nbytes = sum(q.numel() + s.numel() * 2 + z.numel() * 2 + M * K * 2 + M * N * 2 for N, K, q, s, z in sets)
+    us = ms * 1e3 / len(sets)
+    roof = _hbm_roofline("imq_linear_w2 decode kernel", nbytes / len(sets), us, _traffic(f"c3_m{M}"))
+    cfg = {"workload": f"C3 int2 g64 70B shapes 8192->28672 and 28672->8192, M={M}, 8 copies each", "M": M,
+           "launches_per_step": len(sets), "weights": "int2 g64, fp16 scale ~U(0.005,0.05), zero ~U(0,3)"}
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cpu_path
+        n = cpu_path.tune_cpu_threads()
+        g = torch.Generator().manual_seed(1)
+        cs = [(torch.randint(0, 256, (N, K // 4), generator=g, dtype=torch.uint8),
+               (torch.rand(N, K // 64, generator=g) * 0.045 + 0.005).half(),
+               (torch.rand(N, K // 64, generator=g) * 3).half(), K) for N, K in shapes]
+        xc = {K: torch.randn(M, K).to(torch.bfloat16) for _, K in shapes}
+
+        def one():
+            for q, s, z, K in cs:
+                cpu_path.naive_linear(xc[K], q, s, z, K, 64, bits=2)
+
+        med, runs = _cpu_time(one, args.cpu_seconds, min_runs=2)
+        cb = sum(q.numel() + s.numel() * 4 + M * K * 2 + M * q.shape[0] * 2 for q, s, z, K in cs)
+        cpu = {"value": round(cb / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
+               "sample": f"C3 both shapes once, naive dequant + F.linear (the reference's only CPU int2 path), "
+                         f"M={M}, median of {runs}", "cpu": _cpu_model()}
+    return _line(round(nbytes / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
+
+
+# ---------------------------------------------------------------------------------------------
+# C4: prefill dequant-GEMM (int4 g128 or int8 per-row), 4096->14336 and 14336->4096
+# ---------------------------------------------------------------------------------------------
+def bench_c4(args, dev):
+    import torch
+    from infinitemodel_amd import ops, workloads as wl
+    M = args.m or 2048
+    shapes = [(14336, 4096), (4096, 14336)]
+    sets = []
+    for i in range(2):
+        for j, (N, K) in enumerate(shapes):
+            if args.quant == "int4":
+                L = wl.rtn_int4_linear(N, K, 5000 + 2 * i + j, dev)
+                sets.append((N, K, lambda x, y, L=L: ops.linear_w4(x, L.q, 128, (L.s, L.z), out=y)))
+            else:
+                q, s = wl.int8_linear(N, K, 5000 + 2 * i + j, dev)
+                sets.append((N, K, lambda x, y, q=q, s=s: ops.linear_w8(x, q, s, out=y)))
+    xs = {K: wl.activations(M, K, 9, dev) for _, K in shapes}
+    ys = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for N, _ in shapes}
+
+    def step():
+        for N, K, fn in sets:
+            fn(xs[K], ys[N])
+
+    ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
+    flops = sum(2.0 * M * N * K for N, K, _ in sets)
+    tf = flops / (ms * 1e-3)
+    roof = {"bound": "mfma", "achieved": round(tf / 1e12, 2), "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s",
+            "frac": round(tf / BF16_PEAK, 4), "traffic": _traffic(f"c4_{args.quant}_m{M}"),
+            "kernel": f"imq_linear_{'w4' if args.quant == 'int4' else 'w8'} prefill path",
+            "avg_launch_us": round(ms * 1e3 / len(sets), 3), "flops_per_launch": flops / len(sets)}
+    cfg = {"workload": f"C4 prefill {args.quant} 4096->14336 and 14336->4096, M={M}", "M": M,
+           "quant": args.quant, "launches_per_step": len(sets)}
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cpu_path
+        n = cpu_path.tune_cpu_threads()
+        g = torch.Generator().manual_seed(2)
+        xc = {K: torch.randn(M, K).to(torch.bfloat16) for _, K in shapes}
+        if args.quant == "int4":
+            cs = [(K, _cpu_int4_random(N, K, 7 + K)) for N, K in shapes]
+
+            def one():
+                for K, (q, s, z) in cs:
+                    cpu_path.naive_linear(xc[K], q, s, z, K, 128, bits=4)
+        else:
+            cs = [(K, torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8),
+                   (torch.rand(N, 1, generator=g) * 1e-3).half()) for N, K in shapes]
+
+            def one():
+                for K, q, s in cs:
+                    cpu_path.naive_linear_int8(xc[K], q, s)
+
+        med, runs = _cpu_time(one, args.cpu_seconds, min_runs=2)
+        cf = sum(2.0 * M * N * K for N, K in shapes)
+        cpu = {"value": round(cf / med / 1e12, 4), "unit": "TFLOP/s", "cores": n, "kind": "port",
+               "sample": f"C4 both shapes once at M={M}: rows >= 16 -> fp32 dequant + fp32 GEMM "
+                         f"(worker_quant.py:847-852 / 411-417), median of {runs}", "cpu": _cpu_model()}
+    return _line(round(tf / 1e12, 3), "TFLOP/s", ms, args, cfg, roof, cpu)
+
+
+# ---------------------------------------------------------------------------------------------
+# C5: OLMoE fused MoE experts (E=64, top-8, H=2048, I=1024), 4 distinct layers
+# ---------------------------------------------------------------------------------------------
+def bench_c5(args, dev):
+    import torch
+    from infinitemodel_amd import ops, workloads as wl
+    T = args.m or 1
+    layers = [wl.olmoe_layer(dev, seed=3000 + l) for l in range(4)]
+    idx, w = wl.olmoe_routing(T, dev)
+    x = wl.activations(T, 2048, 11, dev)
+
+    def step():
+        for gu, dn in layers:
+            ops.moe_experts_w4(x, idx, w, gu, dn, 128)
+
+    ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
+    U = int(torch.unique(idx).numel())
+    per_expert = 3342336
+    nbytes = U * per_expert + T * 2048 * 2 * 2 + idx.numel() * 6
+    us = ms * 1e3 / len(layers)
+    roof = _hbm_roofline("imq_moe_experts_w4 (one MoE layer)", nbytes, us, _traffic(f"c5_t{T}"))
+    cfg = {"workload": f"C5 OLMoE fused MoE experts, T={T}, top-8 of 64, H=2048, I=1024, 4 layers", "T": T,
+           "distinct_experts": U, "bytes_per_layer": nbytes, "layers_per_step": len(layers)}
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cpu_path
+        n = cpu_path.tune_cpu_threads()
+        cl = wl.olmoe_layer(torch.device("cpu"), seed=3000)
+        xc, ic, wc = x.cpu(), idx.cpu(), w.cpu()
+        med, runs = _cpu_time(lambda: cpu_path.moe_eager_cpu(xc, ic, wc, cl[0], cl[1], 128), args.cpu_seconds,
+                              min_runs=2)
+        cpu = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
+               "sample": f"C5 one layer at T={T}: the eager per-expert loop over bf16 dequantized experts "
+                         f"(modeling_olmoe.py:301-325 over Packed4Tensor3D), median of {runs}",
+               "cpu": _cpu_model()}
+    return _line(round(nbytes * len(layers) / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
+
+
+# ---------------------------------------------------------------------------------------------
+def bench_copy(args, dev):
+    """Plain device copy of 1 GiB (read 1 GiB + write 1 GiB per launch): calibrates the PMC
+    FETCH_SIZE / WRITE_SIZE counters against known bytes."""
+    import torch
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    ms = _time_steps(lambda: b.copy_(a), args.steps, args.warmup)
+    roof = _hbm_roofline("copy (elementwise_kernel)", 2 * n, ms * 1e3, None)
+    return _line(round(2 * n / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args,
+                 {"workload": "device copy 1 GiB -> 1 GiB", "bytes_read": n, "bytes_written": n}, roof, None)
+
+
+BENCH = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "copy": bench_copy}
 
 
 def main():
     args = _parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the quantized-linear hot path runs "
-                                   "per GPU and the GPU boxes here have one GPU; run with --gpus 1"}))
+        print("bench.py measures one GPU only: the quantized-linear hot path runs per GPU and this "
+              "build's GPU boxes have one GPU; use --gpus 1",
+              file=sys.stderr, flush=True)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
-        print(json.dumps({"error": "no ROCm GPU visible"}))
+        print("no ROCm GPU visible", file=sys.stderr, flush=True)
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.config == "c2":
-        line = bench_c2(args, dev, args.m or 1)
-    else:
-        from infinitemodel_amd import bench_configs
-        line = bench_configs.run(args, dev)
+    line = BENCH[args.config](args, dev)
     print(json.dumps(line), flush=True)
 
 

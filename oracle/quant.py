@@ -147,8 +147,11 @@ def pack_linear_int8(W, dt: str = "bf16"):
     amax = np.abs(W).max(axis=1, keepdims=True)
     scale = dt_op(amax, F32(127.0), "/", dt)
     scale = np.maximum(scale, round_to(F32(1e-8), dt))
-    t = dt_op(W, scale, "/", dt)
-    q = np.clip(np.rint(t), -127, 127).astype(np.int8)
+    # fp16 quirk: fp16(1e-8) is 0, so an all-zero row has scale 0 and codes 0/0 = NaN; the
+    # float->int8 cast of NaN then gives 0 on x86 (torch's CPU cast does the same).
+    with np.errstate(invalid="ignore", divide="ignore"):
+        t = dt_op(W, scale, "/", dt)
+        q = np.clip(np.rint(t), -127, 127).astype(np.int8)
     return q, scale
 
 

@@ -1,0 +1,80 @@
+"""The C ABI without a GPU: libimq.so loads, exports exactly what include/imq.h declares with the
+ctypes signatures the Python layer binds, and rejects invalid arguments before touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from infinitemodel_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "imq.h")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    txt = re.sub(r"//[^\n]*", "", txt)
+    return sorted(set(re.findall(r"\b(imq_[a-z0-9_]+)\s*\(", txt)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} is not built (python -m infinitemodel_amd.build)")
+    return _lib.lib()
+
+
+def test_header_and_bindings_agree():
+    assert _declared() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(L):
+    missing = [n for n in _declared() if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_exports_are_c_linkage():
+    """Every declared name is an unmangled dynamic symbol (nm -D), so any FFI can bind it."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    syms = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    for n in _declared():
+        assert n in syms, n
+
+
+def test_abi_version_and_strerror(L):
+    assert L.imq_abi_version() == 1
+    assert L.imq_strerror(0) == b"ok"
+    for rc in (_lib.IMQ_ERR_INVALID, _lib.IMQ_ERR_UNSUPPORTED, _lib.IMQ_ERR_ALIGN):
+        assert len(L.imq_strerror(rc)) > 5
+
+
+def test_moe_workspace_bytes(L):
+    # gu fp32 [B, 2I] + h bf16 [B, I_pad] + z fp32 [B, H], each 256-aligned
+    T, k, E, H, I, G = 3, 8, 64, 2048, 1024, 128
+    B = T * k
+    al = lambda v: -(-v // 256) * 256  # noqa: E731
+    assert L.imq_moe_workspace_bytes(T, k, E, H, I, G) >= al(B * 2 * I * 4) + al(B * I * 2) + al(B * H * 4)
+    assert L.imq_moe_workspace_bytes(-1, k, E, H, I, G) < 0
+
+
+def test_invalid_arguments_are_rejected_on_the_host(L):
+    """Null pointers and inconsistent shapes return IMQ_ERR_INVALID without a device call."""
+    nul = None
+    rc = L.imq_linear_w4(nul, 4096, 1, 4096, nul, 2048, nul, 32, 1, 0, nul, 32, 1, 0, 4096, 128, nul, 4096, nul)
+    assert rc == _lib.IMQ_ERR_INVALID
+    one = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    # K_pad not a multiple of the group
+    rc = L.imq_linear_w4(one, 4096, 1, 4000, one, 2048, one, 32, 1, 0, one, 32, 1, 0, 4096, 128, one, 4096, nul)
+    assert rc == _lib.IMQ_ERR_INVALID
+    # packed row stride shorter than the packed row
+    rc = L.imq_linear_w2(one, 4096, 1, 4096, one, 512, one, 64, 1, 0, one, 64, 1, 0, 4096, 64, one, 4096, nul)
+    assert rc == _lib.IMQ_ERR_INVALID
+    # bad dtype code
+    rc = L.imq_linear_w8(one, 4096, 1, 4096, one, 4096, one, 1, 7, 4096, one, 4096, nul)
+    assert rc == _lib.IMQ_ERR_INVALID
+    rc = L.imq_dequant_w4(one, 2048, one, 32, 1, 0, one, 32, 1, 0, 4096, 4096, 100, one, 4096, 0, nul)
+    assert rc == _lib.IMQ_ERR_INVALID

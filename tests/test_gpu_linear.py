@@ -191,3 +191,64 @@ def test_linear_w4_scale_dtypes(dev, sdt):
     c["Wd"] = oq.dequant_int4(c["q"], c["s"], c["z"], c["in_f"], 128, "bf16")
     for M in (1, 16):
         _linear_check(dev, c, M, seed=M)
+
+
+# ---- int2 (BASELINE C3 style: fp16 s/z, non-integer zeros) and int8 per-row ------------------
+@pytest.mark.parametrize("N,K", [(512, 1024), (96, 448), (28672 // 16, 8192 // 4)])
+@pytest.mark.parametrize("M", [1, 8, 16, 40])
+def test_linear_w2_random_codes(dev, N, K, M):
+    c = dict(C.int2_random_case(N, K, 64, seed=2000 + N, dt="fp16"))
+    _linear_check(dev, c, M, seed=M, bits=2)
+
+
+def test_linear_w2_rtn_and_dealias(dev):
+    c = C.int2_case(256, 1024, 64, seed=8)
+    for M in (1, 5):
+        _linear_check(dev, c, M, seed=M, bits=2, view_pad=64)
+
+
+def _int8_check(dev, N, K, M, sdt, seed):
+    import torch
+    from infinitemodel_amd import ops
+    c = C.int8_case(N, K, seed=seed, dt=sdt)
+    x = C.bf16_normal(C.rng(seed + 1), (M, K))
+    y = ops.linear_w8(C.to_torch(x, "bf16", dev), C.u8(c["q"], dev), C.to_torch(c["s"], sdt, dev))
+    assert y.dtype == torch.bfloat16
+    yn = C.t2np(y)
+    exact = oq.int8_gemm_ref(x, c["q"], c["s"])
+    # the naive path's weight bf16(q * s) (bf16 scale) or fp32 (fp16 scale): within 2^-8 of exact
+    assert oq.max_rel(yn, exact) <= MAX_REL and oq.mean_rel(yn, exact) <= MEAN_REL
+    tol = 2.0 ** -8 * np.abs(exact) + 1e-5 * np.abs(exact).max()
+    assert not (np.abs(yn - exact) > tol).any()
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 48])
+@pytest.mark.parametrize("sdt", ["bf16", "fp16"])
+def test_linear_w8(dev, M, sdt):
+    _int8_check(dev, 384, 1000, M, sdt, seed=M)
+
+
+def test_linear_w8_c4_shape_rows(dev):
+    _int8_check(dev, 14336 // 8, 4096, 16, "fp16", seed=77)
+
+
+# ---- fused MoE rows (the reference _w4a16_moe_op contract) ------------------------------------
+def test_moe_rows_w4(dev):
+    """Each row b against expert eid[b], incl. repeated experts and in_features < K_pad."""
+    import torch
+    from infinitemodel_amd import ops
+    E, N, K, G = 6, 96, 300, 128
+    r = C.rng(40)
+    W3 = C.bf16_normal(r, (E, N, K), 0.02)
+    q, s, z, in_f, _ = oq.pack_linear_int4_3d(W3, G, "bf16")
+    B = 13
+    eid = r.integers(0, E, size=B).astype(np.int32)
+    x = C.bf16_normal(r, (B, K))
+    y = ops.moe_rows_w4(C.to_torch(x, "bf16", dev), torch.from_numpy(eid).to(dev), C.u8(q, dev),
+                        C.to_torch(s, "bf16", dev), C.to_torch(z, "bf16", dev), G, in_f)
+    yn = C.t2np(y)
+    for b in range(B):
+        e = int(eid[b])
+        exact = oq.linear_ref(x[b:b + 1], oq.dequant_exact(oq.unpack_int4(q[e]), s[e], z[e], G, in_f))
+        tol = 2.0 ** -8 * np.abs(exact) + 1e-5 * np.abs(exact).max()
+        assert not (np.abs(yn[b:b + 1] - exact) > tol).any(), b
