@@ -1,22 +1,449 @@
 // Prefill-regime (M > 16) fused dequant GEMM for gfx950.
+//
+// y[M, N] = x[M, K] . dequant(W[N, K])^T with bf16 activations, packed int4 / int2 (group-wise
+// asymmetric) or int8 (per-row symmetric) weights, fp32 accumulation and bf16 output: the
+// contract of the reference's `_k` / `_k2` / `_k8` GEMM kernels (worker_quant.py:1098-1126,
+// 1795-1828, 953-980).
+//
+// Structure (a workgroup computes a BM x 128 output tile; each wave a WM x WN sub-tile with
+// v_mfma_f32_32x32x16_bf16, which issues at twice the rate of the 16x16x32 form on gfx950):
+//   * K advances in steps of 64 through two LDS buffers. Global loads run two steps ahead (one
+//     in registers); at the end of step kt every thread writes step kt+1 into the other buffer --
+//     activations as loaded, weights dequantized to bf16 (q - z) * s rounded once (the exact
+//     product of two bf16 values fits fp32) for int4/int2, the exact integer for int8 (its
+//     per-row scale multiplies the fp32 accumulator in the epilogue) -- then issues the loads of
+//     step kt+2 into the freed registers, all interleaved with the step's MFMAs. One barrier per
+//     step.
+//   * Each weight is dequantized once per workgroup and feeds BM activation rows from LDS.
+//   * LDS rows are 64 bf16 (8 chunks of 16 B) with the chunk index XOR-swizzled by the row, so
+//     the 16-lane row-strided fragment reads spread over the banks.
+//   * Workgroups are mapped XCD-aware: consecutive logical tiles land on one XCD (blockIdx is
+//     dealt round-robin over the 8 XCDs), and logical tiles run in groups of 8 tile-rows so the
+//     activation rows and weight columns a group shares stay in that XCD's L2.
 #include "imq_common.h"
 
 namespace imq {
-int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
-              const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st);
 
+namespace {
+
+constexpr int GROUP_M = 8;
+
+// BM x BN workgroup tile, K steps of BK, WAVES_M x WAVES_N waves, at least MINB workgroups per CU
+// (bounds the registers so that many fit).
+template <int BM_, int BN_, int BK_, int WAVES_M_, int WAVES_N_, int MINB_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, MINB = MINB_;
+  static constexpr int CH = BK / 8;              // 16-byte chunks per LDS row
+  static constexpr int KS = BK / 16;             // MFMA K slices per step
+  static constexpr int SH = BK == 128 ? 0 : (BK == 64 ? 1 : 2);   // swizzle row shift: 256 B / row bytes
+  static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int NTHR = 64 * WAVES_M * WAVES_N;
+  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  static constexpr int XC = BM * CH / NTHR;      // 16-byte activation chunks per thread per step
+  static constexpr int WC = BN * BK / NTHR;      // weight codes per thread per step
+  static constexpr int A_EL = BM * BK, B_EL = BN * BK;
+  static constexpr int LDS = 2 * (A_EL + B_EL) * 2;
+  static_assert(XC >= 1 && (BM * CH) % NTHR == 0, "activation chunks must divide evenly");
+  static_assert(WC == 16 || WC == 32, "16 or 32 weight codes per thread");
+  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile of 32x32 blocks");
+};
+
+struct GemmArgs {
+  const uint16_t* x;
+  int64_t sxm;
+  int M, K;
+  const uint8_t* q;
+  int64_t sqn;
+  const void* sc;
+  int64_t ssn, ssg;
+  const void* zr;
+  int64_t szn, szg;
+  int N, gsh;          // group = 1 << gsh codes
+  uint16_t* y;
+  int64_t sym;
+  int tiles_m, tiles_n;
+};
+
+// LDS element offset of 16-byte chunk c of row `row`: the chunk index is XOR-ed with the row's
+// position inside a 256-byte bank period, so 8 consecutive rows read at one chunk hit 8 bank groups.
+template <class C>
+IMQ_DEV int swz(int row, int c) {
+  return (row * C::CH + (c ^ ((row >> C::SH) & (C::CH - 1)))) * 8;
+}
+
+// 8 codes (BITS 4: nibbles of a dword; BITS 2: crumbs in the low 16 bits) -> 4 dwords of bf16
+// (c - z) * s in K order.
+template <int BITS>
+IMQ_DEV u32x4_t dequant8(uint32_t w, float s, float nzs) {
+  u32x4_t r;
+  if constexpr (BITS == 4) {
+    // even codes in the bytes of lo, odd codes in the bytes of hi: each code is then one
+    // v_cvt_f32_ubyteN away from fp32
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float c0 = (float)((lo >> (8 * i)) & 0xffu);
+      const float c1 = (float)((hi >> (8 * i)) & 0xffu);
+      r[i] = cvt_pk_bf16(fmaf(c0, s, nzs), fmaf(c1, s, nzs));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float c0 = (float)((w >> (4 * i)) & 3u);
+      const float c1 = (float)((w >> (4 * i + 2)) & 3u);
+      r[i] = cvt_pk_bf16(fmaf(c0, s, nzs), fmaf(c1, s, nzs));
+    }
+  }
+  return r;
+}
+
+// 8 int8 codes (two dwords) -> 4 dwords of bf16, exact.
+IMQ_DEV u32x4_t convert8_i8(uint32_t lo, uint32_t hi) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t w = i ? hi : lo;
+    r[2 * i] = cvt_pk_bf16((float)(int8_t)(w & 0xff), (float)(int8_t)((w >> 8) & 0xff));
+    r[2 * i + 1] = cvt_pk_bf16((float)(int8_t)((w >> 16) & 0xff), (float)(int8_t)(w >> 24));
+  }
+  return r;
+}
+
+// Packed weight bytes one thread loads per step: WC codes of BITS bits.
+template <int BITS, int WC>
+struct WRegs {
+  static constexpr int BYTES = WC * BITS / 8;     // 4, 8, 16 or 32
+  static constexpr int DW = BYTES / 4;
+  uint32_t d[DW];
+};
+
+template <int BITS, int WC>
+IMQ_DEV void load_w(WRegs<BITS, WC>& r, const uint8_t* p) {
+  constexpr int B = WRegs<BITS, WC>::BYTES;
+  if constexpr (B == 4) {
+    r.d[0] = *(const uint32_t*)p;
+  } else if constexpr (B == 8) {
+    const u32x2_t v = *(const u32x2_t*)p;
+    r.d[0] = v[0];
+    r.d[1] = v[1];
+  } else if constexpr (B == 16) {
+    const u32x4_t v = *(const u32x4_t*)p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.d[i] = v[i];
+  } else {
+    const u32x4_t v0 = *(const u32x4_t*)p;
+    const u32x4_t v1 = *(const u32x4_t*)(p + 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r.d[i] = v0[i];
+      r.d[4 + i] = v1[i];
+    }
+  }
+}
+
+// Chunk c (8 codes, c < WC/8) of a thread's weight registers -> 4 dwords of bf16.
+template <int BITS, int WC>
+IMQ_DEV u32x4_t weight_chunk(const WRegs<BITS, WC>& r, int c, float s, float nzs) {
+  if constexpr (BITS == 4) {
+    return dequant8<4>(r.d[c], s, nzs);
+  } else if constexpr (BITS == 2) {
+    return dequant8<2>(r.d[c >> 1] >> (16 * (c & 1)), s, nzs);
+  } else {
+    return convert8_i8(r.d[2 * c], r.d[2 * c + 1]);
+  }
+}
+
+template <class C, int BITS, int SDT, int ZDT>
+__global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
+  constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, XC = C::XC, WC = C::WC;
+  constexpr int BK = C::BK, CH = C::CH, KS = C::KS;
+  constexpr int PD = 1;   // register sets of loaded-but-not-yet-stored steps
+  constexpr int NTHR = C::NTHR;
+  extern __shared__ __align__(16) uint16_t lds[];
+  uint16_t* As = lds;
+  uint16_t* Bs = lds + 2 * C::A_EL;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  // ---- tile mapping: XCD-aware, grouped by GROUP_M tile-rows ---------------------------------
+  const int T = a.tiles_m * a.tiles_n;
+  int L = blockIdx.x;
+  if ((T & 7) == 0) L = (L & 7) * (T >> 3) + (L >> 3);
+  const int per_group = GROUP_M * a.tiles_n;
+  const int grp = L / per_group;
+  const int first_m = grp * GROUP_M;
+  const int gm = (a.tiles_m - first_m) < GROUP_M ? (a.tiles_m - first_m) : GROUP_M;
+  const int in_grp = L - grp * per_group;
+  const int tm = first_m + in_grp % gm;
+  const int tn = in_grp / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  // ---- global -> register load plan ----------------------------------------------------------
+  // per-thread element offsets from the tile's first row (32-bit) + a uniform per-step base, so
+  // the loads can take the scalar-base + vector-offset form
+  const uint16_t* xtile = a.x + (int64_t)m0 * a.sxm;
+  int xo[XC];
+  int xl[XC];
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int id = tid + NTHR * j;
+    const int row = id / CH, c = id % CH;
+    int r = row;
+    if (m0 + r >= a.M) r = a.M - 1 - m0;
+    xo[j] = (int)(r * a.sxm) + c * 8;
+    xl[j] = swz<C>(row, c);
+  }
+  constexpr int PARTS = BK / WC;                    // threads per weight row per step
+  const int wrow = tid / PARTS, part = tid % PARTS;
+  int gn = n0 + wrow;
+  gn = gn < a.N ? gn : a.N - 1;
+  constexpr int BYTES_STEP = BK * BITS / 8;
+  const uint8_t* wtile = a.q + (int64_t)n0 * a.sqn;
+  const int wo = (int)((gn - n0) * a.sqn) + part * (WC * BITS / 8);
+  int bl[WC / 8];
+#pragma unroll
+  for (int c = 0; c < WC / 8; ++c) bl[c] = swz<C>(wrow, (WC / 8) * part + c);
+  const int64_t sbase = (int64_t)gn * a.ssn, zbase = (int64_t)gn * a.szn;
+  const int ssg = (int)a.ssg, szg = (int)a.szg;
+
+  u32x4_t xr[PD][XC];
+  WRegs<BITS, WC> wr[PD];
+  uint32_t sraw[PD], zraw[PD];   // raw bits: converted only when consumed (loads stay in flight)
+
+  auto gload = [&](int set, int kt) {
+#pragma unroll
+    for (int j = 0; j < XC; ++j) xr[set][j] = *(const u32x4_t*)(xtile + kt * BK + xo[j]);
+    load_w(wr[set], wtile + kt * BYTES_STEP + wo);
+    if constexpr (BITS != 8) {
+      const int g = (kt * BK + WC * part) >> a.gsh;
+      sraw[set] = load_raw_bits<SDT>(a.sc, sbase + g * ssg);
+      zraw[set] = load_raw_bits<ZDT>(a.zr, zbase + g * szg);
+    }
+  };
+
+  auto lstore = [&](int set, int buf) {
+    uint16_t* A = As + buf * C::A_EL;
+    uint16_t* B = Bs + buf * C::B_EL;
+#pragma unroll
+    for (int j = 0; j < XC; ++j) *(u32x4_t*)(A + xl[j]) = xr[set][j];
+    float s = 0.f, nzs = 0.f;
+    if constexpr (BITS != 8) {
+      // scale / zero taken to bf16 first, as the reference dequant `_dequant(torch.bfloat16)` does
+      s = raw_bits_to_f32<SDT>(sraw[set]);
+      float z = raw_bits_to_f32<ZDT>(zraw[set]);
+      if constexpr (SDT != IMQ_DT_BF16) s = round_to<IMQ_DT_BF16>(s);
+      if constexpr (ZDT != IMQ_DT_BF16) z = round_to<IMQ_DT_BF16>(z);
+      nzs = -z * s;
+    }
+#pragma unroll
+    for (int c = 0; c < WC / 8; ++c) *(u32x4_t*)(B + bl[c]) = weight_chunk(wr[set], c, s, nzs);
+  };
+
+  // ---- compute plan ----------------------------------------------------------------------------
+  // v_mfma_f32_32x32x16_bf16 blocks; a K step is BK/16 slices of 16 (two 16-byte chunks each:
+  // lane l reads chunk 2*slice + l/32 of row l%32 of its block)
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  constexpr int IB = WM / 32, JB = WN / 32;
+  f32x16_t acc[IB][JB];
+#pragma unroll
+  for (int i = 0; i < IB; ++i)
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  int aoff[IB][KS], boff[JB][KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+    for (int i = 0; i < IB; ++i) aoff[i][ks] = swz<C>(wm * WM + i * 32 + (lane & 31), 2 * ks + (lane >> 5));
+#pragma unroll
+    for (int j = 0; j < JB; ++j) boff[j][ks] = swz<C>(wn * WN + j * 32 + (lane & 31), 2 * ks + (lane >> 5));
+  }
+
+  auto compute = [&](int buf) {
+    const uint16_t* A = As + buf * C::A_EL;
+    const uint16_t* B = Bs + buf * C::B_EL;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      bf16x8_t af[IB], bfr[JB];
+#pragma unroll
+      for (int i = 0; i < IB; ++i) af[i] = *(const bf16x8_t*)(A + aoff[i][ks]);
+#pragma unroll
+      for (int j = 0; j < JB; ++j) bfr[j] = *(const bf16x8_t*)(B + boff[j][ks]);
+#pragma unroll
+      for (int i = 0; i < IB; ++i)
+#pragma unroll
+        for (int j = 0; j < JB; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+    }
+  };
+
+  // One step with the next step's LDS writes spread over the K slices: slice ks writes the
+  // activation chunks j == ks (mod KS) and dequantizes / writes the weight chunks c == ks (mod KS),
+  // so the VALU dequant sits between MFMAs instead of after them.
+  auto step = [&](int cur) {
+    const uint16_t* A = As + cur * C::A_EL;
+    const uint16_t* B = Bs + cur * C::B_EL;
+    uint16_t* An = As + (cur ^ 1) * C::A_EL;
+    uint16_t* Bn = Bs + (cur ^ 1) * C::B_EL;
+    float s = 0.f, nzs = 0.f;
+    if constexpr (BITS != 8) {
+      s = raw_bits_to_f32<SDT>(sraw[0]);
+      float z = raw_bits_to_f32<ZDT>(zraw[0]);
+      if constexpr (SDT != IMQ_DT_BF16) s = round_to<IMQ_DT_BF16>(s);
+      if constexpr (ZDT != IMQ_DT_BF16) z = round_to<IMQ_DT_BF16>(z);
+      nzs = -z * s;
+    }
+    // all fragment reads of the step go out first (in order of use), so the LDS latency of slice
+    // ks+1.. hides behind the MFMAs of slice ks
+    bf16x8_t af[KS][IB], bfr[KS][JB];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int i = 0; i < IB; ++i) af[ks][i] = *(const bf16x8_t*)(A + aoff[i][ks]);
+#pragma unroll
+      for (int j = 0; j < JB; ++j) bfr[ks][j] = *(const bf16x8_t*)(B + boff[j][ks]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int i = 0; i < IB; ++i)
+#pragma unroll
+        for (int j = 0; j < JB; ++j) acc[i][j] = mfma32x32x16(af[ks][i], bfr[ks][j], acc[i][j]);
+#pragma unroll
+      for (int j = ks; j < XC; j += KS) *(u32x4_t*)(An + xl[j]) = xr[0][j];
+#pragma unroll
+      for (int c = ks; c < WC / 8; c += KS) *(u32x4_t*)(Bn + bl[c]) = weight_chunk(wr[0], c, s, nzs);
+    }
+  };
+
+  // Prologue: step 0 into LDS buffer 0, step 1 in flight in registers.
+  const int KT = a.K / BK;
+  gload(0, 0);
+  lstore(0, 0);
+  gload(0, KT > 1 ? 1 : 0);
+  __syncthreads();
+
+  // Step kt: MFMAs on buffer kt&1; write step kt+1 (registers) into the other buffer; load step
+  // kt+2. The body is branch-free so the dequant, LDS writes and loads interleave with the
+  // MFMAs: past the end the loads re-read the last step (in bounds) and the final write lands in
+  // the buffer no later step reads.
+  for (int kt = 0; kt < KT; ++kt) {
+    step(kt & 1);
+    gload(0, kt + 2 < KT ? kt + 2 : KT - 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: D lane l holds column l%32, element r at row 8*(r/4) + 4*(l/32) + r%4 -------
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    const int n = n0 + wn * WN + j * 32 + (lane & 31);
+    if (n >= a.N) continue;
+    float sc8 = 1.f;
+    if constexpr (BITS == 8) sc8 = load_as_f32<SDT>(a.sc, (int64_t)n * a.ssn);
+#pragma unroll
+    for (int i = 0; i < IB; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < a.M) a.y[(int64_t)m * a.sym + n] = (uint16_t)cvt_pk_bf16(acc[i][j][r] * sc8, 0.f);
+      }
+    }
+  }
+}
+
+template <class C, int BITS, int SDT, int ZDT>
+int launch_cfg(const GemmArgs& a0, hipStream_t st) {
+  GemmArgs a = a0;
+  a.tiles_m = (a.M + C::BM - 1) / C::BM;
+  a.tiles_n = (a.N + C::BN - 1) / C::BN;
+  const int64_t T = (int64_t)a.tiles_m * a.tiles_n;
+  if (T > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  auto kern = gemm_wq_kernel<C, BITS, SDT, ZDT>;
+  if (C::LDS > 65536) {
+    static int attr_set = 0;   // benign race: every caller sets the same attribute value
+    if (!__atomic_load_n(&attr_set, __ATOMIC_ACQUIRE)) {
+      hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+      if (e != hipSuccess) return (int)e;
+      __atomic_store_n(&attr_set, 1, __ATOMIC_RELEASE);
+    }
+  }
+  kern<<<dim3((unsigned)T), dim3(C::NTHR), C::LDS, st>>>(a);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+// Tile configurations (selected on the host by how many workgroup tiles the shape yields).
+#ifndef IMQ_GEMM_CFG_BIG
+#define IMQ_GEMM_CFG_BIG 256, 128, 64, 4, 2, 1
+#endif
+#ifndef IMQ_GEMM_CFG_SMALL
+#define IMQ_GEMM_CFG_SMALL 128, 128, 64, 2, 2, 2
+#endif
+using CfgBig = Cfg<IMQ_GEMM_CFG_BIG>;
+using CfgSmall = Cfg<IMQ_GEMM_CFG_SMALL>;
+
+template <int BITS, int SDT, int ZDT>
+int launch_gemm(const GemmArgs& a, hipStream_t st) {
+  const int64_t big_tiles = (int64_t)((a.M + CfgBig::BM - 1) / CfgBig::BM) * ((a.N + CfgBig::BN - 1) / CfgBig::BN);
+  if (big_tiles >= 256) return launch_cfg<CfgBig, BITS, SDT, ZDT>(a, st);
+  return launch_cfg<CfgSmall, BITS, SDT, ZDT>(a, st);
+}
+
+template <int BITS, int SDT>
+int gemm_z(const GemmArgs& a, int zdt, hipStream_t st) {
+  if constexpr (BITS == 8) {
+    return launch_gemm<8, SDT, SDT>(a, st);
+  } else {
+    switch (zdt) {
+      case IMQ_DT_BF16: return launch_gemm<BITS, SDT, IMQ_DT_BF16>(a, st);
+      case IMQ_DT_FP16: return launch_gemm<BITS, SDT, IMQ_DT_FP16>(a, st);
+      case IMQ_DT_FP32: return launch_gemm<BITS, SDT, IMQ_DT_FP32>(a, st);
+    }
+    return IMQ_ERR_INVALID;
+  }
+}
+
+template <int BITS>
+int gemm_bits(const GemmArgs& a, int sdt, int zdt, hipStream_t st) {
+  switch (sdt) {
+    case IMQ_DT_BF16: return gemm_z<BITS, IMQ_DT_BF16>(a, zdt, st);
+    case IMQ_DT_FP16: return gemm_z<BITS, IMQ_DT_FP16>(a, zdt, st);
+    case IMQ_DT_FP32: return gemm_z<BITS, IMQ_DT_FP32>(a, zdt, st);
+  }
+  return IMQ_ERR_INVALID;
+}
+
+}  // namespace
+
+// Prefill GEMM entry used by imq_linear_w4 / _w2 / _w8 for M > 16. Returns IMQ_ERR_UNSUPPORTED
+// for shapes the tiled kernel does not cover (K not a multiple of 64, groups below 32 codes or
+// not a power of two, misaligned operands, offsets beyond 32 bits); the caller then uses the
+// generic kernel.
 int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
             const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
             int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st) {
-  if (bits != 4) return IMQ_ERR_UNSUPPORTED;
-  // Interim: 16-row slices through the decode kernel.
-  for (int64_t m0 = 0; m0 < M; m0 += 16) {
-    const int64_t mm = (M - m0) < 16 ? (M - m0) : 16;
-    int rc = skinny_w4(x + m0 * sxm, sxm, mm, K, q, sqn, sc, ssn, ssg, sdt, zr, szn, szg, zdt, N, G,
-                       y + m0 * sym, sym, st);
-    if (rc != IMQ_OK) return rc;
+  if (M <= 0 || N <= 0) return IMQ_OK;
+  if (K % 64 != 0 || M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  int gsh = 0;
+  if (bits != 8) {
+    if (G < 32 || (G & (G - 1)) != 0) return IMQ_ERR_UNSUPPORTED;   // power-of-two groups >= 32
+    while ((1 << gsh) < G) ++gsh;
+    const int64_t gmax = ssg > szg ? ssg : szg;
+    if (ssg < 0 || szg < 0 || (K >> gsh) * gmax > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;   // 32-bit offsets
   }
-  return IMQ_OK;
+  if (((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
+  if (sxm < 0 || sqn < 0 || 256 * sxm > 0x7fffffff || 128 * sqn > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  // widest weight load of either tile configuration: 16 B (int4, int8 as 2 x 16 B), 8 B (int2)
+  const int wbytes = bits == 2 ? 8 : 16;
+  if (((uintptr_t)q % wbytes) || (sqn % wbytes)) return IMQ_ERR_UNSUPPORTED;
+  GemmArgs a{x, sxm, (int)M, (int)K, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, gsh, y, sym, 0, 0};
+  switch (bits) {
+    case 4: return gemm_bits<4>(a, sdt, zdt, st);
+    case 2: return gemm_bits<2>(a, sdt, zdt, st);
+    case 8: return gemm_bits<8>(a, sdt, zdt, st);
+  }
+  return IMQ_ERR_INVALID;
 }
+
 }  // namespace imq

@@ -49,6 +49,21 @@ IMQ_DEV float load_as_f32(const void* p, int64_t idx) {
   }
 }
 
+// Raw bits of element `idx` (16-bit dtypes zero-extended); raw_bits_to_f32 widens them. Loading
+// raw bits lets a kernel keep the load in flight and convert only where the value is consumed.
+template <int DT>
+IMQ_DEV uint32_t load_raw_bits(const void* p, int64_t idx) {
+  if constexpr (DT == IMQ_DT_FP32) return ((const uint32_t*)p)[idx];
+  else return ((const uint16_t*)p)[idx];
+}
+
+template <int DT>
+IMQ_DEV float raw_bits_to_f32(uint32_t b) {
+  if constexpr (DT == IMQ_DT_BF16) return __uint_as_float(b << 16);
+  else if constexpr (DT == IMQ_DT_FP16) return __half2float(__ushort_as_half((unsigned short)b));
+  else return __uint_as_float(b);
+}
+
 // Round an fp32 value to dtype DT (result kept as fp32).
 template <int DT>
 IMQ_DEV float round_to(float f) {
@@ -75,6 +90,14 @@ IMQ_DEV void store_from_f32(void* p, int64_t idx, float v) {
   } else {
     ((float*)p)[idx] = v;
   }
+}
+
+// Two fp32 values -> packed bf16x2 (lo in bits 0..15), round-to-nearest-even: one
+// v_cvt_pk_bf16_f32 on gfx950. Same results as f32_to_bf16_bits for every non-NaN input.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+IMQ_DEV uint32_t cvt_pk_bf16(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // (a & m) | o  -> v_and_or_b32
@@ -116,6 +139,12 @@ IMQ_DEV u32x4_t permute_x8(u32x4_t v) {
   p[2] = perm_b32(v[3], v[1], 0x05040100u);
   p[3] = perm_b32(v[3], v[1], 0x07060302u);
   return p;
+}
+
+// 32x32x16 bf16: A lane l = row l%32, K 8*(l/32)..+8; B lane l = column l%32, same K; D lane l
+// holds column l%32, element r at row 8*(r/4) + 4*(l/32) + r%4. Twice the 16x16x32 rate.
+IMQ_DEV f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 IMQ_DEV f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {

@@ -77,6 +77,12 @@ def test_dequant_w8_promotion(dev):
     assert np.array_equal(C.t2np(out), ref)
 
 
+def _uses_gemm(M, Kpad, G):
+    """Rows > 16 with K_pad a multiple of 64 and a power-of-two group >= 32 take the tiled prefill
+    GEMM (csrc/gemm.hip); the rest take the decode kernels, which keep the weights un-rounded."""
+    return M > 16 and Kpad % 64 == 0 and G >= 32 and (G & (G - 1)) == 0
+
+
 def _linear_check(dev, c, M, seed, bits=4, view_pad=0):
     import torch
     from infinitemodel_amd import ops
@@ -101,7 +107,11 @@ def _linear_check(dev, c, M, seed, bits=4, view_pad=0):
     mr, me = oq.max_rel(yn, ref), oq.mean_rel(yn, ref)
     assert mr <= MAX_REL and me <= MEAN_REL, (M, mr, me)
     unpack = oq.unpack_int4 if bits == 4 else oq.unpack_int2
-    exact = oq.linear_ref(x[:, : c["in_f"]], oq.dequant_exact(unpack(c["q"]), c["s"], c["z"], c["G"], c["in_f"]))
+    w_exact = oq.dequant_exact(unpack(c["q"]), c["s"], c["z"], c["G"], c["in_f"])
+    if _uses_gemm(M, Kpad, c["G"]):
+        # the prefill GEMM feeds MFMA with bf16 weights rounded once from the exact (q - z) * s
+        w_exact = oq.round_to(w_exact.astype(np.float32), "bf16")
+    exact = oq.linear_ref(x[:, : c["in_f"]], w_exact)
     tol = 2.0 ** -8 * np.abs(exact) + 1e-5 * np.abs(exact).max()
     bad = np.abs(yn - exact) > tol
     assert not bad.any(), (M, int(bad.sum()), np.argwhere(bad)[:5].tolist())
@@ -252,3 +262,41 @@ def test_moe_rows_w4(dev):
         exact = oq.linear_ref(x[b:b + 1], oq.dequant_exact(oq.unpack_int4(q[e]), s[e], z[e], G, in_f))
         tol = 2.0 ** -8 * np.abs(exact) + 1e-5 * np.abs(exact).max()
         assert not (np.abs(yn[b:b + 1] - exact) > tol).any(), b
+
+
+# ---- prefill GEMM (M > 16): tiled LDS-dequant MFMA kernel --------------------------------------
+@pytest.mark.parametrize("M,N,K,G", [(17, 256, 512, 128), (128, 128, 1024, 128), (129, 200, 1024, 64),
+                                     (300, 1000, 4096, 128), (512, 1792, 4096, 128)])
+def test_gemm_w4(dev, M, N, K, G):
+    c = C.int4_case(N, K, G, seed=M + N)
+    _linear_check(dev, c, M, seed=M)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_gemm_big_tiles_ragged(dev, bits):
+    """Enough 256 x 128 tiles to take the 8-wave configuration, ragged in M and N."""
+    if bits == 4:
+        c = C.int4_case(4000, 256, 128, seed=77)
+    else:
+        c = dict(C.int2_random_case(4000, 256, 64, seed=78, dt="fp16"))
+    _linear_check(dev, c, 2100, seed=9, bits=bits)
+
+
+def test_gemm_w4_dealias_and_fp16_scales(dev):
+    c = dict(C.int4_case(256, 2048, 128, seed=3))
+    c["s"] = oq.round_to(c["s"], "fp16")
+    c["z"] = oq.round_to(c["z"], "fp16")
+    c["dt"] = "fp16"
+    c["Wd"] = oq.dequant_int4(c["q"], c["s"], c["z"], c["in_f"], 128, "bf16")
+    _linear_check(dev, c, 200, seed=5, view_pad=64)
+
+
+@pytest.mark.parametrize("M", [33, 256])
+def test_gemm_w2(dev, M):
+    c = dict(C.int2_random_case(384, 2048, 64, seed=2002, dt="fp16"))
+    _linear_check(dev, c, M, seed=M, bits=2)
+
+
+@pytest.mark.parametrize("M,sdt", [(64, "fp16"), (300, "bf16")])
+def test_gemm_w8(dev, M, sdt):
+    _int8_check(dev, 640, 2048, M, sdt, seed=M)

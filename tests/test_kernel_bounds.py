@@ -113,3 +113,68 @@ def test_model_catches_oversized_strip_load():
     N, K = 33, 1024          # 8 groups: 16-byte scale rows, S=4 strips of 8 bytes
     _, s_hi, _, strip = skinny_ranges(N, K, 1, 128, 2, K // 2, K // 128, strip_bytes=16)
     assert strip and s_hi > N * (K // 128) * 2
+
+
+# ---- prefill GEMM (csrc/gemm.hip): 128 x 128 tiles, K steps of 64 ------------------------------
+def gemm_cfg(M, N):
+    """launch_gemm in csrc/gemm.hip: (BM, threads) -- 256 x 128 tiles with 512 threads when there
+    are >= 256 of them, else 128 x 128 with 256 threads."""
+    big = (-(-M // 256)) * (-(-N // 128)) >= 256
+    return (256, 512) if big else (128, 256)
+
+
+def gemm_ranges(M, N, K, bits, G, sxm, sqn, ssn, sym):
+    """Max exclusive offsets read from x (elements), q (bytes), scale (elements) and written to y
+    (elements), from the kernel's clamped row indices and per-thread K offsets."""
+    BM, NTHR = gemm_cfg(M, N)
+    BN = 128
+    BK = 64
+    WC = BN * BK // NTHR
+    KT = K // BK
+    tm, tn = -(-M // BM), -(-N // BN)
+    x_hi = q_hi = s_hi = y_hi = 0
+    for t_m in (0, tm - 1):
+        for row in range(BM):
+            gm = min(t_m * BM + row, M - 1)
+            for c in range(8):
+                x_hi = max(x_hi, gm * sxm + c * 8 + (KT - 1) * BK + 8)
+    step_bytes = BK * bits // 8
+    per_part = WC * bits // 8
+    load_bytes = WC * bits // 8
+    for t_n in (0, tn - 1):
+        for wrow in range(BN):
+            gn = min(t_n * BN + wrow, N - 1)
+            for part in range(BK // WC):
+                q_hi = max(q_hi, gn * sqn + part * per_part + (KT - 1) * step_bytes + load_bytes)
+                if bits != 8:
+                    g = ((KT - 1) * BK + WC * part) // G
+                    s_hi = max(s_hi, gn * ssn + g + 1)
+                else:
+                    s_hi = max(s_hi, gn * ssn + 1)
+    # stores are masked to m < M, n < N
+    y_hi = (M - 1) * sym + N
+    return x_hi, q_hi, s_hi, y_hi
+
+
+@pytest.mark.parametrize("M,N,K,bits,G", [(17, 256, 512, 4, 128), (300, 1000, 4096, 4, 128), (129, 200, 1024, 4, 64),
+                                          (40, 1792, 2048, 2, 64), (512, 1000, 1024, 8, 0), (2048, 14336, 4096, 4, 128),
+                                          (512, 4096, 14336, 8, 0), (100, 96, 448, 2, 64)])
+@pytest.mark.parametrize("pad", [0, 64])
+def test_gemm_reads_in_bounds(M, N, K, bits, G, pad):
+    if K % 64:
+        pytest.skip("K not a multiple of 64 goes to the generic kernel")
+    row_bytes = K * bits // 8
+    sqn = row_bytes + pad
+    ng = K // G if G else 1
+    x_hi, q_hi, s_hi, y_hi = gemm_ranges(M, N, K, bits, G, K, sqn, ng, N)
+    assert x_hi <= M * K
+    assert q_hi <= (N - 1) * sqn + row_bytes
+    assert s_hi <= N * ng
+    assert y_hi <= M * N
+
+
+def test_gemm_model_catches_unclamped_rows():
+    """Negative control: without the row clamp the last tile would read past x."""
+    M, K = 130, 256
+    rows_unclamped = (-(-M // 128)) * 128
+    assert (rows_unclamped - 1) * K + K > M * K
