@@ -59,14 +59,14 @@ IMQ_DEV uint32_t load_raw(const void* p, int64_t idx) {
 template <int DT>
 IMQ_DEV float raw_to_bf16_f32(uint32_t r) {
   if constexpr (DT == IMQ_DT_BF16) return __uint_as_float(r << 16);
-  else if constexpr (DT == IMQ_DT_FP16) return round_bf16(__half2float(__ushort_as_half((unsigned short)r)));
-  else return round_bf16(__uint_as_float(r));
+  else if constexpr (DT == IMQ_DT_FP16) return round_bf16_hw(f16_bits_to_f32(r));
+  else return round_bf16_hw(__uint_as_float(r));
 }
 
-// Load exactly NW dwords (NW in {2, 4, 8}) from a 4*NW-byte aligned address.
+// Load exactly NW dwords (NW in {2, 4, 8, 16}) from an address aligned to min(4*NW, 16) bytes.
 template <int NW>
 IMQ_DEV void load_strip(const unsigned char* p, uint32_t* out) {
-  static_assert(NW == 2 || NW == 4 || NW == 8, "strip of 8, 16 or 32 bytes");
+  static_assert(NW == 2 || NW == 4 || NW == 8 || NW == 16, "strip of 8, 16, 32 or 64 bytes");
   if constexpr (NW == 2) {
     const u32x2_t t = *(const u32x2_t*)p;
     out[0] = t[0];
@@ -91,8 +91,8 @@ IMQ_DEV void load_strip(const unsigned char* p, uint32_t* out) {
 // multiple of S, a wave's S scales of a row are S adjacent values: they are fetched with one
 // vector load per row (all four lanes of a row load the same strip) instead of S scattered
 // 2-byte loads, which would cost a cache-line lookup per row per step in the texture path.
-template <int S, int MC, int SDT, int ZDT, bool STRIP>
-__global__ __launch_bounds__(1024) void w4_skinny_kernel(SkinnyArgs a) {
+template <int S, int MC, int SDT, int ZDT, bool STRIP, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void w4_skinny_kernel(SkinnyArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform -> SGPR
@@ -420,6 +420,237 @@ __global__ __launch_bounds__(64 * W) void w4_skinny_chunked_kernel(SkinnyArgs a)
 }
 
 // ---------------------------------------------------------------------------------------------
+// int2 decode kernel (M <= 16). A K-step is one 64-code group: 16 bytes of each packed row.
+// Lane (row nl, quarter jl) works on dword jl = codes [16*jl, 16*jl+16) of each step, which
+// feeds two v_mfma_f32_16x16x32_bf16: MFMA h takes codes {4h..4h+3} and {4h+8..4h+11} of each
+// lane, so every MFMA's 32 K positions lie inside one group and the group's scale/zero apply to
+// its result exactly (y += s*acc - s*(128+z)*sum(x)). The codes arrive as 16-byte loads of four
+// whole steps (a 64-byte line per row) redistributed by a cross-lane 4x4 transpose. Activations
+// are staged in LDS in the matching order (permute_x16); K is staged in chunks when M * K_pad
+// does not fit.
+// ---------------------------------------------------------------------------------------------
+constexpr int kStep2 = 64;
+
+// Two 16-byte blocks lo (elements 0..7), hi (8..15) -> [0,8,1,9,2,10,3,11 | 4,12,5,13,6,14,7,15].
+IMQ_DEV void permute_x16(const u32x4_t& lo, const u32x4_t& hi, u32x4_t& o0, u32x4_t& o1) {
+  o0[0] = perm_b32(hi[0], lo[0], 0x05040100u);
+  o0[1] = perm_b32(hi[0], lo[0], 0x07060302u);
+  o0[2] = perm_b32(hi[1], lo[1], 0x05040100u);
+  o0[3] = perm_b32(hi[1], lo[1], 0x07060302u);
+  o1[0] = perm_b32(hi[2], lo[2], 0x05040100u);
+  o1[1] = perm_b32(hi[2], lo[2], 0x07060302u);
+  o1[2] = perm_b32(hi[3], lo[3], 0x05040100u);
+  o1[3] = perm_b32(hi[3], lo[3], 0x07060302u);
+}
+
+// 4x4 transpose of dwords across the four 16-lane rows: on entry register k of lane row j holds
+// element (k, j); on exit it holds element (j, k). Two v_permlane32_swap (registers k < 2, rows
+// 2-3 <-> registers k+2, rows 0-1) then two v_permlane16_swap (even registers, odd rows <->
+// odd registers, even rows).
+IMQ_DEV void transpose4_lanerows(uint32_t (&d)[4]) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const auto r = __builtin_amdgcn_permlane32_swap(d[k], d[k + 2], false, false);
+    d[k] = r[0];
+    d[k + 2] = r[1];
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k += 2) {
+    const auto r = __builtin_amdgcn_permlane16_swap(d[k], d[k + 1], false, false);
+    d[k] = r[0];
+    d[k + 1] = r[1];
+  }
+}
+
+// 16 crumbs of one dword -> the 8 bf16 (128 + code) of MFMA half h, in the order
+// [c(4h), c(4h+8), c(4h+1), c(4h+9), c(4h+2), c(4h+10), c(4h+3), c(4h+11)].
+IMQ_DEV bf16x8_t unpack_crumb8_bf16(uint32_t w, int h, uint32_t magic) {
+  u32x4_t r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r[k] = ((w >> (2 * (4 * h + k))) & 0x00030003u) | magic;
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+template <int S, int MC, int SDT, int ZDT, bool STRIP, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void w2_skinny_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int nl = lane & 15;
+  const int jl = lane >> 4;
+  constexpr int RC = (MC < 4) ? MC : 4;
+  constexpr int SZB = (SDT == IMQ_DT_FP32) ? 4 : 2;
+  constexpr int ZZB = (ZDT == IMQ_DT_FP32) ? 4 : 2;
+  constexpr int SW = STRIP ? (S * SZB + 3) / 4 : 1;
+  constexpr int ZW = STRIP ? (S * ZZB + 3) / 4 : 1;
+
+  const int KS = a.Kpad / kStep2;
+  const int CS = a.chunk_steps;                      // steps staged per chunk: KS, or a multiple of S
+  const int nchunks = (KS + CS - 1) / CS;
+  const int xls = CS * kStep2 + kXPad;
+  uint16_t* xl = (uint16_t*)smem;                                    // [M][xls]
+  float* xs = (float*)(smem + (size_t)a.M * xls * 2);                // [CS][16]
+  float* red = xs + (size_t)CS * 16;                                 // [2][W][256]
+  const int gsh = 31 - __builtin_clz(a.G / kStep2);                  // steps per group = 2^gsh
+  const int NT = (a.N + 15) / 16;
+  const int64_t ssg_b = a.ssg * SZB, szg_b = a.szg * ZZB;
+
+  // stage steps [c0, c1): each thread handles 16-element pairs; four consecutive pairs make a
+  // step, whose row sum is reduced across those four lanes
+  auto stage = [&](int c0, int c1) {
+    for (int idx = threadIdx.x; idx < 16 * CS; idx += blockDim.x) xs[idx] = 0.f;
+    lds_barrier();
+    const int npair = (c1 - c0) * 4;
+    const int total = a.M * npair;                   // a multiple of 4
+    for (int base = 0; base < total; base += blockDim.x) {
+      const int idx = base + threadIdx.x;
+      const bool valid = idx < total;
+      const int id = valid ? idx : total - 1;
+      const int m = id / npair;
+      const int pr = id - m * npair;
+      const uint16_t* src = a.x + (int64_t)m * a.sxm + (int64_t)c0 * kStep2 + 16 * pr;
+      const u32x4_t lo = *(const u32x4_t*)src;
+      const u32x4_t hi = *(const u32x4_t*)(src + 8);
+      float sum = 0.f;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        sum += __uint_as_float(lo[d] << 16) + __uint_as_float(lo[d] & 0xffff0000u);
+        sum += __uint_as_float(hi[d] << 16) + __uint_as_float(hi[d] & 0xffff0000u);
+      }
+      sum += __shfl_xor(sum, 1, 4);
+      sum += __shfl_xor(sum, 2, 4);
+      if (valid) {
+        u32x4_t o0, o1;
+        permute_x16(lo, hi, o0, o1);
+        *(u32x4_t*)(xl + m * xls + 16 * pr) = o0;
+        *(u32x4_t*)(xl + m * xls + 16 * pr + 8) = o1;
+        if ((pr & 3) == 0) xs[(pr >> 2) * 16 + m] = sum;
+      }
+    }
+    lds_barrier();
+  };
+
+  const uint32_t magic = magic_bf16_128x2();
+  const uint16_t* xlane = xl + (nl < a.M ? nl : a.M - 1) * xls + 16 * jl;
+  const float* xslane = xs + 4 * jl;
+  int buf = 0;
+  bool staged = false;
+
+  for (int tile = blockIdx.x; tile < NT; tile += gridDim.x) {
+    int row = tile * 16 + nl;
+    row = row < a.N ? row : a.N - 1;
+    const uint8_t* qrow = a.q + (int64_t)row * a.sqn + 16 * jl;
+    const unsigned char* srow = (const unsigned char*)a.sc + (int64_t)row * a.ssn * SZB;
+    const unsigned char* zrow = (const unsigned char*)a.zr + (int64_t)row * a.szn * ZZB;
+    float yacc[4] = {0.f, 0.f, 0.f, 0.f};
+
+    for (int c = 0; c < nchunks; ++c) {
+      const int c0 = c * CS;
+      const int c1 = (c0 + CS < KS) ? c0 + CS : KS;
+      if (nchunks > 1 || !staged) {
+        stage(c0, c1);
+        staged = true;
+      }
+      const int R = (c1 - c0 + W * S - 1) / (W * S);
+      for (int rnd = 0; rnd < R; ++rnd) {
+        const int sbase = c0 + (rnd * W + wave) * S;
+        uint32_t wv[S];
+        uint32_t sr[S], zr[S];
+        uint32_t sst[SW], zst[ZW];
+        // 16-byte loads: lane row jl reads step (sb4 + jl) whole (the four lane rows of a tile
+        // row cover one 64-byte line); a 4x4 transpose across the lane rows then hands lane row
+        // jl the dword jl of each of the four steps
+#pragma unroll
+        for (int t = 0; t < S / 4; ++t) {
+          int sb4 = sbase + 4 * t;
+          sb4 = sb4 <= c1 - 4 ? sb4 : c1 - 4;
+          const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)(qrow + (int64_t)sb4 * 16));
+#pragma unroll
+          for (int k = 0; k < 4; ++k) wv[4 * t + k] = v[k];
+        }
+        if constexpr (STRIP) {
+          const int64_t g0 = sbase < c1 ? sbase : c0;     // a strip past the chunk: any valid one
+          load_strip<SW>(srow + g0 * SZB, sst);
+          load_strip<ZW>(zrow + g0 * ZZB, zst);
+        } else {
+#pragma unroll
+          for (int i = 0; i < S; ++i) {
+            int st = sbase + i;
+            st = st < c1 ? st : c1 - 1;
+            const int64_t g = st >> gsh;
+            sr[i] = load_raw<SDT>(srow + g * ssg_b, 0);
+            zr[i] = load_raw<ZDT>(zrow + g * szg_b, 0);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < S / 4; ++t) {
+          uint32_t d[4] = {wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
+          transpose4_lanerows(d);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) wv[4 * t + k] = d[k];
+        }
+        auto s_raw = [&](int i) -> uint32_t {
+          if constexpr (!STRIP) return sr[i];
+          else if constexpr (SZB == 4) return sst[i];
+          else return (i & 1) ? (sst[i >> 1] >> 16) : (sst[i >> 1] & 0xffffu);
+        };
+        auto z_raw = [&](int i) -> uint32_t {
+          if constexpr (!STRIP) return zr[i];
+          else if constexpr (ZZB == 4) return zst[i];
+          else return (i & 1) ? (zst[i >> 1] >> 16) : (zst[i >> 1] & 0xffffu);
+        };
+#pragma unroll
+        for (int i = 0; i < S; i += 2) {
+          const int s0a = sbase + i, s0b = s0a + 1;
+          const bool va = s0a < c1, vb = s0b < c1;
+          const int la = (va ? s0a : c1 - 1) - c0;
+          const int lb = (vb ? s0b : c1 - 1) - c0;
+          const f32x4_t xsa = *(const f32x4_t*)(xslane + la * 16);
+          const f32x4_t xsb = *(const f32x4_t*)(xslane + lb * 16);
+          const bf16x8_t a0 = *(const bf16x8_t*)(xlane + la * kStep2);
+          const bf16x8_t a1 = *(const bf16x8_t*)(xlane + la * kStep2 + 8);
+          const bf16x8_t b0 = *(const bf16x8_t*)(xlane + lb * kStep2);
+          const bf16x8_t b1 = *(const bf16x8_t*)(xlane + lb * kStep2 + 8);
+          const float sca = va ? raw_to_bf16_f32<SDT>(s_raw(i)) : 0.f;
+          const float scb = vb ? raw_to_bf16_f32<SDT>(s_raw(i + 1)) : 0.f;
+          const float cza = -(128.f + raw_to_bf16_f32<ZDT>(z_raw(i))) * sca;
+          const float czb = -(128.f + raw_to_bf16_f32<ZDT>(z_raw(i + 1))) * scb;
+          f32x4_t acca = {0.f, 0.f, 0.f, 0.f}, accb = {0.f, 0.f, 0.f, 0.f};
+          acca = mfma16x16x32(a0, unpack_crumb8_bf16(wv[i], 0, magic), acca);
+          accb = mfma16x16x32(b0, unpack_crumb8_bf16(wv[i + 1], 0, magic), accb);
+          acca = mfma16x16x32(a1, unpack_crumb8_bf16(wv[i], 1, magic), acca);
+          accb = mfma16x16x32(b1, unpack_crumb8_bf16(wv[i + 1], 1, magic), accb);
+#pragma unroll
+          for (int q = 0; q < RC; ++q) {
+            yacc[q] = fmaf(cza, xsa[q], yacc[q]);
+            yacc[q] = fmaf(czb, xsb[q], yacc[q]);
+            yacc[q] = fmaf(sca, acca[q], yacc[q]);
+            yacc[q] = fmaf(scb, accb[q], yacc[q]);
+          }
+        }
+      }
+      if (nchunks > 1) lds_barrier();      // every wave is done with this chunk before restaging
+    }
+
+    // cross-wave reduction in a fixed order; the buffer alternates between tiles
+    float* rb = red + buf * (W * 256);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) rb[wave * 256 + (4 * jl + q) * 16 + nl] = yacc[q];
+    lds_barrier();
+    const int n0 = tile * 16;
+    for (int e = threadIdx.x; e < 16 * a.M; e += blockDim.x) {
+      const int m = e >> 4;
+      const int n = e & 15;
+      float sum = 0.f;
+      for (int w = 0; w < W; ++w) sum += rb[w * 256 + e];
+      if (n0 + n < a.N) a.y[(int64_t)m * a.sym + n0 + n] = (uint16_t)f32_to_bf16_bits(sum);
+    }
+    buf ^= 1;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Generic fallback: any bit width (2/4/8), any group size, any stride/alignment, M <= 16.
 // One wave per output row; every weight is dequantized in fp32 as (q - bf16(z)) * bf16(s), the
 // same un-rounded weight the fast kernels accumulate with, and accumulated in fp32. Slow but
@@ -522,13 +753,23 @@ int launch_with_lds(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t st, c
   return IMQ_OK;
 }
 
+// Register budget: a kernel compiled for up to MAXW waves per workgroup gets 512/(MAXW/4)
+// VGPRs per lane at most; workgroups of <= 8 waves use the MAXW=8 build (no spills with the
+// deep S=8 batches and fp16/fp32 scale conversion).
+template <int S, int SDT, int ZDT, bool STRIP, int MAXW>
+int skinny_resident_mw(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
+  const dim3 g(grid), b(64 * W);
+  if (a.M == 1) return launch_with_lds(w4_skinny_kernel<S, 1, SDT, ZDT, STRIP, MAXW>, g, b, lds, st, a);
+  if (a.M == 2) return launch_with_lds(w4_skinny_kernel<S, 2, SDT, ZDT, STRIP, MAXW>, g, b, lds, st, a);
+  if (a.M <= 4) return launch_with_lds(w4_skinny_kernel<S, 4, SDT, ZDT, STRIP, MAXW>, g, b, lds, st, a);
+  return launch_with_lds(w4_skinny_kernel<S, 16, SDT, ZDT, STRIP, MAXW>, g, b, lds, st, a);
+}
+
 template <int S, int SDT, int ZDT, bool STRIP>
 int skinny_resident_m(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
-  const dim3 g(grid), b(64 * W);
-  if (a.M == 1) return launch_with_lds(w4_skinny_kernel<S, 1, SDT, ZDT, STRIP>, g, b, lds, st, a);
-  if (a.M == 2) return launch_with_lds(w4_skinny_kernel<S, 2, SDT, ZDT, STRIP>, g, b, lds, st, a);
-  if (a.M <= 4) return launch_with_lds(w4_skinny_kernel<S, 4, SDT, ZDT, STRIP>, g, b, lds, st, a);
-  return launch_with_lds(w4_skinny_kernel<S, 16, SDT, ZDT, STRIP>, g, b, lds, st, a);
+  if (W <= 8) return skinny_resident_mw<S, SDT, ZDT, STRIP, 8>(a, lds, grid, W, st);
+  if constexpr (S == 8 && SDT != IMQ_DT_BF16) return IMQ_ERR_UNSUPPORTED;   // never dispatched
+  else return skinny_resident_mw<S, SDT, ZDT, STRIP, 16>(a, lds, grid, W, st);
 }
 
 template <int S, int SDT, int ZDT>
@@ -572,7 +813,8 @@ int skinny_dispatch(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
   // MI355X at Llama-8B shapes: many tiles (N >= 16K) prefer deep batches (S=8) in persistent
   // workgroups; fewer tiles prefer splitting K over more waves (S=4), one tile per workgroup
   // while x is small.
-  const bool wide = NT >= 1024 && KS >= 16;
+  // (S=8 with more than 8 waves and fp16/fp32 scales would exceed the 16-wave register budget)
+  const bool wide = NT >= 1024 && KS >= 16 && (SDT == IMQ_DT_BF16 || (KS + 7) / 8 <= 8);
   int S, W;
   if (wide) { S = 8; W = (KS + 7) / 8; }
   else { S = 4; W = (KS + 3) / 4; }
@@ -671,10 +913,77 @@ template int generic_gemv<8>(const uint16_t*, int64_t, int64_t, int64_t, const u
 
 namespace imq {
 // int2 / int8 decode fast paths: not specialised yet -> caller falls back to the generic kernel.
-int skinny_w2(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, int64_t, const void*, int64_t,
-              int64_t, int, const void*, int64_t, int64_t, int, int64_t, int64_t, uint16_t*, int64_t,
-              hipStream_t) {
-  return IMQ_ERR_UNSUPPORTED;
+template <int S, int SDT, int ZDT, bool STRIP, int MAXW>
+int w2_launch_mw(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
+  const dim3 g(grid), b(64 * W);
+  if (a.M == 1) return launch_with_lds(w2_skinny_kernel<S, 1, SDT, ZDT, STRIP, MAXW>, g, b, lds, st, a);
+  if (a.M <= 4) return launch_with_lds(w2_skinny_kernel<S, 4, SDT, ZDT, STRIP, MAXW>, g, b, lds, st, a);
+  return launch_with_lds(w2_skinny_kernel<S, 16, SDT, ZDT, STRIP, MAXW>, g, b, lds, st, a);
+}
+
+template <int S, int SDT, int ZDT, bool STRIP>
+int w2_launch_m(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
+  if (W <= 8) return w2_launch_mw<S, SDT, ZDT, STRIP, 8>(a, lds, grid, W, st);
+  if constexpr (S == 16 && SDT != IMQ_DT_BF16) return IMQ_ERR_UNSUPPORTED;   // never dispatched
+  else return w2_launch_mw<S, SDT, ZDT, STRIP, 16>(a, lds, grid, W, st);
+}
+
+template <int S, int SDT, int ZDT>
+int w2_dispatch_s(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
+  SkinnyArgs a = a0;
+  constexpr int SZB = (SDT == IMQ_DT_FP32) ? 4 : 2;
+  constexpr int ZZB = (ZDT == IMQ_DT_FP32) ? 4 : 2;
+  const int KS = a.Kpad / kStep2;
+  const int NT = (a.N + 15) / 16;
+  int W = (KS + S - 1) / S;
+  if (W > 16) W = 16;
+  if (W < 1) W = 1;
+  auto need = [&](int cs) { return (size_t)a.M * (cs * kStep2 + kXPad) * 2 + (size_t)cs * 64 + (size_t)2 * W * 256 * 4; };
+  int cs = KS;
+  if (need(cs) > (size_t)di.max_lds) {
+    // chunks of whole rounds (W*S steps) while they fit, else of S steps
+    cs = ((KS + W * S - 1) / (W * S)) * W * S;
+    while (cs > W * S && need(cs) > (size_t)di.max_lds) cs -= W * S;
+    while (cs > S && need(cs) > (size_t)di.max_lds) cs -= S;
+    if (need(cs) > (size_t)di.max_lds) return IMQ_ERR_UNSUPPORTED;
+  }
+  a.chunk_steps = cs;
+  const size_t lds = need(cs);
+  // persistent workgroups: x is staged once per workgroup (resident) and amortized over tiles
+  const int grid = skinny_grid(NT, W, lds, di);
+  const bool strip = a.G == kStep2 && (KS % S) == 0 && (cs % S) == 0 && a.ssg == 1 && a.szg == 1 &&
+                     ((uintptr_t)a.sc % 16) == 0 && ((uintptr_t)a.zr % 16) == 0 &&
+                     ((a.ssn * SZB) % 16) == 0 && ((a.szn * ZZB) % 16) == 0;
+  if (strip) return w2_launch_m<S, SDT, ZDT, true>(a, lds, grid, W, st);
+  return w2_launch_m<S, SDT, ZDT, false>(a, lds, grid, W, st);
+}
+
+// S = 16 steps (4 KB of codes per wave per round); workgroups that need more than 8 waves with
+// fp16/fp32 scale conversion take S = 8 so the 128-VGPR budget of 16-wave workgroups holds.
+template <int SDT, int ZDT>
+int w2_dispatch(const SkinnyArgs& a, const DevInfo& di, hipStream_t st) {
+  const int KS = a.Kpad / kStep2;
+  if (SDT != IMQ_DT_BF16 && (KS + 15) / 16 > 8) return w2_dispatch_s<8, SDT, ZDT>(a, di, st);
+  return w2_dispatch_s<16, SDT, ZDT>(a, di, st);
+}
+
+int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
+              const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st) {
+  if (M < 1 || M > 16 || G % kStep2 != 0 || Kpad % G != 0 || Kpad <= 0) return IMQ_ERR_UNSUPPORTED;
+  if (((G / kStep2) & (G / kStep2 - 1)) != 0) return IMQ_ERR_UNSUPPORTED;   // groups of 2^k steps
+  if (((uintptr_t)q & 15) || (sqn & 15) || ((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
+  if ((Kpad / kStep2) % 4 != 0) return IMQ_ERR_UNSUPPORTED;   // whole 4-step (64-byte) load units
+  if (N > (1 << 30) || Kpad > (1 << 28)) return IMQ_ERR_UNSUPPORTED;
+  if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
+  const DevInfo di = device_info();
+  SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, 0};
+  switch (sdt) {
+    case IMQ_DT_BF16: return w2_dispatch<IMQ_DT_BF16, IMQ_DT_BF16>(a, di, st);
+    case IMQ_DT_FP16: return w2_dispatch<IMQ_DT_FP16, IMQ_DT_FP16>(a, di, st);
+    case IMQ_DT_FP32: return w2_dispatch<IMQ_DT_FP32, IMQ_DT_FP32>(a, di, st);
+  }
+  return IMQ_ERR_INVALID;
 }
 int skinny_w8(const uint16_t*, int64_t, int64_t, int64_t, const int8_t*, int64_t, const void*, int64_t, int,
               int64_t, uint16_t*, int64_t, hipStream_t) {

@@ -35,7 +35,12 @@ IMQ_DEV uint32_t f32_to_bf16_bits(float f) {
 
 IMQ_DEV float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
 
-IMQ_DEV float round_fp16(float f) { return __half2float(__float2half_rn(f)); }
+// fp16 <-> fp32 through _Float16 bit casts (v_cvt_f32_f16 / v_cvt_f16_f32, round to nearest even);
+// the __half helpers go through a union that can leave a stack slot behind in unrolled code.
+IMQ_DEV float f16_bits_to_f32(uint32_t b) { return (float)__builtin_bit_cast(_Float16, (uint16_t)b); }
+IMQ_DEV uint32_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+IMQ_DEV float round_fp16(float f) { return (float)(_Float16)f; }
 
 // Load element `idx` of a dtype-coded array as fp32 (exact widening).
 template <int DT>
@@ -43,7 +48,7 @@ IMQ_DEV float load_as_f32(const void* p, int64_t idx) {
   if constexpr (DT == IMQ_DT_BF16) {
     return bf16_bits_to_f32(((const uint16_t*)p)[idx]);
   } else if constexpr (DT == IMQ_DT_FP16) {
-    return __half2float(((const __half*)p)[idx]);
+    return f16_bits_to_f32(((const uint16_t*)p)[idx]);
   } else {
     return ((const float*)p)[idx];
   }
@@ -60,7 +65,7 @@ IMQ_DEV uint32_t load_raw_bits(const void* p, int64_t idx) {
 template <int DT>
 IMQ_DEV float raw_bits_to_f32(uint32_t b) {
   if constexpr (DT == IMQ_DT_BF16) return __uint_as_float(b << 16);
-  else if constexpr (DT == IMQ_DT_FP16) return __half2float(__ushort_as_half((unsigned short)b));
+  else if constexpr (DT == IMQ_DT_FP16) return f16_bits_to_f32(b);
   else return __uint_as_float(b);
 }
 
@@ -86,7 +91,7 @@ IMQ_DEV void store_from_f32(void* p, int64_t idx, float v) {
   if constexpr (DT == IMQ_DT_BF16) {
     ((uint16_t*)p)[idx] = (uint16_t)f32_to_bf16_bits(v);
   } else if constexpr (DT == IMQ_DT_FP16) {
-    ((__half*)p)[idx] = __float2half_rn(v);
+    ((uint16_t*)p)[idx] = (uint16_t)f32_to_f16_bits(v);
   } else {
     ((float*)p)[idx] = v;
   }
@@ -99,6 +104,10 @@ IMQ_DEV uint32_t cvt_pk_bf16(float lo, float hi) {
   const f32x2_t v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+
+// fp32 -> nearest bf16 (ties to even), kept as fp32: one v_cvt_pk_bf16_f32 and a shift. Equal
+// to round_bf16 for every finite input.
+IMQ_DEV float round_bf16_hw(float f) { return __uint_as_float(cvt_pk_bf16(f, 0.f) << 16); }
 
 // (a & m) | o  -> v_and_or_b32
 IMQ_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) { return (a & m) | o; }

@@ -211,6 +211,19 @@ def test_linear_w2_random_codes(dev, N, K, M):
     _linear_check(dev, c, M, seed=M, bits=2)
 
 
+@pytest.mark.parametrize("M", [1, 8, 16])
+def test_linear_w2_large_k_chunked(dev, M):
+    """C3's 28672 -> 8192 K at M = 8 / 16 does not fit LDS whole: x is staged in K chunks."""
+    c = dict(C.int2_random_case(272, 28672, 64, seed=2003, dt="fp16"))
+    _linear_check(dev, c, M, seed=M, bits=2)
+
+
+def test_linear_w2_fp32_scales(dev):
+    c = dict(C.int2_random_case(160, 4096, 64, seed=2004, dt="fp32"))
+    for M in (1, 3):
+        _linear_check(dev, c, M, seed=M, bits=2)
+
+
 def test_linear_w2_rtn_and_dealias(dev):
     c = C.int2_case(256, 1024, 64, seed=8)
     for M in (1, 5):

@@ -13,11 +13,11 @@ import pytest
 STEP = 128
 
 
-def _dispatch(Kpad, N=16):
+def _dispatch(Kpad, N=16, bf16=True):
     """skinny_dispatch in csrc/gemv.hip."""
     KS = Kpad // STEP
     NT = -(-N // 16)
-    if NT >= 1024 and KS >= 16:
+    if NT >= 1024 and KS >= 16 and (bf16 or -(-KS // 8) <= 8):
         S, W = 8, -(-KS // 8)
     else:
         S, W = 4, -(-KS // 4)
@@ -28,9 +28,9 @@ def _strip_ok(G, KS, S, ssg, szb, ssn_elems, base_align=256):
     return G == STEP and KS % S == 0 and ssg == 1 and (ssn_elems * szb) % 16 == 0 and base_align % 16 == 0
 
 
-def skinny_ranges(N, Kpad, M, G, szb, sqn, ssn, strip_bytes=None):
+def skinny_ranges(N, Kpad, M, G, szb, sqn, ssn, strip_bytes=None, bf16=True):
     """Max exclusive byte offset touched in (qweight, scale, x) for one launch."""
-    KS, S, W = _dispatch(Kpad, N)
+    KS, S, W = _dispatch(Kpad, N, bf16)
     R = -(-KS // (W * S))
     gsh = int(math.log2(G // STEP))
     strip = _strip_ok(G, KS, S, 1, szb, ssn)
@@ -84,7 +84,7 @@ def test_skinny_reads_in_bounds(N, K, szb, pad):
     q_bytes = (N - 1) * sqn + row_bytes          # exact fit: the last row has no padding after it
     s_bytes = N * ng * szb
     for M in (1, 4, 16):
-        q_hi, s_hi, x_hi, _ = skinny_ranges(N, Kpad, M, G, szb, sqn, ng)
+        q_hi, s_hi, x_hi, _ = skinny_ranges(N, Kpad, M, G, szb, sqn, ng, bf16=(szb == 2))
         assert q_hi <= q_bytes, (N, K, M, q_hi, q_bytes)
         assert s_hi <= s_bytes, (N, K, M, s_hi, s_bytes)
         assert x_hi <= M * Kpad * 2
@@ -178,3 +178,63 @@ def test_gemm_model_catches_unclamped_rows():
     M, K = 130, 256
     rows_unclamped = (-(-M // 128)) * 128
     assert (rows_unclamped - 1) * K + K > M * K
+
+
+# ---- int2 decode kernel (csrc/gemv.hip w2_skinny_kernel / w2_dispatch) ------------------------
+def w2_plan(M, Kpad, max_lds=160 * 1024, bf16=False):
+    """w2_dispatch: (S, W, chunk steps, LDS bytes) or None when nothing fits."""
+    KS = Kpad // 64
+    S = 8 if (not bf16 and -(-KS // 16) > 8) else 16
+    W = max(1, min(16, -(-KS // S)))
+    need = lambda cs: M * (cs * 64 + 8) * 2 + cs * 64 + 2 * W * 256 * 4  # noqa: E731
+    cs = KS
+    if need(cs) > max_lds:
+        cs = (-(-KS // (W * S))) * W * S
+        while cs > W * S and need(cs) > max_lds:
+            cs -= W * S
+        while cs > S and need(cs) > max_lds:
+            cs -= S
+        if need(cs) > max_lds:
+            return None
+    return S, W, cs, need(cs)
+
+
+@pytest.mark.parametrize("N,K", [(28672, 8192), (8192, 28672), (512, 1024), (96, 448), (1792, 2048)])
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
+@pytest.mark.parametrize("szb", [2, 4])
+def test_w2_reads_in_bounds(N, K, M, szb):
+    G = 64
+    Kpad = -(-K // G) * G
+    if (Kpad // 64) % 4:
+        pytest.skip("K_pad not a multiple of 256 codes: the generic kernel serves it")
+    plan = w2_plan(M, Kpad)
+    assert plan is not None
+    S, W, CS, lds = plan
+    KS = Kpad // 64
+    assert lds <= 160 * 1024 and (CS % S == 0 or CS == KS)
+    ng = Kpad // G
+    sqn = Kpad // 4
+    strip = KS % S == 0 and CS % S == 0
+    q_hi = s_hi = 0
+    nchunks = -(-KS // CS)
+    for row in (0, N - 1):
+        for c in range(nchunks):
+            c0, c1 = c * CS, min(KS, (c + 1) * CS)
+            R = -(-(c1 - c0) // (W * S))
+            for rnd in range(R):
+                for wave in range(W):
+                    sbase = c0 + (rnd * W + wave) * S
+                    for t in range(S // 4):
+                        sb4 = min(sbase + 4 * t, c1 - 4)
+                        q_hi = max(q_hi, row * sqn + 16 * 3 + 16 * sb4 + 16)
+                    for i in range(S):
+                        st = min(sbase + i, c1 - 1)
+                        if not strip:
+                            s_hi = max(s_hi, (row * ng + st) * szb + szb)
+                    if strip:
+                        g0 = sbase if sbase < c1 else c0
+                        s_hi = max(s_hi, (row * ng + g0) * szb + S * szb)
+            # staging reads x[m, c0*64 + 16*pr .. +16] for pr < 4*(c1-c0)
+            assert c0 * 64 + 16 * (4 * (c1 - c0) - 1) + 16 <= Kpad
+    assert q_hi <= (N - 1) * sqn + Kpad // 4
+    assert s_hi <= N * ng * szb
