@@ -43,7 +43,8 @@ struct SkinnyArgs {
   int G;
   uint16_t* y;
   int64_t sym;
-  int chunk_steps;   // K-steps (128 codes) staged in LDS at once
+  int chunk_steps;   // K-steps staged in LDS at once
+  const int8_t* q8;  // int8 weights (the int8 kernel; q is unused there)
 };
 
 constexpr int kStep = 128;          // codes per K-step
@@ -651,6 +652,147 @@ __global__ __launch_bounds__(64 * MAXW) void w2_skinny_kernel(SkinnyArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// int8 per-row decode kernel (M <= 16). A K-step is 64 codes: 64 bytes of each row, one 16-byte
+// load per lane (lane row jl takes codes [16*jl, 16*jl+16)), feeding two MFMAs whose operands
+// are (q + 128) as bf16 -- exact: q ^ 0x80 is q + 128 in 0..255, 8 significant bits -- against
+// activations in natural order. The per-row scale factors out of K, so one accumulator runs
+// over the whole row: y = s * (acc - 128 * sum(x)), the kernel form of the reference's `_ksk8`.
+// ---------------------------------------------------------------------------------------------
+constexpr int kStep8 = 64;
+
+// 8 int8 codes (two dwords) -> bf16x8 of (q + 128), exact.
+IMQ_DEV bf16x8_t biased_i8x8_bf16(uint32_t lo, uint32_t hi) {
+  u32x4_t r;
+  lo ^= 0x80808080u;
+  hi ^= 0x80808080u;
+  r[0] = cvt_pk_bf16((float)(lo & 0xffu), (float)((lo >> 8) & 0xffu));
+  r[1] = cvt_pk_bf16((float)((lo >> 16) & 0xffu), (float)(lo >> 24));
+  r[2] = cvt_pk_bf16((float)(hi & 0xffu), (float)((hi >> 8) & 0xffu));
+  r[3] = cvt_pk_bf16((float)((hi >> 16) & 0xffu), (float)(hi >> 24));
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+template <int S, int MC, int SDT, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void w8_skinny_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int nl = lane & 15;
+  const int jl = lane >> 4;
+  constexpr int RC = (MC < 4) ? MC : 4;
+
+  const int KS = a.Kpad / kStep8;                   // a.Kpad carries K (a multiple of 64)
+  const int CS = a.chunk_steps;
+  const int nchunks = (KS + CS - 1) / CS;
+  const int xls = CS * kStep8 + kXPad;
+  uint16_t* xl = (uint16_t*)smem;                                    // [M][xls]
+  float* xs = (float*)(smem + (size_t)a.M * xls * 2);                // [CS][16] step sums
+  float* xtot = xs + (size_t)CS * 16;                                // [16] row sums
+  float* red = xtot + 16;                                            // [2][W][256]
+  const int NT = (a.N + 15) / 16;
+
+  // stage steps [c0, c1) in natural order; per-step row sums reduced across the 8 lanes of a
+  // step, then added to the row totals in step order (deterministic)
+  auto stage = [&](int c0, int c1) {
+    const int nblk = (c1 - c0) * 8;
+    const int total = a.M * nblk;                    // a multiple of 8
+    for (int base = 0; base < total; base += blockDim.x) {
+      const int idx = base + threadIdx.x;
+      const bool valid = idx < total;
+      const int id = valid ? idx : total - 1;
+      const int m = id / nblk;
+      const int b = id - m * nblk;
+      const u32x4_t v = *(const u32x4_t*)(a.x + (int64_t)m * a.sxm + (int64_t)c0 * kStep8 + 8 * b);
+      float sum = 0.f;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
+      sum += __shfl_xor(sum, 1, 8);
+      sum += __shfl_xor(sum, 2, 8);
+      sum += __shfl_xor(sum, 4, 8);
+      if (valid) {
+        *(u32x4_t*)(xl + m * xls + 8 * b) = v;
+        if ((b & 7) == 0) xs[(b >> 3) * 16 + m] = sum;
+      }
+    }
+    lds_barrier();
+    if ((int)threadIdx.x < a.M) {
+      float t = xtot[threadIdx.x];
+      for (int st = 0; st < c1 - c0; ++st) t += xs[st * 16 + threadIdx.x];
+      xtot[threadIdx.x] = t;
+    }
+    lds_barrier();
+  };
+
+  const uint16_t* xlane = xl + (nl < a.M ? nl : a.M - 1) * xls + 16 * jl;
+  int buf = 0;
+  bool staged = false;
+
+  for (int tile = blockIdx.x; tile < NT; tile += gridDim.x) {
+    int row = tile * 16 + nl;
+    row = row < a.N ? row : a.N - 1;
+    const int8_t* qrow = a.q8 + (int64_t)row * a.sqn + 16 * jl;
+    f32x4_t acc[4];                          // four independent MFMA chains
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int c = 0; c < nchunks; ++c) {
+      const int c0 = c * CS;
+      const int c1 = (c0 + CS < KS) ? c0 + CS : KS;
+      if (nchunks > 1 || !staged) {
+        if (c == 0) {                          // row totals restart with each pass over K
+          lds_barrier();                       // (the previous tile's reduction has read them)
+          if ((int)threadIdx.x < 16) xtot[threadIdx.x] = 0.f;
+          lds_barrier();
+        }
+        stage(c0, c1);
+        staged = true;
+      }
+      const int R = (c1 - c0 + W * S - 1) / (W * S);
+      for (int rnd = 0; rnd < R; ++rnd) {
+        const int sbase = c0 + (rnd * W + wave) * S;
+        u32x4_t wv[S];
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+          int st = sbase + i;
+          st = st < c1 ? st : c1 - 1;
+          wv[i] = __builtin_nontemporal_load((const u32x4_t*)(qrow + (int64_t)st * kStep8));
+        }
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+          const int s0 = sbase + i;
+          if (s0 < c1) {                               // uniform across the wave
+            const int ls = s0 - c0;
+            const bf16x8_t x0 = *(const bf16x8_t*)(xlane + ls * kStep8);
+            const bf16x8_t x1 = *(const bf16x8_t*)(xlane + ls * kStep8 + 8);
+            acc[2 * (i & 1)] = mfma16x16x32(x0, biased_i8x8_bf16(wv[i][0], wv[i][1]), acc[2 * (i & 1)]);
+            acc[2 * (i & 1) + 1] = mfma16x16x32(x1, biased_i8x8_bf16(wv[i][2], wv[i][3]), acc[2 * (i & 1) + 1]);
+          }
+        }
+      }
+      if (nchunks > 1) lds_barrier();
+    }
+
+    float* rb = red + buf * (W * 256);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) rb[wave * 256 + (4 * jl + q) * 16 + nl] = (acc[0][q] + acc[1][q]) + (acc[2][q] + acc[3][q]);
+    lds_barrier();
+    const int n0 = tile * 16;
+    for (int e = threadIdx.x; e < 16 * a.M; e += blockDim.x) {
+      const int m = e >> 4;
+      const int n = e & 15;
+      float sum = 0.f;
+      for (int w = 0; w < W; ++w) sum += rb[w * 256 + e];
+      if (n0 + n < a.N) {
+        const float sc = load_as_f32<SDT>(a.sc, (int64_t)(n0 + n) * a.ssn);
+        a.y[(int64_t)m * a.sym + n0 + n] = (uint16_t)f32_to_bf16_bits(sc * (sum - 128.f * xtot[m]));
+      }
+    }
+    buf ^= 1;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Generic fallback: any bit width (2/4/8), any group size, any stride/alignment, M <= 16.
 // One wave per output row; every weight is dequantized in fp32 as (q - bf16(z)) * bf16(s), the
 // same un-rounded weight the fast kernels accumulate with, and accumulated in fp32. Slow but
@@ -985,8 +1127,54 @@ int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
   }
   return IMQ_ERR_INVALID;
 }
-int skinny_w8(const uint16_t*, int64_t, int64_t, int64_t, const int8_t*, int64_t, const void*, int64_t, int,
-              int64_t, uint16_t*, int64_t, hipStream_t) {
-  return IMQ_ERR_UNSUPPORTED;
+template <int SDT, int MAXW>
+int w8_launch_mw(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
+  constexpr int S = 8;
+  const dim3 g(grid), b(64 * W);
+  if (a.M == 1) return launch_with_lds(w8_skinny_kernel<S, 1, SDT, MAXW>, g, b, lds, st, a);
+  if (a.M <= 4) return launch_with_lds(w8_skinny_kernel<S, 4, SDT, MAXW>, g, b, lds, st, a);
+  return launch_with_lds(w8_skinny_kernel<S, 16, SDT, MAXW>, g, b, lds, st, a);
+}
+
+template <int SDT>
+int w8_dispatch(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
+  SkinnyArgs a = a0;
+  constexpr int S = 8;                     // 8 x 16 bytes per lane = 8 KB per wave per round
+  const int KS = a.Kpad / kStep8;
+  const int NT = (a.N + 15) / 16;
+  int W = (KS + S - 1) / S;
+  if (W > 16) W = 16;
+  if (W < 1) W = 1;
+  auto need = [&](int cs) {
+    return (size_t)a.M * (cs * kStep8 + kXPad) * 2 + (size_t)cs * 64 + 64 + (size_t)2 * W * 256 * 4;
+  };
+  int cs = KS;
+  if (need(cs) > (size_t)di.max_lds) {
+    cs = ((KS + W * S - 1) / (W * S)) * W * S;
+    while (cs > W * S && need(cs) > (size_t)di.max_lds) cs -= W * S;
+    while (cs > S && need(cs) > (size_t)di.max_lds) cs -= S;
+    if (need(cs) > (size_t)di.max_lds) return IMQ_ERR_UNSUPPORTED;
+  }
+  a.chunk_steps = cs;
+  const size_t lds = need(cs);
+  const int grid = skinny_grid(NT, W, lds, di);
+  if (W <= 8) return w8_launch_mw<SDT, 8>(a, lds, grid, W, st);
+  return w8_launch_mw<SDT, 16>(a, lds, grid, W, st);
+}
+
+int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t* q, int64_t sqn,
+              const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st) {
+  if (M < 1 || M > 16 || K <= 0 || K % kStep8 != 0) return IMQ_ERR_UNSUPPORTED;
+  if (((uintptr_t)q & 15) || (sqn & 15) || ((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
+  if (N > (1 << 30) || K > (1 << 28)) return IMQ_ERR_UNSUPPORTED;
+  const DevInfo di = device_info();
+  SkinnyArgs a{x, sxm, (int)M, (int)K, nullptr, sqn, sc, ssn, 0, nullptr, 0, 0, (int)N, 0, y, sym, 0};
+  a.q8 = q;
+  switch (sdt) {
+    case IMQ_DT_BF16: return w8_dispatch<IMQ_DT_BF16>(a, di, st);
+    case IMQ_DT_FP16: return w8_dispatch<IMQ_DT_FP16>(a, di, st);
+    case IMQ_DT_FP32: return w8_dispatch<IMQ_DT_FP32>(a, di, st);
+  }
+  return IMQ_ERR_INVALID;
 }
 }  // namespace imq

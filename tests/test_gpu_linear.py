@@ -251,6 +251,13 @@ def test_linear_w8(dev, M, sdt):
     _int8_check(dev, 384, 1000, M, sdt, seed=M)
 
 
+@pytest.mark.parametrize("N,K,M,sdt", [(320, 14336, 1, "fp16"), (320, 14336, 5, "bf16"), (320, 14336, 16, "fp16"),
+                                       (1000, 4096, 3, "bf16"), (96, 256, 16, "fp32")])
+def test_linear_w8_decode_kernel(dev, N, K, M, sdt):
+    """K a multiple of 64: the int8 MFMA decode kernel (x staged in chunks at K = 14336, M = 16)."""
+    _int8_check(dev, N, K, M, sdt, seed=N + M)
+
+
 def test_linear_w8_c4_shape_rows(dev):
     _int8_check(dev, 14336 // 8, 4096, 16, "fp16", seed=77)
 

@@ -238,3 +238,44 @@ def test_w2_reads_in_bounds(N, K, M, szb):
             assert c0 * 64 + 16 * (4 * (c1 - c0) - 1) + 16 <= Kpad
     assert q_hi <= (N - 1) * sqn + Kpad // 4
     assert s_hi <= N * ng * szb
+
+
+# ---- int8 decode kernel (csrc/gemv.hip w8_skinny_kernel / w8_dispatch) ------------------------
+def w8_plan(M, K, max_lds=160 * 1024):
+    S = 8
+    KS = K // 64
+    W = max(1, min(16, -(-KS // S)))
+    need = lambda cs: M * (cs * 64 + 8) * 2 + cs * 64 + 64 + 2 * W * 256 * 4  # noqa: E731
+    cs = KS
+    if need(cs) > max_lds:
+        cs = (-(-KS // (W * S))) * W * S
+        while cs > W * S and need(cs) > max_lds:
+            cs -= W * S
+        while cs > S and need(cs) > max_lds:
+            cs -= S
+        if need(cs) > max_lds:
+            return None
+    return S, W, cs, need(cs)
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336), (320, 14336), (1000, 4096), (1792, 4096)])
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_w8_reads_in_bounds(N, K, M):
+    plan = w8_plan(M, K)
+    assert plan is not None
+    S, W, CS, lds = plan
+    KS = K // 64
+    assert lds <= 160 * 1024 and (CS % S == 0 or CS == KS)
+    q_hi = 0
+    for row in (0, N - 1):
+        for c in range(-(-KS // CS)):
+            c0, c1 = c * CS, min(KS, (c + 1) * CS)
+            R = -(-(c1 - c0) // (W * S))
+            for rnd in range(R):
+                for wave in range(W):
+                    sbase = c0 + (rnd * W + wave) * S
+                    for i in range(S):
+                        st = min(sbase + i, c1 - 1)
+                        q_hi = max(q_hi, row * K + 16 * 3 + 64 * st + 16)
+            assert c0 * 64 + 8 * (8 * (c1 - c0) - 1) + 8 <= K
+    assert q_hi <= N * K
