@@ -420,6 +420,203 @@ __global__ __launch_bounds__(64 * W) void w4_skinny_chunked_kernel(SkinnyArgs a)
   }
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// int4 line kernel: the decode path for M <= 4, G == 128.
+//
+// One workgroup = one tile of 16 output rows; its W waves split K into line-steps of 256 codes
+// (128 bytes of every packed row), wave w owning line-steps [w*S2, w*S2 + S2). Per line-step a
+// wave issues two 16-byte loads per lane whose 64 lanes cover FULL 128-byte lines: load L0 reads
+// rows 0-7, load L1 rows 8-15. Lane (c = lane % 16, a = lane / 16) of L0 reads row c & 7 at byte
+// 16a (group 2l, columns c < 8) or 64 + 16a (group 2l+1, columns c >= 8); L1 mirrors it for rows
+// 8-15. Selecting per lane then gives every lane the codes of ONE group of ONE row:
+//   operand A-group (group 2l): c < 8 ? L0 : L1  -> row c
+//   operand B-group (group 2l+1): c < 8 ? L1 : L0  -> row c ^ 8
+// Each group feeds four v_mfma_f32_16x16x32_bf16 (weights = B operand, column = row) with the
+// (code | 0x4300) = 128 + code unpack; the zero point and the +128 bias fold into one correction
+// per group, y += s*acc - s*(128 + z)*sum(x), so every MFMA stays inside one group. The B-group
+// accumulators hold row c ^ 8 in column c and are swapped back with one DPP row rotate.
+//
+// Issue order per wave: its x range, its scale/zero words (16 rows x S2 dwords per array, one
+// dword per lane), then the weights; x and scale/zero are staged in wave-private LDS, so no
+// workgroup barrier precedes the compute, which consumes line-steps as their loads land. The
+// wave partials meet in LDS once at the end (fixed order, deterministic).
+// ---------------------------------------------------------------------------------------------
+constexpr int kLine = 256;
+
+// lane c of each 16-lane row receives the value of lane c ^ 8 (DPP row_ror:8)
+IMQ_DEV float row_swap8(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+}
+
+// LDS bytes of one wave's staging area / of a whole workgroup
+IMQ_HOST_DEV inline int line_wave_lds(int M, int S2, int vb) {
+  return M * (S2 * kLine + 8) * 2 + 2 * S2 * 16 * 4 + 2 * 16 * S2 * vb / 2 * 4;
+}
+
+template <int S2, int MC, int SDT, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;   // bytes per scale / zero value
+  constexpr int DPR = S2 * VB / 2;                   // dwords per row per array (2*S2 values)
+  constexpr int RC = MC < 4 ? MC : 4;                 // D registers that can hold a real row
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int c = lane & 15, ar = lane >> 4;
+  const bool lo8 = c < 8;
+  const int M = a.M;
+  const int KL = a.Kpad / kLine;
+  const int ls0 = wave * S2;
+  const int row0 = blockIdx.x * 16;
+  const int rlast = a.N - 1 - row0;                  // last valid row within the tile
+
+  const int xrow = S2 * kLine + 8;
+  const int wbytes = line_wave_lds(M, S2, VB);
+  unsigned char* wl = smem + (size_t)wave * wbytes;
+  uint16_t* xw = (uint16_t*)wl;
+  float* xs = (float*)(wl + M * xrow * 2);
+  uint32_t* szl = (uint32_t*)(xs + 2 * S2 * 16);
+  float* red = (float*)(smem + (size_t)W * wbytes);
+
+  // 1) x: M rows x 32*S2 16-byte blocks of this wave's K range (clamped into the row)
+  constexpr int XB = 32 * S2;
+  constexpr int XU = (MC * XB + 63) / 64;
+  const int xtot = M * XB;
+  const uint16_t* xbase = a.x + (int64_t)ls0 * kLine;
+  const int xlim = a.Kpad - ls0 * kLine - 8;         // last valid block start in the range
+  u32x4_t xv[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    int idx = lane + 64 * u;
+    idx = idx < xtot ? idx : xtot - 1;
+    const int m = idx / XB, b = idx - m * XB;
+    int kb = 8 * b;
+    kb = kb < xlim ? kb : xlim;
+    xv[u] = *(const u32x4_t*)(xbase + m * (int)a.sxm + kb);
+  }
+  // 2) scale / zero words of groups [2*ls0, 2*ls0 + 2*S2): 2 arrays x 16 rows x DPR dwords
+  constexpr int ZU = (32 * DPR + 63) / 64;
+  const int ngd = a.Kpad / 128 * VB / 4;             // dwords per row holding real groups
+  const unsigned char* sbase = (const unsigned char*)a.sc + (int64_t)row0 * a.ssn * VB;
+  const unsigned char* zbase = (const unsigned char*)a.zr + (int64_t)row0 * a.szn * VB;
+  uint32_t zv[ZU];
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    int d = lane + 64 * u;
+    d = d < 32 * DPR ? d : 32 * DPR - 1;
+    const int arr = d / (16 * DPR);
+    const int rem = d - arr * (16 * DPR);
+    int r = rem / DPR;
+    const int dw = rem - r * DPR;
+    r = r < rlast ? r : rlast;
+    int gd = ls0 * (VB / 2) + dw;                    // dword index within the row (VB/2 per line-step)
+    gd = gd < ngd ? gd : ngd - 1;
+    const unsigned char* p = arr ? zbase + r * (int)a.szn * VB : sbase + r * (int)a.ssn * VB;
+    zv[u] = *(const uint32_t*)(p + 4 * gd);
+  }
+  // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
+  const uint8_t* qt = a.q + (int64_t)row0 * a.sqn;
+  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
+  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
+  const uint8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
+  const uint8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  u32x4_t wb[2 * S2];
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    int l = ls0 + i;
+    l = l < KL ? l : KL - 1;
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+  }
+  // 4) stage x (permuted to the unpack order) with its per-group sums, and scale/zero
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int idx = lane + 64 * u;
+    const bool ok = idx < xtot;
+    const int m = (ok ? idx : 0) / XB, b = (ok ? idx : 0) - m * XB;
+    float sum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
+    // the 16 blocks of one group are 16 consecutive idx (XB is a multiple of 16)
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    if (ok) {
+      *(u32x4_t*)(xw + m * xrow + 8 * b) = permute_x8(xv[u]);
+      if ((b & 15) == 0) xs[(b >> 4) * 16 + m] = sum;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    const int d = lane + 64 * u;
+    if (d < 32 * DPR) szl[d] = zv[u];
+  }
+  // LDS is written and read by this wave only; its LDS operations execute in order
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+  const uint32_t magic = magic_bf16_128x2();
+  const uint16_t* xa = xw + (c < M ? c : M - 1) * xrow + 32 * ar;
+  const uint32_t* sc_c = szl + c * DPR;
+  const uint32_t* sc_x = szl + (c ^ 8) * DPR;
+  const uint32_t* zr_c = szl + 16 * DPR + c * DPR;
+  const uint32_t* zr_x = szl + 16 * DPR + (c ^ 8) * DPR;
+  auto val = [&](const uint32_t* p, int g) -> float {   // group g (0 .. 2*S2) of a staged row
+    if constexpr (VB == 4) return round_bf16_hw(__uint_as_float(p[g]));
+    else return raw_to_bf16_f32<SDT>((g & 1) ? (p[g >> 1] >> 16) : (p[g >> 1] & 0xffffu));
+  };
+  float y0[4] = {0.f, 0.f, 0.f, 0.f}, y1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    const bool v = ls0 + i < KL;
+    const f32x4_t xs0 = *(const f32x4_t*)(xs + (2 * i) * 16 + 4 * ar);
+    const f32x4_t xs1 = *(const f32x4_t*)(xs + (2 * i + 1) * 16 + 4 * ar);
+    bf16x8_t A0[4], A1[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      A0[k] = *(const bf16x8_t*)(xa + i * kLine + 8 * k);
+      A1[k] = *(const bf16x8_t*)(xa + i * kLine + 128 + 8 * k);
+    }
+    const float s0 = v ? val(sc_c, 2 * i) : 0.f;
+    const float s1 = v ? val(sc_x, 2 * i + 1) : 0.f;
+    const float cz0 = -(128.f + val(zr_c, 2 * i)) * s0;
+    const float cz1 = -(128.f + val(zr_x, 2 * i + 1)) * s1;
+    const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
+    u32x4_t gA, gB;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      gA[d] = lo8 ? w0[d] : w1[d];
+      gB[d] = lo8 ? w1[d] : w0[d];
+    }
+    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      acc0 = mfma16x16x32(A0[k], unpack_nib8_bf16(gA[k], magic), acc0);
+      acc1 = mfma16x16x32(A1[k], unpack_nib8_bf16(gB[k], magic), acc1);
+    }
+#pragma unroll
+    for (int r = 0; r < RC; ++r) {
+      y0[r] = fmaf(cz0, xs0[r], y0[r]);
+      y1[r] = fmaf(cz1, xs1[r], y1[r]);
+      y0[r] = fmaf(s0, acc0[r], y0[r]);
+      y1[r] = fmaf(s1, acc1[r], y1[r]);
+    }
+  }
+  // D row m = 4*ar + r; rows m < M <= 4 live in lanes ar == 0
+  float* rb = red + wave * (RC * 16);
+#pragma unroll
+  for (int r = 0; r < RC; ++r) {
+    const float v = y0[r] + row_swap8(y1[r]);
+    if (ar == 0) rb[r * 16 + c] = v;
+  }
+  lds_barrier();
+  for (int e = threadIdx.x; e < 16 * M; e += blockDim.x) {
+    const int m = e >> 4, n = e & 15;
+    float sum = 0.f;
+    for (int w = 0; w < W; ++w) sum += red[w * (RC * 16) + m * 16 + n];
+    if (n <= rlast) a.y[(int64_t)m * a.sym + row0 + n] = (uint16_t)f32_to_bf16_bits(sum);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // int2 decode kernel (M <= 16). A K-step is one 64-code group: 16 bytes of each packed row.
 // Lane (row nl, quarter jl) works on dword jl = codes [16*jl, 16*jl+16) of each step, which
@@ -984,6 +1181,65 @@ int skinny_dispatch(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
   return skinny_chunked<8, SDT, ZDT>(a, need(cs), grid, st);
 }
 
+// Line kernel dispatch (M <= 4, G == 128, K_pad a multiple of 256 and at most 16384, unit group
+// strides, same scale / zero dtype). Line-steps per wave S2: 4 at M == 1, 2 otherwise (measured
+// on MI355X at Llama-8B shapes), raised to 4 when W = ceil(KL / S2) would exceed 16 waves. Deeper
+// S2 (larger K) would exceed the 128-VGPR budget of 16-wave workgroups; such K take the skinny
+// kernel.
+template <int S2, int SDT>
+int line_launch(const SkinnyArgs& a, int W, size_t lds, hipStream_t st) {
+  const dim3 g((unsigned)((a.N + 15) / 16)), b(64 * W);
+  if (a.M == 1) return launch_with_lds(w4_line_kernel<S2, 1, SDT, 16>, g, b, lds, st, a);
+  if (a.M == 2) return launch_with_lds(w4_line_kernel<S2, 2, SDT, 16>, g, b, lds, st, a);
+  return launch_with_lds(w4_line_kernel<S2, 4, SDT, 16>, g, b, lds, st, a);
+}
+
+template <int SDT>
+int line_dispatch_s(const SkinnyArgs& a, int S2, int W, size_t lds, hipStream_t st) {
+  if (S2 == 2) return line_launch<2, SDT>(a, W, lds, st);
+  return line_launch<4, SDT>(a, W, lds, st);
+}
+
+// Eligibility and launch shape of the line kernel (restated by the CPU bounds model in the
+// tests): returns false when the line kernel does not take the call.
+bool line_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
+               int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int* S2o, int* Wo,
+               size_t* ldso) {
+  if (M < 1 || M > 4 || G != 128 || Kpad % kLine != 0 || sdt != zdt) return false;
+  if (ssg != 1 || szg != 1 || N < 1) return false;
+  const int vb = sdt == IMQ_DT_FP32 ? 4 : 2;
+  if ((ssn * vb) % 4 != 0 || (szn * vb) % 4 != 0) return false;
+  // 32-bit in-tile offsets
+  if (16 * sqn >= (int64_t(1) << 31) || M * sxm * 2 >= (int64_t(1) << 31)) return false;
+  if (16 * ssn * vb >= (int64_t(1) << 31) || 16 * szn * vb >= (int64_t(1) << 31)) return false;
+  const int64_t KL = Kpad / kLine;
+  int S2 = M == 1 ? 4 : 2;
+  if ((KL + S2 - 1) / S2 > 16) S2 = 4;
+  const int64_t W = (KL + S2 - 1) / S2;
+  if (W > 16) return false;
+  const int rc = M <= 2 ? (int)M : 4;                // reduction rows of the launched M class
+  const size_t lds = (size_t)W * line_wave_lds((int)M, S2, vb) + (size_t)W * rc * 16 * 4;
+  if (lds > (size_t)max_lds) return false;
+  *S2o = S2;
+  *Wo = (int)W;
+  *ldso = lds;
+  return true;
+}
+
+int line_w4(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
+  int S2, W;
+  size_t lds;
+  if (!line_plan(a.M, a.Kpad, a.G, a.N, a.sqn, a.sxm, a.ssn, a.ssg, a.szn, a.szg, sdt, sdt, di.max_lds,
+                 &S2, &W, &lds))
+    return IMQ_ERR_UNSUPPORTED;
+  switch (sdt) {
+    case IMQ_DT_BF16: return line_dispatch_s<IMQ_DT_BF16>(a, S2, W, lds, st);
+    case IMQ_DT_FP16: return line_dispatch_s<IMQ_DT_FP16>(a, S2, W, lds, st);
+    case IMQ_DT_FP32: return line_dispatch_s<IMQ_DT_FP32>(a, S2, W, lds, st);
+  }
+  return IMQ_ERR_UNSUPPORTED;
+}
+
 // Fast path eligibility + launch. Returns IMQ_ERR_UNSUPPORTED when the caller must fall back.
 int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
@@ -995,6 +1251,10 @@ int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
   if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
   const DevInfo di = device_info();
   SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, 0};
+  if (((uintptr_t)sc & 3) == 0 && ((uintptr_t)zr & 3) == 0) {
+    const int rc = line_w4(a, sdt, di, st);
+    if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+  }
   switch (sdt) {
     case IMQ_DT_BF16: return skinny_dispatch<IMQ_DT_BF16, IMQ_DT_BF16>(a, di, st);
     case IMQ_DT_FP16: return skinny_dispatch<IMQ_DT_FP16, IMQ_DT_FP16>(a, di, st);

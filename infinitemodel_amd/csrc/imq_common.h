@@ -22,6 +22,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 #define IMQ_DEV __device__ __forceinline__
+#define IMQ_HOST_DEV __host__ __device__
 
 // ---- bf16 / fp16 <-> fp32 (bit-level, round-to-nearest-even) --------------------------------
 IMQ_DEV float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }

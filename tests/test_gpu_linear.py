@@ -132,6 +132,28 @@ def test_linear_w4_ragged(dev, N, K, M):
     _linear_check(dev, c, M, seed=M)
 
 
+@pytest.mark.parametrize("N,K", [(37, 512), (100, 768), (512, 14336), (48, 16384), (32, 16640)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_linear_w4_line_kernel_shapes(dev, N, K, M):
+    """Decode shapes of the int4 line kernel (M <= 4, G 128, K_pad % 256 == 0, K_pad <= 16384):
+    a ragged last tile (N % 16), waves with unused line-steps (K 768), Llama down_proj K 14336,
+    the largest K it takes (16384) and the first it leaves to the skinny kernel (16640)."""
+    c = C.int4_case(N, K, 128, seed=N + K)
+    _linear_check(dev, c, M, seed=M)
+
+
+@pytest.mark.parametrize("sdt", ["fp16", "fp32"])
+@pytest.mark.parametrize("M", [1, 3])
+def test_linear_w4_line_kernel_scale_dtypes_dealias(dev, sdt, M):
+    """The line kernel's fp16 / fp32 scale-zero words and the +64-byte de-alias row view."""
+    c = dict(C.int4_case(96, 1024, 128, seed=5))
+    c["s"] = oq.round_to(c["s"], sdt)
+    c["z"] = oq.round_to(c["z"], sdt)
+    c["dt"] = sdt
+    c["Wd"] = oq.dequant_int4(c["q"], c["s"], c["z"], c["in_f"], 128, "bf16")
+    _linear_check(dev, c, M, seed=M, view_pad=64)
+
+
 def test_linear_w4_in_features_not_multiple_of_group(dev):
     c = C.int4_case(80, 300, 128, seed=11)     # K_pad = 384, x zero-padded past 300
     for M in (1, 3, 16):

@@ -279,3 +279,129 @@ def test_w8_reads_in_bounds(N, K, M):
                         q_hi = max(q_hi, row * K + 16 * 3 + 64 * st + 16)
             assert c0 * 64 + 8 * (8 * (c1 - c0) - 1) + 8 <= K
     assert q_hi <= N * K
+
+
+# ---- int4 line kernel (csrc/gemv.hip w4_line_kernel / line_plan) ------------------------------
+LINE = 256
+
+
+def line_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024):
+    """line_plan in csrc/gemv.hip: (S2, W, LDS bytes) or None when the line kernel declines."""
+    if not (1 <= M <= 4) or G != 128 or Kpad % LINE or N < 1:
+        return None
+    if (ssn * vb) % 4:
+        return None
+    if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31 or 16 * ssn * vb >= 2 ** 31:
+        return None
+    KL = Kpad // LINE
+    S2 = 4 if M == 1 else 2
+    if -(-KL // S2) > 16:
+        S2 = 4
+    W = -(-KL // S2)
+    if W > 16:
+        return None
+    wave_lds = M * (S2 * LINE + 8) * 2 + 2 * S2 * 16 * 4 + 2 * 16 * S2 * vb // 2 * 4
+    rc = M if M <= 2 else 4              # M = 3 runs the 4-row instantiation
+    lds = W * wave_lds + W * rc * 16 * 4
+    if lds > max_lds:
+        return None
+    return S2, W, lds
+
+
+def line_ranges(M, Kpad, N, sqn, sxm, ssn, vb, S2, W, sz_dword=None):
+    """Max exclusive byte offsets read from qweight / scale (= zero) / x and written to y, from
+    the kernel's per-lane arithmetic with its clamps. sz_dword(ls0, dw) overrides the scale dword
+    index (negative controls)."""
+    KL = Kpad // LINE
+    DPR = S2 * vb // 2
+    ngd = Kpad // 128 * vb // 4
+    q_hi = s_hi = x_hi = y_hi = 0
+    NT = -(-N // 16)
+    for tile in sorted({0, NT - 1}):
+        row0 = tile * 16
+        rlast = N - 1 - row0
+        for wave in range(W):
+            ls0 = wave * S2
+            # x: idx -> (m, b), kb = min(8b, Kpad - ls0*256 - 8), 8 elements
+            XB = 32 * S2
+            xtot = M * XB
+            xlim = Kpad - ls0 * LINE - 8
+            for idx in range(xtot):
+                m, b = divmod(idx, XB)
+                kb = min(8 * b, xlim)
+                assert kb >= 0
+                x_hi = max(x_hi, (ls0 * LINE + m * sxm + kb + 8) * 2)
+            # scale / zero dwords
+            for d in range(32 * DPR):
+                arr, rem = divmod(d, 16 * DPR)
+                r, dw = divmod(rem, DPR)
+                r = min(r, rlast)
+                gd = sz_dword(ls0, dw) if sz_dword else ls0 * (vb // 2) + dw
+                gd = min(gd, ngd - 1)
+                s_hi = max(s_hi, (row0 + r) * ssn * vb + 4 * gd + 4)
+            # weights: two full-line loads per line-step
+            for c in range(16):
+                for ar in range(4):
+                    lo8 = c < 8
+                    rr0 = min(c & 7, rlast)
+                    rr1 = min(8 + (c & 7), rlast)
+                    for i in range(S2):
+                        l = min(ls0 + i, KL - 1)
+                        q_hi = max(q_hi, (row0 + rr0) * sqn + 16 * ar + (0 if lo8 else 64) + 128 * l + 16)
+                        q_hi = max(q_hi, (row0 + rr1) * sqn + 16 * ar + (64 if lo8 else 0) + 128 * l + 16)
+        for n in range(16):
+            if n <= rlast:
+                y_hi = max(y_hi, row0 + n + 1)
+    return q_hi, s_hi, x_hi, y_hi
+
+
+LINE_SHAPES = [(4096, 4096), (6144, 4096), (28672, 4096), (4096, 14336), (37, 512), (100, 768), (17, 256),
+               (48, 16384), (1000, 256)]
+
+
+@pytest.mark.parametrize("N,K", LINE_SHAPES)
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("vb", [2, 4])
+@pytest.mark.parametrize("pad", [0, 64])
+def test_line_reads_in_bounds(N, K, M, vb, pad):
+    Kpad = K
+    ng = Kpad // 128
+    sqn = Kpad // 2 + pad
+    plan = line_plan(M, Kpad, 128, N, sqn, Kpad, ng, vb)
+    assert plan is not None
+    S2, W, lds = plan
+    assert W * S2 * LINE >= Kpad and (W - 1) * S2 * LINE < Kpad
+    assert lds <= 160 * 1024
+    q_hi, s_hi, x_hi, y_hi = line_ranges(M, Kpad, N, sqn, Kpad, ng, vb, S2, W)
+    # LDS: the reduction area of the launched row class (M = 3 -> 4 rows) lies inside the launch
+    rc = M if M <= 2 else 4
+    xrow = S2 * LINE + 8
+    wave_lds = M * xrow * 2 + 2 * S2 * 16 * 4 + 2 * 16 * S2 * vb // 2 * 4
+    assert W * wave_lds + W * rc * 16 * 4 <= lds
+    assert q_hi <= (N - 1) * sqn + Kpad // 2          # exact fit: no padding after the last row
+    assert s_hi <= N * ng * vb
+    assert x_hi <= ((M - 1) * Kpad + Kpad) * 2
+    assert y_hi <= N
+
+
+def test_line_plan_declines():
+    """Shapes the line kernel leaves to the skinny kernel."""
+    assert line_plan(5, 4096, 128, 4096, 2048, 4096, 32, 2) is None      # M > 4
+    assert line_plan(1, 4096, 64, 4096, 2048, 4096, 64, 2) is None       # G != 128
+    assert line_plan(1, 384, 128, 37, 192, 384, 3, 2) is None            # K_pad % 256
+    assert line_plan(1, 16640, 128, 64, 8320, 16640, 130, 2) is None     # K_pad > 16384 (W > 16)
+    assert line_plan(1, 16384, 128, 64, 8192, 16384, 128, 2) is not None
+
+
+def test_line_model_catches_wrong_scale_index():
+    """Negative control for the scale dword index: line-steps * dwords-per-row (instead of the
+    dwords of one line-step) stays inside the array only because of the in-kernel clamp, and
+    then hands every wave but the first the groups of another K range."""
+    N, K, M, vb = 64, 4096, 1, 2
+    S2, W, _ = line_plan(M, K, 128, N, K // 2, K, K // 128, vb)
+    DPR = S2 * vb // 2
+    wrong = lambda ls0, dw: ls0 * DPR + dw     # noqa: E731
+    # with the clamp to the row the wrong index stays inside the array but reads other groups:
+    # compare the group each wave would use for its first line-step
+    for wave in range(1, W):
+        assert wrong(wave * S2, 0) != wave * S2 * (vb // 2)
