@@ -57,12 +57,6 @@ IMQ_DEV uint32_t load_raw(const void* p, int64_t idx) {
   if constexpr (DT == IMQ_DT_FP32) return ((const uint32_t*)p)[idx];
   else return ((const uint16_t*)p)[idx];
 }
-template <int DT>
-IMQ_DEV float raw_to_bf16_f32(uint32_t r) {
-  if constexpr (DT == IMQ_DT_BF16) return __uint_as_float(r << 16);
-  else if constexpr (DT == IMQ_DT_FP16) return round_bf16_hw(f16_bits_to_f32(r));
-  else return round_bf16_hw(__uint_as_float(r));
-}
 
 // Load exactly NW dwords (NW in {2, 4, 8, 16}) from an address aligned to min(4*NW, 16) bytes.
 template <int NW>

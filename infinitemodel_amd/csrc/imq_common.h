@@ -110,6 +110,15 @@ IMQ_DEV uint32_t cvt_pk_bf16(float lo, float hi) {
 // to round_bf16 for every finite input.
 IMQ_DEV float round_bf16_hw(float f) { return __uint_as_float(cvt_pk_bf16(f, 0.f) << 16); }
 
+// Raw 16/32-bit scale/zero bits -> fp32 value rounded to bf16 (the operand of the reference
+// dequant `_dequant(torch.bfloat16)`), converted where it is consumed.
+template <int DT>
+IMQ_DEV float raw_to_bf16_f32(uint32_t r) {
+  if constexpr (DT == IMQ_DT_BF16) return __uint_as_float(r << 16);
+  else if constexpr (DT == IMQ_DT_FP16) return round_bf16_hw(f16_bits_to_f32(r));
+  else return round_bf16_hw(__uint_as_float(r));
+}
+
 // (a & m) | o  -> v_and_or_b32
 IMQ_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) { return (a & m) | o; }
 

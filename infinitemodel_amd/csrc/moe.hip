@@ -90,6 +90,357 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   }
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// Token-sorted grouped path (G == 128, K of both projections a multiple of 256, I % 32 == 0,
+// H % 64 == 0, unit group strides):
+//   moe_sort_kernel   counting sort of the T*k routed rows by expert -> off[E+1], perm[B] (sorted
+//                     position -> routed row t*k + j), inv[B] (routed row -> sorted position)
+//   moe_line_kernel   one workgroup per (expert, 64-row block): the block's weights are loaded once
+//                     into registers (the decode line kernel's full-line layout) and reused for all
+//                     of the expert's tokens, 16 per MFMA pass. MODE 0 is gate_up: rows
+//                     [32b, 32b+32) of gate and the matching up rows, SwiGLU in the epilogue, bf16 h
+//                     in sorted order. MODE 1 is down: 64 rows of H, fp32 per sorted row.
+//   moe_combine_kernel out[t] = bf16(sum_j w[t, j] * yr[inv[t*k + j]]), slot order.
+// Workgroups of experts no token routes to exit at once.
+// ---------------------------------------------------------------------------------------------
+constexpr int kMoeLine = 256;
+constexpr int kMoeTiles = 4;          // 16-row tiles per workgroup (64 weight rows)
+
+__global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restrict__ idx, int B, int E,
+                                                        int32_t* __restrict__ off, int32_t* __restrict__ perm,
+                                                        int32_t* __restrict__ inv) {
+  extern __shared__ int32_t sh[];     // cnt[E], then the per-thread partial sums [blockDim]
+  int32_t* cnt = sh;
+  int32_t* part = sh + E;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  for (int e = tid; e < E; e += nt) cnt[e] = 0;
+  __syncthreads();
+  for (int b = tid; b < B; b += nt) {
+    int e = idx[b];
+    e = (e >= 0 && e < E) ? e : 0;   // ids outside [0, E) are clamped, so every access stays in bounds
+    atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  // exclusive scan: thread t owns experts [t*per, t*per + per)
+  const int per = (E + nt - 1) / nt;
+  const int e0 = tid * per, e1 = (e0 + per < E) ? e0 + per : E;
+  int local = 0;
+  for (int e = e0; e < e1; ++e) local += cnt[e];
+  part[tid] = local;
+  __syncthreads();
+  for (int d = 1; d < nt; d <<= 1) {     // Hillis-Steele inclusive scan of the partials
+    const int v = tid >= d ? part[tid - d] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int run = part[tid] - local;
+  for (int e = e0; e < e1; ++e) {
+    const int c = cnt[e];
+    off[e] = run;
+    cnt[e] = run;                        // becomes the scatter cursor
+    run += c;
+  }
+  if (tid == nt - 1) off[E] = part[nt - 1];
+  __syncthreads();
+  for (int b = tid; b < B; b += nt) {
+    int e = idx[b];
+    e = (e >= 0 && e < E) ? e : 0;
+    const int p = atomicAdd(&cnt[e], 1);
+    perm[p] = b;
+    inv[b] = p;
+  }
+}
+
+struct MoeLineArgs {
+  const uint16_t* x;     // MODE 0: hidden [T, >= Kpad]; MODE 1: h [B, >= Kpad] in sorted order
+  int64_t sxm;
+  int Kpad;
+  int k;                 // top_k: MODE 0 reads hidden row perm[p] / k
+  const int32_t* off;
+  const int32_t* perm;
+  const uint8_t* q;
+  int64_t sqe, sqn;
+  const void* sc;
+  const void* zr;
+  int64_t sse, ssn;      // scale and zero share strides (expert, row); groups are unit-strided
+  int NB;                // 64-row blocks per expert
+  int I;                 // MODE 0: intermediate size (up rows start at I)
+  void* out;
+  int64_t som;
+};
+
+IMQ_DEV float moe_row_swap8(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+}
+
+template <int S2, int SDT, int MODE>
+__global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NTL = kMoeTiles;
+  constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
+  constexpr int DPR = S2 * VB / 2;                   // scale dwords per row per wave
+  const int e = blockIdx.x / a.NB;
+  const int blk = blockIdx.x - e * a.NB;
+  const int beg = a.off[e], end = a.off[e + 1];
+  if (beg >= end) return;                            // whole workgroup: no token for this expert
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int c = lane & 15, ar = lane >> 4;
+  const bool lo8 = c < 8;
+  const int KL = a.Kpad / kMoeLine;
+  const int ls0 = wave * S2;
+
+  uint32_t* szl = (uint32_t*)smem + wave * (2 * NTL * 16 * DPR);
+  float* red = (float*)(smem + (size_t)W * (2 * NTL * 16 * DPR) * 4);   // [W][NTL][16][16]
+
+  auto rbase = [&](int t) -> int {
+    if constexpr (MODE == 0) return (t < 2) ? 32 * blk + 16 * t : a.I + 32 * blk + 16 * (t - 2);
+    else return 64 * blk + 16 * t;
+  };
+  // ---- scale / zero words of this wave's groups for the 4 tiles -> wave LDS ----
+  constexpr int ZN = 2 * NTL * 16 * DPR;
+  constexpr int ZU = (ZN + 63) / 64;
+  const int ngd = a.Kpad / 128 * VB / 4;
+  const unsigned char* sbase = (const unsigned char*)a.sc + (int64_t)e * a.sse * VB;
+  const unsigned char* zbase = (const unsigned char*)a.zr + (int64_t)e * a.sse * VB;
+  uint32_t zv[ZU];
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    int d = lane + 64 * u;
+    d = d < ZN ? d : ZN - 1;
+    const int arr = d / (NTL * 16 * DPR);
+    const int rem = d - arr * (NTL * 16 * DPR);
+    const int t = rem / (16 * DPR);
+    const int rem2 = rem - t * (16 * DPR);
+    const int r = rem2 / DPR, dw = rem2 - r * DPR;
+    int gd = ls0 * (VB / 2) + dw;
+    gd = gd < ngd ? gd : ngd - 1;
+    const int64_t ro = (int64_t)(rbase(t) + r) * a.ssn * VB + 4 * gd;
+    zv[u] = *(const uint32_t*)((arr ? zbase : sbase) + ro);
+  }
+  // ---- weights: per tile and line-step one full-line load for rows 0-7 and one for rows 8-15 ----
+  const uint8_t* qe = a.q + (int64_t)e * a.sqe;
+  u32x4_t wb[NTL][2 * S2];
+#pragma unroll
+  for (int t = 0; t < NTL; ++t) {
+    const uint8_t* q0 = qe + (int64_t)(rbase(t) + (c & 7)) * a.sqn + 16 * ar + (lo8 ? 0 : 64);
+    const uint8_t* q1 = qe + (int64_t)(rbase(t) + 8 + (c & 7)) * a.sqn + 16 * ar + (lo8 ? 64 : 0);
+#pragma unroll
+    for (int i = 0; i < S2; ++i) {
+      int l = ls0 + i;
+      l = l < KL ? l : KL - 1;
+      wb[t][2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
+      wb[t][2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    const int d = lane + 64 * u;
+    if (d < ZN) szl[d] = zv[u];
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // wave-private LDS, in-order
+
+  auto val = [&](int t, int arr, int row, int g) -> float {   // group g of row `row` of tile t
+    const uint32_t* p = szl + ((arr * NTL + t) * 16 + row) * DPR;
+    if constexpr (VB == 4) return round_bf16_hw(__uint_as_float(p[g]));
+    else return raw_to_bf16_f32<SDT>((g & 1) ? (p[g >> 1] >> 16) : (p[g >> 1] & 0xffffu));
+  };
+  float s0[NTL][S2], s1[NTL][S2], cz0[NTL][S2], cz1[NTL][S2];
+#pragma unroll
+  for (int t = 0; t < NTL; ++t)
+#pragma unroll
+    for (int i = 0; i < S2; ++i) {
+      const bool v = ls0 + i < KL;
+      s0[t][i] = v ? val(t, 0, c, 2 * i) : 0.f;
+      s1[t][i] = v ? val(t, 0, c ^ 8, 2 * i + 1) : 0.f;
+      cz0[t][i] = -(128.f + val(t, 1, c, 2 * i)) * s0[t][i];
+      cz1[t][i] = -(128.f + val(t, 1, c ^ 8, 2 * i + 1)) * s1[t][i];
+    }
+
+  const uint32_t magic = magic_bf16_128x2();
+  for (int p0 = beg; p0 < end; p0 += 16) {
+    if constexpr (S2 > 1) {
+      // keep the unpack inside the token loop: hoisting the unpacked operands of all tiles out of
+      // it would exceed the register budget beyond one line-step per wave
+#pragma unroll
+      for (int t = 0; t < NTL; ++t)
+#pragma unroll
+        for (int i = 0; i < 2 * S2; ++i) asm volatile("" : "+v"(wb[t][i]));
+    }
+    const int nrow = (end - p0) < 16 ? end - p0 : 16;
+    const int pr = p0 + (c < nrow ? c : nrow - 1);    // A row of this lane (rows >= nrow repeat the last)
+    const uint16_t* xr;
+    if constexpr (MODE == 0) xr = a.x + (int64_t)(a.perm[pr] / a.k) * a.sxm;
+    else xr = a.x + (int64_t)pr * a.sxm;
+    f32x4_t y0[NTL], y1[NTL];
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) {
+      y0[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      y1[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < S2; ++i) {
+      int l = ls0 + i;
+      l = l < KL ? l : KL - 1;
+      bf16x8_t A[2][4];
+      float gs[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float sum = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const u32x4_t v = *(const u32x4_t*)(xr + kMoeLine * l + 128 * h + 32 * ar + 8 * kk);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
+          A[h][kk] = __builtin_bit_cast(bf16x8_t, permute_x8(v));
+        }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        gs[h] = sum;                                  // group sum of A row c
+      }
+      // D rows of this lane: m = 4*ar + r
+      f32x4_t xs0, xs1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        xs0[r] = __shfl(gs[0], 4 * ar + r, 64);
+        xs1[r] = __shfl(gs[1], 4 * ar + r, 64);
+      }
+#pragma unroll
+      for (int t = 0; t < NTL; ++t) {
+        const u32x4_t w0 = wb[t][2 * i], w1 = wb[t][2 * i + 1];
+        u32x4_t gA, gB;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          gA[d] = lo8 ? w0[d] : w1[d];
+          gB[d] = lo8 ? w1[d] : w0[d];
+        }
+        f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          acc0 = mfma16x16x32(A[0][kk], unpack_nib8_bf16(gA[kk], magic), acc0);
+          acc1 = mfma16x16x32(A[1][kk], unpack_nib8_bf16(gB[kk], magic), acc1);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          y0[t][r] = fmaf(cz0[t][i], xs0[r], y0[t][r]);
+          y1[t][r] = fmaf(cz1[t][i], xs1[r], y1[t][r]);
+          y0[t][r] = fmaf(s0[t][i], acc0[r], y0[t][r]);
+          y1[t][r] = fmaf(s1[t][i], acc1[r], y1[t][r]);
+        }
+      }
+    }
+    // wave partials -> LDS [wave][tile][m][n]; the B-group columns hold row c ^ 8
+#pragma unroll
+    for (int t = 0; t < NTL; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[((wave * NTL + t) * 16 + 4 * ar + r) * 16 + c] = y0[t][r] + moe_row_swap8(y1[t][r]);
+    lds_barrier();
+    for (int o = threadIdx.x; o < 16 * 64; o += blockDim.x) {
+      const int m = o >> 6, j = o & 63;
+      if (m < nrow) {
+        if constexpr (MODE == 0) {
+          if (j < 32) {
+            const int t = j >> 4, n = j & 15;
+            float g = 0.f, u = 0.f;
+            for (int w = 0; w < W; ++w) {
+              g += red[((w * NTL + t) * 16 + m) * 16 + n];
+              u += red[((w * NTL + t + 2) * 16 + m) * 16 + n];
+            }
+            const float hv = g / (1.f + __expf(-g)) * u;
+            ((uint16_t*)a.out)[(int64_t)(p0 + m) * a.som + 32 * blk + j] = (uint16_t)f32_to_bf16_bits(hv);
+          }
+        } else {
+          const int t = j >> 4, n = j & 15;
+          float v = 0.f;
+          for (int w = 0; w < W; ++w) v += red[((w * NTL + t) * 16 + m) * 16 + n];
+          ((float*)a.out)[(int64_t)(p0 + m) * a.som + 64 * blk + j] = v;
+        }
+      }
+    }
+    lds_barrier();                                     // red is rewritten by the next pass
+  }
+}
+
+// out[t][n] = bf16(sum_j w[t][j] * yr[inv[t*k + j]][n]), slot order; h's pad columns [I, I_pad)
+// are zeroed by the same launch (first B*(I_pad - I) threads' extra work).
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ yr, const int32_t* __restrict__ inv,
+                                                          const uint16_t* __restrict__ w, int64_t T, int64_t k,
+                                                          int64_t H, uint16_t* __restrict__ out, int64_t so) {
+  const int64_t total = T * H;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t tok = t / H;
+    const int64_t n = t - tok * H;
+    float acc = 0.f;
+    for (int64_t j = 0; j < k; ++j)
+      acc = fmaf(bf16_bits_to_f32(w[tok * k + j]), yr[(int64_t)inv[tok * k + j] * H + n], acc);
+    out[tok * so + n] = (uint16_t)f32_to_bf16_bits(acc);
+  }
+}
+
+// zero h's pad columns [I, I_pad) (down reads K = I_pad)
+__global__ __launch_bounds__(256) void moe_zero_pad_kernel(uint16_t* __restrict__ h, int64_t B, int64_t I,
+                                                           int64_t I_pad) {
+  const int64_t wpad = I_pad - I;
+  const int64_t total = B * wpad;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = t / wpad;
+    h[b * I_pad + I + (t - b * wpad)] = 0;
+  }
+}
+
+template <int S2, int SDT, int MODE>
+int moe_line_launch(const MoeLineArgs& a, int E, int W, hipStream_t st) {
+  const size_t lds = (size_t)W * 2 * kMoeTiles * 16 * (S2 * ((SDT == IMQ_DT_FP32) ? 4 : 2) / 2) * 4 +
+                     (size_t)W * kMoeTiles * 256 * 4;
+  auto kern = moe_line_kernel<S2, SDT, MODE>;
+  if (lds > 65536) {
+    hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (err != hipSuccess) return (int)err;
+  }
+  kern<<<dim3((unsigned)(E * a.NB)), dim3(64 * W), lds, st>>>(a);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+// S2 line-steps per wave for K = Kpad: 1 or 2 with at most 8 waves (K <= 4096); deeper
+// line-steps would exceed the register budget.
+bool moe_line_shape(int64_t Kpad, int* S2, int* W) {
+  if (Kpad % kMoeLine) return false;
+  const int64_t KL = Kpad / kMoeLine;
+  for (int s : {1, 2}) {
+    if ((KL + s - 1) / s <= 8) {
+      *S2 = s;
+      *W = (int)((KL + s - 1) / s);
+      return true;
+    }
+  }
+  return false;
+}
+
+template <int SDT, int MODE>
+int moe_line_dispatch(const MoeLineArgs& a, int E, hipStream_t st) {
+  int S2, W;
+  if (!moe_line_shape(a.Kpad, &S2, &W)) return IMQ_ERR_UNSUPPORTED;
+  if (S2 == 1) return moe_line_launch<1, SDT, MODE>(a, E, W, st);
+  return moe_line_launch<2, SDT, MODE>(a, E, W, st);
+}
+
+template <int MODE>
+int moe_line_sdt(const MoeLineArgs& a, int E, int sdt, hipStream_t st) {
+  switch (sdt) {
+    case IMQ_DT_BF16: return moe_line_dispatch<IMQ_DT_BF16, MODE>(a, E, st);
+    case IMQ_DT_FP16: return moe_line_dispatch<IMQ_DT_FP16, MODE>(a, E, st);
+    case IMQ_DT_FP32: return moe_line_dispatch<IMQ_DT_FP32, MODE>(a, E, st);
+  }
+  return IMQ_ERR_INVALID;
+}
+
 template <bool OUT_F32>
 int launch_rows(const uint16_t* x, int64_t sxm, int64_t xdiv, int64_t B, int64_t Kpad, const int32_t* eid,
                 int64_t E, const uint8_t* q, int64_t sqe, int64_t sqn, const void* sc, int64_t sse, int64_t ssn,
@@ -137,14 +488,82 @@ extern "C" int imq_moe_rows_w4(const void* x, int64_t x_row_stride, int64_t B, i
                             (hipStream_t)stream);
 }
 
+namespace {
+// Workspace layout: [gu fp32 B x 2I][h bf16 B x I_pad][z fp32 B x H][off int32 E+1][perm int32 B]
+// [inv int32 B], each 256-byte aligned. The token-sorted path uses h, z, off, perm and inv; the
+// per-row path gu, h and z.
+struct MoeWs {
+  int64_t gu, h, z, off, perm, inv, total;
+};
+
+MoeWs moe_ws(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t G) {
+  const int64_t B = T * top_k;
+  const int64_t I_pad = imq_cdiv(I, G) * G;
+  MoeWs w;
+  w.gu = 0;
+  w.h = w.gu + align_up(B * 2 * I * 4, kAlign);
+  w.z = w.h + align_up(B * I_pad * 2, kAlign);
+  w.off = w.z + align_up(B * H * 4, kAlign);
+  w.perm = w.off + align_up((E + 1) * 4, kAlign);
+  w.inv = w.perm + align_up(B * 4, kAlign);
+  w.total = w.inv + align_up(B * 4, kAlign);
+  return w;
+}
+}  // namespace
+
 extern "C" int64_t imq_moe_workspace_bytes(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I,
                                            int64_t group_size) {
-  (void)E;
-  if (T < 0 || top_k <= 0 || H <= 0 || I <= 0 || group_size <= 0) return -1;
-  const int64_t B = T * top_k;
-  const int64_t I_pad = imq_cdiv(I, group_size) * group_size;
-  return align_up(B * 2 * I * 4, kAlign) + align_up(B * I_pad * 2, kAlign) + align_up(B * H * 4, kAlign);
+  if (T < 0 || top_k <= 0 || E <= 0 || H <= 0 || I <= 0 || group_size <= 0) return -1;
+  return moe_ws(T, top_k, E, H, I, group_size).total;
 }
+
+namespace {
+// Token-sorted grouped path; IMQ_ERR_UNSUPPORTED when the shape or layout does not qualify.
+int moe_sorted(const uint16_t* hidden, int64_t hs, int64_t T, int64_t H, int64_t k, const int32_t* idx,
+               const uint16_t* topk_w, int64_t E, const uint8_t* gq, int64_t gqe, int64_t gqn, const void* gs,
+               const void* gz, int64_t gse, int64_t gsn, int64_t I, const uint8_t* dq, int64_t dqe, int64_t dqn,
+               const void* ds, const void* dz, int64_t dse, int64_t dsn, int sdt, int64_t G, uint16_t* out,
+               int64_t os, char* ws, const MoeWs& L, hipStream_t st) {
+  const int64_t H_pad = imq_cdiv(H, G) * G, I_pad = imq_cdiv(I, G) * G;
+  const int64_t B = T * k;
+  const int vb = sdt == IMQ_DT_FP32 ? 4 : 2;
+  if (G != 128 || H_pad % kMoeLine || I_pad % kMoeLine || I % 32 || H % 64) return IMQ_ERR_UNSUPPORTED;
+  if (E > 16384 || B > 0x7fffffff || T * hs > 0x7fffffffLL * 8) return IMQ_ERR_UNSUPPORTED;
+  if (!aligned(gq, 16) || !aligned(dq, 16) || (gqn % 16) || (dqn % 16) || (gqe % 16) || (dqe % 16))
+    return IMQ_ERR_UNSUPPORTED;
+  if (!aligned(gs, 4) || !aligned(gz, 4) || !aligned(ds, 4) || !aligned(dz, 4) || (gsn * vb) % 4 ||
+      (dsn * vb) % 4 || (gse * vb) % 4 || (dse * vb) % 4)
+    return IMQ_ERR_UNSUPPORTED;
+  int s2, w;
+  if (!moe_line_shape(H_pad, &s2, &w) || !moe_line_shape(I_pad, &s2, &w)) return IMQ_ERR_UNSUPPORTED;
+  int32_t* off = (int32_t*)(ws + L.off);
+  int32_t* perm = (int32_t*)(ws + L.perm);
+  int32_t* inv = (int32_t*)(ws + L.inv);
+  uint16_t* h = (uint16_t*)(ws + L.h);
+  float* yr = (float*)(ws + L.z);
+  const int nt = 1024;
+  moe_sort_kernel<<<dim3(1), dim3(nt), (size_t)(E + nt) * 4, st>>>(idx, (int)B, (int)E, off, perm, inv);
+  IMQ_LAUNCH_CHECK();
+  MoeLineArgs g{hidden, hs, (int)H_pad, (int)k, off, perm, gq, gqe, gqn, gs, gz, gse, gsn, (int)(I / 32), (int)I,
+                h, I_pad};
+  int rc = moe_line_sdt<0>(g, (int)E, sdt, st);
+  if (rc != IMQ_OK) return rc;
+  if (I_pad > I) {
+    const int64_t total = B * (I_pad - I);
+    const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
+    moe_zero_pad_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(h, B, I, I_pad);
+    IMQ_LAUNCH_CHECK();
+  }
+  MoeLineArgs d{h, I_pad, (int)I_pad, (int)k, off, perm, dq, dqe, dqn, ds, dz, dse, dsn, (int)(H / 64), 0, yr, H};
+  rc = moe_line_sdt<1>(d, (int)E, sdt, st);
+  if (rc != IMQ_OK) return rc;
+  const int64_t total = T * H;
+  const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
+  moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, inv, topk_w, T, k, H, out, os);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+}  // namespace
 
 extern "C" int imq_moe_experts_w4(const void* hidden, int64_t h_row_stride, int64_t T, int64_t H, int64_t top_k,
                                   const int32_t* topk_idx, const void* topk_w, int64_t E, const void* gu_q,
@@ -171,9 +590,17 @@ extern "C" int imq_moe_experts_w4(const void* hidden, int64_t h_row_stride, int6
   hipStream_t st = (hipStream_t)stream;
   const int64_t B = T * top_k;
   char* ws = (char*)workspace;
-  float* gu = (float*)ws;
-  uint16_t* h = (uint16_t*)(ws + align_up(B * 2 * I * 4, kAlign));
-  float* z = (float*)(ws + align_up(B * 2 * I * 4, kAlign) + align_up(B * I_pad * 2, kAlign));
+  const MoeWs L = moe_ws(T, top_k, E, H, I, G);
+  {
+    const int rs = moe_sorted((const uint16_t*)hidden, h_row_stride, T, H, top_k, topk_idx, (const uint16_t*)topk_w,
+                              E, (const uint8_t*)gu_q, gu_q_stride_e, gu_q_row_stride, gu_s, gu_z, gu_sz_stride_e,
+                              gu_sz_stride_n, I, (const uint8_t*)dn_q, dn_q_stride_e, dn_q_row_stride, dn_s, dn_z,
+                              dn_sz_stride_e, dn_sz_stride_n, sz_dtype, G, (uint16_t*)out, out_row_stride, ws, L, st);
+    if (rs != IMQ_ERR_UNSUPPORTED) return rs;
+  }
+  float* gu = (float*)(ws + L.gu);
+  uint16_t* h = (uint16_t*)(ws + L.h);
+  float* z = (float*)(ws + L.z);
   const int64_t ng1 = H_pad / G, ng2 = I_pad / G;
   (void)ng1;
   (void)ng2;

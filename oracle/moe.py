@@ -9,7 +9,7 @@ the reference in bench_moe_w4a16.py:132-149) and the reference's fused decode fo
 Pins: ``moe_eager_bf16`` is checked against a live ``OlmoeExperts`` module from the installed
 transformers (a third-party implementation) fed the oracle's dequantized weights;
 ``moe_exact`` against ``moe_eager_bf16`` (agreement to bf16 noise) and a brute-force single-token
-case; ``route_topk`` against ``OlmoeTopKRouter``.
+case; ``moe_exact_grouped`` against ``moe_exact``; ``route_topk`` against ``OlmoeTopKRouter``.
 """
 from __future__ import annotations
 
@@ -39,6 +39,24 @@ def moe_exact(x, idx, wts, Wgu, Wdn) -> np.ndarray:
             g = np.asarray(Wgu[e], np.float64) @ x[t]
             h = silu64(g[:I]) * g[I:]
             out[t] += float(wts[t, j]) * (np.asarray(Wdn[e], np.float64) @ h)
+    return out
+
+
+def moe_exact_grouped(x, idx, wts, Wgu, Wdn) -> np.ndarray:
+    """``moe_exact`` evaluated expert by expert (one float64 product per hit expert over all its
+    routed tokens) -- the same sum, reordered; fast enough for T in the hundreds."""
+    x = np.asarray(x, np.float64)
+    T, H = x.shape
+    I = Wgu.shape[1] // 2
+    idx = np.asarray(idx)
+    w = np.asarray(wts, np.float64)
+    out = np.zeros((T, Wdn.shape[1]), np.float64)
+    for e in np.unique(idx):
+        tok, slot = np.nonzero(idx == e)
+        g = x[tok] @ np.asarray(Wgu[e], np.float64).T
+        h = silu64(g[:, :I]) * g[:, I:]
+        y = h @ np.asarray(Wdn[e], np.float64).T
+        np.add.at(out, tok, w[tok, slot][:, None] * y)
     return out
 
 

@@ -4,6 +4,8 @@ restatement of the eager experts loop, at the OLMoE shape (BASELINE C5) and smal
 Tolerance: normwise max relative error <= 1e-2 and mean relative error <= 5e-3 against the exact
 (float64, no intermediate rounding) MoE over the bit-exact dequantized experts; against the
 reference's bf16 eager loop, the reference's own fused-MoE self-check bounds."""
+import functools
+
 import numpy as np
 import pytest
 
@@ -17,6 +19,7 @@ MAX_REL = 1e-2
 MEAN_REL = 5e-3
 
 
+@functools.lru_cache(maxsize=2)
 def _layer(E, H, I, G, seed):
     r = C.rng(seed)
     Wgu = C.bf16_normal(r, (E, 2 * I, H), 0.02)
@@ -28,21 +31,26 @@ def _layer(E, H, I, G, seed):
     return gu, dn, Dgu, Ddn
 
 
-def _run(dev, E, H, I, k, T, seed, G=128):
+def _run(dev, E, H, I, k, T, seed, G=128, sdt="bf16"):
     import torch
     from infinitemodel_amd import ops
     gu, dn, Dgu, Ddn = _layer(E, H, I, G, seed)
+    if sdt != "bf16":
+        # stored scale / zero in another dtype; the kernels round them to bf16 like the reference
+        gu = (gu[0], oq.round_to(gu[1], sdt), oq.round_to(gu[2], sdt))
+        dn = (dn[0], oq.round_to(dn[1], sdt), oq.round_to(dn[2], sdt))
     r = C.rng(seed + 1)
     logits = r.standard_normal((T, E)).astype(np.float32)
     idx, w = om.route_topk(logits, k)
     x = C.bf16_normal(r, (T, H))
     t = lambda a: C.to_torch(a, "bf16", dev)  # noqa: E731
+    ts = lambda a: C.to_torch(a, sdt, dev)  # noqa: E731
     out = ops.moe_experts_w4(t(x), torch.from_numpy(idx).to(dev), t(w),
-                             (C.u8(gu[0], dev), t(gu[1]), t(gu[2]), H),
-                             (C.u8(dn[0], dev), t(dn[1]), t(dn[2]), I), G)
+                             (C.u8(gu[0], dev), ts(gu[1]), ts(gu[2]), H),
+                             (C.u8(dn[0], dev), ts(dn[1]), ts(dn[2]), I), G)
     assert out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H)
     y = C.t2np(out)
-    exact = om.moe_exact(x, idx, w, Dgu, Ddn)
+    exact = om.moe_exact_grouped(x, idx, w, Dgu, Ddn)
     assert np.isfinite(y).all()
     mr, me = oq.max_rel(y, exact), oq.mean_rel(y, exact)
     assert mr <= MAX_REL and me <= MEAN_REL, (T, mr, me)
@@ -68,6 +76,28 @@ def test_moe_ragged_intermediate(dev):
 def test_moe_olmoe_shape(dev, T):
     """BASELINE C5: E=64, top-8, H=2048, I=1024."""
     _run(dev, E=64, H=2048, I=1024, k=8, T=T, seed=3000)
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 2, 8), (5, 2, 8), (64, 2, 4), (40, 3, 6)])
+def test_moe_token_sorted_path(dev, T, k, E):
+    """Shapes of the token-sorted grouped path (G 128, H and I_pad multiples of 256, I % 32 == 0):
+    one token, a few, and experts with more than 16 routed rows (several MFMA passes)."""
+    _run(dev, E=E, H=512, I=256, k=k, T=T, seed=40 + T)
+
+
+def test_moe_token_sorted_h_pad(dev):
+    """I = 160 < I_pad = 256: h's pad columns are zeroed before the down projection."""
+    _run(dev, E=6, H=512, I=160, k=2, T=9, seed=8)
+
+
+@pytest.mark.parametrize("sdt", ["fp16", "fp32"])
+def test_moe_token_sorted_scale_dtypes(dev, sdt):
+    _run(dev, E=4, H=512, I=256, k=2, T=20, seed=9, sdt=sdt)
+
+
+def test_moe_olmoe_shape_prefill(dev):
+    """BASELINE C5 at T = 256 (every expert hit, ~32 rows each)."""
+    _run(dev, E=64, H=2048, I=1024, k=8, T=256, seed=3000)
 
 
 def test_moe_repeat_identical(dev):

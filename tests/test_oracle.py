@@ -277,3 +277,20 @@ def test_moe_single_token_brute_force():
         h = g[:I] / (1 + np.exp(-g[:I])) * g[I:]
         acc += float(w[0, j]) * (Wdd[e].astype(np.float64) @ h)
     np.testing.assert_allclose(out[0], acc, rtol=1e-12, atol=1e-12)
+
+
+def test_moe_exact_grouped_matches_per_token_loop():
+    """The grouped evaluation (used by the GPU tests at large T) is the per-token float64 sum."""
+    r = np.random.default_rng(5)
+    E, H, I, k, T = 6, 32, 16, 3, 11
+    Wgu = r.standard_normal((E, 2 * I, H)).astype(np.float32) * 0.1
+    Wdn = r.standard_normal((E, H, I)).astype(np.float32) * 0.1
+    x = r.standard_normal((T, H)).astype(np.float32)
+    idx, w = om.route_topk(r.standard_normal((T, E)).astype(np.float32), k)
+    a = om.moe_exact(x, idx, w, Wgu, Wdn)
+    b = om.moe_exact_grouped(x, idx, w, Wgu, Wdn)
+    assert np.allclose(a, b, rtol=1e-12, atol=1e-12)
+    # negative control: dropping one slot's contribution is visible
+    w2 = np.array(w, copy=True)
+    w2[0, 0] = 0
+    assert not np.allclose(om.moe_exact_grouped(x, idx, w2, Wgu, Wdn), a, rtol=1e-6, atol=1e-9)
