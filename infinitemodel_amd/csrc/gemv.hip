@@ -1052,28 +1052,6 @@ __global__ __launch_bounds__(256) void generic_gemv_kernel(GenericArgs a) {
 // ---------------------------------------------------------------------------------------------
 // host dispatch
 // ---------------------------------------------------------------------------------------------
-struct DevInfo {
-  int cus;
-  int max_lds;
-};
-
-DevInfo device_info() {
-  static DevInfo cache[64];
-  static int ready[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DevInfo{256, 65536};
-  if (!__atomic_load_n(&ready[dev], __ATOMIC_ACQUIRE)) {
-    DevInfo d{256, 65536};
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      d.cus = v;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
-      d.max_lds = v;
-    cache[dev] = d;
-    __atomic_store_n(&ready[dev], 1, __ATOMIC_RELEASE);
-  }
-  return cache[dev];
-}
 
 template <typename K>
 int launch_with_lds(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t st, const SkinnyArgs& a) {

@@ -182,3 +182,27 @@ static inline int64_t imq_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
     hipError_t _e = hipGetLastError();                       \
     if (_e != hipSuccess) return (int)_e;                    \
   } while (0)
+
+// Per-device attributes the launchers size grids and LDS with (read once per device).
+struct DevInfo {
+  int cus;
+  int max_lds;
+};
+
+inline DevInfo device_info() {
+  static DevInfo cache[64];
+  static int ready[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DevInfo{256, 65536};
+  if (!__atomic_load_n(&ready[dev], __ATOMIC_ACQUIRE)) {
+    DevInfo d{256, 65536};
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      d.cus = v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
+      d.max_lds = v;
+    cache[dev] = d;
+    __atomic_store_n(&ready[dev], 1, __ATOMIC_RELEASE);
+  }
+  return cache[dev];
+}

@@ -92,27 +92,24 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 
 
 // ---------------------------------------------------------------------------------------------
-// Token-sorted grouped path (G == 128, K of both projections a multiple of 256, I % 32 == 0,
-// H % 64 == 0, unit group strides):
-//   moe_sort_kernel   counting sort of the T*k routed rows by expert -> off[E+1], perm[B] (sorted
-//                     position -> routed row t*k + j), inv[B] (routed row -> sorted position)
-//   moe_line_kernel   one workgroup per (expert, 64-row block): the block's weights are loaded once
-//                     into registers (the decode line kernel's full-line layout) and reused for all
-//                     of the expert's tokens, 16 per MFMA pass. MODE 0 is gate_up: rows
-//                     [32b, 32b+32) of gate and the matching up rows, SwiGLU in the epilogue, bf16 h
-//                     in sorted order. MODE 1 is down: 64 rows of H, fp32 per sorted row.
-//   moe_combine_kernel out[t] = bf16(sum_j w[t, j] * yr[inv[t*k + j]]), slot order.
-// Workgroups of experts no token routes to exit at once.
-// ---------------------------------------------------------------------------------------------
+// Token-sorted grouped path (G == 128, K of both projections a multiple of 256 and at most 4096,
+// I % 32 == 0, H % 64 == 0, unit group strides):
+//   moe_sort_kernel    counting sort of the T*k routed rows by expert -> off[E+1], perm[B] (sorted
+//                      position -> routed row t*k + j) and the ascending list of hit experts
+//                      hit[0 .. hit[E]) -- the work list of the grouped kernels
+//   moe_line_kernel    workgroups over the (hit expert, row block) work list. A block's
+//                      weights (NTL tiles of 16 rows) are loaded once into registers in the decode
+//                      line kernel's full-line layout and reused for all of the expert's tokens, 16
+//                      per MFMA pass. MODE 0 is gate_up: NTL/2 tiles of gate rows and the matching
+//                      up rows, SwiGLU in the epilogue, bf16 h in sorted order. MODE 1 is down:
+//                      NTL tiles of H, fp32 rows written in routed order.
+//   moe_combine_kernel out[t] = bf16(sum_j w[t, j] * yr[t*k + j]), slot order.
 constexpr int kMoeLine = 256;
-constexpr int kMoeTiles = 4;          // 16-row tiles per workgroup (64 weight rows)
 
 __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restrict__ idx, int B, int E,
                                                         int32_t* __restrict__ off, int32_t* __restrict__ perm,
-                                                        int32_t* __restrict__ inv) {
-  extern __shared__ int32_t sh[];     // cnt[E], then the per-thread partial sums [blockDim]
-  int32_t* cnt = sh;
-  int32_t* part = sh + E;
+                                                        int32_t* __restrict__ hit) {
+  extern __shared__ int32_t cnt[];     // [E]: counts, then scatter cursors
   const int tid = threadIdx.x, nt = blockDim.x;
   for (int e = tid; e < E; e += nt) cnt[e] = 0;
   __syncthreads();
@@ -122,34 +119,43 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
     atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  // exclusive scan: thread t owns experts [t*per, t*per + per)
-  const int per = (E + nt - 1) / nt;
-  const int e0 = tid * per, e1 = (e0 + per < E) ? e0 + per : E;
-  int local = 0;
-  for (int e = e0; e < e1; ++e) local += cnt[e];
-  part[tid] = local;
-  __syncthreads();
-  for (int d = 1; d < nt; d <<= 1) {     // Hillis-Steele inclusive scan of the partials
-    const int v = tid >= d ? part[tid - d] : 0;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
+  if (tid < 64) {
+    // wave 0: lane l owns experts [l*per, l*per + per); exclusive scans of the row counts and of
+    // the hit flags give the sorted offsets and the ascending list of hit experts
+    const int per = (E + 63) / 64;
+    const int e0 = tid * per, e1 = (e0 + per < E) ? e0 + per : E;
+    int rows = 0, hits = 0;
+    for (int e = e0; e < e1; ++e) {
+      rows += cnt[e];
+      hits += cnt[e] > 0;
+    }
+    int rs = rows, hs = hits;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int r = __shfl_up(rs, d, 64), h = __shfl_up(hs, d, 64);
+      if (tid >= d) {
+        rs += r;
+        hs += h;
+      }
+    }
+    int run = rs - rows, hrun = hs - hits;
+    for (int e = e0; e < e1; ++e) {
+      const int c = cnt[e];
+      off[e] = run;
+      if (c > 0) hit[hrun++] = e;
+      cnt[e] = run;
+      run += c;
+    }
+    if (tid == 63) {
+      off[E] = rs;
+      hit[E] = hs;                        // number of hit experts
+    }
   }
-  int run = part[tid] - local;
-  for (int e = e0; e < e1; ++e) {
-    const int c = cnt[e];
-    off[e] = run;
-    cnt[e] = run;                        // becomes the scatter cursor
-    run += c;
-  }
-  if (tid == nt - 1) off[E] = part[nt - 1];
   __syncthreads();
   for (int b = tid; b < B; b += nt) {
     int e = idx[b];
     e = (e >= 0 && e < E) ? e : 0;
-    const int p = atomicAdd(&cnt[e], 1);
-    perm[p] = b;
-    inv[b] = p;
+    perm[atomicAdd(&cnt[e], 1)] = b;
   }
 }
 
@@ -160,14 +166,16 @@ struct MoeLineArgs {
   int k;                 // top_k: MODE 0 reads hidden row perm[p] / k
   const int32_t* off;
   const int32_t* perm;
+  const int32_t* hit;    // [E + 1]: ascending hit experts, hit[E] = their number
   const uint8_t* q;
   int64_t sqe, sqn;
   const void* sc;
   const void* zr;
   int64_t sse, ssn;      // scale and zero share strides (expert, row); groups are unit-strided
-  int NB;                // 64-row blocks per expert
+  int E;
+  int NB;                // row blocks (NTL * 16 rows) per expert
   int I;                 // MODE 0: intermediate size (up rows start at I)
-  void* out;
+  void* out;             // MODE 0: h bf16 [B, I_pad] sorted order; MODE 1: fp32 [B, H] routed order
   int64_t som;
 };
 
@@ -175,16 +183,12 @@ IMQ_DEV float moe_row_swap8(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
 }
 
-template <int S2, int SDT, int MODE>
+template <int S2, int NTL, int SDT, int MODE>
 __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  constexpr int NTL = kMoeTiles;
   constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
   constexpr int DPR = S2 * VB / 2;                   // scale dwords per row per wave
-  const int e = blockIdx.x / a.NB;
-  const int blk = blockIdx.x - e * a.NB;
-  const int beg = a.off[e], end = a.off[e + 1];
-  if (beg >= end) return;                            // whole workgroup: no token for this expert
+  constexpr int HALF = NTL / 2;                      // MODE 0: gate tiles (= up tiles) per block
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
@@ -192,13 +196,18 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   const bool lo8 = c < 8;
   const int KL = a.Kpad / kMoeLine;
   const int ls0 = wave * S2;
+  const int items = a.hit[a.E] * a.NB;              // (hit expert, row block) work items
 
   uint32_t* szl = (uint32_t*)smem + wave * (2 * NTL * 16 * DPR);
   float* red = (float*)(smem + (size_t)W * (2 * NTL * 16 * DPR) * 4);   // [W][NTL][16][16]
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+  const int e = a.hit[item / a.NB];
+  const int blk = item - (item / a.NB) * a.NB;
+  const int beg = a.off[e], end = a.off[e + 1];
 
   auto rbase = [&](int t) -> int {
-    if constexpr (MODE == 0) return (t < 2) ? 32 * blk + 16 * t : a.I + 32 * blk + 16 * (t - 2);
-    else return 64 * blk + 16 * t;
+    if constexpr (MODE == 0) return (t < HALF) ? 16 * HALF * blk + 16 * t : a.I + 16 * HALF * blk + 16 * (t - HALF);
+    else return 16 * NTL * blk + 16 * t;
   };
   // ---- scale / zero words of this wave's groups for the 4 tiles -> wave LDS ----
   constexpr int ZN = 2 * NTL * 16 * DPR;
@@ -339,46 +348,58 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
       for (int r = 0; r < 4; ++r)
         red[((wave * NTL + t) * 16 + 4 * ar + r) * 16 + c] = y0[t][r] + moe_row_swap8(y1[t][r]);
     lds_barrier();
-    for (int o = threadIdx.x; o < 16 * 64; o += blockDim.x) {
-      const int m = o >> 6, j = o & 63;
+    for (int o = threadIdx.x; o < 16 * 16 * NTL; o += blockDim.x) {
+      const int m = o / (16 * NTL), j = o - m * (16 * NTL);
       if (m < nrow) {
         if constexpr (MODE == 0) {
-          if (j < 32) {
+          if (j < 16 * HALF) {
             const int t = j >> 4, n = j & 15;
             float g = 0.f, u = 0.f;
             for (int w = 0; w < W; ++w) {
               g += red[((w * NTL + t) * 16 + m) * 16 + n];
-              u += red[((w * NTL + t + 2) * 16 + m) * 16 + n];
+              u += red[((w * NTL + t + HALF) * 16 + m) * 16 + n];
             }
             const float hv = g / (1.f + __expf(-g)) * u;
-            ((uint16_t*)a.out)[(int64_t)(p0 + m) * a.som + 32 * blk + j] = (uint16_t)f32_to_bf16_bits(hv);
+            ((uint16_t*)a.out)[(int64_t)(p0 + m) * a.som + 16 * HALF * blk + j] = (uint16_t)f32_to_bf16_bits(hv);
           }
         } else {
           const int t = j >> 4, n = j & 15;
           float v = 0.f;
           for (int w = 0; w < W; ++w) v += red[((w * NTL + t) * 16 + m) * 16 + n];
-          ((float*)a.out)[(int64_t)(p0 + m) * a.som + 64 * blk + j] = v;
+          ((float*)a.out)[(int64_t)a.perm[p0 + m] * a.som + 16 * NTL * blk + j] = v;
         }
       }
     }
     lds_barrier();                                     // red is rewritten by the next pass
   }
+  }
 }
 
-// out[t][n] = bf16(sum_j w[t][j] * yr[inv[t*k + j]][n]), slot order; h's pad columns [I, I_pad)
-// are zeroed by the same launch (first B*(I_pad - I) threads' extra work).
-__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ yr, const int32_t* __restrict__ inv,
-                                                          const uint16_t* __restrict__ w, int64_t T, int64_t k,
-                                                          int64_t H, uint16_t* __restrict__ out, int64_t so) {
-  const int64_t total = T * H;
+// out[t][n .. n+7] = bf16(sum_j w[t][j] * yr[t*k + j][n .. n+7]), slot order; H % 8 == 0.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ yr, const uint16_t* __restrict__ w,
+                                                          int64_t T, int64_t k, int64_t H,
+                                                          uint16_t* __restrict__ out, int64_t so) {
+  const int64_t H8 = H / 8;
+  const int64_t total = T * H8;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t tok = t / H;
-    const int64_t n = t - tok * H;
-    float acc = 0.f;
-    for (int64_t j = 0; j < k; ++j)
-      acc = fmaf(bf16_bits_to_f32(w[tok * k + j]), yr[(int64_t)inv[tok * k + j] * H + n], acc);
-    out[tok * so + n] = (uint16_t)f32_to_bf16_bits(acc);
+    const int64_t tok = t / H8;
+    const int64_t n = 8 * (t - tok * H8);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int64_t j = 0; j < k; ++j) {
+      const float wj = bf16_bits_to_f32(w[tok * k + j]);
+      const float* src = yr + (tok * k + j) * H + n;
+      const f32x4_t v0 = *(const f32x4_t*)src, v1 = *(const f32x4_t*)(src + 4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[q] = fmaf(wj, v0[q], acc[q]);
+        acc[4 + q] = fmaf(wj, v1[q], acc[4 + q]);
+      }
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = cvt_pk_bf16(acc[2 * q], acc[2 * q + 1]);
+    *(u32x4_t*)(out + tok * so + n) = o;
   }
 }
 
@@ -394,49 +415,54 @@ __global__ __launch_bounds__(256) void moe_zero_pad_kernel(uint16_t* __restrict_
   }
 }
 
-template <int S2, int SDT, int MODE>
-int moe_line_launch(const MoeLineArgs& a, int E, int W, hipStream_t st) {
-  const size_t lds = (size_t)W * 2 * kMoeTiles * 16 * (S2 * ((SDT == IMQ_DT_FP32) ? 4 : 2) / 2) * 4 +
-                     (size_t)W * kMoeTiles * 256 * 4;
-  auto kern = moe_line_kernel<S2, SDT, MODE>;
+template <int S2, int NTL, int SDT, int MODE>
+int moe_line_launch(const MoeLineArgs& a, int W, int grid, hipStream_t st) {
+  const size_t lds = (size_t)W * 2 * NTL * 16 * (S2 * ((SDT == IMQ_DT_FP32) ? 4 : 2) / 2) * 4 +
+                     (size_t)W * NTL * 256 * 4;
+  auto kern = moe_line_kernel<S2, NTL, SDT, MODE>;
   if (lds > 65536) {
     hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (err != hipSuccess) return (int)err;
   }
-  kern<<<dim3((unsigned)(E * a.NB)), dim3(64 * W), lds, st>>>(a);
+  kern<<<dim3((unsigned)grid), dim3(64 * W), lds, st>>>(a);
   IMQ_LAUNCH_CHECK();
   return IMQ_OK;
 }
 
-// S2 line-steps per wave for K = Kpad: 1 or 2 with at most 8 waves (K <= 4096); deeper
-// line-steps would exceed the register budget.
+// Line-steps per wave S2 (2 when K spans at least two, else 1) and waves W = ceil(KL / S2) <= 8,
+// i.e. K <= 4096; deeper line-steps would exceed the register budget.
 bool moe_line_shape(int64_t Kpad, int* S2, int* W) {
   if (Kpad % kMoeLine) return false;
   const int64_t KL = Kpad / kMoeLine;
-  for (int s : {1, 2}) {
-    if ((KL + s - 1) / s <= 8) {
-      *S2 = s;
-      *W = (int)((KL + s - 1) / s);
-      return true;
-    }
-  }
-  return false;
+  const int s = KL >= 2 ? 2 : 1;
+  if ((KL + s - 1) / s > 8) return false;
+  *S2 = s;
+  *W = (int)((KL + s - 1) / s);
+  return true;
 }
 
+// One workgroup per possible (expert, row block) item; those past the device-side work list
+// exit after reading its length. Measured on MI355X at the OLMoE shape against persistent grids
+// of 2-4 workgroups per CU and 32-row blocks: 64-row blocks with two line-steps per wave were
+// fastest at T = 1, 16 and 256.
 template <int SDT, int MODE>
-int moe_line_dispatch(const MoeLineArgs& a, int E, hipStream_t st) {
+int moe_line_dispatch(MoeLineArgs a, int rows, hipStream_t st) {
+  constexpr int NTL = 4;
   int S2, W;
   if (!moe_line_shape(a.Kpad, &S2, &W)) return IMQ_ERR_UNSUPPORTED;
-  if (S2 == 1) return moe_line_launch<1, SDT, MODE>(a, E, W, st);
-  return moe_line_launch<2, SDT, MODE>(a, E, W, st);
+  a.NB = rows / (16 * NTL);
+  const int64_t items = (int64_t)a.E * a.NB;
+  if (items > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE>(a, W, (int)items, st);
+  return moe_line_launch<2, NTL, SDT, MODE>(a, W, (int)items, st);
 }
 
 template <int MODE>
-int moe_line_sdt(const MoeLineArgs& a, int E, int sdt, hipStream_t st) {
+int moe_line_sdt(const MoeLineArgs& a, int rows, int sdt, hipStream_t st) {
   switch (sdt) {
-    case IMQ_DT_BF16: return moe_line_dispatch<IMQ_DT_BF16, MODE>(a, E, st);
-    case IMQ_DT_FP16: return moe_line_dispatch<IMQ_DT_FP16, MODE>(a, E, st);
-    case IMQ_DT_FP32: return moe_line_dispatch<IMQ_DT_FP32, MODE>(a, E, st);
+    case IMQ_DT_BF16: return moe_line_dispatch<IMQ_DT_BF16, MODE>(a, rows, st);
+    case IMQ_DT_FP16: return moe_line_dispatch<IMQ_DT_FP16, MODE>(a, rows, st);
+    case IMQ_DT_FP32: return moe_line_dispatch<IMQ_DT_FP32, MODE>(a, rows, st);
   }
   return IMQ_ERR_INVALID;
 }
@@ -490,10 +516,10 @@ extern "C" int imq_moe_rows_w4(const void* x, int64_t x_row_stride, int64_t B, i
 
 namespace {
 // Workspace layout: [gu fp32 B x 2I][h bf16 B x I_pad][z fp32 B x H][off int32 E+1][perm int32 B]
-// [inv int32 B], each 256-byte aligned. The token-sorted path uses h, z, off, perm and inv; the
-// per-row path gu, h and z.
+// [hit int32 E+1], each 256-byte aligned. The token-sorted path uses h, z, off, perm and hit;
+// the per-row path gu, h and z.
 struct MoeWs {
-  int64_t gu, h, z, off, perm, inv, total;
+  int64_t gu, h, z, off, perm, hit, total;
 };
 
 MoeWs moe_ws(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t G) {
@@ -505,8 +531,8 @@ MoeWs moe_ws(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t 
   w.z = w.h + align_up(B * I_pad * 2, kAlign);
   w.off = w.z + align_up(B * H * 4, kAlign);
   w.perm = w.off + align_up((E + 1) * 4, kAlign);
-  w.inv = w.perm + align_up(B * 4, kAlign);
-  w.total = w.inv + align_up(B * 4, kAlign);
+  w.hit = w.perm + align_up(B * 4, kAlign);
+  w.total = w.hit + align_up((E + 1) * 4, kAlign);
   return w;
 }
 }  // namespace
@@ -528,6 +554,7 @@ int moe_sorted(const uint16_t* hidden, int64_t hs, int64_t T, int64_t H, int64_t
   const int64_t B = T * k;
   const int vb = sdt == IMQ_DT_FP32 ? 4 : 2;
   if (G != 128 || H_pad % kMoeLine || I_pad % kMoeLine || I % 32 || H % 64) return IMQ_ERR_UNSUPPORTED;
+  if (!aligned(out, 16) || (os % 8)) return IMQ_ERR_UNSUPPORTED;
   if (E > 16384 || B > 0x7fffffff || T * hs > 0x7fffffffLL * 8) return IMQ_ERR_UNSUPPORTED;
   if (!aligned(gq, 16) || !aligned(dq, 16) || (gqn % 16) || (dqn % 16) || (gqe % 16) || (dqe % 16))
     return IMQ_ERR_UNSUPPORTED;
@@ -538,15 +565,14 @@ int moe_sorted(const uint16_t* hidden, int64_t hs, int64_t T, int64_t H, int64_t
   if (!moe_line_shape(H_pad, &s2, &w) || !moe_line_shape(I_pad, &s2, &w)) return IMQ_ERR_UNSUPPORTED;
   int32_t* off = (int32_t*)(ws + L.off);
   int32_t* perm = (int32_t*)(ws + L.perm);
-  int32_t* inv = (int32_t*)(ws + L.inv);
+  int32_t* hit = (int32_t*)(ws + L.hit);
   uint16_t* h = (uint16_t*)(ws + L.h);
   float* yr = (float*)(ws + L.z);
-  const int nt = 1024;
-  moe_sort_kernel<<<dim3(1), dim3(nt), (size_t)(E + nt) * 4, st>>>(idx, (int)B, (int)E, off, perm, inv);
+  moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)E * 4, st>>>(idx, (int)B, (int)E, off, perm, hit);
   IMQ_LAUNCH_CHECK();
-  MoeLineArgs g{hidden, hs, (int)H_pad, (int)k, off, perm, gq, gqe, gqn, gs, gz, gse, gsn, (int)(I / 32), (int)I,
+  MoeLineArgs g{hidden, hs, (int)H_pad, (int)k, off, perm, hit, gq, gqe, gqn, gs, gz, gse, gsn, (int)E, 0, (int)I,
                 h, I_pad};
-  int rc = moe_line_sdt<0>(g, (int)E, sdt, st);
+  int rc = moe_line_sdt<0>(g, (int)(2 * I), sdt, st);
   if (rc != IMQ_OK) return rc;
   if (I_pad > I) {
     const int64_t total = B * (I_pad - I);
@@ -554,12 +580,12 @@ int moe_sorted(const uint16_t* hidden, int64_t hs, int64_t T, int64_t H, int64_t
     moe_zero_pad_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(h, B, I, I_pad);
     IMQ_LAUNCH_CHECK();
   }
-  MoeLineArgs d{h, I_pad, (int)I_pad, (int)k, off, perm, dq, dqe, dqn, ds, dz, dse, dsn, (int)(H / 64), 0, yr, H};
-  rc = moe_line_sdt<1>(d, (int)E, sdt, st);
+  MoeLineArgs d{h, I_pad, (int)I_pad, (int)k, off, perm, hit, dq, dqe, dqn, ds, dz, dse, dsn, (int)E, 0, 0, yr, H};
+  rc = moe_line_sdt<1>(d, (int)H, sdt, st);
   if (rc != IMQ_OK) return rc;
-  const int64_t total = T * H;
+  const int64_t total = T * (H / 8);
   const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
-  moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, inv, topk_w, T, k, H, out, os);
+  moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, topk_w, T, k, H, out, os);
   IMQ_LAUNCH_CHECK();
   return IMQ_OK;
 }
