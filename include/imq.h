@@ -14,7 +14,8 @@
  *   - `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream).
  *   - Return 0 on success, IMQ_ERR_* (< 0) for rejected arguments, or a positive hipError_t
  *     when a launch fails. No call allocates, frees or synchronizes; all are re-entrant and
- *     keep no state between calls except a per-device immutable attribute cache.
+ *     keep no state between calls except a per-device immutable attribute cache. Scratch memory
+ *     (split-K partials, MoE intermediates) is a caller-provided workspace argument.
  */
 #ifndef IMQ_H
 #define IMQ_H
@@ -25,7 +26,7 @@
 extern "C" {
 #endif
 
-#define IMQ_ABI_VERSION 1
+#define IMQ_ABI_VERSION 2
 
 #define IMQ_DT_BF16 0
 #define IMQ_DT_FP16 1
@@ -65,25 +66,35 @@ int imq_dequant_w8(const void* qweight, int64_t q_row_stride, const void* scale,
  * Replaces the op returned by _w4a16_triton_op() (worker_quant.py:1079-1225: `_ksk` M==1 split-K
  * GEMV, `_k` M>1 tl.dot GEMM), called as op(x[M,Kpad] bf16, qweight, group, (scale, zero)).
  * K_pad = 2 * qweight columns; x must be zero beyond in_features (the module pads, 839-840).
- * Any M >= 1; the library picks the decode (MFMA skinny GEMV) or prefill (LDS-dequant MFMA
- * GEMM) kernel. Scale/zero are rounded to bf16 as _dequant(torch.bfloat16) does. */
+ * Any M >= 1; the library picks the decode (MFMA line / skinny GEMV) or prefill (LDS-dequant MFMA
+ * GEMM) kernel. Scale/zero are rounded to bf16 as _dequant(torch.bfloat16) does.
+ *
+ * workspace (optional, may be NULL): device memory of at least imq_linear_workspace_bytes(M, N,
+ * K_pad) bytes, 16-byte aligned, contents need not be initialised. With it, prefill shapes whose
+ * tiles do not fill the CUs split K across workgroups; a second launch sums the fp32 partials in
+ * split order (deterministic). Calls that share a workspace must be ordered on one stream.
+ * Without it (or when too small) K is not split. */
+int64_t imq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K_pad);
+
 int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad, const void* qweight,
                   int64_t q_row_stride, const void* scale, int64_t s_stride_n, int64_t s_stride_g,
                   int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
-                  int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* stream);
+                  int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
+                  int64_t workspace_bytes, void* stream);
 
 /* int2 twin: replaces _w2a16_triton_op() (worker_quant.py:1775-1918: `_ksk2`, `_k2`).
  * K_pad = 4 * qweight columns. */
 int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad, const void* qweight,
                   int64_t q_row_stride, const void* scale, int64_t s_stride_n, int64_t s_stride_g,
                   int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
-                  int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* stream);
+                  int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
+                  int64_t workspace_bytes, void* stream);
 
 /* int8 per-row symmetric: y = bf16(scale[n] * sum_k x[m,k] * q[n,k]). Replaces
  * _w8a16_triton_op() (worker_quant.py:926-1057: `_ksk8`, `_k8`), op(x, qweight, scale). */
 int imq_linear_w8(const void* x, int64_t x_row_stride, int64_t M, int64_t K, const void* qweight,
                   int64_t q_row_stride, const void* scale, int64_t s_stride_n, int s_dtype, int64_t N,
-                  void* y, int64_t y_row_stride, void* stream);
+                  void* y, int64_t y_row_stride, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- fused MoE experts (int4 g-wise, [E, N, K_pad/2] stacks) ----------------------------------
  * Per-row grouped GEMV: y[b, :] = x[b, :] @ dequant(W[eid[b]])^T for b < B (fp32 accumulate,

@@ -22,6 +22,8 @@
 //     activation rows and weight columns a group shares stay in that XCD's L2.
 #include "imq_common.h"
 
+#include <type_traits>
+
 namespace imq {
 
 namespace {
@@ -44,7 +46,7 @@ struct Cfg {
   static constexpr int A_EL = BM * BK, B_EL = BN * BK;
   static constexpr int LDS = 2 * (A_EL + B_EL) * 2;
   static_assert(XC >= 1 && (BM * CH) % NTHR == 0, "activation chunks must divide evenly");
-  static_assert(WC == 16 || WC == 32, "16 or 32 weight codes per thread");
+  static_assert(WC == 16 || WC == 32 || WC == 64, "16, 32 or 64 weight codes per thread");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile of 32x32 blocks");
 };
 
@@ -62,6 +64,8 @@ struct GemmArgs {
   uint16_t* y;
   int64_t sym;
   int tiles_m, tiles_n;
+  int splits, kps;     // split-K: K steps [split * kps, +kps) per workgroup; 1 = no split
+  float* part;         // split-K partials [splits][M][N] fp32
 };
 
 // LDS element offset of 16-byte chunk c of row `row`: the chunk index is XOR-ed with the row's
@@ -131,12 +135,11 @@ IMQ_DEV void load_w(WRegs<BITS, WC>& r, const uint8_t* p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.d[i] = v[i];
   } else {
-    const u32x4_t v0 = *(const u32x4_t*)p;
-    const u32x4_t v1 = *(const u32x4_t*)(p + 16);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      r.d[i] = v0[i];
-      r.d[4 + i] = v1[i];
+    for (int v = 0; v < B / 16; ++v) {
+      const u32x4_t t = *(const u32x4_t*)(p + 16 * v);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r.d[4 * v + i] = t[i];
     }
   }
 }
@@ -157,7 +160,7 @@ template <class C, int BITS, int SDT, int ZDT>
 __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, XC = C::XC, WC = C::WC;
   constexpr int BK = C::BK, CH = C::CH, KS = C::KS;
-  constexpr int PD = 1;   // register sets of loaded-but-not-yet-stored steps
+  constexpr int PD = 2;   // register sets of loaded-but-not-yet-stored steps
   constexpr int NTHR = C::NTHR;
   extern __shared__ __align__(16) uint16_t lds[];
   uint16_t* As = lds;
@@ -166,9 +169,11 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  // ---- tile mapping: XCD-aware, grouped by GROUP_M tile-rows ---------------------------------
+  // ---- tile mapping: XCD-aware, grouped by GROUP_M tile-rows; split-K index outermost ---------
   const int T = a.tiles_m * a.tiles_n;
-  int L = blockIdx.x;
+  const int split = blockIdx.x / T;                 // the splits of one tile run the same XCD
+  const int tile_id = blockIdx.x - split * T;
+  int L = tile_id;
   if ((T & 7) == 0) L = (L & 7) * (T >> 3) + (L >> 3);
   const int per_group = GROUP_M * a.tiles_n;
   const int grp = L / per_group;
@@ -211,7 +216,9 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
   WRegs<BITS, WC> wr[PD];
   uint32_t sraw[PD], zraw[PD];   // raw bits: converted only when consumed (loads stay in flight)
 
-  auto gload = [&](int set, int kt) {
+  const int kt0 = split * a.kps;                    // first K step of this workgroup
+  auto gload = [&](int set, int ktl) {
+    const int kt = kt0 + ktl;
 #pragma unroll
     for (int j = 0; j < XC; ++j) xr[set][j] = *(const u32x4_t*)(xtile + kt * BK + xo[j]);
     load_w(wr[set], wtile + kt * BYTES_STEP + wo);
@@ -281,15 +288,16 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
   // One step with the next step's LDS writes spread over the K slices: slice ks writes the
   // activation chunks j == ks (mod KS) and dequantizes / writes the weight chunks c == ks (mod KS),
   // so the VALU dequant sits between MFMAs instead of after them.
-  auto step = [&](int cur) {
+  auto step = [&](int cur, auto rsc) {
+    constexpr int rs = decltype(rsc)::value;          // register set holding the next step
     const uint16_t* A = As + cur * C::A_EL;
     const uint16_t* B = Bs + cur * C::B_EL;
     uint16_t* An = As + (cur ^ 1) * C::A_EL;
     uint16_t* Bn = Bs + (cur ^ 1) * C::B_EL;
     float s = 0.f, nzs = 0.f;
     if constexpr (BITS != 8) {
-      s = raw_bits_to_f32<SDT>(sraw[0]);
-      float z = raw_bits_to_f32<ZDT>(zraw[0]);
+      s = raw_bits_to_f32<SDT>(sraw[rs]);
+      float z = raw_bits_to_f32<ZDT>(zraw[rs]);
       if constexpr (SDT != IMQ_DT_BF16) s = round_to<IMQ_DT_BF16>(s);
       if constexpr (ZDT != IMQ_DT_BF16) z = round_to<IMQ_DT_BF16>(z);
       nzs = -z * s;
@@ -311,27 +319,57 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < JB; ++j) acc[i][j] = mfma32x32x16(af[ks][i], bfr[ks][j], acc[i][j]);
 #pragma unroll
-      for (int j = ks; j < XC; j += KS) *(u32x4_t*)(An + xl[j]) = xr[0][j];
+      for (int j = ks; j < XC; j += KS) *(u32x4_t*)(An + xl[j]) = xr[rs][j];
 #pragma unroll
-      for (int c = ks; c < WC / 8; c += KS) *(u32x4_t*)(Bn + bl[c]) = weight_chunk(wr[0], c, s, nzs);
+      for (int c = ks; c < WC / 8; c += KS) *(u32x4_t*)(Bn + bl[c]) = weight_chunk(wr[rs], c, s, nzs);
     }
   };
 
-  // Prologue: step 0 into LDS buffer 0, step 1 in flight in registers.
-  const int KT = a.K / BK;
+  // Prologue: step 0 into LDS buffer 0; step 1 in register set 1.
+  const int KT = (a.K / BK - kt0) < a.kps ? (a.K / BK - kt0) : a.kps;   // this workgroup's K steps
   gload(0, 0);
   lstore(0, 0);
-  gload(0, KT > 1 ? 1 : 0);
+  gload(1, KT > 1 ? 1 : 0);
   __syncthreads();
 
-  // Step kt: MFMAs on buffer kt&1; write step kt+1 (registers) into the other buffer; load step
-  // kt+2. The body is branch-free so the dequant, LDS writes and loads interleave with the
-  // MFMAs: past the end the loads re-read the last step (in bounds) and the final write lands in
-  // the buffer no later step reads.
-  for (int kt = 0; kt < KT; ++kt) {
-    step(kt & 1);
-    gload(0, kt + 2 < KT ? kt + 2 : KT - 1);
+  // Step kt: load step kt+2 into the register set freed by step kt (written to LDS during step
+  // kt-1), then MFMAs on LDS buffer kt&1 while register set (kt+1)&1 -- loaded a whole step
+  // earlier -- is dequantized into the other buffer. The body is branch-free so the dequant, LDS
+  // writes and loads interleave with the MFMAs: past the end the loads re-read the last step (in
+  // bounds) and the final writes land in the buffer no later step reads. Unrolled by two so the
+  // register sets are compile-time indexed.
+  auto iter = [&](int kt, auto setc) {
+    constexpr int set = decltype(setc)::value;       // == kt & 1
+    gload(set, kt + 2 < KT ? kt + 2 : KT - 1);
+    step(set, std::integral_constant<int, 1 - set>{});
     __syncthreads();
+  };
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    iter(kt, std::integral_constant<int, 0>{});
+    iter(kt + 1, std::integral_constant<int, 1>{});
+  }
+  if (kt < KT) iter(kt, std::integral_constant<int, 0>{});
+
+  // ---- split-K: each split stores its fp32 partial tile into [split][M][N]; splitk_reduce_kernel
+  // sums the splits in order (deterministic) and writes y. A second launch instead of arrival
+  // counters: the device-scope fences a last-arriving reduction needs would write back and
+  // invalidate the XCD's whole L2 once per workgroup, evicting the shared activation tiles.
+  if (a.splits > 1) {
+    float* pbase = a.part + (size_t)split * a.M * a.N;
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const int n = n0 + wn * WN + j * 32 + (lane & 31);
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int i = 0; i < IB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (m < a.M) pbase[(size_t)m * a.N + n] = acc[i][j][r];
+        }
+    }
+    return;
   }
 
   // ---- epilogue: D lane l holds column l%32, element r at row 8*(r/4) + 4*(l/32) + r%4 -------
@@ -352,13 +390,67 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
   }
 }
 
+// y[m, n] = bf16(sum_s part[s][m][n] * scale[n]) over the splits in order; 4 columns per thread.
+template <int BITS, int SDT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
+                                                            const void* __restrict__ sc, int64_t ssn,
+                                                            uint16_t* __restrict__ y, int64_t sym) {
+  const int64_t n4 = (N + 3) / 4;
+  const int64_t total = (int64_t)M * n4;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int m = (int)(t / n4);
+    const int n = 4 * (int)(t - (int64_t)m * n4);
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < splits; ++sp) {
+      const float* src = part + ((size_t)sp * M + m) * N + n;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n + q < N) v[q] += src[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (n + q >= N) break;
+      float o = v[q];
+      if constexpr (BITS == 8) o *= load_as_f32<SDT>(sc, (int64_t)(n + q) * ssn);
+      y[(int64_t)m * sym + n + q] = (uint16_t)cvt_pk_bf16(o, 0.f);
+    }
+  }
+}
+
+// Split-K factor for a launch of T tiles over KT steps of K: 1 while the tiles fill at least
+// three quarters of the CUs, else the smallest power of two reaching one tile per CU, capped at 8
+// and at 8 K steps per split.
+inline int split_plan(int64_t T, int KT, int cus) {
+  if (4 * T >= 3 * (int64_t)cus) return 1;
+  int s = 1;
+  while (s < 8 && T * s < cus && KT / (2 * s) >= 8) s *= 2;
+  return s;
+}
+
+template <class C>
+int64_t split_bytes(int64_t M, int64_t N, int64_t K, int cus, int* splits_out = nullptr) {
+  const int64_t T = imq_cdiv(M, C::BM) * imq_cdiv(N, C::BN);
+  const int s = split_plan(T, (int)(K / C::BK), cus);
+  if (splits_out) *splits_out = s;
+  if (s == 1) return 0;
+  return (int64_t)s * M * N * 4;
+}
+
 template <class C, int BITS, int SDT, int ZDT>
-int launch_cfg(const GemmArgs& a0, hipStream_t st) {
+int launch_cfg(const GemmArgs& a0, void* ws, int64_t ws_bytes, hipStream_t st) {
   GemmArgs a = a0;
   a.tiles_m = (a.M + C::BM - 1) / C::BM;
   a.tiles_n = (a.N + C::BN - 1) / C::BN;
   const int64_t T = (int64_t)a.tiles_m * a.tiles_n;
   if (T > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  const int KT = a.K / C::BK;
+  int s = 1;
+  const int64_t need = split_bytes<C>(a.M, a.N, a.K, device_info().cus, &s);
+  if (s > 1 && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) s = 1;
+  a.splits = s;
+  a.kps = (KT + s - 1) / s;
+  a.part = s > 1 ? (float*)ws : nullptr;
+  if (T * s > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   auto kern = gemm_wq_kernel<C, BITS, SDT, ZDT>;
   if (C::LDS > 65536) {
     static int attr_set = 0;   // benign race: every caller sets the same attribute value
@@ -368,8 +460,15 @@ int launch_cfg(const GemmArgs& a0, hipStream_t st) {
       __atomic_store_n(&attr_set, 1, __ATOMIC_RELEASE);
     }
   }
-  kern<<<dim3((unsigned)T), dim3(C::NTHR), C::LDS, st>>>(a);
+  kern<<<dim3((unsigned)(T * s)), dim3(C::NTHR), C::LDS, st>>>(a);
   IMQ_LAUNCH_CHECK();
+  if (s > 1) {
+    const int64_t total = (int64_t)a.M * ((a.N + 3) / 4);
+    const int64_t blocks = imq_cdiv(total, 256) < 8192 ? imq_cdiv(total, 256) : 8192;
+    splitk_reduce_kernel<BITS, SDT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a.part, s, a.M, a.N, a.sc, a.ssn,
+                                                                                 a.y, a.sym);
+    IMQ_LAUNCH_CHECK();
+  }
   return IMQ_OK;
 }
 
@@ -383,46 +482,56 @@ int launch_cfg(const GemmArgs& a0, hipStream_t st) {
 using CfgBig = Cfg<IMQ_GEMM_CFG_BIG>;
 using CfgSmall = Cfg<IMQ_GEMM_CFG_SMALL>;
 
+// 256 x 128 tiles once M spans two 128-row tiles, else 128 x 128; either splits K when its tiles
+// do not fill the CUs.
+inline bool use_big(int64_t M) { return M > 128; }
+
 template <int BITS, int SDT, int ZDT>
-int launch_gemm(const GemmArgs& a, hipStream_t st) {
-  const int64_t big_tiles = (int64_t)((a.M + CfgBig::BM - 1) / CfgBig::BM) * ((a.N + CfgBig::BN - 1) / CfgBig::BN);
-  if (big_tiles >= 256) return launch_cfg<CfgBig, BITS, SDT, ZDT>(a, st);
-  return launch_cfg<CfgSmall, BITS, SDT, ZDT>(a, st);
+int launch_gemm(const GemmArgs& a, void* ws, int64_t wsb, hipStream_t st) {
+  if (use_big(a.M)) return launch_cfg<CfgBig, BITS, SDT, ZDT>(a, ws, wsb, st);
+  return launch_cfg<CfgSmall, BITS, SDT, ZDT>(a, ws, wsb, st);
 }
 
 template <int BITS, int SDT>
-int gemm_z(const GemmArgs& a, int zdt, hipStream_t st) {
+int gemm_z(const GemmArgs& a, int zdt, void* ws, int64_t wsb, hipStream_t st) {
   if constexpr (BITS == 8) {
-    return launch_gemm<8, SDT, SDT>(a, st);
+    return launch_gemm<8, SDT, SDT>(a, ws, wsb, st);
   } else {
     switch (zdt) {
-      case IMQ_DT_BF16: return launch_gemm<BITS, SDT, IMQ_DT_BF16>(a, st);
-      case IMQ_DT_FP16: return launch_gemm<BITS, SDT, IMQ_DT_FP16>(a, st);
-      case IMQ_DT_FP32: return launch_gemm<BITS, SDT, IMQ_DT_FP32>(a, st);
+      case IMQ_DT_BF16: return launch_gemm<BITS, SDT, IMQ_DT_BF16>(a, ws, wsb, st);
+      case IMQ_DT_FP16: return launch_gemm<BITS, SDT, IMQ_DT_FP16>(a, ws, wsb, st);
+      case IMQ_DT_FP32: return launch_gemm<BITS, SDT, IMQ_DT_FP32>(a, ws, wsb, st);
     }
     return IMQ_ERR_INVALID;
   }
 }
 
 template <int BITS>
-int gemm_bits(const GemmArgs& a, int sdt, int zdt, hipStream_t st) {
+int gemm_bits(const GemmArgs& a, int sdt, int zdt, void* ws, int64_t wsb, hipStream_t st) {
   switch (sdt) {
-    case IMQ_DT_BF16: return gemm_z<BITS, IMQ_DT_BF16>(a, zdt, st);
-    case IMQ_DT_FP16: return gemm_z<BITS, IMQ_DT_FP16>(a, zdt, st);
-    case IMQ_DT_FP32: return gemm_z<BITS, IMQ_DT_FP32>(a, zdt, st);
+    case IMQ_DT_BF16: return gemm_z<BITS, IMQ_DT_BF16>(a, zdt, ws, wsb, st);
+    case IMQ_DT_FP16: return gemm_z<BITS, IMQ_DT_FP16>(a, zdt, ws, wsb, st);
+    case IMQ_DT_FP32: return gemm_z<BITS, IMQ_DT_FP32>(a, zdt, ws, wsb, st);
   }
   return IMQ_ERR_INVALID;
 }
 
 }  // namespace
 
+// Workspace bytes a split-K launch of this shape uses (0: the launch does not split K).
+int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 16 || N <= 0 || K % 64 != 0) return 0;
+  const int cus = device_info().cus;
+  return use_big(M) ? split_bytes<CfgBig>(M, N, K, cus) : split_bytes<CfgSmall>(M, N, K, cus);
+}
+
 // Prefill GEMM entry used by imq_linear_w4 / _w2 / _w8 for M > 16. Returns IMQ_ERR_UNSUPPORTED
 // for shapes the tiled kernel does not cover (K not a multiple of 64, groups below 32 codes or
 // not a power of two, misaligned operands, offsets beyond 32 bits); the caller then uses the
-// generic kernel.
+// generic kernel. Without a large enough workspace the launch does not split K.
 int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
             const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-            int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st) {
+            int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
   if (M <= 0 || N <= 0) return IMQ_OK;
   if (K % 64 != 0 || M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   int gsh = 0;
@@ -437,11 +546,12 @@ int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, cons
   // widest weight load of either tile configuration: 16 B (int4, int8 as 2 x 16 B), 8 B (int2)
   const int wbytes = bits == 2 ? 8 : 16;
   if (((uintptr_t)q % wbytes) || (sqn % wbytes)) return IMQ_ERR_UNSUPPORTED;
-  GemmArgs a{x, sxm, (int)M, (int)K, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, gsh, y, sym, 0, 0};
+  GemmArgs a{x, sxm, (int)M, (int)K, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, gsh, y, sym, 0, 0, 1, 0,
+             nullptr};
   switch (bits) {
-    case 4: return gemm_bits<4>(a, sdt, zdt, st);
-    case 2: return gemm_bits<2>(a, sdt, zdt, st);
-    case 8: return gemm_bits<8>(a, sdt, zdt, st);
+    case 4: return gemm_bits<4>(a, sdt, zdt, ws, wsb, st);
+    case 2: return gemm_bits<2>(a, sdt, zdt, ws, wsb, st);
+    case 8: return gemm_bits<8>(a, sdt, zdt, ws, wsb, st);
   }
   return IMQ_ERR_INVALID;
 }

@@ -15,7 +15,8 @@ int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t
               const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st);
 int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
             const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-            int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st);
+            int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
+int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 template <int BITS>
 int generic_gemv(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
                  const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn,
@@ -42,6 +43,11 @@ int check_g(int bits, const void* x, int64_t sxm, int64_t M, int64_t Kpad, const
 
 extern "C" int imq_abi_version(void) { return IMQ_ABI_VERSION; }
 
+extern "C" int64_t imq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K_pad) {
+  if (M < 0 || N < 0 || K_pad <= 0) return -1;
+  return imq::gemm_workspace_bytes(M, N, K_pad);
+}
+
 extern "C" const char* imq_strerror(int status) {
   switch (status) {
     case IMQ_OK: return "ok";
@@ -57,7 +63,8 @@ extern "C" int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int
                              const void* qweight, int64_t q_row_stride, const void* scale,
                              int64_t s_stride_n, int64_t s_stride_g, int s_dtype, const void* zero,
                              int64_t z_stride_n, int64_t z_stride_g, int z_dtype, int64_t N,
-                             int64_t group_size, void* y, int64_t y_row_stride, void* stream) {
+                             int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
   int rc = check_g(4, x, x_row_stride, M, K_pad, qweight, q_row_stride, scale, s_dtype, zero, z_dtype, N,
                    group_size, y, y_row_stride);
   if (rc != IMQ_OK) return rc;
@@ -71,7 +78,8 @@ extern "C" int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int
                         zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
   } else {
     rc = imq::gemm_wq(4, xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
-                      s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
+                      s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride,
+                      workspace, workspace_bytes, st);
   }
   if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   return imq::generic_gemv<4>(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
@@ -83,7 +91,8 @@ extern "C" int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int
                              const void* qweight, int64_t q_row_stride, const void* scale,
                              int64_t s_stride_n, int64_t s_stride_g, int s_dtype, const void* zero,
                              int64_t z_stride_n, int64_t z_stride_g, int z_dtype, int64_t N,
-                             int64_t group_size, void* y, int64_t y_row_stride, void* stream) {
+                             int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
   int rc = check_g(2, x, x_row_stride, M, K_pad, qweight, q_row_stride, scale, s_dtype, zero, z_dtype, N,
                    group_size, y, y_row_stride);
   if (rc != IMQ_OK) return rc;
@@ -97,7 +106,8 @@ extern "C" int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int
                         zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
   } else {
     rc = imq::gemm_wq(2, xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
-                      s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
+                      s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride,
+                      workspace, workspace_bytes, st);
   }
   if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   return imq::generic_gemv<2>(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
@@ -108,7 +118,7 @@ extern "C" int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int
 extern "C" int imq_linear_w8(const void* x, int64_t x_row_stride, int64_t M, int64_t K,
                              const void* qweight, int64_t q_row_stride, const void* scale,
                              int64_t s_stride_n, int s_dtype, int64_t N, void* y, int64_t y_row_stride,
-                             void* stream) {
+                             void* workspace, int64_t workspace_bytes, void* stream) {
   if (!x || !qweight || !scale || !y || M < 0 || N < 0 || K <= 0) return IMQ_ERR_INVALID;
   if (q_row_stride < K || x_row_stride < K || y_row_stride < N || !dt_ok(s_dtype)) return IMQ_ERR_INVALID;
   if (M == 0 || N == 0) return IMQ_OK;
@@ -121,7 +131,7 @@ extern "C" int imq_linear_w8(const void* x, int64_t x_row_stride, int64_t M, int
                         s_dtype, N, yb, y_row_stride, st);
   } else {
     rc = imq::gemm_wq(8, xb, x_row_stride, M, K, (const uint8_t*)qweight, q_row_stride, scale, s_stride_n,
-                      0, s_dtype, nullptr, 0, 0, s_dtype, N, 0, yb, y_row_stride, st);
+                      0, s_dtype, nullptr, 0, 0, s_dtype, N, 0, yb, y_row_stride, workspace, workspace_bytes, st);
   }
   if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   return imq::generic_gemv<8>(xb, x_row_stride, M, K, (const uint8_t*)qweight, q_row_stride, scale,

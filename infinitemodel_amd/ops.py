@@ -44,6 +44,24 @@ def _rows2d(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
+# Split-K workspaces of the fused linears, one per (device, stream): calls sharing one must be
+# stream-ordered. Its contents need no initialization, so a cached workspace is reusable (also
+# inside captured HIP graphs).
+_WS: dict = {}
+
+
+def _workspace(dev: torch.device, M: int, N: int, K: int):
+    need = int(_lib.lib().imq_linear_workspace_bytes(M, N, K))
+    if need <= 0:
+        return 0, 0
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        _WS[key] = ws
+    return ws.data_ptr(), ws.numel()
+
+
 def _check_packed(q: torch.Tensor, dt=torch.uint8):
     if q.dtype != dt or q.dim() < 2 or q.stride(-1) != 1:
         raise ValueError(f"packed weight must be {dt} with a unit last stride, got {q.dtype} {tuple(q.stride())}")
@@ -109,9 +127,10 @@ def _linear_g(fn: str, codes_per_byte: int, x, qweight, group_size: int, sz, out
         raise ValueError("out must be a bf16 [M, N] tensor with unit column stride")
     y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
+        ws, wsb = _workspace(dev, M, N, Kpad)
         call(fn, _ptr(x), x.stride(0), M, Kpad, _ptr(qweight), qweight.stride(0), _ptr(scale), scale.stride(0),
              scale.stride(1), dtype_code(scale.dtype), _ptr(zero), zero.stride(0), zero.stride(1),
-             dtype_code(zero.dtype), N, group_size, _ptr(y), y.stride(0), _stream(dev))
+             dtype_code(zero.dtype), N, group_size, _ptr(y), y.stride(0), ws, wsb, _stream(dev))
     return y
 
 
@@ -137,8 +156,9 @@ def linear_w8(x, qweight, scale, out=None):
         raise ValueError(f"x has {K} columns, qweight {qweight.shape[1]}")
     y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
+        ws, wsb = _workspace(dev, M, N, K)
         call("imq_linear_w8", _ptr(x), x.stride(0), M, K, _ptr(qweight), qweight.stride(0), _ptr(scale),
-             scale.stride(0), dtype_code(scale.dtype), N, _ptr(y), y.stride(0), _stream(dev))
+             scale.stride(0), dtype_code(scale.dtype), N, _ptr(y), y.stride(0), ws, wsb, _stream(dev))
     return y
 
 

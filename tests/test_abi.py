@@ -46,7 +46,7 @@ def test_exports_are_c_linkage():
 
 
 def test_abi_version_and_strerror(L):
-    assert L.imq_abi_version() == 1
+    assert L.imq_abi_version() == 2
     assert L.imq_strerror(0) == b"ok"
     for rc in (_lib.IMQ_ERR_INVALID, _lib.IMQ_ERR_UNSUPPORTED, _lib.IMQ_ERR_ALIGN):
         assert len(L.imq_strerror(rc)) > 5
@@ -61,20 +61,29 @@ def test_moe_workspace_bytes(L):
     assert L.imq_moe_workspace_bytes(-1, k, E, H, I, G) < 0
 
 
+def test_linear_workspace_bytes_host_rules(L):
+    """Decode shapes never split K (no workspace); negative sizes are rejected."""
+    assert L.imq_linear_workspace_bytes(1, 4096, 4096) == 0
+    assert L.imq_linear_workspace_bytes(16, 4096, 14336) == 0
+    assert L.imq_linear_workspace_bytes(-1, 4096, 4096) < 0
+
+
 def test_invalid_arguments_are_rejected_on_the_host(L):
     """Null pointers and inconsistent shapes return IMQ_ERR_INVALID without a device call."""
     nul = None
-    rc = L.imq_linear_w4(nul, 4096, 1, 4096, nul, 2048, nul, 32, 1, 0, nul, 32, 1, 0, 4096, 128, nul, 4096, nul)
+    rc = L.imq_linear_w4(nul, 4096, 1, 4096, nul, 2048, nul, 32, 1, 0, nul, 32, 1, 0, 4096, 128, nul, 4096, nul, 0,
+                         nul)
     assert rc == _lib.IMQ_ERR_INVALID
     one = ctypes.c_void_p(16)   # never dereferenced: validation fails first
     # K_pad not a multiple of the group
-    rc = L.imq_linear_w4(one, 4096, 1, 4000, one, 2048, one, 32, 1, 0, one, 32, 1, 0, 4096, 128, one, 4096, nul)
+    rc = L.imq_linear_w4(one, 4096, 1, 4000, one, 2048, one, 32, 1, 0, one, 32, 1, 0, 4096, 128, one, 4096, nul, 0,
+                         nul)
     assert rc == _lib.IMQ_ERR_INVALID
     # packed row stride shorter than the packed row
-    rc = L.imq_linear_w2(one, 4096, 1, 4096, one, 512, one, 64, 1, 0, one, 64, 1, 0, 4096, 64, one, 4096, nul)
+    rc = L.imq_linear_w2(one, 4096, 1, 4096, one, 512, one, 64, 1, 0, one, 64, 1, 0, 4096, 64, one, 4096, nul, 0, nul)
     assert rc == _lib.IMQ_ERR_INVALID
     # bad dtype code
-    rc = L.imq_linear_w8(one, 4096, 1, 4096, one, 4096, one, 1, 7, 4096, one, 4096, nul)
+    rc = L.imq_linear_w8(one, 4096, 1, 4096, one, 4096, one, 1, 7, 4096, one, 4096, nul, 0, nul)
     assert rc == _lib.IMQ_ERR_INVALID
     rc = L.imq_dequant_w4(one, 2048, one, 32, 1, 0, one, 32, 1, 0, 4096, 4096, 100, one, 4096, 0, nul)
     assert rc == _lib.IMQ_ERR_INVALID

@@ -342,3 +342,25 @@ def test_gemm_w2(dev, M):
 @pytest.mark.parametrize("M,sdt", [(64, "fp16"), (300, "bf16")])
 def test_gemm_w8(dev, M, sdt):
     _int8_check(dev, 640, 2048, M, sdt, seed=M)
+
+
+# ---- split-K prefill GEMM (tiles fewer than the CUs): last-arriving split reduces ------------
+@pytest.mark.parametrize("M,N,K", [(40, 256, 2048), (300, 512, 4096), (512, 4096, 14336), (150, 1000, 8192)])
+def test_gemm_w4_split_k(dev, M, N, K):
+    """Shapes whose tiles do not fill the CUs split K (2, 4 or 8 ways); repeated calls reuse the
+    workspace and give bit-identical results (fixed-order reduction)."""
+    import torch
+    from infinitemodel_amd import _lib, ops
+    assert _lib.lib().imq_linear_workspace_bytes(M, N, K) > 0
+    c = C.int4_case(N, K, 128, seed=M + N + K)
+    y = _linear_check(dev, c, M, seed=M)
+    x = torch.zeros((M, K), dtype=torch.bfloat16, device=dev)
+    x[:, : c["in_f"]] = C.to_torch(C.bf16_normal(C.rng(M), (M, c["in_f"])), "bf16", dev)
+    q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev), C.to_torch(c["z"], "bf16", dev)
+    for _ in range(3):
+        assert torch.equal(ops.linear_w4(x, q, 128, (s, z)), y)
+
+
+def test_gemm_w8_split_k(dev):
+    """int8 per-row prefill at the C4 14336 -> 4096 shape, M = 512 (8 x 32 tiles -> split 4)."""
+    _int8_check(dev, 4096, 14336, 512, "fp16", seed=4)

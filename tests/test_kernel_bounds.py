@@ -117,10 +117,19 @@ def test_model_catches_oversized_strip_load():
 
 # ---- prefill GEMM (csrc/gemm.hip): 128 x 128 tiles, K steps of 64 ------------------------------
 def gemm_cfg(M, N):
-    """launch_gemm in csrc/gemm.hip: (BM, threads) -- 256 x 128 tiles with 512 threads when there
-    are >= 256 of them, else 128 x 128 with 256 threads."""
-    big = (-(-M // 256)) * (-(-N // 128)) >= 256
-    return (256, 512) if big else (128, 256)
+    """launch_gemm in csrc/gemm.hip: (BM, threads) -- 256 x 128 tiles with 512 threads once M
+    exceeds 128 rows, else 128 x 128 with 256 threads."""
+    return (256, 512) if M > 128 else (128, 256)
+
+
+def split_plan(T, KT, cus=256):
+    """split_plan in csrc/gemm.hip."""
+    if 4 * T >= 3 * cus:
+        return 1
+    s = 1
+    while s < 8 and T * s < cus and KT // (2 * s) >= 8:
+        s *= 2
+    return s
 
 
 def gemm_ranges(M, N, K, bits, G, sxm, sqn, ssn, sym):
@@ -405,3 +414,27 @@ def test_line_model_catches_wrong_scale_index():
     # compare the group each wave would use for its first line-step
     for wave in range(1, W):
         assert wrong(wave * S2, 0) != wave * S2 * (vb // 2)
+
+
+
+@pytest.mark.parametrize("M,N,K", [(40, 256, 2048), (300, 512, 4096), (512, 4096, 14336), (150, 1000, 8192),
+                                   (512, 14336, 4096), (2048, 4096, 14336), (17, 64, 256)])
+def test_gemm_split_k_ranges(M, N, K):
+    """Every split owns >= 1 K step, the splits tile [0, K/64) exactly, and the [split][M][N]
+    partials fit the workspace the host sized."""
+    BM, NTHR = gemm_cfg(M, N)
+    BN, BK = 128, 64
+    T = (-(-M // BM)) * (-(-N // BN))
+    KT = K // BK
+    S = split_plan(T, KT)
+    kps = -(-KT // S)
+    covered = []
+    for sp in range(S):
+        kt0 = sp * kps
+        n = min(KT - kt0, kps)
+        assert n >= 1, (sp, kt0, n)
+        covered += list(range(kt0, kt0 + n))
+    assert covered == list(range(KT))
+    if S > 1:
+        # stores are masked to m < M, n < N: the last partial element is ((S-1)*M + M-1)*N + N-1
+        assert (((S - 1) * M + M - 1) * N + N - 1 + 1) * 4 == S * M * N * 4
