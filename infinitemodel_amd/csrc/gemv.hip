@@ -45,6 +45,7 @@ struct SkinnyArgs {
   int64_t sym;
   int chunk_steps;   // K-steps staged in LDS at once
   const int8_t* q8;  // int8 weights (the int8 kernel; q is unused there)
+  float* part;       // split-K partials [splits][M][N] fp32 (the K-split kernel)
 };
 
 constexpr int kStep = 128;          // codes per K-step
@@ -570,8 +571,11 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
       A0[k] = *(const bf16x8_t*)(xa + i * kLine + 8 * k);
       A1[k] = *(const bf16x8_t*)(xa + i * kLine + 128 + 8 * k);
     }
-    const float s0 = v ? val(sc_c, 2 * i) : 0.f;
-    const float s1 = v ? val(sc_x, 2 * i + 1) : 0.f;
+    // read unconditionally (the staged strip covers every i), then select: a conditional read
+    // becomes a branch with an LDS round trip inside each line-step
+    float s0 = val(sc_c, 2 * i), s1 = val(sc_x, 2 * i + 1);
+    s0 = v ? s0 : 0.f;
+    s1 = v ? s1 : 0.f;
     const float cz0 = -(128.f + val(zr_c, 2 * i)) * s0;
     const float cz1 = -(128.f + val(zr_x, 2 * i + 1)) * s1;
     const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
@@ -609,6 +613,216 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
     for (int w = 0; w < W; ++w) sum += red[w * (RC * 16) + m * 16 + n];
     if (n <= rlast) a.y[(int64_t)m * a.sym + row0 + n] = (uint16_t)f32_to_bf16_bits(sum);
   }
+}
+
+// ---------------------------------------------------------------------------------------------
+// int4 decode kernel for 4 < M <= 16 (G = 128): K split across workgroups.
+//
+// At M = 16 the activations of a whole row (M * K_pad * 2 bytes: 128 KB at K = 4096, 448 KB at
+// K = 14336) no longer fit a workgroup's LDS next to enough waves, and a 16-row tile per
+// workgroup would restage them once per 16 weight rows (4x the weight bytes through L2). Here a
+// workgroup owns NW row tiles (16 * NW rows) and one split of S2 line-steps (S2 * 256 codes):
+//   * its activations chunk x[0:M, split] (M x S2*256 bf16) is staged once in LDS, permuted to
+//     the unpack order with per-group row sums, and shared by the NW waves;
+//   * wave w streams rows [16 w, 16 w + 16) of the tile over the split exactly like the line
+//     kernel (two full-line loads per line-step, MFMA 16x16x32 with the +128 bias fold), so every
+//     packed byte is read once;
+//   * D registers hold all 16 activation rows (m = 4 * (lane / 16) + r), and each wave writes its
+//     fp32 partial y[m, n] of this split to part[split][m][n]; no cross-wave reduction.
+// splitk_rows_reduce_kernel then sums the splits in order (deterministic) into bf16 y.
+// ---------------------------------------------------------------------------------------------
+IMQ_HOST_DEV inline int ksplit_lds(int M, int S2, int NW, int vb) {
+  return M * (S2 * kLine + 8) * 2 + 2 * S2 * 16 * 4 + NW * 2 * 16 * (S2 * vb / 2) * 4;
+}
+
+template <int S2, int MC, int SDT, int NW>
+__global__ __launch_bounds__(64 * NW) void w4_ksplit_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;   // bytes per scale / zero value
+  constexpr int DPR = S2 * VB / 2;                   // dwords per row per array (2*S2 values)
+  constexpr int NT = 64 * NW;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, ar = lane >> 4;
+  const bool lo8 = c < 8;
+  const int M = a.M;
+  const int KL = a.Kpad / kLine;
+  const int RB = (a.N + 16 * NW - 1) / (16 * NW);
+  const int split = blockIdx.x / RB;
+  const int rb = blockIdx.x - split * RB;
+  const int ls0 = split * S2;                        // first line-step of this split
+  const int row0 = (rb * NW + wave) * 16;
+  const bool tile_ok = row0 < a.N;                   // a partial last row block has idle waves
+  const int rowa = tile_ok ? row0 : 0;               // addressing base (any valid rows when idle)
+  const int rlast = a.N - 1 - rowa;                  // last valid row within the tile
+
+  const int xrow = S2 * kLine + 8;
+  uint16_t* xw = (uint16_t*)smem;                                  // [M][xrow] permuted x
+  float* xs = (float*)(smem + (size_t)M * xrow * 2);               // [2*S2 groups][16 rows]
+  uint32_t* szl = (uint32_t*)(xs + 2 * S2 * 16) + wave * (2 * 16 * DPR);   // this wave's s/z
+
+  // 1) x chunk: M rows x 32*S2 16-byte blocks, spread over the workgroup (clamped into the row)
+  constexpr int XB = 32 * S2;
+  constexpr int XU = (MC * XB + NT - 1) / NT;
+  const int xtot = M * XB;
+  const uint16_t* xbase = a.x + (int64_t)ls0 * kLine;
+  const int xlim = a.Kpad - ls0 * kLine - 8;         // last valid block start in the split
+  u32x4_t xv[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    int idx = threadIdx.x + NT * u;
+    idx = idx < xtot ? idx : xtot - 1;
+    const int m = idx / XB, b = idx - m * XB;
+    int kb = 8 * b;
+    kb = kb < xlim ? kb : xlim;
+    xv[u] = *(const u32x4_t*)(xbase + m * (int)a.sxm + kb);
+  }
+  // 2) scale / zero words of groups [2*ls0, 2*ls0 + 2*S2) of this wave's 16 rows
+  constexpr int ZU = (32 * DPR + 63) / 64;
+  const int ngd = a.Kpad / 128 * VB / 4;             // dwords per row holding real groups
+  const unsigned char* sbase = (const unsigned char*)a.sc + (int64_t)rowa * a.ssn * VB;
+  const unsigned char* zbase = (const unsigned char*)a.zr + (int64_t)rowa * a.szn * VB;
+  uint32_t zv[ZU];
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    int d = lane + 64 * u;
+    d = d < 32 * DPR ? d : 32 * DPR - 1;
+    const int arr = d / (16 * DPR);
+    const int rem = d - arr * (16 * DPR);
+    int r = rem / DPR;
+    const int dw = rem - r * DPR;
+    r = r < rlast ? r : rlast;
+    int gd = ls0 * (VB / 2) + dw;
+    gd = gd < ngd ? gd : ngd - 1;
+    const unsigned char* p = arr ? zbase + r * (int)a.szn * VB : sbase + r * (int)a.ssn * VB;
+    zv[u] = *(const uint32_t*)(p + 4 * gd);
+  }
+  // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
+  const uint8_t* qt = a.q + (int64_t)rowa * a.sqn;
+  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
+  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
+  const uint8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
+  const uint8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  u32x4_t wb[2 * S2];
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    int l = ls0 + i;
+    l = l < KL ? l : KL - 1;
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+  }
+  // 4) stage x (permuted) with per-group row sums, and this wave's scale / zero words
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int idx = threadIdx.x + NT * u;
+    const bool ok = idx < xtot;
+    const int m = (ok ? idx : 0) / XB, b = (ok ? idx : 0) - m * XB;
+    float sum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
+    // the 16 blocks of one group are 16 consecutive idx (XB and NT are multiples of 16)
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    if (ok) {
+      *(u32x4_t*)(xw + m * xrow + 8 * b) = permute_x8(xv[u]);
+      if ((b & 15) == 0) xs[(b >> 4) * 16 + m] = sum;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    const int d = lane + 64 * u;
+    if (d < 32 * DPR) szl[d] = zv[u];
+  }
+  lds_barrier();   // x and its sums are shared by the waves; weights stay in flight
+
+  const uint32_t magic = magic_bf16_128x2();
+  const uint16_t* xa = xw + (c < M ? c : M - 1) * xrow + 32 * ar;   // A rows m >= M repeat M-1
+  const uint32_t* sc_c = szl + c * DPR;
+  const uint32_t* sc_x = szl + (c ^ 8) * DPR;
+  const uint32_t* zr_c = szl + 16 * DPR + c * DPR;
+  const uint32_t* zr_x = szl + 16 * DPR + (c ^ 8) * DPR;
+  auto val = [&](const uint32_t* p, int g) -> float {   // group g (0 .. 2*S2) of a staged row
+    if constexpr (VB == 4) return round_bf16_hw(__uint_as_float(p[g]));
+    else return raw_to_bf16_f32<SDT>((g & 1) ? (p[g >> 1] >> 16) : (p[g >> 1] & 0xffffu));
+  };
+  float y0[4] = {0.f, 0.f, 0.f, 0.f}, y1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    const bool v = ls0 + i < KL;
+    const f32x4_t xs0 = *(const f32x4_t*)(xs + (2 * i) * 16 + 4 * ar);
+    const f32x4_t xs1 = *(const f32x4_t*)(xs + (2 * i + 1) * 16 + 4 * ar);
+    bf16x8_t A0[4], A1[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      A0[k] = *(const bf16x8_t*)(xa + i * kLine + 8 * k);
+      A1[k] = *(const bf16x8_t*)(xa + i * kLine + 128 + 8 * k);
+    }
+    float s0 = val(sc_c, 2 * i), s1 = val(sc_x, 2 * i + 1);   // read, then select
+    s0 = v ? s0 : 0.f;
+    s1 = v ? s1 : 0.f;
+    const float cz0 = -(128.f + val(zr_c, 2 * i)) * s0;
+    const float cz1 = -(128.f + val(zr_x, 2 * i + 1)) * s1;
+    const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
+    u32x4_t gA, gB;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      gA[d] = lo8 ? w0[d] : w1[d];
+      gB[d] = lo8 ? w1[d] : w0[d];
+    }
+    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      acc0 = mfma16x16x32(A0[k], unpack_nib8_bf16(gA[k], magic), acc0);
+      acc1 = mfma16x16x32(A1[k], unpack_nib8_bf16(gB[k], magic), acc1);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      y0[r] = fmaf(cz0, xs0[r], y0[r]);
+      y1[r] = fmaf(cz1, xs1[r], y1[r]);
+      y0[r] = fmaf(s0, acc0[r], y0[r]);
+      y1[r] = fmaf(s1, acc1[r], y1[r]);
+    }
+  }
+  // lane (c, ar) holds rows m = 4*ar + r of output column row0 + c (group 2i+1 of row c came
+  // from lane c ^ 8)
+  float* pbase = a.part + (size_t)split * M * a.N + row0 + c;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float v = y0[r] + row_swap8(y1[r]);
+    const int m = 4 * ar + r;
+    if (tile_ok && m < M && c <= rlast) pbase[(size_t)m * a.N] = v;
+  }
+}
+
+// y[m, n] = bf16(sum over splits s of part[s][m][n]), summed in split order; 4 columns per thread
+// (N % 4 == 0: one 16-byte load per split). The loads of up to 16 splits are issued before any is
+// consumed: the partials were just written by another kernel and sit in the memory-side cache.
+__global__ __launch_bounds__(256) void splitk_rows_reduce_kernel(const float* __restrict__ part, int splits,
+                                                                 int M, int N, uint16_t* __restrict__ y,
+                                                                 int64_t sym) {
+  const int n4 = N / 4;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= M * n4) return;
+  const int m = t / n4;
+  const int n = 4 * (t - m * n4);
+  const size_t sstride = (size_t)M * N;
+  const float* src = part + (size_t)m * N + n;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < splits; s0 += 16) {
+    f32x4_t v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int sp = s0 + j < splits ? s0 + j : splits - 1;
+      v[j] = *(const f32x4_t*)(src + sp * sstride);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (s0 + j < splits) acc += v[j];
+  }
+  u32x2_t o;
+  o[0] = cvt_pk_bf16(acc[0], acc[1]);
+  o[1] = cvt_pk_bf16(acc[2], acc[3]);
+  *(u32x2_t*)(y + (int64_t)m * sym + n) = o;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1212,10 +1426,88 @@ int line_w4(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
   return IMQ_ERR_UNSUPPORTED;
 }
 
+// K-split kernel plan (4 < M <= 16, G == 128, K_pad a multiple of 256, unit group strides, same
+// scale / zero dtype, N % 4 == 0 for the vector reduction; restated by the CPU bounds model in the
+// tests): S2 = 4 line-steps (1024 codes) per split, NW = 8 or 4 row tiles per workgroup. Returns
+// false when the kernel does not take the call.
+constexpr int kKsS2 = 4;
+bool ksplit_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
+                 int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int cus, int* splitso,
+                 int* nwo, size_t* ldso) {
+  if (M <= 4 || M > 16 || G != 128 || Kpad % kLine != 0 || Kpad <= 0 || sdt != zdt) return false;
+  if (N % 4 != 0 || sxm % 8 != 0) return false;
+  if (ssg != 1 || szg != 1 || N < 1 || N > (1 << 30) || Kpad > (1 << 28)) return false;
+  const int vb = sdt == IMQ_DT_FP32 ? 4 : 2;
+  if ((ssn * vb) % 4 != 0 || (szn * vb) % 4 != 0) return false;
+  if (16 * sqn >= (int64_t(1) << 31) || M * sxm * 2 >= (int64_t(1) << 31)) return false;
+  if (16 * ssn * vb >= (int64_t(1) << 31) || 16 * szn * vb >= (int64_t(1) << 31)) return false;
+  const int64_t splits = (Kpad / kLine + kKsS2 - 1) / kKsS2;
+  // 8 row tiles per workgroup (half the activation staging per weight byte) while that still
+  // yields two workgroups per CU, else 4
+  const int nw = splits * ((N + 127) / 128) >= 2 * (int64_t)cus ? 8 : 4;
+  const int64_t rbs = (N + 16 * nw - 1) / (16 * nw);
+  if (splits * rbs > 0x7fffffff) return false;
+  const size_t lds = (size_t)ksplit_lds((int)M, kKsS2, nw, vb);
+  if (lds > (size_t)max_lds) return false;
+  *splitso = (int)splits;
+  *nwo = nw;
+  *ldso = lds;
+  return true;
+}
+
+// Workspace bytes of the K-split decode path for this shape (0: the shape does not use it).
+int64_t ksplit_workspace_bytes(int64_t M, int64_t N, int64_t Kpad) {
+  if (M <= 4 || M > 16 || N <= 0 || Kpad <= 0 || Kpad % kLine != 0) return 0;
+  return (Kpad / kLine + kKsS2 - 1) / kKsS2 * M * N * 4;
+}
+
+template <int SDT, int NW>
+int ksplit_launch(const SkinnyArgs& a, int splits, size_t lds, hipStream_t st) {
+  const int rbs = (a.N + 16 * NW - 1) / (16 * NW);
+  const dim3 g((unsigned)(splits * rbs)), b(64 * NW);
+  int rc;
+  if (a.M <= 8) rc = launch_with_lds(w4_ksplit_kernel<kKsS2, 8, SDT, NW>, g, b, lds, st, a);
+  else rc = launch_with_lds(w4_ksplit_kernel<kKsS2, 16, SDT, NW>, g, b, lds, st, a);
+  if (rc != IMQ_OK) return rc;
+  const int n4 = a.N / 4;
+  splitk_rows_reduce_kernel<<<dim3((unsigned)((a.M * n4 + 255) / 256)), dim3(256), 0, st>>>(a.part, splits, a.M,
+                                                                                           a.N, a.y, a.sym);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+int ksplit_w4(const SkinnyArgs& a0, int sdt, void* ws, int64_t wsb, const DevInfo& di, hipStream_t st) {
+  int splits, nw;
+  size_t lds;
+  if (!ksplit_plan(a0.M, a0.Kpad, a0.G, a0.N, a0.sqn, a0.sxm, a0.ssn, a0.ssg, a0.szn, a0.szg, sdt, sdt,
+                   di.max_lds, di.cus, &splits, &nw, &lds))
+    return IMQ_ERR_UNSUPPORTED;
+  const int64_t need = (int64_t)splits * a0.M * a0.N * 4;
+  if (!ws || wsb < need || ((uintptr_t)ws & 15)) return IMQ_ERR_UNSUPPORTED;
+  if (((uintptr_t)a0.y & 7) || (a0.sym & 3)) return IMQ_ERR_UNSUPPORTED;   // 8-byte y stores
+  SkinnyArgs a = a0;
+  a.part = (float*)ws;
+  if (nw == 8) {
+    switch (sdt) {
+      case IMQ_DT_BF16: return ksplit_launch<IMQ_DT_BF16, 8>(a, splits, lds, st);
+      case IMQ_DT_FP16: return ksplit_launch<IMQ_DT_FP16, 8>(a, splits, lds, st);
+      case IMQ_DT_FP32: return ksplit_launch<IMQ_DT_FP32, 8>(a, splits, lds, st);
+    }
+  } else {
+    switch (sdt) {
+      case IMQ_DT_BF16: return ksplit_launch<IMQ_DT_BF16, 4>(a, splits, lds, st);
+      case IMQ_DT_FP16: return ksplit_launch<IMQ_DT_FP16, 4>(a, splits, lds, st);
+      case IMQ_DT_FP32: return ksplit_launch<IMQ_DT_FP32, 4>(a, splits, lds, st);
+    }
+  }
+  return IMQ_ERR_UNSUPPORTED;
+}
+
 // Fast path eligibility + launch. Returns IMQ_ERR_UNSUPPORTED when the caller must fall back.
+// ws / wsb: the caller's optional workspace (the K-split path of 4 < M <= 16 needs one).
 int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st) {
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
   if (M < 1 || M > 16 || G % kStep != 0 || Kpad % G != 0 || Kpad <= 0) return IMQ_ERR_UNSUPPORTED;
   if (((G / kStep) & (G / kStep - 1)) != 0) return IMQ_ERR_UNSUPPORTED;   // groups of 2^k steps
   if (((uintptr_t)q & 15) || (sqn & 15) || ((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
@@ -1224,7 +1516,9 @@ int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
   const DevInfo di = device_info();
   SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, 0};
   if (((uintptr_t)sc & 3) == 0 && ((uintptr_t)zr & 3) == 0) {
-    const int rc = line_w4(a, sdt, di, st);
+    int rc = line_w4(a, sdt, di, st);
+    if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+    rc = ksplit_w4(a, sdt, ws, wsb, di, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }
   switch (sdt) {

@@ -7,7 +7,8 @@
 namespace imq {
 int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st);
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
+int64_t ksplit_workspace_bytes(int64_t M, int64_t N, int64_t Kpad);
 int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
               int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st);
@@ -45,7 +46,9 @@ extern "C" int imq_abi_version(void) { return IMQ_ABI_VERSION; }
 
 extern "C" int64_t imq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K_pad) {
   if (M < 0 || N < 0 || K_pad <= 0) return -1;
-  return imq::gemm_workspace_bytes(M, N, K_pad);
+  const int64_t g = imq::gemm_workspace_bytes(M, N, K_pad);
+  const int64_t d = imq::ksplit_workspace_bytes(M, N, K_pad);
+  return g > d ? g : d;
 }
 
 extern "C" const char* imq_strerror(int status) {
@@ -75,7 +78,8 @@ extern "C" int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int
   const uint8_t* q = (const uint8_t*)qweight;
   if (M <= 16) {
     rc = imq::skinny_w4(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g, s_dtype,
-                        zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
+                        zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, workspace,
+                        workspace_bytes, st);
   } else {
     rc = imq::gemm_wq(4, xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
                       s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride,

@@ -263,8 +263,9 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
 #pragma unroll
     for (int i = 0; i < S2; ++i) {
       const bool v = ls0 + i < KL;
-      s0[t][i] = v ? val(t, 0, c, 2 * i) : 0.f;
-      s1[t][i] = v ? val(t, 0, c ^ 8, 2 * i + 1) : 0.f;
+      const float r0 = val(t, 0, c, 2 * i), r1 = val(t, 0, c ^ 8, 2 * i + 1);   // read, then select
+      s0[t][i] = v ? r0 : 0.f;
+      s1[t][i] = v ? r1 : 0.f;
       cz0[t][i] = -(128.f + val(t, 1, c, 2 * i)) * s0[t][i];
       cz1[t][i] = -(128.f + val(t, 1, c ^ 8, 2 * i + 1)) * s1[t][i];
     }

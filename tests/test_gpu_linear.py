@@ -154,6 +154,52 @@ def test_linear_w4_line_kernel_scale_dtypes_dealias(dev, sdt, M):
     _linear_check(dev, c, M, seed=M, view_pad=64)
 
 
+@pytest.mark.parametrize("N,K", [(36, 768), (100, 1280), (20, 256), (4096, 14336), (6144, 4096), (28672, 4096)])
+@pytest.mark.parametrize("M", [5, 8, 9, 16])
+def test_linear_w4_ksplit_shapes(dev, N, K, M):
+    """Decode rows 4 < M <= 16 take the K-split kernel (workspace from ops): a partial last row
+    block (N % 64), splits with unused line-steps (K 768, 1280), Llama down_proj K 14336 (14
+    splits), gate_up (8-tile workgroups), both activation-row instantiations (M <= 8, <= 16)."""
+    from infinitemodel_amd import _lib
+    assert _lib.lib().imq_linear_workspace_bytes(M, N, K) == -(-K // 1024) * M * N * 4
+    c = C.int4_case(N, K, 128, seed=N + K + M)
+    _linear_check(dev, c, M, seed=M)
+
+
+@pytest.mark.parametrize("sdt", ["fp16", "fp32"])
+def test_linear_w4_ksplit_scale_dtypes_dealias(dev, sdt):
+    """The K-split kernel's fp16 / fp32 scale-zero words and the +64-byte de-alias row view."""
+    c = dict(C.int4_case(96, 1280, 128, seed=6))
+    c["s"] = oq.round_to(c["s"], sdt)
+    c["z"] = oq.round_to(c["z"], sdt)
+    c["dt"] = sdt
+    c["Wd"] = oq.dequant_int4(c["q"], c["s"], c["z"], c["in_f"], 128, "bf16")
+    for M in (6, 16):
+        _linear_check(dev, c, M, seed=M, view_pad=64)
+
+
+def test_linear_w4_ksplit_without_workspace_matches(dev):
+    """Without a workspace the C ABI takes the skinny kernel for 4 < M <= 16; both paths agree
+    within fp32 accumulation order, and repeated K-split calls are bit-identical."""
+    import torch
+    from infinitemodel_amd import _lib, ops
+    N, K, M = 512, 2048, 12
+    c = C.int4_case(N, K, 128, seed=3)
+    q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev), C.to_torch(c["z"], "bf16", dev)
+    x = C.to_torch(C.bf16_normal(C.rng(4), (M, K)), "bf16", dev)
+    y1 = ops.linear_w4(x, q, 128, (s, z))
+    y2 = torch.empty_like(y1)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    rc = _lib.lib().imq_linear_w4(x.data_ptr(), K, M, K, q.data_ptr(), q.stride(0), s.data_ptr(), s.stride(0), 1,
+                                  0, z.data_ptr(), z.stride(0), 1, 0, N, 128, y2.data_ptr(), N, None, 0, st)
+    assert rc == 0
+    torch.cuda.synchronize()
+    d = (y1.float() - y2.float()).abs().max().item()
+    assert d <= 2 ** -7 * y1.float().abs().max().item()
+    for _ in range(3):
+        assert torch.equal(ops.linear_w4(x, q, 128, (s, z)), y1)
+
+
 def test_linear_w4_in_features_not_multiple_of_group(dev):
     c = C.int4_case(80, 300, 128, seed=11)     # K_pad = 384, x zero-padded past 300
     for M in (1, 3, 16):

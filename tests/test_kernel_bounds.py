@@ -417,6 +417,154 @@ def test_line_model_catches_wrong_scale_index():
 
 
 
+
+# ---- int4 K-split decode kernel (csrc/gemv.hip w4_ksplit_kernel / ksplit_plan) -----------------
+KS_S2 = 4
+
+
+def ksplit_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024, cus=256):
+    """ksplit_plan in csrc/gemv.hip: (splits, NW, LDS bytes) or None when the K-split kernel
+    declines."""
+    if not (4 < M <= 16) or G != 128 or Kpad % LINE or Kpad <= 0 or N < 1:
+        return None
+    if N % 4 or sxm % 8 or (ssn * vb) % 4:
+        return None
+    if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31 or 16 * ssn * vb >= 2 ** 31:
+        return None
+    splits = -(-(Kpad // LINE) // KS_S2)
+    nw = 8 if splits * -(-N // 128) >= 2 * cus else 4
+    lds = M * (KS_S2 * LINE + 8) * 2 + 2 * KS_S2 * 16 * 4 + nw * 2 * 16 * (KS_S2 * vb // 2) * 4
+    if lds > max_lds:
+        return None
+    return splits, nw, lds
+
+
+def ksplit_ranges(M, Kpad, N, sqn, sxm, ssn, vb):
+    """Max exclusive offsets the K-split kernel reads (qweight bytes, scale bytes, x elements) and
+    writes (partials, LDS x elements / xs floats / s-z dwords), per the kernel's index arithmetic
+    and clamps, over the first and last split and row block; plus the set of (split, m, n) partial
+    elements written over every workgroup."""
+    splits, NW, _ = ksplit_plan(M, Kpad, 128, N, sqn, sxm, ssn, vb)
+    S2 = KS_S2
+    MC = 8 if M <= 8 else 16
+    NT = 64 * NW
+    KL = Kpad // LINE
+    RB = -(-N // (16 * NW))
+    DPR = S2 * vb // 2
+    ngd = Kpad // 128 * vb // 4
+    XB = 32 * S2
+    XU = -(-(MC * XB) // NT)
+    xrow = S2 * LINE + 8
+    r = dict(q=0, s=0, x=0, part=0, lds_x=0, lds_xs=0, lds_sz=0, lds_xa=0)
+    written = set()
+    for split in range(splits):
+        ls0 = split * S2
+        xlim = Kpad - ls0 * LINE - 8
+        for rb in range(RB):
+            full = split in (0, splits - 1) and rb in (0, RB - 1)
+            if full:
+                xtot = M * XB
+                for t in range(NT):
+                    for u in range(XU):
+                        idx = min(t + NT * u, xtot - 1)
+                        m, b = divmod(idx, XB)
+                        kb = min(8 * b, xlim)
+                        assert kb >= 0
+                        r["x"] = max(r["x"], ls0 * LINE + m * sxm + kb + 8)
+                        if t + NT * u < xtot:
+                            r["lds_x"] = max(r["lds_x"], m * xrow + 8 * b + 8)
+                            if b % 16 == 0:
+                                r["lds_xs"] = max(r["lds_xs"], (b >> 4) * 16 + m + 1)
+            for wave in range(NW):
+                row0 = (rb * NW + wave) * 16
+                tile_ok = row0 < N
+                rowa = row0 if tile_ok else 0
+                rlast = N - 1 - rowa
+                assert rlast >= 0
+                if full:
+                    for d in range(32 * DPR):
+                        arr, rem = divmod(d, 16 * DPR)
+                        rr, dw = divmod(rem, DPR)
+                        rr = min(rr, rlast)
+                        gd = min(ls0 * (vb // 2) + dw, ngd - 1)
+                        r["s"] = max(r["s"], (rowa + rr) * ssn * vb + 4 * gd + 4)
+                        r["lds_sz"] = max(r["lds_sz"], wave * 2 * 16 * DPR + d + 1)
+                    for c in range(16):
+                        for ar in range(4):
+                            lo8 = c < 8
+                            rr0 = min(c & 7, rlast)
+                            rr1 = min(8 + (c & 7), rlast)
+                            mrow = c if c < M else M - 1
+                            for i in range(S2):
+                                l = min(ls0 + i, KL - 1)
+                                r["q"] = max(r["q"], (rowa + rr0) * sqn + 16 * ar + (0 if lo8 else 64) + 128 * l + 16)
+                                r["q"] = max(r["q"], (rowa + rr1) * sqn + 16 * ar + (64 if lo8 else 0) + 128 * l + 16)
+                                r["lds_xa"] = max(r["lds_xa"], mrow * xrow + 32 * ar + i * LINE + 128 + 8 * 3 + 8)
+                for c in range(16):
+                    for ar in range(4):
+                        for rr in range(4):
+                            m = 4 * ar + rr
+                            if tile_ok and m < M and c <= rlast:
+                                off = split * M * N + m * N + row0 + c
+                                r["part"] = max(r["part"], off + 1)
+                                written.add(off)
+    return splits, r, written
+
+
+KS_SHAPES = [(4096, 4096), (6144, 4096), (28672, 4096), (4096, 14336), (36, 768), (100, 1280), (20, 256),
+             (80, 512)]
+
+
+@pytest.mark.parametrize("N,K", KS_SHAPES)
+@pytest.mark.parametrize("M", [5, 8, 9, 16])
+@pytest.mark.parametrize("vb", [2, 4])
+@pytest.mark.parametrize("pad", [0, 64])
+def test_ksplit_in_bounds_and_covering(N, K, M, vb, pad):
+    """Every K-split read lies inside its operand, every LDS access inside the launch's dynamic
+    LDS, the partials stay inside the workspace the host sizes (splits * M * N fp32), and the
+    kernel writes every partial element the reduction reads."""
+    Kpad = K
+    ng = Kpad // 128
+    sqn = Kpad // 2 + pad
+    plan = ksplit_plan(M, Kpad, 128, N, sqn, Kpad, ng, vb)
+    assert plan is not None
+    splits, nw, lds = plan
+    if N == 28672:
+        assert nw == 8
+    assert splits * KS_S2 * LINE >= Kpad and (splits - 1) * KS_S2 * LINE < Kpad
+    _, r, written = ksplit_ranges(M, Kpad, N, sqn, Kpad, ng, vb)
+    assert r["q"] <= (N - 1) * sqn + Kpad // 2
+    assert r["s"] <= N * ng * vb
+    assert r["x"] <= (M - 1) * Kpad + Kpad
+    assert r["part"] <= splits * M * N
+    assert len(written) == splits * M * N            # complete: the reduction reads no stale value
+    xrow = KS_S2 * LINE + 8
+    x_bytes = M * xrow * 2
+    assert r["lds_x"] * 2 <= x_bytes and r["lds_xa"] * 2 <= x_bytes
+    assert r["lds_xs"] <= 2 * KS_S2 * 16
+    sz_off = x_bytes + 2 * KS_S2 * 16 * 4
+    assert sz_off + r["lds_sz"] * 4 <= lds
+
+
+def test_ksplit_plan_declines():
+    assert ksplit_plan(4, 4096, 128, 4096, 2048, 4096, 32, 2) is None     # M <= 4: line kernel
+    assert ksplit_plan(17, 4096, 128, 4096, 2048, 4096, 32, 2) is None    # prefill rows
+    assert ksplit_plan(8, 4096, 64, 4096, 2048, 4096, 64, 2) is None      # G != 128
+    assert ksplit_plan(8, 384, 128, 36, 192, 384, 3, 2) is None           # K_pad % 256
+    assert ksplit_plan(8, 512, 128, 37, 256, 512, 4, 2) is None           # N % 4 (vector reduction)
+    assert ksplit_plan(16, 14336, 128, 4096, 7168, 14336, 112, 2) is not None
+
+
+def test_ksplit_model_catches_missing_row_clamp():
+    """Negative control: without the idle-wave clamp (rowa = row0 for every wave), a partial last
+    row block would address rows past N."""
+    N, K, M = 100, 1024, 8
+    _, NW, _ = ksplit_plan(M, K, 128, N, K // 2, K, K // 128, 2)
+    RB = -(-N // (16 * NW))
+    row0 = ((RB - 1) * NW + NW - 1) * 16
+    assert row0 >= N and N - 1 - row0 < 0
+
+
 @pytest.mark.parametrize("M,N,K", [(40, 256, 2048), (300, 512, 4096), (512, 4096, 14336), (150, 1000, 8192),
                                    (512, 14336, 4096), (2048, 4096, 14336), (17, 64, 256)])
 def test_gemm_split_k_ranges(M, N, K):
