@@ -1057,6 +1057,211 @@ __global__ __launch_bounds__(64 * MAXW) void w2_skinny_kernel(SkinnyArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// int2 decode line kernel (M <= 4, G = 64): the int4 line kernel's structure for 2-bit codes.
+// A line-step is 128 bytes of a row = 512 codes = 8 groups. One workgroup owns a 16-row tile and
+// all of K; W waves split K in S2 line-steps each and issue all of their loads up front:
+//   * two 16-byte loads per line-step, each covering 8 rows x a whole 128-byte line: lane (c, ar)
+//     gets group ar of row c (gA) and group 4 + ar of row c ^ 8 (gB), one group per dword set;
+//   * a 4x4 cross-lane transpose (transpose4_lanerows) turns that into dword ar of each of the
+//     four groups, so each MFMA pair's 64 K positions lie inside one group and the group's scale
+//     and zero apply to its accumulator exactly: y += s*acc - s*(128 + z)*sum(x);
+//   * activations of the wave's K range are staged in the wave's LDS (permute_x16 order) with
+//     per-group row sums; scale / zero words of the 16 rows likewise.
+// Rows c ^ 8 of gB are folded back with a row swap, partials reduce across waves in LDS.
+// ---------------------------------------------------------------------------------------------
+constexpr int kLine2 = 512;   // codes per int2 line-step (128 bytes of a row, 8 groups of 64)
+
+IMQ_HOST_DEV inline int line2_wave_lds(int M, int S2, int vb) {
+  return M * (S2 * kLine2 + 8) * 2 + S2 * 8 * 16 * 4 + 2 * 16 * (S2 * 8 * vb / 4) * 4;
+}
+
+template <int S2, int MC, int SDT, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;   // bytes per scale / zero value
+  constexpr int GPL = 8;                              // groups per line-step
+  constexpr int DPR = S2 * GPL * VB / 4;              // scale dwords per row per array
+  constexpr int RC = MC < 4 ? MC : 4;                 // D registers that can hold a real row
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int c = lane & 15, ar = lane >> 4;
+  const bool lo8 = c < 8;
+  const int M = a.M;
+  const int KL = a.Kpad / kLine2;
+  const int ls0 = wave * S2;
+  const int row0 = blockIdx.x * 16;
+  const int rlast = a.N - 1 - row0;
+
+  const int xrow = S2 * kLine2 + 8;
+  const int wbytes = line2_wave_lds(M, S2, VB);
+  unsigned char* wl = smem + (size_t)wave * wbytes;
+  uint16_t* xw = (uint16_t*)wl;                       // [M][xrow], permute_x16 order
+  float* xs = (float*)(wl + M * xrow * 2);           // [S2 * 8 groups][16 rows]
+  uint32_t* szl = (uint32_t*)(xs + S2 * GPL * 16);   // [2 arrays][16 rows][DPR]
+  float* red = (float*)(smem + (size_t)W * wbytes);
+
+  // 1) x: M rows x S2*32 pairs of 16 elements (two 16-byte loads each), clamped into the row
+  constexpr int XP = 32 * S2;
+  constexpr int XU = (MC * XP + 63) / 64;
+  const int xtot = M * XP;
+  const uint16_t* xbase = a.x + (int64_t)ls0 * kLine2;
+  const int plim = a.Kpad - ls0 * kLine2 - 16;       // last valid pair start in the range
+  u32x4_t xlo[XU], xhi[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    int idx = lane + 64 * u;
+    idx = idx < xtot ? idx : xtot - 1;
+    const int m = idx / XP, p = idx - m * XP;
+    int kb = 16 * p;
+    kb = kb < plim ? kb : plim;
+    const uint16_t* src = xbase + m * (int)a.sxm + kb;
+    xlo[u] = *(const u32x4_t*)src;
+    xhi[u] = *(const u32x4_t*)(src + 8);
+  }
+  // 2) scale / zero words of groups [8*ls0, 8*ls0 + 8*S2): 2 arrays x 16 rows x DPR dwords
+  constexpr int ZU = (32 * DPR + 63) / 64;
+  const int ngd = a.Kpad / 64 * VB / 4;              // dwords per row holding real groups
+  const unsigned char* sbase = (const unsigned char*)a.sc + (int64_t)row0 * a.ssn * VB;
+  const unsigned char* zbase = (const unsigned char*)a.zr + (int64_t)row0 * a.szn * VB;
+  uint32_t zv[ZU];
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    int d = lane + 64 * u;
+    d = d < 32 * DPR ? d : 32 * DPR - 1;
+    const int arr = d / (16 * DPR);
+    const int rem = d - arr * (16 * DPR);
+    int r = rem / DPR;
+    const int dw = rem - r * DPR;
+    r = r < rlast ? r : rlast;
+    int gd = ls0 * (GPL * VB / 4) + dw;
+    gd = gd < ngd ? gd : ngd - 1;
+    const unsigned char* p = arr ? zbase + r * (int)a.szn * VB : sbase + r * (int)a.ssn * VB;
+    zv[u] = *(const uint32_t*)(p + 4 * gd);
+  }
+  // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
+  const uint8_t* qt = a.q + (int64_t)row0 * a.sqn;
+  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
+  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
+  const uint8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
+  const uint8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  u32x4_t wb[2 * S2];
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    int l = ls0 + i;
+    l = l < KL ? l : KL - 1;
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+  }
+  // 4) stage x (permute_x16 per pair) with per-group sums, and scale / zero words
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int idx = lane + 64 * u;
+    const bool ok = idx < xtot;
+    const int m = (ok ? idx : 0) / XP, p = (ok ? idx : 0) - m * XP;
+    float sum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      sum += __uint_as_float(xlo[u][d] << 16) + __uint_as_float(xlo[u][d] & 0xffff0000u);
+      sum += __uint_as_float(xhi[u][d] << 16) + __uint_as_float(xhi[u][d] & 0xffff0000u);
+    }
+    // the 4 pairs of one group are 4 consecutive idx (XP is a multiple of 4)
+    sum += __shfl_xor(sum, 1, 4);
+    sum += __shfl_xor(sum, 2, 4);
+    if (ok) {
+      u32x4_t o0, o1;
+      permute_x16(xlo[u], xhi[u], o0, o1);
+      *(u32x4_t*)(xw + m * xrow + 16 * p) = o0;
+      *(u32x4_t*)(xw + m * xrow + 16 * p + 8) = o1;
+      if ((p & 3) == 0) xs[(p >> 2) * 16 + m] = sum;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    const int d = lane + 64 * u;
+    if (d < 32 * DPR) szl[d] = zv[u];
+  }
+  // LDS is written and read by this wave only; its LDS operations execute in order
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+  const uint32_t magic = magic_bf16_128x2();
+  const uint16_t* xa = xw + (c < M ? c : M - 1) * xrow + 16 * ar;
+  const uint32_t* sc_c = szl + c * DPR;
+  const uint32_t* sc_x = szl + (c ^ 8) * DPR;
+  const uint32_t* zr_c = szl + 16 * DPR + c * DPR;
+  const uint32_t* zr_x = szl + 16 * DPR + (c ^ 8) * DPR;
+  auto val = [&](const uint32_t* p, int g) -> float {   // group g (0 .. 8*S2) of a staged row
+    if constexpr (VB == 4) return round_bf16_hw(__uint_as_float(p[g]));
+    else return raw_to_bf16_f32<SDT>((g & 1) ? (p[g >> 1] >> 16) : (p[g >> 1] & 0xffffu));
+  };
+  auto xsum = [&](int g) -> f32x4_t {                   // sums of D rows 4*ar .. 4*ar + RC - 1
+    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+    const float* p = xs + g * 16 + 4 * ar;
+    if constexpr (RC == 1) v[0] = p[0];
+    else if constexpr (RC == 2) {
+      const f32x2_t t = *(const f32x2_t*)p;
+      v[0] = t[0];
+      v[1] = t[1];
+    } else v = *(const f32x4_t*)p;
+    return v;
+  };
+  float y0[4] = {0.f, 0.f, 0.f, 0.f}, y1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    const bool v = ls0 + i < KL;
+    const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
+    uint32_t dA[4], dB[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      dA[d] = lo8 ? w0[d] : w1[d];
+      dB[d] = lo8 ? w1[d] : w0[d];
+    }
+    transpose4_lanerows(dA);      // dA[k]: dword ar of group k of row c
+    transpose4_lanerows(dB);      // dB[k]: dword ar of group 4 + k of row c ^ 8
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int gA = GPL * i + k, gB = GPL * i + 4 + k;
+      const f32x4_t xsA = xsum(gA), xsB = xsum(gB);
+      const bf16x8_t a0 = *(const bf16x8_t*)(xa + 64 * gA);
+      const bf16x8_t a1 = *(const bf16x8_t*)(xa + 64 * gA + 8);
+      const bf16x8_t b0 = *(const bf16x8_t*)(xa + 64 * gB);
+      const bf16x8_t b1 = *(const bf16x8_t*)(xa + 64 * gB + 8);
+      float sA = val(sc_c, gA), sB = val(sc_x, gB);   // read, then select
+      sA = v ? sA : 0.f;
+      sB = v ? sB : 0.f;
+      const float czA = -(128.f + val(zr_c, gA)) * sA;
+      const float czB = -(128.f + val(zr_x, gB)) * sB;
+      f32x4_t accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
+      accA = mfma16x16x32(a0, unpack_crumb8_bf16(dA[k], 0, magic), accA);
+      accB = mfma16x16x32(b0, unpack_crumb8_bf16(dB[k], 0, magic), accB);
+      accA = mfma16x16x32(a1, unpack_crumb8_bf16(dA[k], 1, magic), accA);
+      accB = mfma16x16x32(b1, unpack_crumb8_bf16(dB[k], 1, magic), accB);
+#pragma unroll
+      for (int r = 0; r < RC; ++r) {
+        y0[r] = fmaf(czA, xsA[r], y0[r]);
+        y1[r] = fmaf(czB, xsB[r], y1[r]);
+        y0[r] = fmaf(sA, accA[r], y0[r]);
+        y1[r] = fmaf(sB, accB[r], y1[r]);
+      }
+    }
+  }
+  // D row m = 4*ar + r; rows m < M <= 4 live in lanes ar == 0
+  float* rb = red + wave * (RC * 16);
+#pragma unroll
+  for (int r = 0; r < RC; ++r) {
+    const float vv = y0[r] + row_swap8(y1[r]);
+    if (ar == 0) rb[r * 16 + c] = vv;
+  }
+  lds_barrier();
+  for (int e = threadIdx.x; e < 16 * M; e += blockDim.x) {
+    const int m = e >> 4, n = e & 15;
+    float sum = 0.f;
+    for (int w = 0; w < W; ++w) sum += red[w * (RC * 16) + m * 16 + n];
+    if (n <= rlast) a.y[(int64_t)m * a.sym + row0 + n] = (uint16_t)f32_to_bf16_bits(sum);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // int8 per-row decode kernel (M <= 16). A K-step is 64 codes: 64 bytes of each row, one 16-byte
 // load per lane (lane row jl takes codes [16*jl, 16*jl+16)), feeding two MFMAs whose operands
 // are (q + 128) as bf16 -- exact: q ^ 0x80 is q + 128 in 0..255, 8 significant bits -- against
@@ -1635,6 +1840,53 @@ int w2_dispatch(const SkinnyArgs& a, const DevInfo& di, hipStream_t st) {
   return w2_dispatch_s<16, SDT, ZDT>(a, di, st);
 }
 
+// int2 line kernel plan (M <= 2, G == 64, K_pad a multiple of 512, unit group strides, same
+// scale / zero dtype; restated by the CPU bounds model in the tests): S2 = 4 line-steps per wave
+// at M == 1 (K_pad <= 32768), S2 = 2 at M == 2 (K_pad <= 16384). Larger M or K would hold more
+// activation registers across the weight issue than the 16-wave budget of 128 VGPRs allows; they
+// take the skinny kernel. Returns false when the line kernel does not take the call.
+bool line2_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
+                int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int* S2o, int* Wo,
+                size_t* ldso) {
+  if (M < 1 || M > 2 || G != 64 || Kpad % kLine2 != 0 || sdt != zdt) return false;
+  if (ssg != 1 || szg != 1 || N < 1) return false;
+  const int vb = sdt == IMQ_DT_FP32 ? 4 : 2;
+  if ((ssn * vb) % 4 != 0 || (szn * vb) % 4 != 0) return false;
+  if (16 * sqn >= (int64_t(1) << 31) || M * sxm * 2 >= (int64_t(1) << 31)) return false;
+  if (16 * ssn * vb >= (int64_t(1) << 31) || 16 * szn * vb >= (int64_t(1) << 31)) return false;
+  const int64_t KL = Kpad / kLine2;
+  const int S2 = M == 1 ? 4 : 2;
+  const int64_t W = (KL + S2 - 1) / S2;
+  if (W > 16) return false;
+  const size_t lds = (size_t)W * line2_wave_lds((int)M, S2, vb) + (size_t)W * M * 16 * 4;
+  if (lds > (size_t)max_lds) return false;
+  *S2o = S2;
+  *Wo = (int)W;
+  *ldso = lds;
+  return true;
+}
+
+template <int SDT>
+int line2_launch(const SkinnyArgs& a, int W, size_t lds, hipStream_t st) {
+  const dim3 g((unsigned)((a.N + 15) / 16)), b(64 * W);
+  if (a.M == 1) return launch_with_lds(w2_line_kernel<4, 1, SDT, 16>, g, b, lds, st, a);
+  return launch_with_lds(w2_line_kernel<2, 2, SDT, 16>, g, b, lds, st, a);
+}
+
+int line_w2(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
+  int S2, W;
+  size_t lds;
+  if (!line2_plan(a.M, a.Kpad, a.G, a.N, a.sqn, a.sxm, a.ssn, a.ssg, a.szn, a.szg, sdt, sdt, di.max_lds, &S2, &W,
+                  &lds))
+    return IMQ_ERR_UNSUPPORTED;
+  switch (sdt) {
+    case IMQ_DT_BF16: return line2_launch<IMQ_DT_BF16>(a, W, lds, st);
+    case IMQ_DT_FP16: return line2_launch<IMQ_DT_FP16>(a, W, lds, st);
+    case IMQ_DT_FP32: return line2_launch<IMQ_DT_FP32>(a, W, lds, st);
+  }
+  return IMQ_ERR_UNSUPPORTED;
+}
+
 int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
               int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st) {
@@ -1646,6 +1898,10 @@ int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
   if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
   const DevInfo di = device_info();
   SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, 0};
+  if (((uintptr_t)sc & 3) == 0 && ((uintptr_t)zr & 3) == 0) {
+    const int rc = line_w2(a, sdt, di, st);
+    if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+  }
   switch (sdt) {
     case IMQ_DT_BF16: return w2_dispatch<IMQ_DT_BF16, IMQ_DT_BF16>(a, di, st);
     case IMQ_DT_FP16: return w2_dispatch<IMQ_DT_FP16, IMQ_DT_FP16>(a, di, st);

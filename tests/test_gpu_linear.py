@@ -286,6 +286,24 @@ def test_linear_w2_large_k_chunked(dev, M):
     _linear_check(dev, c, M, seed=M, bits=2)
 
 
+@pytest.mark.parametrize("N,K", [(36, 512), (100, 1536), (512, 8192), (272, 28672), (1792, 2048)])
+@pytest.mark.parametrize("M", [1, 2])
+def test_linear_w2_line_kernel_shapes(dev, N, K, M):
+    """Decode shapes of the int2 line kernel (M <= 2, G 64, K_pad % 512 == 0): a ragged last tile,
+    waves with unused line-steps (K 1536 = 3 line-steps), C3's K 8192 and 28672 (the largest K
+    at M = 1 uses 14 waves; at M = 2 it exceeds the kernel's K range and takes the skinny kernel)."""
+    c = dict(C.int2_random_case(N, K, 64, seed=2100 + N + M, dt="fp16"))
+    _linear_check(dev, c, M, seed=M, bits=2)
+
+
+@pytest.mark.parametrize("sdt", ["bf16", "fp32"])
+def test_linear_w2_line_kernel_scale_dtypes_dealias(dev, sdt):
+    """The int2 line kernel's bf16 / fp32 scale-zero words and the +64-byte de-alias row view."""
+    c = dict(C.int2_random_case(80, 2048, 64, seed=2200, dt=sdt))
+    for M in (1, 2):
+        _linear_check(dev, c, M, seed=M, bits=2, view_pad=64)
+
+
 def test_linear_w2_fp32_scales(dev):
     c = dict(C.int2_random_case(160, 4096, 64, seed=2004, dt="fp32"))
     for M in (1, 3):

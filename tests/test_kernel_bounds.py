@@ -565,6 +565,115 @@ def test_ksplit_model_catches_missing_row_clamp():
     assert row0 >= N and N - 1 - row0 < 0
 
 
+
+# ---- int2 line kernel (csrc/gemv.hip w2_line_kernel / line2_plan) -----------------------------
+LINE2 = 512
+
+
+def line2_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024):
+    """line2_plan in csrc/gemv.hip: (S2, W, LDS bytes) or None when the int2 line kernel declines."""
+    if not (1 <= M <= 2) or G != 64 or Kpad % LINE2 or N < 1:
+        return None
+    if (ssn * vb) % 4:
+        return None
+    if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31 or 16 * ssn * vb >= 2 ** 31:
+        return None
+    KL = Kpad // LINE2
+    S2 = 4 if M == 1 else 2
+    W = -(-KL // S2)
+    if W > 16:
+        return None
+    wave_lds = M * (S2 * LINE2 + 8) * 2 + S2 * 8 * 16 * 4 + 2 * 16 * (S2 * 8 * vb // 4) * 4
+    lds = W * wave_lds + W * M * 16 * 4
+    if lds > max_lds:
+        return None
+    return S2, W, lds
+
+
+def line2_ranges(M, Kpad, N, sqn, sxm, ssn, vb, S2, W):
+    """Max exclusive offsets the int2 line kernel reads from qweight (bytes), scale (bytes) and x
+    (elements) and the LDS bytes its wave areas touch, from its per-lane arithmetic and clamps."""
+    KL = Kpad // LINE2
+    GPL = 8
+    DPR = S2 * GPL * vb // 4
+    ngd = Kpad // 64 * vb // 4
+    XP = 32 * S2
+    xrow = S2 * LINE2 + 8
+    wave_lds = M * xrow * 2 + S2 * GPL * 16 * 4 + 2 * 16 * DPR * 4
+    r = dict(q=0, s=0, x=0, lds=0)
+    NT = -(-N // 16)
+    for tile in sorted({0, NT - 1}):
+        row0 = tile * 16
+        rlast = N - 1 - row0
+        for wave in range(W):
+            ls0 = wave * S2
+            base = wave * wave_lds
+            plim = Kpad - ls0 * LINE2 - 16
+            for idx in range(M * XP):
+                m, p = divmod(idx, XP)
+                kb = min(16 * p, plim)
+                assert kb >= 0
+                r["x"] = max(r["x"], ls0 * LINE2 + m * sxm + kb + 16)
+                r["lds"] = max(r["lds"], base + (m * xrow + 16 * p + 16) * 2)
+                if p % 4 == 0:
+                    r["lds"] = max(r["lds"], base + M * xrow * 2 + ((p >> 2) * 16 + m + 1) * 4)
+            for d in range(32 * DPR):
+                arr, rem = divmod(d, 16 * DPR)
+                rr, dw = divmod(rem, DPR)
+                rr = min(rr, rlast)
+                gd = min(ls0 * (GPL * vb // 4) + dw, ngd - 1)
+                r["s"] = max(r["s"], (row0 + rr) * ssn * vb + 4 * gd + 4)
+                r["lds"] = max(r["lds"], base + M * xrow * 2 + S2 * GPL * 16 * 4 + (d + 1) * 4)
+            for c in range(16):
+                lo8 = c < 8
+                rr0 = min(c & 7, rlast)
+                rr1 = min(8 + (c & 7), rlast)
+                mrow = c if c < M else M - 1
+                for ar in range(4):
+                    for i in range(S2):
+                        l = min(ls0 + i, KL - 1)
+                        r["q"] = max(r["q"], (row0 + rr0) * sqn + 16 * ar + (0 if lo8 else 64) + 128 * l + 16)
+                        r["q"] = max(r["q"], (row0 + rr1) * sqn + 16 * ar + (64 if lo8 else 0) + 128 * l + 16)
+                        for k in range(8):        # A reads: groups gA = 8i + k (k < 4), gB = 8i + 4 + k
+                            g = GPL * i + k
+                            r["lds"] = max(r["lds"], base + (mrow * xrow + 16 * ar + 64 * g + 16) * 2)
+                            r["lds"] = max(r["lds"], base + M * xrow * 2 + (g * 16 + 4 * ar + M) * 4)
+    return r
+
+
+LINE2_SHAPES = [(28672, 8192), (8192, 28672), (36, 512), (100, 1536), (17, 1024), (64, 16384)]
+
+
+@pytest.mark.parametrize("N,K", LINE2_SHAPES)
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("vb", [2, 4])
+@pytest.mark.parametrize("pad", [0, 64])
+def test_line2_reads_in_bounds(N, K, M, vb, pad):
+    Kpad = K
+    ng = Kpad // 64
+    sqn = Kpad // 4 + pad
+    plan = line2_plan(M, Kpad, 64, N, sqn, Kpad, ng, vb)
+    if M == 2 and Kpad > 16384:
+        assert plan is None            # M = 2 with K_pad > 16384 takes the skinny kernel
+        return
+    assert plan is not None
+    S2, W, lds = plan
+    assert W * S2 * LINE2 >= Kpad and (W - 1) * S2 * LINE2 < Kpad
+    r = line2_ranges(M, Kpad, N, sqn, Kpad, ng, vb, S2, W)
+    assert r["q"] <= (N - 1) * sqn + Kpad // 4
+    assert r["s"] <= N * ng * vb
+    assert r["x"] <= (M - 1) * Kpad + Kpad
+    assert r["lds"] <= lds - W * M * 16 * 4          # wave areas end where the reduction area starts
+
+
+def test_line2_plan_declines():
+    assert line2_plan(3, 4096, 64, 4096, 1024, 4096, 64, 2) is None      # M > 2
+    assert line2_plan(1, 4096, 128, 4096, 1024, 4096, 32, 2) is None     # G != 64
+    assert line2_plan(1, 448, 64, 96, 112, 448, 7, 2) is None            # K_pad % 512
+    assert line2_plan(1, 33280, 64, 64, 8320, 33280, 520, 2) is None     # W > 16
+    assert line2_plan(1, 32768, 64, 64, 8192, 32768, 512, 2) is not None
+
+
 @pytest.mark.parametrize("M,N,K", [(40, 256, 2048), (300, 512, 4096), (512, 4096, 14336), (150, 1000, 8192),
                                    (512, 14336, 4096), (2048, 4096, 14336), (17, 64, 256)])
 def test_gemm_split_k_ranges(M, N, K):
