@@ -460,7 +460,7 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
   const int W = blockDim.x >> 6;
   const int c = lane & 15, ar = lane >> 4;
   const bool lo8 = c < 8;
-  const int M = a.M;
+  const int M = MC <= 2 ? MC : a.M;                 // MC 1 and 2 launch exactly that M
   const int KL = a.Kpad / kLine;
   const int ls0 = wave * S2;
   const int row0 = blockIdx.x * 16;
@@ -1087,7 +1087,7 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
   const int W = blockDim.x >> 6;
   const int c = lane & 15, ar = lane >> 4;
   const bool lo8 = c < 8;
-  const int M = a.M;
+  const int M = MC <= 2 ? MC : a.M;                 // MC 1 and 2 launch exactly that M
   const int KL = a.Kpad / kLine2;
   const int ls0 = wave * S2;
   const int row0 = blockIdx.x * 16;
