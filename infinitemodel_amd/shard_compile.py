@@ -114,6 +114,37 @@ def _sha256_file(path: str) -> str:
     return h.hexdigest()
 
 
+_ROUTER_LEAF = frozenset({"gate", "router", "wg"})   # == worker_quant._ROUTER_LEAF_NAMES
+
+
+def quant_scope(model) -> tuple:
+    """(linear2d_names, expert3d_names): the exact weights a cold load quantizes, from the model
+    skeleton (shard_compile.py:367-419 without the config loading): every nn.Linear ``.weight``
+    inside a decoder layer except routers (a *Router / *Gate ancestor, or a leaf named gate /
+    router / wg), and every fused 3D ``.experts.*.gate_up_proj`` / ``down_proj``. Names are the
+    model's own parameter names."""
+    from torch import nn
+    by_name = dict(model.named_modules())
+
+    def under_router(nm: str) -> bool:
+        parts = nm.split(".")
+        for i in range(1, len(parts)):
+            anc = by_name.get(".".join(parts[:i]))
+            if anc is not None and type(anc).__name__.endswith(("Router", "Gate")):
+                return True
+        return False
+
+    lin2d, exp3d = set(), set()
+    for name, mod in model.named_modules():
+        if (isinstance(mod, nn.Linear) and ".layers." in name and not under_router(name)
+                and name.rsplit(".", 1)[-1] not in _ROUTER_LEAF):
+            lin2d.add(name + ".weight")
+    for name, p in model.named_parameters():
+        if p.dim() == 3 and ".experts." in name and (name.endswith(".gate_up_proj") or name.endswith(".down_proj")):
+            exp3d.add(name)
+    return lin2d, exp3d
+
+
 def pack_unit_tensors(raw: dict, lin2d: Optional[set] = None, quant: str = "int4",
                       group_size: int = INT4_GROUP):
     """Pack one unit's tensors (logical 'model.*' names) into the cache dict + manifest fragments,
