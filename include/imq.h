@@ -62,6 +62,24 @@ int imq_dequant_w8(const void* qweight, int64_t q_row_stride, const void* scale,
                    int s_dtype, int64_t N, int64_t K, void* out, int64_t out_row_stride, int out_dtype,
                    void* stream);
 
+/* ---- RTN packers on the device, bit-identical to the host packers -------------------------------
+ * pack_linear_int4 / pack_linear_int2 (shard_compile.py:50-94, == worker_quant.py:1588-1608 /
+ * 1921-1944): W [N, in_features] (w_dtype: bf16 / fp16 / fp32, row stride in elements) ->
+ * qweight u8 [N, K_pad * bits / 8] (row stride in bytes), scale and zero [N, ng] in w_dtype (row
+ * stride sz_row_stride elements, groups contiguous). K_pad = ng * group_size; group_size 64, 128
+ * or 256. fp32 min / max over each zero-padded group, IEEE division, round-half-even. */
+int imq_pack_w4(const void* W, int64_t w_row_stride, int w_dtype, int64_t N, int64_t in_features,
+                int64_t group_size, void* qweight, int64_t q_row_stride, void* scale, void* zero,
+                int64_t sz_row_stride, void* stream);
+int imq_pack_w2(const void* W, int64_t w_row_stride, int w_dtype, int64_t N, int64_t in_features,
+                int64_t group_size, void* qweight, int64_t q_row_stride, void* scale, void* zero,
+                int64_t sz_row_stride, void* stream);
+
+/* pack_linear_int8 (shard_compile.py:170-178, == worker_quant.py:511-536): per-row symmetric in
+ * W's own dtype; qweight int8 [N, K], scale [N, 1] in w_dtype. */
+int imq_pack_w8(const void* W, int64_t w_row_stride, int w_dtype, int64_t N, int64_t K, void* qweight,
+                int64_t q_row_stride, void* scale, int64_t s_stride_n, void* stream);
+
 /* ---- fused dequant linear: y[M, N] = x[M, K_pad] @ dequant(W)^T, fp32 accumulate, bf16 out ---
  * Replaces the op returned by _w4a16_triton_op() (worker_quant.py:1079-1225: `_ksk` M==1 split-K
  * GEMV, `_k` M>1 tl.dot GEMM), called as op(x[M,Kpad] bf16, qweight, group, (scale, zero)).

@@ -35,6 +35,11 @@ SIGNATURES = {
                                 _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_int, _c_vp]),
     "imq_dequant_w8": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_int,
                                 _c_vp]),
+    "imq_pack_w4": (_c_int, [_c_vp, _c_i64, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp,
+                             _c_i64, _c_vp]),
+    "imq_pack_w2": (_c_int, [_c_vp, _c_i64, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp,
+                             _c_i64, _c_vp]),
+    "imq_pack_w8": (_c_int, [_c_vp, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
     "imq_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "imq_linear_w4": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_int,
                                _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,

@@ -107,6 +107,55 @@ def dequant_w8(qweight, scale, dtype):
 
 
 # ---------------------------------------------------------------------------------------------
+# RTN packers on the device (bit-identical to shard_compile.pack_linear_int4 / int2 / int8)
+# ---------------------------------------------------------------------------------------------
+def _pack_g(fn: str, bits: int, W, group_size: int):
+    dev = _check_dev(W)
+    if W.dim() != 2 or W.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"W must be a 2D bf16 / fp16 / fp32 tensor, got {W.dtype} {tuple(W.shape)}")
+    if W.stride(1) != 1:
+        W = W.contiguous()
+    N, in_f = W.shape
+    ng = -(-in_f // group_size)
+    q = torch.empty((N, ng * group_size * bits // 8), dtype=torch.uint8, device=dev)
+    scale = torch.empty((N, ng), dtype=W.dtype, device=dev)
+    zero = torch.empty((N, ng), dtype=W.dtype, device=dev)
+    with torch.cuda.device(dev):
+        call(fn, _ptr(W), W.stride(0), dtype_code(W.dtype), N, in_f, group_size, _ptr(q), q.stride(0),
+             _ptr(scale), _ptr(zero), scale.stride(0), _stream(dev))
+    return q, scale, zero, in_f
+
+
+def pack_w4(W, group_size: int = 128):
+    """``pack_linear_int4`` on the device: (qweight u8 [N, K_pad/2], scale, zero, in_features)
+    (shard_compile.py:74-94)."""
+    return _pack_g("imq_pack_w4", 4, W, group_size)
+
+
+def pack_w2(W, group_size: int = 64):
+    """``pack_linear_int2`` on the device: (qweight u8 [N, K_pad/4], scale, zero, in_features)
+    (shard_compile.py:50-71)."""
+    return _pack_g("imq_pack_w2", 2, W, group_size)
+
+
+def pack_w8(W):
+    """``pack_linear_int8`` on the device: (qweight int8 [N, K], scale [N, 1] in W's dtype)
+    (shard_compile.py:170-178)."""
+    dev = _check_dev(W)
+    if W.dim() != 2 or W.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"W must be a 2D bf16 / fp16 / fp32 tensor, got {W.dtype} {tuple(W.shape)}")
+    if W.stride(1) != 1:
+        W = W.contiguous()
+    N, K = W.shape
+    q = torch.empty((N, K), dtype=torch.int8, device=dev)
+    scale = torch.empty((N, 1), dtype=W.dtype, device=dev)
+    with torch.cuda.device(dev):
+        call("imq_pack_w8", _ptr(W), W.stride(0), dtype_code(W.dtype), N, K, _ptr(q), q.stride(0), _ptr(scale),
+             scale.stride(0), _stream(dev))
+    return q, scale
+
+
+# ---------------------------------------------------------------------------------------------
 # fused dequant linears
 # ---------------------------------------------------------------------------------------------
 def _linear_g(fn: str, codes_per_byte: int, x, qweight, group_size: int, sz, out=None):

@@ -56,8 +56,22 @@ def _rtn(W, G: int, qmax: int):
     return q.reshape(out, in_pad), scale, zero, in_f
 
 
+def _device_packer(W, group_size: int):
+    """libimq's device packer for a weight on a ROCm device (bit-identical to the host packers
+    below; the torch expression stays the definition on other devices and group sizes)."""
+    if getattr(W, "is_cuda", False) and W.dim() == 2 and group_size in (64, 128, 256):
+        import torch
+        if getattr(torch.version, "hip", None) and W.dtype in (torch.bfloat16, torch.float16, torch.float32):
+            from . import ops
+            return ops
+    return None
+
+
 def pack_linear_int4(W, group_size: int = INT4_GROUP):
     """Returns (qweight u8 [out, in_pad/2], scale, zero, in_features) (shard_compile.py:74-94)."""
+    dev_ops = _device_packer(W, group_size)
+    if dev_ops is not None:
+        return dev_ops.pack_w4(W, group_size)
     q, scale, zero, in_f = _rtn(W, group_size, 15)
     qpacked = (q[:, 0::2] | (q[:, 1::2] << 4)).contiguous()
     return qpacked, scale.to(W.dtype), zero.to(W.dtype), in_f
@@ -65,6 +79,9 @@ def pack_linear_int4(W, group_size: int = INT4_GROUP):
 
 def pack_linear_int2(W, group_size: int = INT2_GROUP):
     """Returns (qweight u8 [out, in_pad/4], scale, zero, in_features) (shard_compile.py:50-71)."""
+    dev_ops = _device_packer(W, group_size)
+    if dev_ops is not None:
+        return dev_ops.pack_w2(W, group_size)
     q, scale, zero, in_f = _rtn(W, group_size, 3)
     qpacked = (q[:, 0::4] | (q[:, 1::4] << 2) | (q[:, 2::4] << 4) | (q[:, 3::4] << 6)).contiguous()
     return qpacked, scale.to(W.dtype), zero.to(W.dtype), in_f
@@ -94,6 +111,9 @@ def pack_linear_int8(W):
     """Per-row symmetric int8 in W's own dtype (shard_compile.py:170-178): returns
     (qweight int8 [out, in], scale [out, 1])."""
     import torch
+    dev_ops = _device_packer(W, 128)
+    if dev_ops is not None:
+        return dev_ops.pack_w8(W)
     scale = (W.abs().amax(dim=1, keepdim=True) / 127.0).clamp(min=1e-8)
     qW = (W / scale).round().clamp(-127, 127).to(torch.int8).contiguous()
     return qW, scale.to(W.dtype)
