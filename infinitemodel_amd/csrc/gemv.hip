@@ -1071,8 +1071,69 @@ __global__ __launch_bounds__(64 * MAXW) void w2_skinny_kernel(SkinnyArgs a) {
 // ---------------------------------------------------------------------------------------------
 constexpr int kLine2 = 512;   // codes per int2 line-step (128 bytes of a row, 8 groups of 64)
 
-IMQ_HOST_DEV inline int line2_wave_lds(int M, int S2, int vb) {
-  return M * (S2 * kLine2 + 8) * 2 + S2 * 8 * 16 * 4 + 2 * 16 * (S2 * 8 * vb / 4) * 4;
+// Scale / zero of a wave's 16 rows over NGW groups, staged in LDS as float pairs
+// (s, -(128 + z) * s) with the bf16 rounding of s and z applied once per (row, group) instead of
+// in every lane that uses them; groups past K_pad are staged as (0, 0). Row stride 2 * NGW + 2
+// floats spreads the 16 rows over the LDS banks.
+IMQ_HOST_DEV constexpr int sz2_row(int ngw) { return 2 * ngw + 2; }
+IMQ_HOST_DEV constexpr int sz2_bytes(int ngw) { return 16 * sz2_row(ngw) * 4; }
+
+template <int SDT, int NGW>
+struct SzPairs {
+  static constexpr int VB = SDT == IMQ_DT_FP32 ? 4 : 2;
+  static constexpr int GPD = 4 / VB;                 // groups per dword
+  static constexpr int DPR = NGW / GPD;              // dwords per row
+  static constexpr int ZU = (16 * DPR + 63) / 64;    // dword pairs per lane
+  uint32_t sv[ZU], zv[ZU];
+
+  // rows [0, 16) of the tile (clamped to rlast), dwords gd0 .. gd0 + DPR (clamped below ngd)
+  IMQ_DEV void load(int lane, const unsigned char* sbase, const unsigned char* zbase, int ssnb, int sznb,
+                    int rlast, int gd0, int ngd) {
+#pragma unroll
+    for (int u = 0; u < ZU; ++u) {
+      int d = lane + 64 * u;
+      d = d < 16 * DPR ? d : 16 * DPR - 1;
+      int r = d / DPR;
+      const int dw = d - r * DPR;
+      r = r < rlast ? r : rlast;
+      int gd = gd0 + dw;
+      gd = gd < ngd ? gd : ngd - 1;
+      sv[u] = *(const uint32_t*)(sbase + r * ssnb + 4 * gd);
+      zv[u] = *(const uint32_t*)(zbase + r * sznb + 4 * gd);
+    }
+  }
+  // local groups >= gvalid lie past K_pad
+  IMQ_DEV void store(int lane, float* szf, int gvalid) const {
+#pragma unroll
+    for (int u = 0; u < ZU; ++u) {
+      const int d = lane + 64 * u;
+      if (d < 16 * DPR) {
+        const int r = d / DPR;
+        const int dw = d - r * DPR;
+#pragma unroll
+        for (int e = 0; e < GPD; ++e) {
+          const int g = dw * GPD + e;
+          float sc, zr;
+          if constexpr (VB == 4) {
+            sc = round_bf16_hw(__uint_as_float(sv[u]));
+            zr = round_bf16_hw(__uint_as_float(zv[u]));
+          } else {
+            sc = raw_to_bf16_f32<SDT>(e ? (sv[u] >> 16) : (sv[u] & 0xffffu));
+            zr = raw_to_bf16_f32<SDT>(e ? (zv[u] >> 16) : (zv[u] & 0xffffu));
+          }
+          sc = g < gvalid ? sc : 0.f;
+          f32x2_t v;
+          v[0] = sc;
+          v[1] = -(128.f + zr) * sc;
+          *(f32x2_t*)(szf + r * sz2_row(NGW) + 2 * g) = v;
+        }
+      }
+    }
+  }
+};
+
+IMQ_HOST_DEV inline int line2_wave_lds(int M, int S2) {
+  return M * (S2 * kLine2 + 8) * 2 + S2 * 8 * 16 * 4 + sz2_bytes(S2 * 8);
 }
 
 template <int S2, int MC, int SDT, int MAXW>
@@ -1080,7 +1141,7 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;   // bytes per scale / zero value
   constexpr int GPL = 8;                              // groups per line-step
-  constexpr int DPR = S2 * GPL * VB / 4;              // scale dwords per row per array
+  constexpr int NGW = S2 * GPL;                       // groups of the wave's K range
   constexpr int RC = MC < 4 ? MC : 4;                 // D registers that can hold a real row
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1094,11 +1155,11 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
   const int rlast = a.N - 1 - row0;
 
   const int xrow = S2 * kLine2 + 8;
-  const int wbytes = line2_wave_lds(M, S2, VB);
+  const int wbytes = line2_wave_lds(M, S2);
   unsigned char* wl = smem + (size_t)wave * wbytes;
   uint16_t* xw = (uint16_t*)wl;                       // [M][xrow], permute_x16 order
   float* xs = (float*)(wl + M * xrow * 2);           // [S2 * 8 groups][16 rows]
-  uint32_t* szl = (uint32_t*)(xs + S2 * GPL * 16);   // [2 arrays][16 rows][DPR]
+  float* szf = xs + NGW * 16;                         // [16 rows][sz2_row(NGW)]: (s, cz) pairs
   float* red = (float*)(smem + (size_t)W * wbytes);
 
   // 1) x: M rows x S2*32 pairs of 16 elements (two 16-byte loads each), clamped into the row
@@ -1119,26 +1180,11 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
     xlo[u] = *(const u32x4_t*)src;
     xhi[u] = *(const u32x4_t*)(src + 8);
   }
-  // 2) scale / zero words of groups [8*ls0, 8*ls0 + 8*S2): 2 arrays x 16 rows x DPR dwords
-  constexpr int ZU = (32 * DPR + 63) / 64;
-  const int ngd = a.Kpad / 64 * VB / 4;              // dwords per row holding real groups
-  const unsigned char* sbase = (const unsigned char*)a.sc + (int64_t)row0 * a.ssn * VB;
-  const unsigned char* zbase = (const unsigned char*)a.zr + (int64_t)row0 * a.szn * VB;
-  uint32_t zv[ZU];
-#pragma unroll
-  for (int u = 0; u < ZU; ++u) {
-    int d = lane + 64 * u;
-    d = d < 32 * DPR ? d : 32 * DPR - 1;
-    const int arr = d / (16 * DPR);
-    const int rem = d - arr * (16 * DPR);
-    int r = rem / DPR;
-    const int dw = rem - r * DPR;
-    r = r < rlast ? r : rlast;
-    int gd = ls0 * (GPL * VB / 4) + dw;
-    gd = gd < ngd ? gd : ngd - 1;
-    const unsigned char* p = arr ? zbase + r * (int)a.szn * VB : sbase + r * (int)a.ssn * VB;
-    zv[u] = *(const uint32_t*)(p + 4 * gd);
-  }
+  // 2) scale / zero words of groups [8*ls0, 8*ls0 + 8*S2) of the 16 rows
+  SzPairs<SDT, NGW> szp;
+  szp.load(lane, (const unsigned char*)a.sc + (int64_t)row0 * a.ssn * VB,
+           (const unsigned char*)a.zr + (int64_t)row0 * a.szn * VB, (int)a.ssn * VB, (int)a.szn * VB, rlast,
+           ls0 * (GPL * VB / 4), a.Kpad / 64 * VB / 4);
   // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
   const uint8_t* qt = a.q + (int64_t)row0 * a.sqn;
   const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
@@ -1176,24 +1222,14 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
       if ((p & 3) == 0) xs[(p >> 2) * 16 + m] = sum;
     }
   }
-#pragma unroll
-  for (int u = 0; u < ZU; ++u) {
-    const int d = lane + 64 * u;
-    if (d < 32 * DPR) szl[d] = zv[u];
-  }
+  szp.store(lane, szf, (KL - ls0) * GPL);
   // LDS is written and read by this wave only; its LDS operations execute in order
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
   const uint32_t magic = magic_bf16_128x2();
   const uint16_t* xa = xw + (c < M ? c : M - 1) * xrow + 16 * ar;
-  const uint32_t* sc_c = szl + c * DPR;
-  const uint32_t* sc_x = szl + (c ^ 8) * DPR;
-  const uint32_t* zr_c = szl + 16 * DPR + c * DPR;
-  const uint32_t* zr_x = szl + 16 * DPR + (c ^ 8) * DPR;
-  auto val = [&](const uint32_t* p, int g) -> float {   // group g (0 .. 8*S2) of a staged row
-    if constexpr (VB == 4) return round_bf16_hw(__uint_as_float(p[g]));
-    else return raw_to_bf16_f32<SDT>((g & 1) ? (p[g >> 1] >> 16) : (p[g >> 1] & 0xffffu));
-  };
+  const float* sz_c = szf + c * sz2_row(NGW);
+  const float* sz_x = szf + (c ^ 8) * sz2_row(NGW);
   auto xsum = [&](int g) -> f32x4_t {                   // sums of D rows 4*ar .. 4*ar + RC - 1
     f32x4_t v = {0.f, 0.f, 0.f, 0.f};
     const float* p = xs + g * 16 + 4 * ar;
@@ -1208,7 +1244,6 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
   float y0[4] = {0.f, 0.f, 0.f, 0.f}, y1[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
-    const bool v = ls0 + i < KL;
     const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
     uint32_t dA[4], dB[4];
 #pragma unroll
@@ -1226,11 +1261,9 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
       const bf16x8_t a1 = *(const bf16x8_t*)(xa + 64 * gA + 8);
       const bf16x8_t b0 = *(const bf16x8_t*)(xa + 64 * gB);
       const bf16x8_t b1 = *(const bf16x8_t*)(xa + 64 * gB + 8);
-      float sA = val(sc_c, gA), sB = val(sc_x, gB);   // read, then select
-      sA = v ? sA : 0.f;
-      sB = v ? sB : 0.f;
-      const float czA = -(128.f + val(zr_c, gA)) * sA;
-      const float czB = -(128.f + val(zr_x, gB)) * sB;
+      const f32x2_t pA = *(const f32x2_t*)(sz_c + 2 * gA);   // (s, -(128 + z) * s)
+      const f32x2_t pB = *(const f32x2_t*)(sz_x + 2 * gB);
+      const float sA = pA[0], czA = pA[1], sB = pB[0], czB = pB[1];
       f32x4_t accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
       accA = mfma16x16x32(a0, unpack_crumb8_bf16(dA[k], 0, magic), accA);
       accB = mfma16x16x32(b0, unpack_crumb8_bf16(dB[k], 0, magic), accB);
@@ -1258,6 +1291,159 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
     float sum = 0.f;
     for (int w = 0; w < W; ++w) sum += red[w * (RC * 16) + m * 16 + n];
     if (n <= rlast) a.y[(int64_t)m * a.sym + row0 + n] = (uint16_t)f32_to_bf16_bits(sum);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// int2 decode kernel for 4 < M <= 16 (G = 64): the int4 K-split structure with the int2 line-step
+// of the int2 line kernel. A workgroup owns NW row tiles and one split of S2 line-steps (S2 * 512
+// codes); the activation chunk x[0:M, split] is staged once in LDS (permute_x16 order, per-group
+// row sums) and shared by the waves; wave w streams rows [16 w, 16 w + 16) of the tile over the
+// split with two full-line loads per line-step and the cross-lane group transpose; the fp32
+// partials go to part[split][m][n] and splitk_rows_reduce_kernel sums the splits in order.
+// ---------------------------------------------------------------------------------------------
+IMQ_HOST_DEV inline int ksplit2_lds(int M, int S2, int NW) {
+  return M * (S2 * kLine2 + 8) * 2 + S2 * 8 * 16 * 4 + NW * sz2_bytes(S2 * 8);
+}
+
+template <int S2, int MC, int SDT, int NW>
+__global__ __launch_bounds__(64 * NW) void w2_ksplit_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
+  constexpr int GPL = 8;                              // groups per line-step
+  constexpr int NGW = S2 * GPL;                       // groups of the split
+  constexpr int NT = 64 * NW;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, ar = lane >> 4;
+  const bool lo8 = c < 8;
+  const int M = a.M;
+  const int KL = a.Kpad / kLine2;
+  const int RB = (a.N + 16 * NW - 1) / (16 * NW);
+  const int split = blockIdx.x / RB;
+  const int rb = blockIdx.x - split * RB;
+  const int ls0 = split * S2;
+  const int row0 = (rb * NW + wave) * 16;
+  const bool tile_ok = row0 < a.N;
+  const int rowa = tile_ok ? row0 : 0;
+  const int rlast = a.N - 1 - rowa;
+
+  const int xrow = S2 * kLine2 + 8;
+  uint16_t* xw = (uint16_t*)smem;                                      // [M][xrow]
+  float* xs = (float*)(smem + (size_t)M * xrow * 2);                   // [S2 * 8 groups][16 rows]
+  float* szf = xs + NGW * 16 + wave * (16 * sz2_row(NGW));             // this wave's (s, cz) pairs
+
+  // 1) x chunk: M rows x S2*32 pairs of 16 elements over the workgroup (clamped into the row)
+  constexpr int XP = 32 * S2;
+  constexpr int XU = (MC * XP + NT - 1) / NT;
+  const int xtot = M * XP;
+  const uint16_t* xbase = a.x + (int64_t)ls0 * kLine2;
+  const int plim = a.Kpad - ls0 * kLine2 - 16;
+  u32x4_t xlo[XU], xhi[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    int idx = threadIdx.x + NT * u;
+    idx = idx < xtot ? idx : xtot - 1;
+    const int m = idx / XP, p = idx - m * XP;
+    int kb = 16 * p;
+    kb = kb < plim ? kb : plim;
+    const uint16_t* src = xbase + m * (int)a.sxm + kb;
+    xlo[u] = *(const u32x4_t*)src;
+    xhi[u] = *(const u32x4_t*)(src + 8);
+  }
+  // 2) scale / zero words of this wave's 16 rows for groups [8*ls0, 8*ls0 + 8*S2)
+  SzPairs<SDT, NGW> szp;
+  szp.load(lane, (const unsigned char*)a.sc + (int64_t)rowa * a.ssn * VB,
+           (const unsigned char*)a.zr + (int64_t)rowa * a.szn * VB, (int)a.ssn * VB, (int)a.szn * VB, rlast,
+           ls0 * (GPL * VB / 4), a.Kpad / 64 * VB / 4);
+  // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
+  const uint8_t* qt = a.q + (int64_t)rowa * a.sqn;
+  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
+  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
+  const uint8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
+  const uint8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  u32x4_t wb[2 * S2];
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    int l = ls0 + i;
+    l = l < KL ? l : KL - 1;
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+  }
+  // 4) stage x (permute_x16 per pair) with per-group sums, and this wave's scale / zero words
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int idx = threadIdx.x + NT * u;
+    const bool ok = idx < xtot;
+    const int m = (ok ? idx : 0) / XP, p = (ok ? idx : 0) - m * XP;
+    float sum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      sum += __uint_as_float(xlo[u][d] << 16) + __uint_as_float(xlo[u][d] & 0xffff0000u);
+      sum += __uint_as_float(xhi[u][d] << 16) + __uint_as_float(xhi[u][d] & 0xffff0000u);
+    }
+    // the 4 pairs of one group are 4 consecutive idx (XP and NT are multiples of 4)
+    sum += __shfl_xor(sum, 1, 4);
+    sum += __shfl_xor(sum, 2, 4);
+    if (ok) {
+      u32x4_t o0, o1;
+      permute_x16(xlo[u], xhi[u], o0, o1);
+      *(u32x4_t*)(xw + m * xrow + 16 * p) = o0;
+      *(u32x4_t*)(xw + m * xrow + 16 * p + 8) = o1;
+      if ((p & 3) == 0) xs[(p >> 2) * 16 + m] = sum;
+    }
+  }
+  szp.store(lane, szf, (KL - ls0) * GPL);
+  lds_barrier();   // x and its sums are shared by the waves; weights stay in flight
+
+  const uint32_t magic = magic_bf16_128x2();
+  const uint16_t* xa = xw + (c < M ? c : M - 1) * xrow + 16 * ar;
+  const float* sz_c = szf + c * sz2_row(NGW);
+  const float* sz_x = szf + (c ^ 8) * sz2_row(NGW);
+  float y0[4] = {0.f, 0.f, 0.f, 0.f}, y1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
+    uint32_t dA[4], dB[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      dA[d] = lo8 ? w0[d] : w1[d];
+      dB[d] = lo8 ? w1[d] : w0[d];
+    }
+    transpose4_lanerows(dA);      // dA[k]: dword ar of group k of row c
+    transpose4_lanerows(dB);      // dB[k]: dword ar of group 4 + k of row c ^ 8
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int gA = GPL * i + k, gB = GPL * i + 4 + k;
+      const f32x4_t xsA = *(const f32x4_t*)(xs + gA * 16 + 4 * ar);
+      const f32x4_t xsB = *(const f32x4_t*)(xs + gB * 16 + 4 * ar);
+      const bf16x8_t a0 = *(const bf16x8_t*)(xa + 64 * gA);
+      const bf16x8_t a1 = *(const bf16x8_t*)(xa + 64 * gA + 8);
+      const bf16x8_t b0 = *(const bf16x8_t*)(xa + 64 * gB);
+      const bf16x8_t b1 = *(const bf16x8_t*)(xa + 64 * gB + 8);
+      const f32x2_t pA = *(const f32x2_t*)(sz_c + 2 * gA);   // (s, -(128 + z) * s)
+      const f32x2_t pB = *(const f32x2_t*)(sz_x + 2 * gB);
+      const float sA = pA[0], czA = pA[1], sB = pB[0], czB = pB[1];
+      f32x4_t accA = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
+      accA = mfma16x16x32(a0, unpack_crumb8_bf16(dA[k], 0, magic), accA);
+      accB = mfma16x16x32(b0, unpack_crumb8_bf16(dB[k], 0, magic), accB);
+      accA = mfma16x16x32(a1, unpack_crumb8_bf16(dA[k], 1, magic), accA);
+      accB = mfma16x16x32(b1, unpack_crumb8_bf16(dB[k], 1, magic), accB);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        y0[r] = fmaf(czA, xsA[r], y0[r]);
+        y1[r] = fmaf(czB, xsB[r], y1[r]);
+        y0[r] = fmaf(sA, accA[r], y0[r]);
+        y1[r] = fmaf(sB, accB[r], y1[r]);
+      }
+    }
+  }
+  float* pbase = a.part + (size_t)split * M * a.N + row0 + c;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float vv = y0[r] + row_swap8(y1[r]);
+    const int m = 4 * ar + r;
+    if (tile_ok && m < M && c <= rlast) pbase[(size_t)m * a.N] = vv;
   }
 }
 
@@ -1858,7 +2044,7 @@ bool line2_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int6
   const int S2 = M == 1 ? 4 : 2;
   const int64_t W = (KL + S2 - 1) / S2;
   if (W > 16) return false;
-  const size_t lds = (size_t)W * line2_wave_lds((int)M, S2, vb) + (size_t)W * M * 16 * 4;
+  const size_t lds = (size_t)W * line2_wave_lds((int)M, S2) + (size_t)W * M * 16 * 4;
   if (lds > (size_t)max_lds) return false;
   *S2o = S2;
   *Wo = (int)W;
@@ -1887,9 +2073,79 @@ int line_w2(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
   return IMQ_ERR_UNSUPPORTED;
 }
 
+// int2 K-split plan (4 < M <= 16, G == 64, K_pad a multiple of 512, N % 4 == 0, unit group strides,
+// same scale / zero dtype; restated by the CPU bounds model in the tests): S2 = 2 line-steps (1024
+// codes, the int4 K-split's split width) per split, NW = 8 row tiles when that still yields two
+// workgroups per CU, else 4.
+constexpr int kKs2S2 = 2;
+bool ksplit2_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
+                  int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int cus, int* splitso,
+                  int* nwo, size_t* ldso) {
+  if (M <= 4 || M > 16 || G != 64 || Kpad % kLine2 != 0 || Kpad <= 0 || sdt != zdt) return false;
+  if (N % 4 != 0 || sxm % 8 != 0 || ssg != 1 || szg != 1 || N < 1 || N > (1 << 30) || Kpad > (1 << 28))
+    return false;
+  const int vb = sdt == IMQ_DT_FP32 ? 4 : 2;
+  if ((ssn * vb) % 4 != 0 || (szn * vb) % 4 != 0) return false;
+  if (16 * sqn >= (int64_t(1) << 31) || M * sxm * 2 >= (int64_t(1) << 31)) return false;
+  if (16 * ssn * vb >= (int64_t(1) << 31) || 16 * szn * vb >= (int64_t(1) << 31)) return false;
+  const int64_t splits = (Kpad / kLine2 + kKs2S2 - 1) / kKs2S2;
+  const int nw = splits * ((N + 127) / 128) >= 2 * (int64_t)cus ? 8 : 4;
+  const int64_t rbs = (N + 16 * nw - 1) / (16 * nw);
+  if (splits * rbs > 0x7fffffff) return false;
+  const size_t lds = (size_t)ksplit2_lds((int)M, kKs2S2, nw);
+  if (lds > (size_t)max_lds) return false;
+  *splitso = (int)splits;
+  *nwo = nw;
+  *ldso = lds;
+  return true;
+}
+
+template <int SDT, int NW>
+int ksplit2_launch(const SkinnyArgs& a, int splits, size_t lds, hipStream_t st) {
+  const int rbs = (a.N + 16 * NW - 1) / (16 * NW);
+  const dim3 g((unsigned)(splits * rbs)), b(64 * NW);
+  int rc;
+  if (a.M <= 8) rc = launch_with_lds(w2_ksplit_kernel<kKs2S2, 8, SDT, NW>, g, b, lds, st, a);
+  else rc = launch_with_lds(w2_ksplit_kernel<kKs2S2, 16, SDT, NW>, g, b, lds, st, a);
+  if (rc != IMQ_OK) return rc;
+  const int n4 = a.N / 4;
+  splitk_rows_reduce_kernel<<<dim3((unsigned)((a.M * n4 + 255) / 256)), dim3(256), 0, st>>>(a.part, splits, a.M,
+                                                                                           a.N, a.y, a.sym);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+int ksplit_w2(const SkinnyArgs& a0, int sdt, void* ws, int64_t wsb, const DevInfo& di, hipStream_t st) {
+  int splits, nw;
+  size_t lds;
+  if (!ksplit2_plan(a0.M, a0.Kpad, a0.G, a0.N, a0.sqn, a0.sxm, a0.ssn, a0.ssg, a0.szn, a0.szg, sdt, sdt,
+                    di.max_lds, di.cus, &splits, &nw, &lds))
+    return IMQ_ERR_UNSUPPORTED;
+  const int64_t need = (int64_t)splits * a0.M * a0.N * 4;
+  if (!ws || wsb < need || ((uintptr_t)ws & 15)) return IMQ_ERR_UNSUPPORTED;
+  if (((uintptr_t)a0.y & 7) || (a0.sym & 3)) return IMQ_ERR_UNSUPPORTED;   // 8-byte y stores
+  SkinnyArgs a = a0;
+  a.part = (float*)ws;
+  if (nw == 8) {
+    switch (sdt) {
+      case IMQ_DT_BF16: return ksplit2_launch<IMQ_DT_BF16, 8>(a, splits, lds, st);
+      case IMQ_DT_FP16: return ksplit2_launch<IMQ_DT_FP16, 8>(a, splits, lds, st);
+      case IMQ_DT_FP32: return ksplit2_launch<IMQ_DT_FP32, 8>(a, splits, lds, st);
+    }
+  } else {
+    switch (sdt) {
+      case IMQ_DT_BF16: return ksplit2_launch<IMQ_DT_BF16, 4>(a, splits, lds, st);
+      case IMQ_DT_FP16: return ksplit2_launch<IMQ_DT_FP16, 4>(a, splits, lds, st);
+      case IMQ_DT_FP32: return ksplit2_launch<IMQ_DT_FP32, 4>(a, splits, lds, st);
+    }
+  }
+  return IMQ_ERR_UNSUPPORTED;
+}
+
+// ws / wsb: the caller's optional workspace (the K-split path of 4 < M <= 16 needs one).
 int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st) {
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
   if (M < 1 || M > 16 || G % kStep2 != 0 || Kpad % G != 0 || Kpad <= 0) return IMQ_ERR_UNSUPPORTED;
   if (((G / kStep2) & (G / kStep2 - 1)) != 0) return IMQ_ERR_UNSUPPORTED;   // groups of 2^k steps
   if (((uintptr_t)q & 15) || (sqn & 15) || ((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
@@ -1899,7 +2155,9 @@ int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
   const DevInfo di = device_info();
   SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, 0};
   if (((uintptr_t)sc & 3) == 0 && ((uintptr_t)zr & 3) == 0) {
-    const int rc = line_w2(a, sdt, di, st);
+    int rc = line_w2(a, sdt, di, st);
+    if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+    rc = ksplit_w2(a, sdt, ws, wsb, di, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }
   switch (sdt) {

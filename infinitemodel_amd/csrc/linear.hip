@@ -11,7 +11,7 @@ int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
 int64_t ksplit_workspace_bytes(int64_t M, int64_t N, int64_t Kpad);
 int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, hipStream_t st);
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
 int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st);
 int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
@@ -107,7 +107,8 @@ extern "C" int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int
   const uint8_t* q = (const uint8_t*)qweight;
   if (M <= 16) {
     rc = imq::skinny_w2(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g, s_dtype,
-                        zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, st);
+                        zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, workspace,
+                        workspace_bytes, st);
   } else {
     rc = imq::gemm_wq(2, xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
                       s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride,

@@ -304,6 +304,46 @@ def test_linear_w2_line_kernel_scale_dtypes_dealias(dev, sdt):
         _linear_check(dev, c, M, seed=M, bits=2, view_pad=64)
 
 
+@pytest.mark.parametrize("N,K", [(36, 512), (100, 1536), (20, 1024), (272, 28672), (1792, 2048), (512, 8192)])
+@pytest.mark.parametrize("M", [5, 8, 16])
+def test_linear_w2_ksplit_shapes(dev, N, K, M):
+    """Decode rows 4 < M <= 16 of int2 take the K-split kernel (workspace from ops): a partial last
+    row block, a split with an unused line-step (K 512, 1536), C3's K 8192 and 28672 (28 splits),
+    both activation-row instantiations (M <= 8, <= 16)."""
+    c = dict(C.int2_random_case(N, K, 64, seed=2300 + N + M, dt="fp16"))
+    _linear_check(dev, c, M, seed=M, bits=2)
+
+
+@pytest.mark.parametrize("sdt", ["bf16", "fp32"])
+def test_linear_w2_ksplit_scale_dtypes_dealias(dev, sdt):
+    """The int2 K-split kernel's bf16 / fp32 scale-zero words and the +64-byte de-alias row view."""
+    c = dict(C.int2_random_case(96, 2560, 64, seed=2400, dt=sdt))
+    for M in (6, 16):
+        _linear_check(dev, c, M, seed=M, bits=2, view_pad=64)
+
+
+def test_linear_w2_ksplit_without_workspace_matches(dev):
+    """Without a workspace the C ABI takes the skinny int2 kernel for 4 < M <= 16; both paths agree
+    within fp32 accumulation order, and repeated K-split calls are bit-identical."""
+    import torch
+    from infinitemodel_amd import _lib, ops
+    N, K, M = 512, 4096, 12
+    c = C.int2_random_case(N, K, 64, seed=5, dt="fp16")
+    q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "fp16", dev), C.to_torch(c["z"], "fp16", dev)
+    x = C.to_torch(C.bf16_normal(C.rng(4), (M, K)), "bf16", dev)
+    y1 = ops.linear_w2(x, q, 64, (s, z))
+    y2 = torch.empty_like(y1)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    rc = _lib.lib().imq_linear_w2(x.data_ptr(), K, M, K, q.data_ptr(), q.stride(0), s.data_ptr(), s.stride(0), 1,
+                                  1, z.data_ptr(), z.stride(0), 1, 1, N, 64, y2.data_ptr(), N, None, 0, st)
+    assert rc == 0
+    torch.cuda.synchronize()
+    d = (y1.float() - y2.float()).abs().max().item()
+    assert d <= 2 ** -7 * y1.float().abs().max().item()
+    for _ in range(3):
+        assert torch.equal(ops.linear_w2(x, q, 64, (s, z)), y1)
+
+
 def test_linear_w2_fp32_scales(dev):
     c = dict(C.int2_random_case(160, 4096, 64, seed=2004, dt="fp32"))
     for M in (1, 3):

@@ -534,7 +534,7 @@ def test_ksplit_in_bounds_and_covering(N, K, M, vb, pad):
     assert splits * KS_S2 * LINE >= Kpad and (splits - 1) * KS_S2 * LINE < Kpad
     _, r, written = ksplit_ranges(M, Kpad, N, sqn, Kpad, ng, vb)
     assert r["q"] <= (N - 1) * sqn + Kpad // 2
-    assert r["s"] <= N * ng * vb
+    assert r["s"] <= N * ng * vb and r["z"] <= N * ng * vb
     assert r["x"] <= (M - 1) * Kpad + Kpad
     assert r["part"] <= splits * M * N
     assert len(written) == splits * M * N            # complete: the reduction reads no stale value
@@ -570,6 +570,32 @@ def test_ksplit_model_catches_missing_row_clamp():
 LINE2 = 512
 
 
+def sz2_row(ngw):
+    """Row stride (floats) of the staged (s, -(128 + z) * s) pairs of NGW groups."""
+    return 2 * ngw + 2
+
+
+def sz2_bytes(ngw):
+    return 16 * sz2_row(ngw) * 4
+
+
+def sz2_ranges(r, lds_base, row0, rlast, ssn, szn, vb, ngw, gd0, ngd):
+    """SzPairs::load / store of csrc/gemv.hip: the scale and zero bytes read for 16 rows x NGW
+    groups (row clamp rlast, dword clamp ngd) and the LDS bytes the pairs occupy."""
+    GPD = 4 // vb
+    DPR = ngw // GPD
+    for d in range(16 * DPR):
+        rr, dw = divmod(d, DPR)
+        rc = min(rr, rlast)
+        gd = min(gd0 + dw, ngd - 1)
+        r["s"] = max(r["s"], (row0 + rc) * ssn * vb + 4 * gd + 4)
+        r["z"] = max(r["z"], (row0 + rc) * szn * vb + 4 * gd + 4)
+        for e in range(GPD):
+            g = dw * GPD + e
+            assert g < ngw
+            r["lds"] = max(r["lds"], lds_base + (rr * sz2_row(ngw) + 2 * g + 2) * 4)
+
+
 def line2_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024):
     """line2_plan in csrc/gemv.hip: (S2, W, LDS bytes) or None when the int2 line kernel declines."""
     if not (1 <= M <= 2) or G != 64 or Kpad % LINE2 or N < 1:
@@ -583,7 +609,7 @@ def line2_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024):
     W = -(-KL // S2)
     if W > 16:
         return None
-    wave_lds = M * (S2 * LINE2 + 8) * 2 + S2 * 8 * 16 * 4 + 2 * 16 * (S2 * 8 * vb // 4) * 4
+    wave_lds = M * (S2 * LINE2 + 8) * 2 + S2 * 8 * 16 * 4 + sz2_bytes(S2 * 8)
     lds = W * wave_lds + W * M * 16 * 4
     if lds > max_lds:
         return None
@@ -595,12 +621,13 @@ def line2_ranges(M, Kpad, N, sqn, sxm, ssn, vb, S2, W):
     (elements) and the LDS bytes its wave areas touch, from its per-lane arithmetic and clamps."""
     KL = Kpad // LINE2
     GPL = 8
-    DPR = S2 * GPL * vb // 4
+    NGW = S2 * GPL
     ngd = Kpad // 64 * vb // 4
     XP = 32 * S2
     xrow = S2 * LINE2 + 8
-    wave_lds = M * xrow * 2 + S2 * GPL * 16 * 4 + 2 * 16 * DPR * 4
-    r = dict(q=0, s=0, x=0, lds=0)
+    wave_lds = M * xrow * 2 + S2 * GPL * 16 * 4 + sz2_bytes(NGW)
+    szo = M * xrow * 2 + S2 * GPL * 16 * 4
+    r = dict(q=0, s=0, z=0, x=0, lds=0)
     NT = -(-N // 16)
     for tile in sorted({0, NT - 1}):
         row0 = tile * 16
@@ -617,13 +644,7 @@ def line2_ranges(M, Kpad, N, sqn, sxm, ssn, vb, S2, W):
                 r["lds"] = max(r["lds"], base + (m * xrow + 16 * p + 16) * 2)
                 if p % 4 == 0:
                     r["lds"] = max(r["lds"], base + M * xrow * 2 + ((p >> 2) * 16 + m + 1) * 4)
-            for d in range(32 * DPR):
-                arr, rem = divmod(d, 16 * DPR)
-                rr, dw = divmod(rem, DPR)
-                rr = min(rr, rlast)
-                gd = min(ls0 * (GPL * vb // 4) + dw, ngd - 1)
-                r["s"] = max(r["s"], (row0 + rr) * ssn * vb + 4 * gd + 4)
-                r["lds"] = max(r["lds"], base + M * xrow * 2 + S2 * GPL * 16 * 4 + (d + 1) * 4)
+            sz2_ranges(r, base + szo, row0, rlast, ssn, ssn, vb, NGW, ls0 * (GPL * vb // 4), ngd)
             for c in range(16):
                 lo8 = c < 8
                 rr0 = min(c & 7, rlast)
@@ -638,6 +659,8 @@ def line2_ranges(M, Kpad, N, sqn, sxm, ssn, vb, S2, W):
                             g = GPL * i + k
                             r["lds"] = max(r["lds"], base + (mrow * xrow + 16 * ar + 64 * g + 16) * 2)
                             r["lds"] = max(r["lds"], base + M * xrow * 2 + (g * 16 + 4 * ar + M) * 4)
+                            row = c if k < 4 else c ^ 8
+                            r["lds"] = max(r["lds"], base + szo + (row * sz2_row(NGW) + 2 * g + 2) * 4)
     return r
 
 
@@ -661,7 +684,7 @@ def test_line2_reads_in_bounds(N, K, M, vb, pad):
     assert W * S2 * LINE2 >= Kpad and (W - 1) * S2 * LINE2 < Kpad
     r = line2_ranges(M, Kpad, N, sqn, Kpad, ng, vb, S2, W)
     assert r["q"] <= (N - 1) * sqn + Kpad // 4
-    assert r["s"] <= N * ng * vb
+    assert r["s"] <= N * ng * vb and r["z"] <= N * ng * vb
     assert r["x"] <= (M - 1) * Kpad + Kpad
     assert r["lds"] <= lds - W * M * 16 * 4          # wave areas end where the reduction area starts
 
@@ -671,7 +694,137 @@ def test_line2_plan_declines():
     assert line2_plan(1, 4096, 128, 4096, 1024, 4096, 32, 2) is None     # G != 64
     assert line2_plan(1, 448, 64, 96, 112, 448, 7, 2) is None            # K_pad % 512
     assert line2_plan(1, 33280, 64, 64, 8320, 33280, 520, 2) is None     # W > 16
-    assert line2_plan(1, 32768, 64, 64, 8192, 32768, 512, 2) is not None
+    assert line2_plan(1, 32768, 64, 64, 8192, 32768, 512, 2) is None     # 16 waves exceed LDS
+    assert line2_plan(1, 30720, 64, 64, 7680, 30720, 480, 4) is not None
+
+
+# ---- int2 K-split decode kernel (csrc/gemv.hip w2_ksplit_kernel / ksplit2_plan) --------------
+KS2_S2 = 2
+
+
+def ksplit2_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024, cus=256):
+    """ksplit2_plan in csrc/gemv.hip: (splits, NW, LDS bytes) or None when it declines."""
+    if not (4 < M <= 16) or G != 64 or Kpad % LINE2 or Kpad <= 0 or N < 1:
+        return None
+    if N % 4 or sxm % 8 or (ssn * vb) % 4:
+        return None
+    if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31 or 16 * ssn * vb >= 2 ** 31:
+        return None
+    splits = -(-(Kpad // LINE2) // KS2_S2)
+    nw = 8 if splits * -(-N // 128) >= 2 * cus else 4
+    lds = M * (KS2_S2 * LINE2 + 8) * 2 + KS2_S2 * 8 * 16 * 4 + nw * sz2_bytes(KS2_S2 * 8)
+    if lds > max_lds:
+        return None
+    return splits, nw, lds
+
+
+def ksplit2_ranges(M, Kpad, N, sqn, sxm, ssn, vb):
+    """Max exclusive offsets the int2 K-split kernel reads and writes (qweight / scale bytes, x
+    elements, partials, LDS bytes), from its index arithmetic and clamps, over the first and last
+    split and row block; plus the set of partial elements written over every workgroup."""
+    splits, NW, _ = ksplit2_plan(M, Kpad, 64, N, sqn, sxm, ssn, vb)
+    S2, GPL = KS2_S2, 8
+    MC = 8 if M <= 8 else 16
+    NT = 64 * NW
+    KL = Kpad // LINE2
+    RB = -(-N // (16 * NW))
+    NGW = S2 * GPL
+    ngd = Kpad // 64 * vb // 4
+    XP = 32 * S2
+    XU = -(-(MC * XP) // NT)
+    xrow = S2 * LINE2 + 8
+    xs_off = M * xrow * 2
+    sz_off = xs_off + S2 * GPL * 16 * 4
+    r = dict(q=0, s=0, z=0, x=0, part=0, lds=0)
+    written = set()
+    for split in range(splits):
+        ls0 = split * S2
+        plim = Kpad - ls0 * LINE2 - 16
+        for rb in range(RB):
+            full = split in (0, splits - 1) and rb in (0, RB - 1)
+            if full:
+                xtot = M * XP
+                for t in range(NT):
+                    for u in range(XU):
+                        idx = min(t + NT * u, xtot - 1)
+                        m, p = divmod(idx, XP)
+                        kb = min(16 * p, plim)
+                        assert kb >= 0
+                        r["x"] = max(r["x"], ls0 * LINE2 + m * sxm + kb + 16)
+                        if t + NT * u < xtot:
+                            r["lds"] = max(r["lds"], (m * xrow + 16 * p + 16) * 2)
+                            if p % 4 == 0:
+                                r["lds"] = max(r["lds"], xs_off + ((p >> 2) * 16 + m + 1) * 4)
+            for wave in range(NW):
+                row0 = (rb * NW + wave) * 16
+                tile_ok = row0 < N
+                rowa = row0 if tile_ok else 0
+                rlast = N - 1 - rowa
+                assert rlast >= 0
+                if full:
+                    wbase = sz_off + wave * sz2_bytes(NGW)
+                    sz2_ranges(r, wbase, rowa, rlast, ssn, ssn, vb, NGW, ls0 * (GPL * vb // 4), ngd)
+                    for c in range(16):
+                        lo8 = c < 8
+                        rr0 = min(c & 7, rlast)
+                        rr1 = min(8 + (c & 7), rlast)
+                        mrow = c if c < M else M - 1
+                        for ar in range(4):
+                            for i in range(S2):
+                                l = min(ls0 + i, KL - 1)
+                                r["q"] = max(r["q"], (rowa + rr0) * sqn + 16 * ar + (0 if lo8 else 64) + 128 * l + 16)
+                                r["q"] = max(r["q"], (rowa + rr1) * sqn + 16 * ar + (64 if lo8 else 0) + 128 * l + 16)
+                                for k in range(8):
+                                    g = GPL * i + k
+                                    r["lds"] = max(r["lds"], (mrow * xrow + 16 * ar + 64 * g + 16) * 2)
+                                    r["lds"] = max(r["lds"], xs_off + (g * 16 + 4 * ar + 4) * 4)
+                                    row = c if k < 4 else c ^ 8
+                                    r["lds"] = max(r["lds"], wbase + (row * sz2_row(NGW) + 2 * g + 2) * 4)
+                for c in range(16):
+                    for ar in range(4):
+                        for rr in range(4):
+                            m = 4 * ar + rr
+                            if tile_ok and m < M and c <= rlast:
+                                off = split * M * N + m * N + row0 + c
+                                r["part"] = max(r["part"], off + 1)
+                                written.add(off)
+    return splits, r, written
+
+
+KS2_SHAPES = [(28672, 8192), (8192, 28672), (4096, 4096), (36, 512), (100, 1536), (20, 1024), (80, 2560)]
+
+
+@pytest.mark.parametrize("N,K", KS2_SHAPES)
+@pytest.mark.parametrize("M", [5, 8, 16])
+@pytest.mark.parametrize("vb", [2, 4])
+@pytest.mark.parametrize("pad", [0, 64])
+def test_ksplit2_in_bounds_and_covering(N, K, M, vb, pad):
+    """Every int2 K-split read lies inside its operand, every LDS access inside the launch's
+    dynamic LDS, the partials inside the workspace the host sizes (ceil(K_pad / 1024) * M * N fp32,
+    the int4 K-split's formula), and every partial the reduction reads is written."""
+    Kpad = K
+    ng = Kpad // 64
+    sqn = Kpad // 4 + pad
+    plan = ksplit2_plan(M, Kpad, 64, N, sqn, Kpad, ng, vb)
+    assert plan is not None
+    splits, nw, lds = plan
+    assert splits == -(-Kpad // 1024)
+    splits_, r, written = ksplit2_ranges(M, Kpad, N, sqn, Kpad, ng, vb)
+    assert r["q"] <= (N - 1) * sqn + Kpad // 4
+    assert r["s"] <= N * ng * vb
+    assert r["x"] <= (M - 1) * Kpad + Kpad
+    assert r["part"] <= splits * M * N
+    assert len(written) == splits * M * N
+    assert r["lds"] <= lds
+
+
+def test_ksplit2_plan_declines():
+    assert ksplit2_plan(4, 4096, 64, 4096, 1024, 4096, 64, 2) is None     # M <= 4
+    assert ksplit2_plan(17, 4096, 64, 4096, 1024, 4096, 64, 2) is None    # prefill rows
+    assert ksplit2_plan(8, 4096, 128, 4096, 1024, 4096, 32, 2) is None    # G != 64
+    assert ksplit2_plan(8, 768, 64, 36, 192, 768, 12, 2) is None          # K_pad % 512
+    assert ksplit2_plan(8, 512, 64, 37, 128, 512, 8, 2) is None           # N % 4
+    assert ksplit2_plan(16, 28672, 64, 8192, 7168, 28672, 448, 4) is not None
 
 
 @pytest.mark.parametrize("M,N,K", [(40, 256, 2048), (300, 512, 4096), (512, 4096, 14336), (150, 1000, 8192),
