@@ -534,7 +534,7 @@ def test_ksplit_in_bounds_and_covering(N, K, M, vb, pad):
     assert splits * KS_S2 * LINE >= Kpad and (splits - 1) * KS_S2 * LINE < Kpad
     _, r, written = ksplit_ranges(M, Kpad, N, sqn, Kpad, ng, vb)
     assert r["q"] <= (N - 1) * sqn + Kpad // 2
-    assert r["s"] <= N * ng * vb and r["z"] <= N * ng * vb
+    assert r["s"] <= N * ng * vb
     assert r["x"] <= (M - 1) * Kpad + Kpad
     assert r["part"] <= splits * M * N
     assert len(written) == splits * M * N            # complete: the reduction reads no stale value
@@ -811,7 +811,7 @@ def test_ksplit2_in_bounds_and_covering(N, K, M, vb, pad):
     assert splits == -(-Kpad // 1024)
     splits_, r, written = ksplit2_ranges(M, Kpad, N, sqn, Kpad, ng, vb)
     assert r["q"] <= (N - 1) * sqn + Kpad // 4
-    assert r["s"] <= N * ng * vb
+    assert r["s"] <= N * ng * vb and r["z"] <= N * ng * vb
     assert r["x"] <= (M - 1) * Kpad + Kpad
     assert r["part"] <= splits * M * N
     assert len(written) == splits * M * N
