@@ -26,11 +26,15 @@
 extern "C" {
 #endif
 
-#define IMQ_ABI_VERSION 2
+#define IMQ_ABI_VERSION 3
 
 #define IMQ_DT_BF16 0
 #define IMQ_DT_FP16 1
 #define IMQ_DT_FP32 2
+
+/* MoE expert activations (imq_moe_experts_w4_ex) */
+#define IMQ_ACT_SILU_GLU 0 /* gate_up rows [gate (I) | up (I)]: h = silu(gate) * up */
+#define IMQ_ACT_GPTOSS 1   /* rows interleaved (gate 2i, up 2i+1): gpt-oss clamped GLU */
 
 #define IMQ_OK 0
 #define IMQ_ERR_INVALID (-1)     /* bad shape / stride / dtype / null pointer */
@@ -145,6 +149,30 @@ int imq_moe_experts_w4(const void* hidden, int64_t h_row_stride, int64_t T, int6
                        const void* dn_s, const void* dn_z, int64_t dn_sz_stride_e, int64_t dn_sz_stride_n,
                        int sz_dtype, int64_t group_size, void* out, int64_t out_row_stride,
                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* imq_moe_experts_w4 generalized to the gpt-oss experts forward (_install_gptoss_fused_forward,
+ * worker_quant.py:2280-2314) and to kernel-layout row padding:
+ *   gu_K_pad / dn_K_pad: K of each projection as laid out in qweight / scale / zero -- a multiple
+ *     of group_size, >= H (resp. I), dn_K_pad <= I_pad rounded up to 256; codes and scales of
+ *     columns past in_features must be zero (a holder padded past the reference's K_pad).
+ *   gu_bias [E, 2I] / dn_bias [E, H] (expert stride, unit row stride, bias_dtype), or NULL: added
+ *     to the projection outputs before the activation / before the routing weight.
+ *   act IMQ_ACT_SILU_GLU (alpha, limit unused) or IMQ_ACT_GPTOSS: gate = y[2i] + b (<= limit),
+ *     up = y[2i+1] + b (clamped to [-limit, limit]), h = (up + 1) * gate * sigmoid(alpha * gate).
+ *   out[t] = sum_j w[t,j] * (down_e(h) + dn_bias[e]), e = topk_idx[t,j]. Same workspace as
+ *   imq_moe_experts_w4. gpt-oss experts are transpose-packed: gate_up [E, 2I, H_pad/2] with the
+ *   interleaved rows, down [E, H, I_pad/2]. */
+int imq_moe_experts_w4_ex(const void* hidden, int64_t h_row_stride, int64_t T, int64_t H, int64_t top_k,
+                          const int32_t* topk_idx, const void* topk_w, int64_t E,
+                          const void* gu_q, int64_t gu_q_stride_e, int64_t gu_q_row_stride, int64_t gu_K_pad,
+                          const void* gu_s, const void* gu_z, int64_t gu_sz_stride_e, int64_t gu_sz_stride_n,
+                          int64_t I, const void* dn_q, int64_t dn_q_stride_e, int64_t dn_q_row_stride,
+                          int64_t dn_K_pad, const void* dn_s, const void* dn_z, int64_t dn_sz_stride_e,
+                          int64_t dn_sz_stride_n, int sz_dtype, int64_t group_size,
+                          const void* gu_bias, int64_t gu_bias_stride_e, const void* dn_bias,
+                          int64_t dn_bias_stride_e, int bias_dtype, int act, float alpha, float limit,
+                          void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,7 @@ IMQ_OK, IMQ_ERR_INVALID, IMQ_ERR_UNSUPPORTED, IMQ_ERR_ALIGN = 0, -1, -2, -3
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
 _c_vp = ctypes.c_void_p
+_c_float = ctypes.c_float
 
 # name -> (restype, argtypes); must match include/imq.h exactly.
 SIGNATURES = {
@@ -57,6 +58,11 @@ SIGNATURES = {
                                     _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                                     _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64,
                                     _c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
+    "imq_moe_experts_w4_ex": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64,
+                                       _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                       _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64,
+                                       _c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int,
+                                       _c_float, _c_float, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
 }
 
 

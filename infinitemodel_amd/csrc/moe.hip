@@ -9,6 +9,13 @@
 //                      gate_up rows -> silu(gate) * up -> down rows -> weighted combine,
 //                    with fp32 intermediates (the eager path rounds each stage to bf16; only h,
 //                    the down projection's activation, is rounded to bf16 here).
+// imq_moe_experts_w4_ex: the same with the kernel layout's K_pad of each projection given
+//                    explicitly (rows padded past in_features with zero codes and zero scales),
+//                    optional per-expert row biases and a choice of activation: SiLU-GLU over
+//                    [gate | up] halves, or gpt-oss's clamped GLU over interleaved gate / up rows
+//                    (worker_quant.py:2280-2314: gate = y[::2] <= limit, up = y[1::2] in
+//                    [-limit, limit], h = (up + 1) * gate * sigmoid(alpha * gate), biases added
+//                    to both projections' outputs).
 #include "imq_common.h"
 
 namespace {
@@ -57,27 +64,56 @@ __global__ __launch_bounds__(256) void moe_rows_kernel(
   }
 }
 
-// h[b][i] = bf16(silu(g) * u), g = gu[b][i], u = gu[b][I + i]; zero for I <= i < I_pad.
-__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ gu, int64_t B, int64_t I,
-                                                     int64_t I_pad, uint16_t* __restrict__ h) {
-  const int64_t total = B * I_pad;
+// Element i of a per-expert bias row in the bias dtype.
+IMQ_DEV float load_bias(const void* p, int dt, int64_t i) {
+  if (dt == IMQ_DT_FP32) return ((const float*)p)[i];
+  if (dt == IMQ_DT_FP16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+  return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+// gpt-oss's clamped GLU: gate <= limit, up in [-limit, limit] (comparisons, so NaN propagates as
+// in torch's clamp), h = (up + 1) * gate * sigmoid(alpha * gate).
+IMQ_DEV float gptoss_glu(float g, float u, float alpha, float limit) {
+  g = g > limit ? limit : g;
+  u = u > limit ? limit : (u < -limit ? -limit : u);
+  return (u + 1.f) * (g / (1.f + __expf(-alpha * g)));
+}
+
+// h[b][i] (row stride hs) = bf16(act(gate, up)) for i < I, zero for I <= i < hk. ACT 0: gate =
+// gu[b][i], up = gu[b][I + i]; ACT 1: gate = gu[b][2i], up = gu[b][2i + 1]. The row bias of the
+// routed expert eid[b] (stride sbe, dtype bdt) is added to gu first when given.
+template <int ACT>
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ gu, int64_t B, int64_t I, int64_t hk,
+                                                     int64_t hs, const int32_t* __restrict__ eid, int64_t E,
+                                                     const void* __restrict__ bias, int64_t sbe, int bdt,
+                                                     float alpha, float limit, uint16_t* __restrict__ h) {
+  const int64_t total = B * hk;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = t / I_pad;
-    const int64_t i = t - b * I_pad;
+    const int64_t b = t / hk;
+    const int64_t i = t - b * hk;
     float v = 0.f;
     if (i < I) {
-      const float g = gu[b * 2 * I + i];
-      const float u = gu[b * 2 * I + I + i];
-      v = g / (1.f + __expf(-g)) * u;
+      const int64_t ig = ACT == 0 ? i : 2 * i, iu = ACT == 0 ? I + i : 2 * i + 1;
+      float g = gu[b * 2 * I + ig];
+      float u = gu[b * 2 * I + iu];
+      if (bias) {
+        int64_t e = eid[b];
+        e = (e >= 0 && e < E) ? e : 0;
+        g += load_bias(bias, bdt, e * sbe + ig);
+        u += load_bias(bias, bdt, e * sbe + iu);
+      }
+      if constexpr (ACT == 0) v = g / (1.f + __expf(-g)) * u;
+      else v = gptoss_glu(g, u, alpha, limit);
     }
-    h[t] = (uint16_t)f32_to_bf16_bits(v);
+    h[b * hs + i] = (uint16_t)f32_to_bf16_bits(v);
   }
 }
 
-// out[t][n] = bf16(sum_j w[t][j] * z[t*k + j][n]), j in slot order (fixed).
+// out[t][n] = bf16(sum_j w[t][j] * (z[t*k + j][n] + bias[e(t, j)][n])), j in slot order (fixed).
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ z, const uint16_t* __restrict__ w,
-                                                      int64_t T, int64_t k, int64_t H,
+                                                      int64_t T, int64_t k, int64_t H, const int32_t* __restrict__ eid,
+                                                      int64_t E, const void* __restrict__ bias, int64_t sbe, int bdt,
                                                       uint16_t* __restrict__ out, int64_t so) {
   const int64_t total = T * H;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
@@ -85,7 +121,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     const int64_t tok = t / H;
     const int64_t n = t - tok * H;
     float acc = 0.f;
-    for (int64_t j = 0; j < k; ++j) acc = fmaf(bf16_bits_to_f32(w[tok * k + j]), z[(tok * k + j) * H + n], acc);
+    for (int64_t j = 0; j < k; ++j) {
+      float v = z[(tok * k + j) * H + n];
+      if (bias) {
+        int64_t e = eid[tok * k + j];
+        e = (e >= 0 && e < E) ? e : 0;
+        v += load_bias(bias, bdt, e * sbe + n);
+      }
+      acc = fmaf(bf16_bits_to_f32(w[tok * k + j]), v, acc);
+    }
     out[tok * so + n] = (uint16_t)f32_to_bf16_bits(acc);
   }
 }
@@ -101,8 +145,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 //                      weights (NTL tiles of 16 rows) are loaded once into registers in the decode
 //                      line kernel's full-line layout and reused for all of the expert's tokens, 16
 //                      per MFMA pass. MODE 0 is gate_up: NTL/2 tiles of gate rows and the matching
-//                      up rows, SwiGLU in the epilogue, bf16 h in sorted order. MODE 1 is down:
-//                      NTL tiles of H, fp32 rows written in routed order.
+//                      up rows, SwiGLU in the epilogue, bf16 h in sorted order. MODE 2 is gpt-oss's
+//                      gate_up: NTL tiles of interleaved (gate, up) row pairs, its clamped GLU in
+//                      the epilogue. MODE 1 is down: NTL tiles of H, fp32 rows written in routed
+//                      order. Row biases, when given, are added to the sums in the epilogue.
 //   moe_combine_kernel out[t] = bf16(sum_j w[t, j] * yr[t*k + j]), slot order.
 constexpr int kMoeLine = 256;
 
@@ -160,10 +206,10 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
 }
 
 struct MoeLineArgs {
-  const uint16_t* x;     // MODE 0: hidden [T, >= Kpad]; MODE 1: h [B, >= Kpad] in sorted order
+  const uint16_t* x;     // MODE 0 / 2: hidden [T, >= Kpad]; MODE 1: h [B, >= Kpad] in sorted order
   int64_t sxm;
   int Kpad;
-  int k;                 // top_k: MODE 0 reads hidden row perm[p] / k
+  int k;                 // top_k: MODE 0 / 2 read hidden row perm[p] / k
   const int32_t* off;
   const int32_t* perm;
   const int32_t* hit;    // [E + 1]: ascending hit experts, hit[E] = their number
@@ -175,8 +221,12 @@ struct MoeLineArgs {
   int E;
   int NB;                // row blocks (NTL * 16 rows) per expert
   int I;                 // MODE 0: intermediate size (up rows start at I)
-  void* out;             // MODE 0: h bf16 [B, I_pad] sorted order; MODE 1: fp32 [B, H] routed order
+  void* out;             // MODE 0 / 2: h bf16 [B, >= I] sorted order; MODE 1: fp32 [B, H] routed order
   int64_t som;
+  const void* bias;      // per-expert row bias [E][rows] (expert stride sbe, dtype bdt), or null
+  int64_t sbe;
+  int bdt;
+  float alpha, limit;    // MODE 2 activation
 };
 
 IMQ_DEV float moe_row_swap8(float v) {
@@ -208,6 +258,9 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   auto rbase = [&](int t) -> int {
     if constexpr (MODE == 0) return (t < HALF) ? 16 * HALF * blk + 16 * t : a.I + 16 * HALF * blk + 16 * (t - HALF);
     else return 16 * NTL * blk + 16 * t;
+  };
+  auto bias_at = [&](int row) -> float {
+    return a.bias != nullptr ? load_bias(a.bias, a.bdt, (int64_t)e * a.sbe + row) : 0.f;
   };
   // ---- scale / zero words of this wave's groups for the 4 tiles -> wave LDS ----
   constexpr int ZN = 2 * NTL * 16 * DPR;
@@ -283,7 +336,7 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
     const int nrow = (end - p0) < 16 ? end - p0 : 16;
     const int pr = p0 + (c < nrow ? c : nrow - 1);    // A row of this lane (rows >= nrow repeat the last)
     const uint16_t* xr;
-    if constexpr (MODE == 0) xr = a.x + (int64_t)(a.perm[pr] / a.k) * a.sxm;
+    if constexpr (MODE != 1) xr = a.x + (int64_t)(a.perm[pr] / a.k) * a.sxm;   // gate_up: gather hidden rows
     else xr = a.x + (int64_t)pr * a.sxm;
     f32x4_t y0[NTL], y1[NTL];
 #pragma unroll
@@ -360,13 +413,29 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
               g += red[((w * NTL + t) * 16 + m) * 16 + n];
               u += red[((w * NTL + t + HALF) * 16 + m) * 16 + n];
             }
+            g += bias_at(16 * HALF * blk + j);
+            u += bias_at(a.I + 16 * HALF * blk + j);
             const float hv = g / (1.f + __expf(-g)) * u;
             ((uint16_t*)a.out)[(int64_t)(p0 + m) * a.som + 16 * HALF * blk + j] = (uint16_t)f32_to_bf16_bits(hv);
+          }
+        } else if constexpr (MODE == 2) {
+          if (j < 8 * NTL) {                     // h column 8*NTL*blk + j from rows 2j (gate), 2j + 1 (up)
+            const int rg = 2 * j, ru = 2 * j + 1;
+            float g = 0.f, u = 0.f;
+            for (int w = 0; w < W; ++w) {
+              g += red[((w * NTL + (rg >> 4)) * 16 + m) * 16 + (rg & 15)];
+              u += red[((w * NTL + (ru >> 4)) * 16 + m) * 16 + (ru & 15)];
+            }
+            g += bias_at(16 * NTL * blk + rg);
+            u += bias_at(16 * NTL * blk + ru);
+            const float hv = gptoss_glu(g, u, a.alpha, a.limit);
+            ((uint16_t*)a.out)[(int64_t)(p0 + m) * a.som + 8 * NTL * blk + j] = (uint16_t)f32_to_bf16_bits(hv);
           }
         } else {
           const int t = j >> 4, n = j & 15;
           float v = 0.f;
           for (int w = 0; w < W; ++w) v += red[((w * NTL + t) * 16 + m) * 16 + n];
+          v += bias_at(16 * NTL * blk + j);
           ((float*)a.out)[(int64_t)a.perm[p0 + m] * a.som + 16 * NTL * blk + j] = v;
         }
       }
@@ -404,15 +473,15 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   }
 }
 
-// zero h's pad columns [I, I_pad) (down reads K = I_pad)
+// zero h's pad columns [I, hk) of rows with stride hs (down reads K = hk)
 __global__ __launch_bounds__(256) void moe_zero_pad_kernel(uint16_t* __restrict__ h, int64_t B, int64_t I,
-                                                           int64_t I_pad) {
-  const int64_t wpad = I_pad - I;
+                                                           int64_t hk, int64_t hs) {
+  const int64_t wpad = hk - I;
   const int64_t total = B * wpad;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
     const int64_t b = t / wpad;
-    h[b * I_pad + I + (t - b * wpad)] = 0;
+    h[b * hs + I + (t - b * wpad)] = 0;
   }
 }
 
@@ -516,20 +585,22 @@ extern "C" int imq_moe_rows_w4(const void* x, int64_t x_row_stride, int64_t B, i
 }
 
 namespace {
-// Workspace layout: [gu fp32 B x 2I][h bf16 B x I_pad][z fp32 B x H][off int32 E+1][perm int32 B]
-// [hit int32 E+1], each 256-byte aligned. The token-sorted path uses h, z, off, perm and hit;
-// the per-row path gu, h and z.
+// Workspace layout: [gu fp32 B x 2I][h bf16 B x hw][z fp32 B x H][off int32 E+1][perm int32 B]
+// [hit int32 E+1], each 256-byte aligned; hw = I_pad rounded up to a multiple of 256, the widest
+// down K_pad a kernel layout may use. The token-sorted path uses h, z, off, perm and hit; the
+// per-row path gu, h and z.
 struct MoeWs {
-  int64_t gu, h, z, off, perm, hit, total;
+  int64_t gu, h, z, off, perm, hit, total, hw;
 };
 
 MoeWs moe_ws(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t G) {
   const int64_t B = T * top_k;
   const int64_t I_pad = imq_cdiv(I, G) * G;
   MoeWs w;
+  w.hw = imq_cdiv(I_pad, 256) * 256;
   w.gu = 0;
   w.h = w.gu + align_up(B * 2 * I * 4, kAlign);
-  w.z = w.h + align_up(B * I_pad * 2, kAlign);
+  w.z = w.h + align_up(B * w.hw * 2, kAlign);
   w.off = w.z + align_up(B * H * 4, kAlign);
   w.perm = w.off + align_up((E + 1) * 4, kAlign);
   w.hit = w.perm + align_up(B * 4, kAlign);
@@ -545,52 +616,148 @@ extern "C" int64_t imq_moe_workspace_bytes(int64_t T, int64_t top_k, int64_t E, 
 }
 
 namespace {
+struct MoeCall {
+  const uint16_t* hidden;
+  int64_t hs, T, H, k;
+  const int32_t* idx;
+  const uint16_t* topk_w;
+  int64_t E;
+  const uint8_t* gq;
+  int64_t gqe, gqn, gK;
+  const void *gs, *gz;
+  int64_t gse, gsn, I;
+  const uint8_t* dq;
+  int64_t dqe, dqn, dK;
+  const void *ds, *dz;
+  int64_t dse, dsn;
+  int sdt;
+  int64_t G;
+  const void* gb;
+  int64_t gbe;
+  const void* db;
+  int64_t dbe;
+  int bdt, act;
+  float alpha, limit;
+  uint16_t* out;
+  int64_t os;
+};
+
 // Token-sorted grouped path; IMQ_ERR_UNSUPPORTED when the shape or layout does not qualify.
-int moe_sorted(const uint16_t* hidden, int64_t hs, int64_t T, int64_t H, int64_t k, const int32_t* idx,
-               const uint16_t* topk_w, int64_t E, const uint8_t* gq, int64_t gqe, int64_t gqn, const void* gs,
-               const void* gz, int64_t gse, int64_t gsn, int64_t I, const uint8_t* dq, int64_t dqe, int64_t dqn,
-               const void* ds, const void* dz, int64_t dse, int64_t dsn, int sdt, int64_t G, uint16_t* out,
-               int64_t os, char* ws, const MoeWs& L, hipStream_t st) {
-  const int64_t H_pad = imq_cdiv(H, G) * G, I_pad = imq_cdiv(I, G) * G;
-  const int64_t B = T * k;
-  const int vb = sdt == IMQ_DT_FP32 ? 4 : 2;
-  if (G != 128 || H_pad % kMoeLine || I_pad % kMoeLine || I % 32 || H % 64) return IMQ_ERR_UNSUPPORTED;
-  if (!aligned(out, 16) || (os % 8)) return IMQ_ERR_UNSUPPORTED;
-  if (E > 16384 || B > 0x7fffffff || T * hs > 0x7fffffffLL * 8) return IMQ_ERR_UNSUPPORTED;
-  if (!aligned(gq, 16) || !aligned(dq, 16) || (gqn % 16) || (dqn % 16) || (gqe % 16) || (dqe % 16))
+int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
+  const int64_t B = c.T * c.k;
+  const int vb = c.sdt == IMQ_DT_FP32 ? 4 : 2;
+  if (c.G != 128 || c.gK % kMoeLine || c.dK % kMoeLine || c.I % 32 || c.H % 64) return IMQ_ERR_UNSUPPORTED;
+  if (!aligned(c.out, 16) || (c.os % 8)) return IMQ_ERR_UNSUPPORTED;
+  if (c.E > 16384 || B > 0x7fffffff || c.T * c.hs > 0x7fffffffLL * 8) return IMQ_ERR_UNSUPPORTED;
+  if (!aligned(c.gq, 16) || !aligned(c.dq, 16) || (c.gqn % 16) || (c.dqn % 16) || (c.gqe % 16) || (c.dqe % 16))
     return IMQ_ERR_UNSUPPORTED;
-  if (!aligned(gs, 4) || !aligned(gz, 4) || !aligned(ds, 4) || !aligned(dz, 4) || (gsn * vb) % 4 ||
-      (dsn * vb) % 4 || (gse * vb) % 4 || (dse * vb) % 4)
+  if (!aligned(c.gs, 4) || !aligned(c.gz, 4) || !aligned(c.ds, 4) || !aligned(c.dz, 4) || (c.gsn * vb) % 4 ||
+      (c.dsn * vb) % 4 || (c.gse * vb) % 4 || (c.dse * vb) % 4)
     return IMQ_ERR_UNSUPPORTED;
   int s2, w;
-  if (!moe_line_shape(H_pad, &s2, &w) || !moe_line_shape(I_pad, &s2, &w)) return IMQ_ERR_UNSUPPORTED;
+  if (!moe_line_shape(c.gK, &s2, &w) || !moe_line_shape(c.dK, &s2, &w)) return IMQ_ERR_UNSUPPORTED;
   int32_t* off = (int32_t*)(ws + L.off);
   int32_t* perm = (int32_t*)(ws + L.perm);
   int32_t* hit = (int32_t*)(ws + L.hit);
   uint16_t* h = (uint16_t*)(ws + L.h);
   float* yr = (float*)(ws + L.z);
-  moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)E * 4, st>>>(idx, (int)B, (int)E, off, perm, hit);
+  moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit);
   IMQ_LAUNCH_CHECK();
-  MoeLineArgs g{hidden, hs, (int)H_pad, (int)k, off, perm, hit, gq, gqe, gqn, gs, gz, gse, gsn, (int)E, 0, (int)I,
-                h, I_pad};
-  int rc = moe_line_sdt<0>(g, (int)(2 * I), sdt, st);
+  MoeLineArgs g{c.hidden, c.hs, (int)c.gK, (int)c.k, off, perm, hit, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn,
+                (int)c.E, 0, (int)c.I, h, L.hw, c.gb, c.gbe, c.bdt, c.alpha, c.limit};
+  int rc = c.act == IMQ_ACT_GPTOSS ? moe_line_sdt<2>(g, (int)(2 * c.I), c.sdt, st)
+                                   : moe_line_sdt<0>(g, (int)(2 * c.I), c.sdt, st);
   if (rc != IMQ_OK) return rc;
-  if (I_pad > I) {
-    const int64_t total = B * (I_pad - I);
+  if (c.dK > c.I) {
+    const int64_t total = B * (c.dK - c.I);
     const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
-    moe_zero_pad_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(h, B, I, I_pad);
+    moe_zero_pad_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(h, B, c.I, c.dK, L.hw);
     IMQ_LAUNCH_CHECK();
   }
-  MoeLineArgs d{h, I_pad, (int)I_pad, (int)k, off, perm, hit, dq, dqe, dqn, ds, dz, dse, dsn, (int)E, 0, 0, yr, H};
-  rc = moe_line_sdt<1>(d, (int)H, sdt, st);
+  MoeLineArgs d{h, L.hw, (int)c.dK, (int)c.k, off, perm, hit, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn,
+                (int)c.E, 0, 0, yr, c.H, c.db, c.dbe, c.bdt, 0.f, 0.f};
+  rc = moe_line_sdt<1>(d, (int)c.H, c.sdt, st);
   if (rc != IMQ_OK) return rc;
-  const int64_t total = T * (H / 8);
+  const int64_t total = c.T * (c.H / 8);
   const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
-  moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, topk_w, T, k, H, out, os);
+  moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, c.topk_w, c.T, c.k, c.H, c.out, c.os);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+// Per-row path for every other shape: gate_up rows, activation, down rows, combine.
+int moe_per_row(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
+  const int64_t B = c.T * c.k;
+  float* gu = (float*)(ws + L.gu);
+  uint16_t* h = (uint16_t*)(ws + L.h);
+  float* z = (float*)(ws + L.z);
+  int rc = launch_rows<true>(c.hidden, c.hs, c.k, B, c.gK, c.idx, c.E, c.gq, c.gqe, c.gqn, c.gs, c.gse, c.gsn, 1,
+                             c.gz, c.gse, c.gsn, 1, c.sdt, 2 * c.I, c.G, gu, 2 * c.I, st);
+  if (rc != IMQ_OK) return rc;
+  {
+    const int64_t total = B * c.dK;
+    const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
+    if (c.act == IMQ_ACT_GPTOSS)
+      swiglu_kernel<1><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(gu, B, c.I, c.dK, L.hw, c.idx, c.E, c.gb, c.gbe,
+                                                                   c.bdt, c.alpha, c.limit, h);
+    else
+      swiglu_kernel<0><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(gu, B, c.I, c.dK, L.hw, c.idx, c.E, c.gb, c.gbe,
+                                                                   c.bdt, c.alpha, c.limit, h);
+    IMQ_LAUNCH_CHECK();
+  }
+  rc = launch_rows<true>(h, L.hw, 1, B, c.dK, c.idx, c.E, c.dq, c.dqe, c.dqn, c.ds, c.dse, c.dsn, 1, c.dz, c.dse,
+                         c.dsn, 1, c.sdt, c.H, c.G, z, c.H, st);
+  if (rc != IMQ_OK) return rc;
+  const int64_t total = c.T * c.H;
+  const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
+  combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(z, c.topk_w, c.T, c.k, c.H, c.idx, c.E, c.db, c.dbe,
+                                                             c.bdt, c.out, c.os);
   IMQ_LAUNCH_CHECK();
   return IMQ_OK;
 }
 }  // namespace
+
+extern "C" int imq_moe_experts_w4_ex(
+    const void* hidden, int64_t h_row_stride, int64_t T, int64_t H, int64_t top_k, const int32_t* topk_idx,
+    const void* topk_w, int64_t E, const void* gu_q, int64_t gu_q_stride_e, int64_t gu_q_row_stride, int64_t gu_K_pad,
+    const void* gu_s, const void* gu_z, int64_t gu_sz_stride_e, int64_t gu_sz_stride_n, int64_t I, const void* dn_q,
+    int64_t dn_q_stride_e, int64_t dn_q_row_stride, int64_t dn_K_pad, const void* dn_s, const void* dn_z,
+    int64_t dn_sz_stride_e, int64_t dn_sz_stride_n, int sz_dtype, int64_t group_size, const void* gu_bias,
+    int64_t gu_bias_stride_e, const void* dn_bias, int64_t dn_bias_stride_e, int bias_dtype, int act, float alpha,
+    float limit, void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!hidden || !topk_idx || !topk_w || !gu_q || !gu_s || !gu_z || !dn_q || !dn_s || !dn_z || !out)
+    return IMQ_ERR_INVALID;
+  if (T < 0 || H <= 0 || top_k <= 0 || E <= 0 || I <= 0 || group_size <= 0 || group_size % 8) return IMQ_ERR_INVALID;
+  if (sz_dtype != IMQ_DT_BF16 && sz_dtype != IMQ_DT_FP16 && sz_dtype != IMQ_DT_FP32) return IMQ_ERR_INVALID;
+  if (act != IMQ_ACT_SILU_GLU && act != IMQ_ACT_GPTOSS) return IMQ_ERR_INVALID;
+  if ((gu_bias || dn_bias) && bias_dtype != IMQ_DT_BF16 && bias_dtype != IMQ_DT_FP16 && bias_dtype != IMQ_DT_FP32)
+    return IMQ_ERR_INVALID;
+  if (gu_bias && gu_bias_stride_e < 2 * I) return IMQ_ERR_INVALID;
+  if (dn_bias && dn_bias_stride_e < H) return IMQ_ERR_INVALID;
+  const int64_t G = group_size;
+  const MoeWs L = moe_ws(T, top_k, E, H, I, G);
+  // kernel K_pads: multiples of the group covering in_features; down's fits the workspace's h rows
+  if (gu_K_pad < H || gu_K_pad % G || dn_K_pad < I || dn_K_pad % G || dn_K_pad > L.hw) return IMQ_ERR_INVALID;
+  if (gu_q_row_stride < gu_K_pad / 2 || dn_q_row_stride < dn_K_pad / 2) return IMQ_ERR_INVALID;
+  if (gu_sz_stride_n < gu_K_pad / G || dn_sz_stride_n < dn_K_pad / G) return IMQ_ERR_INVALID;
+  if (T == 0) return IMQ_OK;
+  if (!workspace || workspace_bytes < L.total) return IMQ_ERR_INVALID;
+  if (h_row_stride < gu_K_pad || out_row_stride < H) return IMQ_ERR_INVALID;
+  if (!aligned(gu_q, 4) || !aligned(dn_q, 4) || (gu_q_row_stride % 4) || (dn_q_row_stride % 4) ||
+      (gu_q_stride_e % 4) || (dn_q_stride_e % 4) || !aligned(hidden, 16) || (h_row_stride % 8) ||
+      !aligned(workspace, 256))
+    return IMQ_ERR_ALIGN;
+  const MoeCall c{(const uint16_t*)hidden, h_row_stride, T, H, top_k, topk_idx, (const uint16_t*)topk_w, E,
+                  (const uint8_t*)gu_q, gu_q_stride_e, gu_q_row_stride, gu_K_pad, gu_s, gu_z, gu_sz_stride_e,
+                  gu_sz_stride_n, I, (const uint8_t*)dn_q, dn_q_stride_e, dn_q_row_stride, dn_K_pad, dn_s, dn_z,
+                  dn_sz_stride_e, dn_sz_stride_n, sz_dtype, G, gu_bias, gu_bias_stride_e, dn_bias, dn_bias_stride_e,
+                  bias_dtype, act, alpha, limit, (uint16_t*)out, out_row_stride};
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const int rs = moe_sorted(c, ws, L, st);
+  if (rs != IMQ_ERR_UNSUPPORTED) return rs;
+  return moe_per_row(c, ws, L, st);
+}
 
 extern "C" int imq_moe_experts_w4(const void* hidden, int64_t h_row_stride, int64_t T, int64_t H, int64_t top_k,
                                   const int32_t* topk_idx, const void* topk_w, int64_t E, const void* gu_q,
@@ -600,58 +767,12 @@ extern "C" int imq_moe_experts_w4(const void* hidden, int64_t h_row_stride, int6
                                   int64_t dn_sz_stride_e, int64_t dn_sz_stride_n, int sz_dtype, int64_t group_size,
                                   void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
                                   void* stream) {
-  if (!hidden || !topk_idx || !topk_w || !gu_q || !gu_s || !gu_z || !dn_q || !dn_s || !dn_z || !out)
-    return IMQ_ERR_INVALID;
-  if (T < 0 || H <= 0 || top_k <= 0 || E <= 0 || I <= 0 || group_size <= 0 || group_size % 8) return IMQ_ERR_INVALID;
-  if (T == 0) return IMQ_OK;
-  const int64_t G = group_size;
-  const int64_t H_pad = imq_cdiv(H, G) * G;
-  const int64_t I_pad = imq_cdiv(I, G) * G;
-  const int64_t need = imq_moe_workspace_bytes(T, top_k, E, H, I, G);
-  if (!workspace || workspace_bytes < need) return IMQ_ERR_INVALID;
-  if (h_row_stride < H_pad || out_row_stride < H) return IMQ_ERR_INVALID;
-  if (!aligned(gu_q, 4) || !aligned(dn_q, 4) || (gu_q_row_stride % 4) || (dn_q_row_stride % 4) ||
-      (gu_q_stride_e % 4) || (dn_q_stride_e % 4) || !aligned(hidden, 16) || (h_row_stride % 8) ||
-      !aligned(workspace, 256))
-    return IMQ_ERR_ALIGN;
-  hipStream_t st = (hipStream_t)stream;
-  const int64_t B = T * top_k;
-  char* ws = (char*)workspace;
-  const MoeWs L = moe_ws(T, top_k, E, H, I, G);
-  {
-    const int rs = moe_sorted((const uint16_t*)hidden, h_row_stride, T, H, top_k, topk_idx, (const uint16_t*)topk_w,
-                              E, (const uint8_t*)gu_q, gu_q_stride_e, gu_q_row_stride, gu_s, gu_z, gu_sz_stride_e,
-                              gu_sz_stride_n, I, (const uint8_t*)dn_q, dn_q_stride_e, dn_q_row_stride, dn_s, dn_z,
-                              dn_sz_stride_e, dn_sz_stride_n, sz_dtype, G, (uint16_t*)out, out_row_stride, ws, L, st);
-    if (rs != IMQ_ERR_UNSUPPORTED) return rs;
-  }
-  float* gu = (float*)(ws + L.gu);
-  uint16_t* h = (uint16_t*)(ws + L.h);
-  float* z = (float*)(ws + L.z);
-  const int64_t ng1 = H_pad / G, ng2 = I_pad / G;
-  (void)ng1;
-  (void)ng2;
-  int rc = launch_rows<true>((const uint16_t*)hidden, h_row_stride, top_k, B, H_pad, topk_idx, E,
-                             (const uint8_t*)gu_q, gu_q_stride_e, gu_q_row_stride, gu_s, gu_sz_stride_e,
-                             gu_sz_stride_n, 1, gu_z, gu_sz_stride_e, gu_sz_stride_n, 1, sz_dtype, 2 * I, G, gu,
-                             2 * I, st);
-  if (rc != IMQ_OK) return rc;
-  {
-    const int64_t total = B * I_pad;
-    const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
-    swiglu_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(gu, B, I, I_pad, h);
-    IMQ_LAUNCH_CHECK();
-  }
-  rc = launch_rows<true>(h, I_pad, 1, B, I_pad, topk_idx, E, (const uint8_t*)dn_q, dn_q_stride_e, dn_q_row_stride,
-                         dn_s, dn_sz_stride_e, dn_sz_stride_n, 1, dn_z, dn_sz_stride_e, dn_sz_stride_n, 1, sz_dtype,
-                         H, G, z, H, st);
-  if (rc != IMQ_OK) return rc;
-  {
-    const int64_t total = T * H;
-    const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
-    combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(z, (const uint16_t*)topk_w, T, top_k, H,
-                                                               (uint16_t*)out, out_row_stride);
-    IMQ_LAUNCH_CHECK();
-  }
-  return IMQ_OK;
+  if (group_size <= 0) return IMQ_ERR_INVALID;
+  const int64_t H_pad = imq_cdiv(H, group_size) * group_size;
+  const int64_t I_pad = imq_cdiv(I, group_size) * group_size;
+  return imq_moe_experts_w4_ex(hidden, h_row_stride, T, H, top_k, topk_idx, topk_w, E, gu_q, gu_q_stride_e,
+                               gu_q_row_stride, H_pad, gu_s, gu_z, gu_sz_stride_e, gu_sz_stride_n, I, dn_q,
+                               dn_q_stride_e, dn_q_row_stride, I_pad, dn_s, dn_z, dn_sz_stride_e, dn_sz_stride_n,
+                               sz_dtype, group_size, nullptr, 0, nullptr, 0, IMQ_DT_BF16, IMQ_ACT_SILU_GLU, 0.f, 0.f,
+                               out, out_row_stride, workspace, workspace_bytes, stream);
 }

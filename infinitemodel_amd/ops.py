@@ -244,17 +244,28 @@ def moe_workspace_bytes(T: int, top_k: int, E: int, H: int, I: int, group_size: 
     return int(_lib.lib().imq_moe_workspace_bytes(T, top_k, E, H, I, group_size))
 
 
-def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=None):
-    """One MoE layer's experts forward: ``out[t] = sum_j w[t,j] * down_e(silu(gate) * up)``.
+_ACT = {"silu_glu": 0, "gptoss": 1}
 
-    ``gu`` / ``dn`` are (qweight, scale, zero, in_features) of the gate_up [E, 2I, H_pad/2] and
-    down [E, H, I_pad/2] Packed4Tensor3D holders. Semantics of the transformers eager experts
-    loop (modeling_olmoe.py:301-325) as fused by worker_quant.py:2167-2191."""
+
+def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=None, *, act: str = "silu_glu",
+                   gu_bias=None, dn_bias=None, alpha: float = 1.702, limit: float = 7.0):
+    """One MoE layer's experts forward: ``out[t] = sum_j w[t,j] * (down_e(act(gate_up_e(x_t))) + b_dn[e])``.
+
+    ``gu`` / ``dn`` are (qweight, scale, zero, in_features) of the gate_up [E, 2I, K1/2] and down
+    [E, H, K2/2] int4 stacks, K1 / K2 the kernel layout's padded K (any multiple of the group
+    >= in_features; columns past in_features carry zero codes and zero scales).
+
+    ``act="silu_glu"``: rows [gate | up], h = silu(gate) * up -- the transformers eager experts
+    loop (modeling_olmoe.py:301-325) as fused by worker_quant.py:2167-2191. ``act="gptoss"``:
+    rows interleaved (gate 2i, up 2i+1) with per-expert biases ``gu_bias`` [E, 2I] and ``dn_bias``
+    [E, H] and gpt-oss's clamped GLU (worker_quant.py:2280-2314)."""
     gq, gs, gz, H = gu
     dq, ds, dz, I = dn
     dev = _check_dev(hidden, topk_idx, topk_w, gq, gs, gz, dq, ds, dz)
     for t in (gq, dq):
         _check_packed(t)
+    if act not in _ACT:
+        raise ValueError(f"act must be one of {sorted(_ACT)} (got {act!r})")
     T = hidden.shape[0]
     k = topk_idx.shape[1]
     E = gq.shape[0]
@@ -268,13 +279,26 @@ def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=
         if t.stride(2) != 1:
             raise ValueError("scale/zero need a unit last stride")
     if gs.stride() != gz.stride() or ds.stride() != dz.stride():
-        gz = gz.contiguous() if gz.stride() != gs.stride() else gz
         gs, gz = gs.contiguous(), gz.contiguous()
         ds, dz = ds.contiguous(), dz.contiguous()
+    bdt = None
+    biases = []
+    for b, rows in ((gu_bias, 2 * I), (dn_bias, H)):
+        if b is not None:
+            _check_dev(hidden, b)
+            if b.dim() != 2 or b.shape[0] != E or b.shape[1] != rows:
+                raise ValueError(f"bias must be [E, {rows}] (got {tuple(b.shape)})")
+            if b.stride(1) != 1:
+                b = b.contiguous()
+            if bdt is not None and b.dtype != bdt:
+                b = b.to(bdt)
+            bdt = b.dtype
+        biases.append(b)
+    gb, db = biases
+    gK, dK = gq.shape[2] * 2, dq.shape[2] * 2
     x = _rows2d(hidden)
-    H_pad = gq.shape[2] * 2
-    if x.shape[1] != H_pad:
-        x = torch.nn.functional.pad(x, (0, H_pad - x.shape[1])).contiguous()
+    if x.shape[1] != gK:
+        x = torch.nn.functional.pad(x, (0, gK - x.shape[1])).contiguous()
     idx = topk_idx.to(torch.int32).contiguous()
     w = topk_w.to(torch.bfloat16).contiguous()
     need = moe_workspace_bytes(T, k, E, H, I, group_size)
@@ -282,9 +306,13 @@ def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
     out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
-        call("imq_moe_experts_w4", _ptr(x), x.stride(0), T, H, k, _ptr(idx), _ptr(w), E,
-             _ptr(gq), gq.stride(0), gq.stride(1), _ptr(gs), _ptr(gz), gs.stride(0), gs.stride(1), I,
-             _ptr(dq), dq.stride(0), dq.stride(1), _ptr(ds), _ptr(dz), ds.stride(0), ds.stride(1),
-             dtype_code(sdt), group_size, _ptr(out), out.stride(0), _ptr(workspace),
-             workspace.numel() * workspace.element_size(), _stream(dev))
+        call("imq_moe_experts_w4_ex", _ptr(x), x.stride(0), T, H, k, _ptr(idx), _ptr(w), E,
+             _ptr(gq), gq.stride(0), gq.stride(1), gK, _ptr(gs), _ptr(gz), gs.stride(0), gs.stride(1), I,
+             _ptr(dq), dq.stride(0), dq.stride(1), dK, _ptr(ds), _ptr(dz), ds.stride(0), ds.stride(1),
+             dtype_code(sdt), group_size,
+             _ptr(gb) if gb is not None else None, gb.stride(0) if gb is not None else 0,
+             _ptr(db) if db is not None else None, db.stride(0) if db is not None else 0,
+             dtype_code(bdt) if bdt is not None else 0, _ACT[act], float(alpha), float(limit),
+             _ptr(out), out.stride(0), _ptr(workspace), workspace.numel() * workspace.element_size(),
+             _stream(dev))
     return out

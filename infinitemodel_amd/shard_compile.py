@@ -165,6 +165,14 @@ def quant_scope(model) -> tuple:
     return lin2d, exp3d
 
 
+def _in_major_expert_names(raw: dict) -> set:
+    """Fused 3D expert tensors whose layout is in-major [E, in, out] (shard_compile.py:143-167):
+    the ones with a per-expert ``<name>_bias`` beside them, the gpt-oss signature that survives
+    checkpoint normalization. Packing such a tensor as [E, out, in] would write a cache that loads
+    and verifies but serves the wrong axis."""
+    return {n for n, W in raw.items() if W.dim() == 3 and (n + "_bias") in raw}
+
+
 def pack_unit_tensors(raw: dict, lin2d: Optional[set] = None, quant: str = "int4",
                       group_size: int = INT4_GROUP):
     """Pack one unit's tensors (logical 'model.*' names) into the cache dict + manifest fragments,
@@ -175,11 +183,18 @@ def pack_unit_tensors(raw: dict, lin2d: Optional[set] = None, quant: str = "int4
     if quant not in ("int4", "int8", "int2"):
         raise ValueError(f"shard pack supports quant int4|int8|int2 (got {quant!r})")
     group_size = _default_group(quant, group_size)
+    in_major = _in_major_expert_names(raw) if quant == "int4" else set()
     out_sd: dict = {}
     mt: dict = {}
     for name, W in raw.items():
         is_expert3d = (quant == "int4" and W.dim() == 3 and ".experts." in name
                        and (name.endswith(".gate_up_proj") or name.endswith(".down_proj")))
+        if is_expert3d and name in in_major:
+            # shard_compile.py:315-330: the serve side cannot install transpose-packed gpt-oss
+            # experts from a cache, so the compile refuses rather than writing one
+            raise ValueError(f"{name}: in-major fused MoE experts (gpt-oss, [E, in, out]) are not "
+                             "shard-cacheable; load gpt-oss at int4 without a shard cache, or at "
+                             "quant=none")
         if lin2d is not None:
             is_lin = W.dim() == 2 and name in lin2d
         else:

@@ -617,7 +617,36 @@ def _packed4_3d_cls():
                 return _dequant_g(self.qweight[e], self.scale[e], self.zero[e], self.in_features,
                                   self.group_size, self.scale.dtype, 4)
 
-            def _dealias_ms(self, op, q, iters=25):
+            def _kernel_tensors(self):
+                """(qweight, scale, zero) in the fused kernels' layout: K padded to a multiple of
+                256 with zero codes and zero scales, so every row is whole 128-byte lines and an
+                even number of groups (gpt-oss-20b's 2880 columns pad to 3072). The module's own
+                buffers become views of the padded storage -- same shapes and values, no second
+                copy. Idempotent; call on the final device."""
+                qw, sc, ze = self.qweight, self.scale, self.zero
+                kt = self.__dict__.get("_kt")
+                if kt is not None and kt[3] is qw:
+                    return kt[:3]
+                E, N, rs = qw.shape
+                G = int(self.group_size)
+                ng = int(sc.shape[2])
+                kpad = rs * 2
+                if (kpad % 256 == 0 and (ng * sc.element_size()) % 4 == 0) or 256 % G != 0:
+                    kt = (qw, sc, ze, qw)
+                else:
+                    k2 = -(-kpad // 256) * 256
+                    q2 = torch.zeros((E, N, k2 // 2), dtype=torch.uint8, device=qw.device)
+                    q2[:, :, :rs].copy_(qw)
+                    s2 = torch.zeros((E, N, k2 // G), dtype=sc.dtype, device=sc.device)
+                    s2[:, :, :ng].copy_(sc)
+                    z2 = torch.zeros((E, N, k2 // G), dtype=ze.dtype, device=ze.device)
+                    z2[:, :, :ng].copy_(ze)
+                    self.qweight, self.scale, self.zero = q2[:, :, :rs], s2[:, :, :ng], z2[:, :, :ng]
+                    kt = (q2, s2, z2, self.qweight)
+                self._kt = kt
+                return kt[:3]
+
+            def _dealias_ms(self, op, q, sc, ze, iters=25):
                 """Fused expert GEMV time on ``q`` at a decode shape over fresh random expert
                 subsets, in ms."""
                 E = q.shape[0]
@@ -625,26 +654,32 @@ def _packed4_3d_cls():
                 x = torch.randn(B, self.in_features, device=q.device, dtype=torch.bfloat16) * 0.1
                 eids = [torch.randperm(E, device=q.device)[:B].to(torch.int32) for _ in range(iters + 3)]
                 for i in range(3):
-                    op(x, eids[i], q, self.scale, self.zero, self.group_size, self.in_features)
+                    op(x, eids[i], q, sc, ze, self.group_size, self.in_features)
                 torch.cuda.synchronize(q.device)
                 t0 = time.perf_counter()
                 for i in range(iters):
-                    op(x, eids[3 + i], q, self.scale, self.zero, self.group_size, self.in_features)
+                    op(x, eids[3 + i], q, sc, ze, self.group_size, self.in_features)
                 torch.cuda.synchronize(q.device)
                 return (time.perf_counter() - t0) / iters * 1e3
 
             def prepare_fused(self):
-                """Measured expert-row de-alias: keep ``[E, N, rs+64]`` padded rows only when the
-                fused op runs >= 15% faster on them; decision cached per (E, N, rs). Idempotent;
-                never raises (worker_quant.py:2067-2122)."""
+                """Kernel layout (``_kernel_tensors``), then the measured expert-row de-alias:
+                keep ``[E, N, rs+64]`` padded rows only when the fused op runs >= 15% faster on
+                them; decision cached per (E, N, rs). Idempotent; never raises
+                (worker_quant.py:2067-2122)."""
                 if getattr(self, "_dealiased", False):
                     return
                 self._dealiased = True
                 qw = self.qweight
                 if qw is None or qw.dim() != 3 or not _is_rocm_device(qw.device):
                     return
-                E, N, rs = qw.shape
-                if rs % 128 != 0 or qw.stride(2) != 1 or qw.stride(1) != rs:
+                try:
+                    kq, ks, kz = self._kernel_tensors()
+                except Exception as exc:
+                    _log(f"[int4] moe kernel layout skipped ({exc!r})")
+                    return
+                E, N, rs = kq.shape
+                if rs % 128 != 0 or kq.stride(2) != 1 or kq.stride(1) != rs:
                     return
                 op = _w4a16_moe_hip_op()
                 if op is None:
@@ -653,19 +688,20 @@ def _packed4_3d_cls():
                     choice = Packed4Tensor3D._pad_choice.get((E, N, rs))
                     buf = None
                     if choice is None:
-                        buf = torch.zeros((E, N, rs + 64), dtype=torch.uint8, device=qw.device)
-                        buf[:, :, :rs].copy_(qw)
-                        t_un = self._dealias_ms(op, qw)
-                        t_pad = self._dealias_ms(op, buf[:, :, :rs])
+                        buf = torch.zeros((E, N, rs + 64), dtype=torch.uint8, device=kq.device)
+                        buf[:, :, :rs].copy_(kq)
+                        t_un = self._dealias_ms(op, kq, ks, kz)
+                        t_pad = self._dealias_ms(op, buf[:, :, :rs], ks, kz)
                         choice = t_pad < t_un * 0.87
                         Packed4Tensor3D._pad_choice[(E, N, rs)] = choice
                         _log(f"[int4] moe row de-alias [E={E},N={N},rs={rs}]: unpadded={t_un:.3f}ms "
                              f"padded={t_pad:.3f}ms -> {'PAD' if choice else 'keep unpadded'}")
                     if choice:
                         if buf is None:
-                            buf = torch.zeros((E, N, rs + 64), dtype=torch.uint8, device=qw.device)
-                            buf[:, :, :rs].copy_(qw)
-                        self.qweight = buf[:, :, :rs]
+                            buf = torch.zeros((E, N, rs + 64), dtype=torch.uint8, device=kq.device)
+                            buf[:, :, :rs].copy_(kq)
+                        self.qweight = buf[:, :, :self.qweight.shape[2]]
+                        self._kt = (buf[:, :, :rs], ks, kz, self.qweight)
                 except Exception as exc:
                     _log(f"[int4] moe row de-alias skipped ({exc!r})")
 
@@ -681,8 +717,8 @@ def _moe_fused_compute(experts_mod, hidden_states, top_k_index, top_k_weights):
     gu, dn = experts_mod.gate_up_proj, experts_mod.down_proj
     I = int(dn.in_features)
     out = ops.moe_experts_w4(hidden_states, top_k_index, top_k_weights,
-                             (gu.qweight, gu.scale, gu.zero, int(gu.in_features)),
-                             (dn.qweight, dn.scale, dn.zero, I), int(gu.group_size))
+                             (*gu._kernel_tensors(), int(gu.in_features)),
+                             (*dn._kernel_tensors(), I), int(gu.group_size))
     return out.to(hidden_states.dtype)
 
 
@@ -763,6 +799,54 @@ def _install_fused_moe_forward(experts_mod) -> None:
     experts_mod.forward = types.MethodType(_fused_forward, experts_mod)
 
 
+# ---- gpt-oss fused experts (worker_quant.py:2250-2314) ---------------------------------------
+def _is_gptoss_experts(module) -> bool:
+    """A gpt-oss fused-expert block: interleaved clamped SwiGLU with per-expert biases
+    (worker_quant.py:2257-2262)."""
+    if type(module).__name__ == "GptOssExperts":
+        return True
+    return (hasattr(module, "gate_up_proj_bias") and hasattr(module, "down_proj_bias")
+            and hasattr(module, "alpha") and hasattr(module, "limit"))
+
+
+def _gptoss_fused_ok() -> bool:
+    """gpt-oss int4 needs the fused MoE kernel: its experts are transpose-packed, so there is no
+    eager host path to fall back to (worker_quant.py:2265-2276). True when libimq loads, unless
+    INFINITEMODEL_NO_FUSED_MOE is set."""
+    if os.environ.get("INFINITEMODEL_NO_FUSED_MOE"):
+        return False
+    return _w4a16_moe_hip_op() is not None
+
+
+def _gptoss_fused_compute(experts_mod, hidden_states, router_indices, routing_weights):
+    """gpt-oss experts forward in one libimq call: transpose-packed gate_up (interleaved gate /
+    up rows) + bias, clamped GLU, down + bias, routing-weighted combine."""
+    from . import ops
+    gu, dn = experts_mod.gate_up_proj, experts_mod.down_proj
+    out = ops.moe_experts_w4(hidden_states, router_indices, routing_weights,
+                             (*gu._kernel_tensors(), int(gu.in_features)),
+                             (*dn._kernel_tensors(), int(dn.in_features)), int(gu.group_size),
+                             act="gptoss", gu_bias=experts_mod.gate_up_proj_bias,
+                             dn_bias=experts_mod.down_proj_bias,
+                             alpha=float(getattr(experts_mod, "alpha", 1.702)),
+                             limit=float(getattr(experts_mod, "limit", 7.0)))
+    return out.to(hidden_states.dtype)
+
+
+def _install_gptoss_fused_forward(experts_mod) -> None:
+    """Install gpt-oss's int4 fused-expert forward (worker_quant.py:2280-2314) for every token
+    count: once the experts are transpose-packed there is no eager fallback. The caller has
+    transpose-packed the experts and checked ``_gptoss_fused_ok()``."""
+    import types
+
+    def _forward(self, hidden_states, router_indices=None, routing_weights=None):
+        return _gptoss_fused_compute(self, hidden_states, router_indices, routing_weights)
+
+    experts_mod._gptoss_fused_installed = True
+    experts_mod.forward = types.MethodType(_forward, experts_mod)
+    _log("[int4] gpt-oss fused experts active (transpose-packed w4a16 + interleaved SwiGLU)")
+
+
 # ---- packers (worker_quant.py:511-536, 1588-1608, 1921-1944, 2394-2436) ---------------------
 def _pack8_expert(W2d):
     """Per-row symmetric int8 of one ``[out, in]`` weight in W's own dtype -> (int8, scale)."""
@@ -829,30 +913,43 @@ def _quantize_int8_linears_(module) -> None:
 
 
 def _quantize_experts4_(module) -> None:
-    """Replace 3D ``gate_up_proj``/``down_proj`` expert Parameters with Packed4Tensor3D, force the
-    eager experts implementation on their config, and install the fused forward."""
+    """Replace 3D ``gate_up_proj``/``down_proj`` expert Parameters with Packed4Tensor3D
+    (worker_quant.py:2439-2483). gpt-oss blocks store their experts in-major [E, in, out] and are
+    transposed to [E, out, in] before packing; they get the dedicated fused forward (and need it:
+    RuntimeError when it is unavailable). Every other block gets the eager experts implementation
+    on its config and the fused-MoE forward."""
     from torch import nn
     targets = []
     for sub in module.modules():
+        is_go = _is_gptoss_experts(sub)
         for attr in ("gate_up_proj", "down_proj"):
             p = sub._parameters.get(attr)
             if isinstance(p, nn.Parameter) and p.dim() == 3:
-                targets.append((sub, attr))
-    for sub, attr in targets:
+                targets.append((sub, attr, is_go))
+    if any(is_go for _s, _a, is_go in targets) and not _gptoss_fused_ok():
+        raise RuntimeError("gpt-oss int4 requires the fused w4a16 MoE kernel (libimq on a ROCm "
+                           "device) -- load gpt-oss at quant=none (bf16) here")
+    for sub, attr, is_go in targets:
         p = getattr(sub, attr)
         delattr(sub, attr)
-        setattr(sub, attr, _pack4_3d(p.data))
+        w = p.data.transpose(1, 2).contiguous() if is_go else p.data
+        setattr(sub, attr, _pack4_3d(w))
     seen = set()
-    for sub, _attr in targets:
+    for sub, _attr, is_go in targets:
+        if is_go:
+            continue
         cfg = getattr(sub, "config", None)
         if cfg is not None and hasattr(cfg, "_experts_implementation") and id(cfg) not in seen:
             cfg._experts_implementation = "eager"
             seen.add(id(cfg))
     done = set()
-    for sub, _attr in targets:
+    for sub, _attr, is_go in targets:
         if id(sub) not in done:
             done.add(id(sub))
-            _install_fused_moe_forward(sub)
+            if is_go:
+                _install_gptoss_fused_forward(sub)
+            else:
+                _install_fused_moe_forward(sub)
 
 
 def finalize_placement(model) -> int:

@@ -9,7 +9,9 @@ the reference in bench_moe_w4a16.py:132-149) and the reference's fused decode fo
 Pins: ``moe_eager_bf16`` is checked against a live ``OlmoeExperts`` module from the installed
 transformers (a third-party implementation) fed the oracle's dequantized weights;
 ``moe_exact`` against ``moe_eager_bf16`` (agreement to bf16 noise) and a brute-force single-token
-case; ``moe_exact_grouped`` against ``moe_exact``; ``route_topk`` against ``OlmoeTopKRouter``.
+case; ``moe_exact_grouped`` against ``moe_exact``; ``route_topk`` against ``OlmoeTopKRouter``;
+``gptoss_exact`` against a live ``GptOssExperts`` module (float64, in-major weights = the
+transpose of the oracle's) and against hand-evaluated activation cases (clamp on and off).
 """
 from __future__ import annotations
 
@@ -103,3 +105,30 @@ def route_topk(logits, k: int, out_dt: str = "bf16"):
     top = np.take_along_axis(p, idx, axis=1)
     top = (top / top.sum(axis=1, keepdims=True)).astype(F32)
     return idx.astype(np.int64), round_to(top, out_dt)
+
+
+def gptoss_glu64(gate, up, alpha: float = 1.702, limit: float = 7.0):
+    """gpt-oss's clamped GLU in float64 (worker_quant.py:2301-2303): gate <= limit, up in
+    [-limit, limit], (up + 1) * gate * sigmoid(alpha * gate)."""
+    g = np.minimum(np.asarray(gate, np.float64), limit)
+    u = np.clip(np.asarray(up, np.float64), -limit, limit)
+    return (u + 1.0) * (g / (1.0 + np.exp(-alpha * g)))
+
+
+def gptoss_exact(x, idx, wts, Wgu, bgu, Wdn, bdn, alpha: float = 1.702, limit: float = 7.0) -> np.ndarray:
+    """float64 gpt-oss experts forward (worker_quant.py:2292-2309) over transpose-packed weights:
+    ``gu = Wgu[e] @ x[t] + bgu[e]`` with Wgu [E, 2I, H] (rows interleaved gate 2i / up 2i+1),
+    ``h = glu(gu[::2], gu[1::2])``, ``out[t] += w[t,j] * (Wdn[e] @ h + bdn[e])`` with Wdn [E, H, I],
+    evaluated expert by expert; no intermediate rounding."""
+    x = np.asarray(x, np.float64)
+    T, H = x.shape
+    idx = np.asarray(idx)
+    w = np.asarray(wts, np.float64)
+    out = np.zeros((T, np.asarray(Wdn).shape[1]), np.float64)
+    for e in np.unique(idx):
+        tok, slot = np.nonzero(idx == e)
+        gu = x[tok] @ np.asarray(Wgu[e], np.float64).T + np.asarray(bgu[e], np.float64)
+        h = gptoss_glu64(gu[:, 0::2], gu[:, 1::2], alpha, limit)
+        y = h @ np.asarray(Wdn[e], np.float64).T + np.asarray(bdn[e], np.float64)
+        np.add.at(out, tok, w[tok, slot][:, None] * y)
+    return out

@@ -30,6 +30,41 @@ def test_header_and_bindings_agree():
     assert _declared() == sorted(_lib.SIGNATURES)
 
 
+def _prototypes():
+    """name -> (return type, [parameter types]) of every declaration in the header."""
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    txt = re.sub(r"//[^\n]*", "", txt)
+    out = {}
+    for m in re.finditer(r"([A-Za-z_][A-Za-z0-9_ \*]*?)\b(imq_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", txt):
+        ret, name, params = m.group(1).strip(), m.group(2), m.group(3).strip()
+        types = []
+        if params and params != "void":
+            for p in params.split(","):
+                p = " ".join(p.split())
+                types.append(re.sub(r"\s*\b[a-zA-Z_][a-zA-Z0-9_]*$", "", p) if not p.endswith("*") else p)
+        out[name] = (ret, types)
+    return out
+
+
+def _ctype(c: str):
+    c = c.replace("const ", "").strip()
+    if c.endswith("*"):
+        return ctypes.c_char_p if c == "char*" or c == "char *" else ctypes.c_void_p
+    return {"int64_t": ctypes.c_int64, "int": ctypes.c_int, "float": ctypes.c_float,
+            "void": None}[c]
+
+
+def test_bindings_match_header_prototypes():
+    """Every SIGNATURES entry has the header's return type and parameter types, in order."""
+    protos = _prototypes()
+    assert sorted(protos) == sorted(_lib.SIGNATURES)
+    for name, (ret, params) in protos.items():
+        rt, at = _lib.SIGNATURES[name]
+        assert _ctype(ret) == rt, (name, ret)
+        assert [_ctype(p) for p in params] == list(at), name
+
+
 def test_library_exports_every_declared_symbol(L):
     missing = [n for n in _declared() if not hasattr(L, n)]
     assert not missing, missing
@@ -46,7 +81,7 @@ def test_exports_are_c_linkage():
 
 
 def test_abi_version_and_strerror(L):
-    assert L.imq_abi_version() == 2
+    assert L.imq_abi_version() == 3
     assert L.imq_strerror(0) == b"ok"
     for rc in (_lib.IMQ_ERR_INVALID, _lib.IMQ_ERR_UNSUPPORTED, _lib.IMQ_ERR_ALIGN):
         assert len(L.imq_strerror(rc)) > 5

@@ -113,3 +113,111 @@ def test_moe_repeat_identical(dev):
     b = (C.u8(dn[0], dev), t(dn[1]), t(dn[2]), I)
     ys = [ops.moe_experts_w4(x, idx, w, a, b, G) for _ in range(3)]
     assert all(torch.equal(ys[0], y) for y in ys[1:])
+
+
+# ---- gpt-oss experts (imq_moe_experts_w4_ex, act gptoss) ------------------------------------
+@functools.lru_cache(maxsize=2)
+def _gptoss_layer(E, H, I, seed, bias_std):
+    """gpt-oss stores its experts in-major ([E, H, 2I], [E, I, H]); they are transpose-packed."""
+    r = C.rng(seed)
+    Wgu_in = C.bf16_normal(r, (E, H, 2 * I), 0.02)
+    Wdn_in = C.bf16_normal(r, (E, I, H), 0.02)
+    bgu = C.bf16_normal(r, (E, 2 * I), bias_std)
+    bdn = C.bf16_normal(r, (E, H), 0.02)
+    gu = oq.pack_linear_int4_3d(Wgu_in, 128, "bf16", in_major=True)
+    dn = oq.pack_linear_int4_3d(Wdn_in, 128, "bf16", in_major=True)
+    Dgu = np.stack([oq.dequant_int4_3d(gu[0], gu[1], gu[2], e, H, 128) for e in range(E)])
+    Ddn = np.stack([oq.dequant_int4_3d(dn[0], dn[1], dn[2], e, I, 128) for e in range(E)])
+    return gu, dn, bgu, bdn, Dgu, Ddn
+
+
+def _run_gptoss(dev, E, H, I, k, T, seed, bias_std=0.02, pad_to_256=False):
+    import torch
+    from infinitemodel_amd import ops
+    gu, dn, bgu, bdn, Dgu, Ddn = _gptoss_layer(E, H, I, seed, bias_std)
+    r = C.rng(seed + 1)
+    idx, w = om.route_topk(r.standard_normal((T, E)).astype(np.float32), k)
+    x = C.bf16_normal(r, (T, H))
+    t = lambda a: C.to_torch(a, "bf16", dev)  # noqa: E731
+
+    def hold(p):
+        q, s, z = C.u8(p[0], dev), t(p[1]), t(p[2])
+        if pad_to_256 and (q.shape[2] * 2) % 256:
+            # the kernel layout of a holder: K padded with zero codes and zero scales
+            k2 = -(-q.shape[2] * 2 // 256) * 256
+            q2 = torch.zeros((*q.shape[:2], k2 // 2), dtype=torch.uint8, device=dev)
+            q2[:, :, :q.shape[2]] = q
+            s2 = torch.zeros((*s.shape[:2], k2 // 128), dtype=s.dtype, device=dev)
+            z2 = torch.zeros_like(s2)
+            s2[:, :, :s.shape[2]], z2[:, :, :z.shape[2]] = s, z
+            q, s, z = q2, s2, z2
+        return q, s, z
+
+    out = ops.moe_experts_w4(t(x), torch.from_numpy(idx).to(dev), t(w), (*hold(gu), H), (*hold(dn), I), 128,
+                             act="gptoss", gu_bias=t(bgu), dn_bias=t(bdn))
+    y = C.t2np(out)
+    exact = om.gptoss_exact(x, idx, w, Dgu, bgu, Ddn, bdn)
+    assert np.isfinite(y).all()
+    mr, me = oq.max_rel(y, exact), oq.mean_rel(y, exact)
+    assert mr <= MAX_REL and me <= MEAN_REL, (T, mr, me)
+    return y, exact
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_gptoss_token_sorted(dev, T):
+    """Token-sorted path (H, I multiples of 256): interleaved gate / up row pairs, biases."""
+    _run_gptoss(dev, E=8, H=512, I=256, k=2, T=T, seed=70 + T)
+
+
+def test_gptoss_clamps_active(dev):
+    """Gate-up biases of std 6 push many gate values above +limit and up values past +-limit."""
+    _, exact = _run_gptoss(dev, E=6, H=256, I=128, k=2, T=24, seed=77, bias_std=6.0)
+    assert np.isfinite(exact).all()
+
+
+@pytest.mark.parametrize("pad", [False, True])
+def test_gptoss_width_2880(dev, pad):
+    """gpt-oss-20b's widths H = I = 2880 (K_pad 2944, 23 groups): the per-row path as packed,
+    the token-sorted path once K is padded to 3072 with zero codes and scales."""
+    _run_gptoss(dev, E=4, H=2880, I=2880, k=2, T=3, seed=90, pad_to_256=pad)
+
+
+def test_gptoss_per_row_path(dev):
+    """H % 64 != 0 takes the per-row kernels with the gpt-oss activation and biases."""
+    _run_gptoss(dev, E=5, H=200, I=96, k=3, T=6, seed=91)
+
+
+def test_gptoss_module_install(dev):
+    """transformers GptOssExperts quantized by _quantize_experts4_ (transpose-pack, dedicated
+    forward, kernel layout after placement) against the oracle over its own packed weights."""
+    import torch
+    from transformers import GptOssConfig
+    from transformers.models.gpt_oss.modeling_gpt_oss import GptOssExperts
+    from infinitemodel_amd import worker_quant as wq
+    E, H, I, k, T = 6, 320, 160, 2, 9
+    cfg = GptOssConfig(hidden_size=H, intermediate_size=I, num_local_experts=E, num_experts_per_tok=k,
+                       num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=4, head_dim=16)
+    mod = GptOssExperts(cfg).to(torch.bfloat16)
+    r = C.rng(93)
+    with torch.no_grad():
+        for p, std in ((mod.gate_up_proj, 0.02), (mod.down_proj, 0.02), (mod.gate_up_proj_bias, 0.5),
+                       (mod.down_proj_bias, 0.02)):
+            p.copy_(torch.from_numpy(C.bf16_normal(r, tuple(p.shape), std)))
+    bgu = mod.gate_up_proj_bias.detach().float().numpy()
+    bdn = mod.down_proj_bias.detach().float().numpy()
+    wq._quantize_experts4_(mod)
+    assert getattr(mod, "_gptoss_fused_installed", False)
+    gu, dn = mod.gate_up_proj, mod.down_proj
+    Dgu = np.stack([oq.dequant_int4_3d(gu.qweight.numpy(), gu.scale.float().numpy(), gu.zero.float().numpy(),
+                                       e, H, 128) for e in range(E)])
+    Ddn = np.stack([oq.dequant_int4_3d(dn.qweight.numpy(), dn.scale.float().numpy(), dn.zero.float().numpy(),
+                                       e, I, 128) for e in range(E)])
+    mod.to(dev)
+    wq.finalize_placement(mod)
+    assert gu._kernel_tensors()[0].shape[2] * 2 == 512       # K_pad 384 -> kernel layout 512
+    idx, w = om.route_topk(r.standard_normal((T, E)).astype(np.float32), k)
+    x = C.bf16_normal(r, (T, H))
+    with torch.no_grad():
+        y = C.t2np(mod(C.to_torch(x, "bf16", dev), torch.from_numpy(idx).to(dev), C.to_torch(w, "bf16", dev)))
+    exact = om.gptoss_exact(x, idx, w, Dgu, bgu, Ddn, bdn)
+    assert oq.max_rel(y, exact) <= MAX_REL and oq.mean_rel(y, exact) <= MEAN_REL

@@ -294,3 +294,69 @@ def test_moe_exact_grouped_matches_per_token_loop():
     w2 = np.array(w, copy=True)
     w2[0, 0] = 0
     assert not np.allclose(om.moe_exact_grouped(x, idx, w2, Wgu, Wdn), a, rtol=1e-6, atol=1e-9)
+
+
+# --------------------------------------------------------------------------------------------
+# gpt-oss experts vs transformers' GptOssExperts
+# --------------------------------------------------------------------------------------------
+def _gptoss_case(E=6, H=64, I=48, k=2, T=7, seed=70, wscale=0.3):
+    r = np.random.default_rng(seed)
+    Wgu = r.standard_normal((E, 2 * I, H)) * wscale / np.sqrt(H)     # transpose-packed [E, 2I, H]
+    Wdn = r.standard_normal((E, H, I)) * 0.2 / np.sqrt(I)
+    bgu = r.standard_normal((E, 2 * I)) * 0.5
+    bdn = r.standard_normal((E, H)) * 0.5
+    x = r.standard_normal((T, H)) * 2.0
+    idx, w = om.route_topk(r.standard_normal((T, E)).astype(np.float32), k, out_dt="fp32")
+    return x, idx, w.astype(np.float64), Wgu, bgu, Wdn, bdn
+
+
+def _gptoss_module(E, H, I, k, Wgu, bgu, Wdn, bdn):
+    import torch
+    from transformers import GptOssConfig
+    from transformers.models.gpt_oss.modeling_gpt_oss import GptOssExperts
+    cfg = GptOssConfig(hidden_size=H, intermediate_size=I, num_local_experts=E, num_experts_per_tok=k,
+                       num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=4, head_dim=16)
+    mod = GptOssExperts(cfg).to(torch.float64)
+    with torch.no_grad():
+        mod.gate_up_proj.copy_(torch.from_numpy(np.ascontiguousarray(Wgu.transpose(0, 2, 1))))   # in-major
+        mod.gate_up_proj_bias.copy_(torch.from_numpy(bgu))
+        mod.down_proj.copy_(torch.from_numpy(np.ascontiguousarray(Wdn.transpose(0, 2, 1))))
+        mod.down_proj_bias.copy_(torch.from_numpy(bdn))
+    return mod
+
+
+@pytest.mark.parametrize("wscale", [0.3, 6.0])
+def test_gptoss_exact_matches_transformers_gptoss_experts(wscale):
+    """float64 agreement with a live GptOssExperts fed the in-major transpose of the oracle's
+    weights; wscale 6 drives gate / up past +-limit so both clamps take part."""
+    import torch
+    E, H, I, k = 6, 64, 48, 2
+    x, idx, w, Wgu, bgu, Wdn, bdn = _gptoss_case(E, H, I, k, wscale=wscale)
+    mod = _gptoss_module(E, H, I, k, Wgu, bgu, Wdn, bdn)
+    with torch.no_grad():
+        ref = mod(torch.from_numpy(x), torch.from_numpy(idx), torch.from_numpy(w)).numpy()
+    ours = om.gptoss_exact(x, idx, w, Wgu, bgu, Wdn, bdn, mod.alpha, mod.limit)
+    np.testing.assert_allclose(ours, ref, rtol=1e-10, atol=1e-12)
+    gu = np.einsum("th,eoh->teo", x, Wgu) + bgu[None]
+    clamped = (gu[..., 0::2] > mod.limit).any() and (np.abs(gu[..., 1::2]) > mod.limit).any()
+    assert clamped == (wscale > 1)
+    # negative controls: gate / up swapped, a dropped bias, and (when active) no clamp
+    sw = np.empty_like(Wgu)
+    sw[:, 0::2], sw[:, 1::2] = Wgu[:, 1::2], Wgu[:, 0::2]
+    bsw = np.empty_like(bgu)
+    bsw[:, 0::2], bsw[:, 1::2] = bgu[:, 1::2], bgu[:, 0::2]
+    assert oq.max_rel(om.gptoss_exact(x, idx, w, sw, bsw, Wdn, bdn), ref) > 0.05
+    assert oq.max_rel(om.gptoss_exact(x, idx, w, Wgu, bgu, Wdn, 0 * bdn), ref) > 0.05
+    if clamped:
+        assert oq.max_rel(om.gptoss_exact(x, idx, w, Wgu, bgu, Wdn, bdn, limit=1e30), ref) > 0.05
+
+
+def test_gptoss_glu_hand_cases():
+    """(up + 1) * gate * sigmoid(alpha * gate) with gate clamped above at limit and up clamped to
+    [-limit, limit], evaluated by hand."""
+    a, L = 1.702, 7.0
+    sig = lambda v: 1.0 / (1.0 + np.exp(-v))
+    cases = [(0.5, 0.25, 1.25 * 0.5 * sig(a * 0.5)), (9.0, 2.0, 3.0 * 7.0 * sig(a * 7.0)),
+             (-9.0, 20.0, 8.0 * -9.0 * sig(-a * 9.0)), (1.0, -8.0, -6.0 * 1.0 * sig(a)), (0.0, 3.0, 0.0)]
+    for g, u, want in cases:
+        assert om.gptoss_glu64(g, u, a, L) == pytest.approx(want, rel=1e-15, abs=1e-300)
