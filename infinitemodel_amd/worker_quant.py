@@ -382,6 +382,8 @@ _QUANT_LINEAR2 = None
 _QUANT_LINEAR = None
 _PACKED4_3D = None
 _W4A16_EXPERT = None
+_PACKED8_3D = None
+_W8A16_EXPERT = None
 
 
 def _quant4_linear_cls():
@@ -845,6 +847,228 @@ def _install_gptoss_fused_forward(experts_mod) -> None:
     experts_mod._gptoss_fused_installed = True
     experts_mod.forward = types.MethodType(_forward, experts_mod)
     _log("[int4] gpt-oss fused experts active (transpose-packed w4a16 + interleaved SwiGLU)")
+
+
+# ---- int8 fused 3D experts (worker_quant.py:2707-2990) ---------------------------------------
+def _w8a16_experts_ok(dev) -> bool:
+    """Should Packed8Tensor3D hand the eager MoE loop the w8a16 expert subclass instead of a
+    dequantized weight (worker_quant.py:2711-2731)? On a ROCm device unless IM_W8A16_EXPERTS=0 or
+    IM_FUSED_W8A16=0; never on the CPU."""
+    if os.environ.get("IM_W8A16_EXPERTS", "") == "0" or not _FUSED_W8A16:
+        return False
+    return _is_rocm_device(dev)
+
+
+def _w8a16_expert_cls():
+    """Tensor subclass for one expert's int8 weight (worker_quant.py:2734-2806): ``F.linear`` of
+    a bf16 activation runs the HIP w8a16 op on the int8 bytes; every other op materializes
+    ``qweight.to(scale.dtype) * scale``. None when libimq is unavailable."""
+    global _W8A16_EXPERT
+    if _W8A16_EXPERT is not None:
+        return _W8A16_EXPERT
+    with _BUILD_LOCK:
+        if _W8A16_EXPERT is not None:
+            return _W8A16_EXPERT
+        op = _w8a16_hip_op()
+        if op is None:
+            return None
+        import torch
+        import torch.nn.functional as F
+
+        class _W8A16Weight(torch.Tensor):
+            @staticmethod
+            def __new__(cls, packed, scale):
+                out, in_f = packed.shape
+                t = torch.Tensor._make_wrapper_subclass(cls, (out, in_f), dtype=scale.dtype,
+                                                        device=packed.device, requires_grad=False)
+                t._packed = packed          # int8 [out, in]
+                t._scale = scale            # [out, 1]
+                return t
+
+            def _materialize(self):
+                return (self._packed.to(self._scale.dtype) * self._scale).contiguous()
+
+            @classmethod
+            def __torch_function__(cls, func, types, args=(), kwargs=None):
+                kwargs = kwargs or {}
+                if func is F.linear or getattr(func, "__name__", "") == "linear":
+                    inp = args[0]
+                    w = args[1] if len(args) > 1 else kwargs.get("weight")
+                    bias = args[2] if len(args) > 2 else kwargs.get("bias")
+                    # bf16 activations only, as the dense int8 path gates (worker_quant.py:2770-2774)
+                    if isinstance(w, cls) and getattr(inp, "dtype", None) is torch.bfloat16:
+                        y = op(inp, w._packed, w._scale)
+                        if inp.dim() > 2:
+                            y = y.reshape(*inp.shape[:-1], y.shape[-1])
+                        return y if bias is None else y + bias.to(y.dtype)
+                mat = [a._materialize() if isinstance(a, cls) else a for a in args]
+                mkw = {k: (v._materialize() if isinstance(v, cls) else v) for k, v in kwargs.items()}
+                return func(*mat, **mkw)
+
+            @classmethod
+            def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+                kwargs = kwargs or {}
+                mat = [a._materialize() if isinstance(a, cls) else a for a in args]
+                mkw = {k: (v._materialize() if isinstance(v, cls) else v) for k, v in kwargs.items()}
+                return func(*mat, **mkw)
+
+        _W8A16_EXPERT = _W8A16Weight
+    return _W8A16_EXPERT
+
+
+def _packed8_3d_cls():
+    """Packed8Tensor3D(qweight int8 [E, out, in], scale [E, out, 1], in_features)
+    (worker_quant.py:2813-2897): all of one projection's experts at int8 behind the eager
+    experts loop's ``self.gate_up_proj[e]`` indexing."""
+    global _PACKED8_3D
+    if _PACKED8_3D is not None:
+        return _PACKED8_3D
+    with _BUILD_LOCK:
+        if _PACKED8_3D is not None:
+            return _PACKED8_3D
+        import torch
+        from torch import nn
+
+        class Packed8Tensor3D(nn.Module):
+            def __init__(self, qweight, scale, in_features):
+                super().__init__()
+                self.register_buffer("qweight", qweight)   # int8 [E, out, in]
+                self.register_buffer("scale", scale)        # [E, out, 1]
+                self.in_features = in_features
+                self._expert_triton = None                  # fused-expert weights enabled (lazy)
+
+            def _expert_selfcheck(self) -> bool:
+                """One-time check of the w8a16 expert subclass against the dequant it replaces,
+                at M = 1 and M = 8 (mean rel < 0.05)."""
+                import torch.nn.functional as F
+                wc = _w8a16_expert_cls()
+                if wc is None:
+                    return False
+                w0 = wc(self.qweight[0], self.scale[0])
+                wref = w0._materialize()
+                for M in (1, 8):
+                    xt = torch.randn(M, self.in_features, device=self.qweight.device, dtype=torch.bfloat16)
+                    yn = F.linear(xt, wref).float()
+                    yf = F.linear(xt, w0).float()
+                    rel = ((yf - yn).abs().mean() / (yn.abs().mean() + 1e-6)).item()
+                    if not (rel < 0.05):
+                        _log(f"[int8] hip w8a16 experts self-check rel={rel:.3f} at M={M} -> dequant")
+                        return False
+                _log(f"[int8] hip w8a16 experts active (rel={rel:.4f})")
+                return True
+
+            def __getitem__(self, e):
+                """Expert e's weight for ``F.linear(bf16_x, w)``: the w8a16 subclass on a ROCm
+                device with a bf16 scale once it self-checks, else ``q.to(dt) * scale``."""
+                e = int(e)
+                if self._expert_triton is None:
+                    self._expert_triton = False
+                    with contextlib.suppress(Exception):
+                        if _w8a16_experts_ok(self.qweight.device) and self.scale.dtype is torch.bfloat16:
+                            self._expert_triton = self._expert_selfcheck()
+                if self._expert_triton:
+                    return _w8a16_expert_cls()(self.qweight[e], self.scale[e])
+                return (self.qweight[e].to(self.scale.dtype) * self.scale[e]).contiguous()
+
+        _PACKED8_3D = Packed8Tensor3D
+    return _PACKED8_3D
+
+
+def _pack8_3d(W3):
+    """Fused expert tensor [E, out, in] -> Packed8Tensor3D, one expert at a time through the 2D
+    int8 packer (worker_quant.py:2900-2921): per-row scales never cross an expert, so this equals
+    the 2D packer on every expert slice."""
+    import torch
+    E, out, in_f = W3.shape
+    q = torch.empty((E, out, in_f), dtype=torch.int8, device=W3.device)
+    sc = torch.empty((E, out, 1), dtype=W3.dtype, device=W3.device)
+    for e in range(E):
+        qe, se = _pack8_expert(W3[e])
+        q[e] = qe
+        sc[e] = se
+    return _packed8_3d_cls()(q, sc, in_f)
+
+
+def _quantize_experts8_(module) -> None:
+    """int8 twin of ``_quantize_experts4_`` (worker_quant.py:2924-2987): 3D ``gate_up_proj`` /
+    ``down_proj`` Parameters -> Packed8Tensor3D and the eager experts implementation. Refuses
+    gpt-oss (no int8 form of its transpose-packed fused forward) and meta experts (streaming is
+    int4-only). No fused-MoE forward is installed: int8 experts run the eager loop, each routed
+    expert through the w8a16 subclass."""
+    from torch import nn
+    targets = []
+    for sub in module.modules():
+        is_go = _is_gptoss_experts(sub)
+        for attr in ("gate_up_proj", "down_proj"):
+            p = sub._parameters.get(attr)
+            if isinstance(p, nn.Parameter) and p.dim() == 3:
+                targets.append((sub, attr, is_go))
+    if not targets:
+        return
+    if any(is_go for _s, _a, is_go in targets):
+        raise RuntimeError("gpt-oss fused experts have no int8 path (in-major transpose-packed "
+                           "weights need the fused w4a16 MoE forward) -- load gpt-oss at int4")
+    for sub, attr, _is_go in targets:
+        p = getattr(sub, attr)
+        if getattr(p, "is_meta", False):
+            raise RuntimeError(f"int8 MoE: {type(sub).__name__}.{attr} is META -- per-expert "
+                               "expert streaming is int4-only; load this model at int4")
+        delattr(sub, attr)
+        setattr(sub, attr, _pack8_3d(p.data))
+    seen = set()
+    for sub, _attr, _is_go in targets:
+        cfg = getattr(sub, "config", None)
+        if cfg is not None and hasattr(cfg, "_experts_implementation") and id(cfg) not in seen:
+            cfg._experts_implementation = "eager"
+            seen.add(id(cfg))
+
+
+def _quantize_int8_(module) -> None:
+    """int8 a decoder layer (worker_quant.py:578-596): every nn.Linear except routers, then the
+    fused 3D routed experts."""
+    _quantize_int8_linears_(module)
+    _quantize_experts8_(module)
+
+
+def apply_head_quant(model, head, head_quant: str, head_device=None):
+    """The ``head_quant`` load option (client.py:799-840): ``"int8"`` packs a GPU-resident
+    ``nn.Linear`` lm_head to an int8 QuantLinear (kept bf16 on the CPU, when tied to the
+    embedding, or when the load tier already packed it); ``"bf16"`` keeps the head. Returns the
+    head to use (also set as ``model.lm_head`` when replaced). Any failure keeps the head as built."""
+    import torch
+    hq = (head_quant or "").strip().lower()
+    if not hq or head is None:
+        return head
+    try:
+        if hq not in ("int8", "bf16"):
+            raise ValueError(f"head_quant={hq!r} unsupported (int8 | bf16); int4 on the lm_head was "
+                             "measured and rejected")
+        dev = head_device if head_device is not None else next(head.parameters()).device
+        dev = torch.device(dev)
+        tied = bool(getattr(getattr(model, "config", None), "tie_word_embeddings", False))
+        if hq == "int8" and dev.type != "cuda":
+            _log(f"[head-quant] int8 head SKIPPED: lm_head is on {dev} and the w8a16 kernel is "
+                 "GPU-only -- bf16 is faster there")
+        elif hq == "int8" and not isinstance(head, torch.nn.Linear):
+            _log(f"[head-quant] int8 head already packed by the load tier ({type(head).__name__})")
+        elif hq == "int8" and tied:
+            _log("[head-quant] int8 head SKIPPED: tie_word_embeddings -- lm_head aliases "
+                 "embed_tokens, so packing it would add a copy, not replace one")
+        elif hq == "int8":
+            nbytes = head.weight.numel() * head.weight.element_size()
+            q = _quantize_linear(head.to("cpu")).to(dev)
+            head = q
+            if hasattr(model, "lm_head"):
+                model.lm_head = q
+            pk = q.qweight.numel() + q.scale.numel() * q.scale.element_size()
+            _log(f"[head-quant] lm_head int8: {nbytes / 2**30:.2f} GB bf16 -> {pk / 2**30:.2f} GB "
+                 f"({nbytes / max(1, pk):.1f}x fewer bytes read per decoded token)")
+        elif hq == "bf16" and not isinstance(head, torch.nn.Linear):
+            _log("[head-quant] bf16 head requested but the head is already quantized by the load "
+                 "tier -- leaving it")
+    except Exception as exc:
+        _log(f"[head-quant] FAILED ({exc!r}) -> leaving the lm_head as built")
+    return head
 
 
 # ---- packers (worker_quant.py:511-536, 1588-1608, 1921-1944, 2394-2436) ---------------------
