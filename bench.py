@@ -18,7 +18,9 @@ linears, launched back to back on one stream and replayed as a HIP graph.
 
 Other configs print lines of the same shape: --config c1 (single 1x4096->4096 linear), c3 (int2
 g64 70B shapes), c4 (prefill, --quant int4|int8, --m 512|2048), c5 (OLMoE fused MoE, --m = T),
-and ``copy`` (the plain device copy used to calibrate the PMC byte counters).
+gptoss (gpt-oss-20b fused experts, --m = T), head (int8 lm_head decode at the Qwen2.5-7B head,
+152064 x 3584, --m rows) and ``copy`` (the plain device copy used to calibrate the PMC byte
+counters).
 """
 from __future__ import annotations
 
@@ -40,7 +42,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "gptoss", "head", "copy"])
     ap.add_argument("--m", type=int, default=None, help="rows: C2/C3/C4 M, C5 tokens T")
     ap.add_argument("--quant", default="int4", choices=["int4", "int8"], help="C4 weight format")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -400,6 +402,68 @@ def bench_c5(args, dev):
 
 
 # ---------------------------------------------------------------------------------------------
+# gpt-oss-20b fused experts (transpose-packed int4, interleaved clamped GLU, per-expert biases)
+# ---------------------------------------------------------------------------------------------
+def bench_gptoss(args, dev):
+    import torch
+    from infinitemodel_amd import ops, workloads as wl
+    T = args.m or 1
+    E, k, H, I = 32, 4, 2880, 2880
+    layers = [wl.gptoss_layer(dev, seed=5000 + 7 * l) for l in range(4)]
+    idx, w = wl.olmoe_routing(T, dev, E=E, k=k)
+    x = wl.activations(T, H, 13, dev)
+
+    def step():
+        for gu, dn, bgu, bdn in layers:
+            ops.moe_experts_w4(x, idx, w, gu, dn, 128, act="gptoss", gu_bias=bgu, dn_bias=bdn)
+
+    ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
+    U = int(torch.unique(idx).numel())
+    ng = -(-H // 128)                      # 23 groups: the reference's packed K_pad 2944
+    per_expert = (2 * I + H) * (ng * 64 + ng * 2 * 2) + (2 * I + H) * 2     # codes + s/z + biases
+    nbytes = U * per_expert + T * H * 2 * 2 + idx.numel() * 6
+    us = ms * 1e3 / len(layers)
+    roof = _hbm_roofline("imq_moe_experts_w4_ex gptoss (one MoE layer)", nbytes, us, _traffic(f"gptoss_t{T}"))
+    cfg = {"workload": f"gpt-oss-20b fused experts, T={T}, top-{k} of {E}, H=I={H}, 4 layers", "T": T,
+           "distinct_experts": U, "bytes_per_layer": nbytes, "layers_per_step": len(layers),
+           "note": "algorithmic bytes count the reference's K_pad 2944 packing; the kernel layout "
+                   "reads rows padded to 3072"}
+    return _line(round(nbytes * len(layers) / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, None)
+
+
+# ---------------------------------------------------------------------------------------------
+# int8 lm_head decode (head_quant=int8) at the Qwen2.5-7B head
+# ---------------------------------------------------------------------------------------------
+def bench_head(args, dev):
+    import torch
+    from infinitemodel_amd import ops, workloads as wl
+    M = args.m or 1
+    N, K = 152064, 3584
+    q, s = wl.int8_linear(N, K, 17, dev, dtype=torch.bfloat16)
+    x = wl.activations(M, K, 18, dev)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ms = _time_steps(_graph_or_eager(lambda: ops.linear_w8(x, q, s, out=y), not args.no_graph), args.steps,
+                     args.warmup)
+    nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
+    roof = _hbm_roofline("imq_linear_w8 decode kernel", nbytes, ms * 1e3, _traffic(f"head_m{M}"))
+    cfg = {"workload": f"int8 lm_head 3584 -> 152064 (Qwen2.5-7B), M={M}", "M": M,
+           "weights": "int8 per-row symmetric, bf16 scale"}
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cpu_path
+        n = cpu_path.tune_cpu_threads()
+        rows = 16384
+        qc, sc_, xc = q[:rows].cpu(), s[:rows].cpu(), x.cpu()
+        med, runs = _cpu_time(lambda: cpu_path.naive_linear_int8(xc, qc, sc_), args.cpu_seconds)
+        cb = rows * K + rows * 2 + M * K * 2 + M * rows * 2
+        cpu = {"value": round(cb / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
+               "sample": f"the reference's CPU int8 forward (naive dequant + F.linear, worker_quant.py:"
+                         f"411-417, 439-440) over the first {rows} head rows, median of {runs}",
+               "cpu": _cpu_model()}
+    return _line(round(nbytes / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
+
+
+# ---------------------------------------------------------------------------------------------
 def bench_copy(args, dev):
     """Plain device copy of 1 GiB (read 1 GiB + write 1 GiB per launch): calibrates the PMC
     FETCH_SIZE / WRITE_SIZE counters against known bytes."""
@@ -413,7 +477,8 @@ def bench_copy(args, dev):
                  {"workload": "device copy 1 GiB -> 1 GiB", "bytes_read": n, "bytes_written": n}, roof, None)
 
 
-BENCH = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "copy": bench_copy}
+BENCH = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "gptoss": bench_gptoss,
+         "head": bench_head, "copy": bench_copy}
 
 
 def main():

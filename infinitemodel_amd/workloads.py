@@ -102,3 +102,24 @@ def olmoe_routing(T: int, dev, E: int = 64, k: int = 8, seed: int = 4):
     top, idx = torch.topk(p, k, dim=-1)
     top = top / top.sum(dim=-1, keepdim=True)
     return idx, top.to(torch.bfloat16)
+
+
+def gptoss_layer(dev, seed: int = 5000, E: int = 32, H: int = 2880, I: int = 2880, G: int = 128):
+    """gpt-oss-20b experts: gate_up / down transpose-packed to [E, 2I, H] / [E, H, I] (rows of
+    gate_up interleaved gate / up), RTN int4 g128 of N(0, 0.02), bf16 s/z and per-expert bf16
+    biases N(0, 0.02); returned in the fused kernels' layout (Packed4Tensor3D._kernel_tensors:
+    K 2880 padded to 3072 with zero codes and scales)."""
+    import torch
+    from . import worker_quant as wq
+    PT = wq._packed4_3d_cls()
+    Wg = (torch.randn(E, 2 * I, H, generator=_gen(seed, dev), device=dev) * 0.02).to(torch.bfloat16)
+    gq, gs, gz, _, _ = pack_linear_int4_3d(Wg, G)
+    del Wg
+    Wd = (torch.randn(E, H, I, generator=_gen(seed + 500, dev), device=dev) * 0.02).to(torch.bfloat16)
+    dq, ds, dz, _, _ = pack_linear_int4_3d(Wd, G)
+    del Wd
+    gh, dh = PT(gq, gs, gz, H, G), PT(dq, ds, dz, I, G)
+    g = _gen(seed + 900, dev)
+    bgu = (torch.randn(E, 2 * I, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    bdn = (torch.randn(E, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    return (*gh._kernel_tensors(), H), (*dh._kernel_tensors(), I), bgu, bdn
