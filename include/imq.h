@@ -134,9 +134,10 @@ int imq_moe_rows_w4(const void* x, int64_t x_row_stride, int64_t B, int64_t K_pa
  * _install_fused_moe_forward, worker_quant.py:2131-2248, whose semantics are the transformers
  * eager experts loop): out[t] = sum_j w[t,j] * down_e( silu(gate) * up ), [gate | up] =
  * gate_up_e(x[t]), e = topk_idx[t,j].
- *   hidden bf16 [T, H_pad] (row stride; zero beyond H when H_pad > H), topk_idx int32 [T, k]
- *   contiguous, topk_w bf16 [T, k] contiguous, gate_up stack [E, 2I, H_pad/2] + s/z [E, 2I, ng1],
- *   down stack [E, H, I_pad/2] + s/z [E, H, ng2] (scale and zero share strides), out bf16 [T, H].
+ *   hidden bf16 [T, H_pad] (row stride; zero beyond H when H_pad > H), or rows of just H
+ *   columns when H % 8 == 0 (read as zero past H); topk_idx int32 [T, k] contiguous, topk_w
+ *   bf16 [T, k] contiguous, gate_up stack [E, 2I, H_pad/2] + s/z [E, 2I, ng1], down stack
+ *   [E, H, I_pad/2] + s/z [E, H, ng2] (scale and zero share strides), out bf16 [T, H].
  *   workspace: device bytes >= imq_moe_workspace_bytes(T, k, E, H, I, G); contents need not be
  *   initialised; calls sharing a workspace must be stream-ordered. */
 int64_t imq_moe_workspace_bytes(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I,

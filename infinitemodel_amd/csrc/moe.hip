@@ -24,10 +24,12 @@ constexpr int64_t kAlign = 256;
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // One wave per (row b, output channel n). Lane l handles 8-code words l, l+64, ...
-// Output fp32 (OUT_F32) or bf16. x row for b is x + (b / xdiv) * sxm.
+// Output fp32 (OUT_F32) or bf16. x row for b is x + (b / xdiv) * sxm; its columns >= xk (a
+// multiple of 8) are never read but taken as zero, as the reference's zero-padded activation
+// (the read is clamped into the row, the value replaced by zeros).
 template <int SDT, bool OUT_F32>
 __global__ __launch_bounds__(256) void moe_rows_kernel(
-    const uint16_t* __restrict__ x, int64_t sxm, int64_t xdiv, int64_t B, int64_t Kpad,
+    const uint16_t* __restrict__ x, int64_t sxm, int64_t xdiv, int64_t xk, int64_t B, int64_t Kpad,
     const int32_t* __restrict__ eid, int64_t E, const uint8_t* __restrict__ q, int64_t sqe, int64_t sqn,
     const void* __restrict__ sc, int64_t sse, int64_t ssn, int64_t ssg, const void* __restrict__ zr,
     int64_t sze, int64_t szn, int64_t szg, int64_t N, int64_t G, void* __restrict__ y, int64_t sym) {
@@ -43,7 +45,9 @@ __global__ __launch_bounds__(256) void moe_rows_kernel(
   const int64_t words = Kpad / 8;
   for (int64_t wd = lane; wd < words; wd += 64) {
     const uint32_t w = *(const uint32_t*)(qr + wd * 4);
-    const u32x4_t xv = *(const u32x4_t*)(xr + wd * 8);
+    const bool xin = wd * 8 < xk;
+    u32x4_t xv = *(const u32x4_t*)(xr + (xin ? wd * 8 : xk - 8));
+    if (!xin) xv = u32x4_t{0u, 0u, 0u, 0u};
     const int64_t g = (wd * 8) / G;
     const float s = load_as_bf16_f32<SDT>(sc, e * sse + n * ssn + g * ssg);
     const float z = load_as_bf16_f32<SDT>(zr, e * sze + n * szn + g * szg);
@@ -227,13 +231,15 @@ struct MoeLineArgs {
   int64_t sbe;
   int bdt;
   float alpha, limit;    // MODE 2 activation
+  int xk;                // valid x columns (a multiple of 8): columns past them read as zero
 };
 
 IMQ_DEV float moe_row_swap8(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
 }
 
-template <int S2, int NTL, int SDT, int MODE>
+// XCL: activation rows shorter than K (a.xk < a.Kpad), read with the clamp-and-zero of xk.
+template <int S2, int NTL, int SDT, int MODE, bool XCL>
 __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
@@ -355,7 +361,15 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
         float sum = 0.f;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const u32x4_t v = *(const u32x4_t*)(xr + kMoeLine * l + 128 * h + 32 * ar + 8 * kk);
+          const int col = kMoeLine * l + 128 * h + 32 * ar + 8 * kk;
+          u32x4_t v;
+          if constexpr (XCL) {
+            const bool xin = col < a.xk;
+            v = *(const u32x4_t*)(xr + (xin ? col : a.xk - 8));
+            if (!xin) v = u32x4_t{0u, 0u, 0u, 0u};
+          } else {
+            v = *(const u32x4_t*)(xr + col);
+          }
 #pragma unroll
           for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
           A[h][kk] = __builtin_bit_cast(bf16x8_t, permute_x8(v));
@@ -485,11 +499,11 @@ __global__ __launch_bounds__(256) void moe_zero_pad_kernel(uint16_t* __restrict_
   }
 }
 
-template <int S2, int NTL, int SDT, int MODE>
+template <int S2, int NTL, int SDT, int MODE, bool XCL>
 int moe_line_launch(const MoeLineArgs& a, int W, int grid, hipStream_t st) {
   const size_t lds = (size_t)W * 2 * NTL * 16 * (S2 * ((SDT == IMQ_DT_FP32) ? 4 : 2) / 2) * 4 +
                      (size_t)W * NTL * 256 * 4;
-  auto kern = moe_line_kernel<S2, NTL, SDT, MODE>;
+  auto kern = moe_line_kernel<S2, NTL, SDT, MODE, XCL>;
   if (lds > 65536) {
     hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (err != hipSuccess) return (int)err;
@@ -523,8 +537,12 @@ int moe_line_dispatch(MoeLineArgs a, int rows, hipStream_t st) {
   a.NB = rows / (16 * NTL);
   const int64_t items = (int64_t)a.E * a.NB;
   if (items > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
-  if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE>(a, W, (int)items, st);
-  return moe_line_launch<2, NTL, SDT, MODE>(a, W, (int)items, st);
+  if (a.xk < a.Kpad) {
+    if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, true>(a, W, (int)items, st);
+    return moe_line_launch<2, NTL, SDT, MODE, true>(a, W, (int)items, st);
+  }
+  if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, false>(a, W, (int)items, st);
+  return moe_line_launch<2, NTL, SDT, MODE, false>(a, W, (int)items, st);
 }
 
 template <int MODE>
@@ -538,7 +556,7 @@ int moe_line_sdt(const MoeLineArgs& a, int rows, int sdt, hipStream_t st) {
 }
 
 template <bool OUT_F32>
-int launch_rows(const uint16_t* x, int64_t sxm, int64_t xdiv, int64_t B, int64_t Kpad, const int32_t* eid,
+int launch_rows(const uint16_t* x, int64_t sxm, int64_t xdiv, int64_t xk, int64_t B, int64_t Kpad, const int32_t* eid,
                 int64_t E, const uint8_t* q, int64_t sqe, int64_t sqn, const void* sc, int64_t sse, int64_t ssn,
                 int64_t ssg, const void* zr, int64_t sze, int64_t szn, int64_t szg, int sdt, int64_t N, int64_t G,
                 void* y, int64_t sym, hipStream_t st) {
@@ -547,13 +565,13 @@ int launch_rows(const uint16_t* x, int64_t sxm, int64_t xdiv, int64_t B, int64_t
   dim3 grid((unsigned)imq_cdiv(N, 4), (unsigned)B);
   switch (sdt) {
     case IMQ_DT_BF16:
-      moe_rows_kernel<IMQ_DT_BF16, OUT_F32><<<grid, dim3(256), 0, st>>>(x, sxm, xdiv, B, Kpad, eid, E, q, sqe, sqn, sc, sse, ssn, ssg, zr, sze, szn, szg, N, G, y, sym);
+      moe_rows_kernel<IMQ_DT_BF16, OUT_F32><<<grid, dim3(256), 0, st>>>(x, sxm, xdiv, xk, B, Kpad, eid, E, q, sqe, sqn, sc, sse, ssn, ssg, zr, sze, szn, szg, N, G, y, sym);
       break;
     case IMQ_DT_FP16:
-      moe_rows_kernel<IMQ_DT_FP16, OUT_F32><<<grid, dim3(256), 0, st>>>(x, sxm, xdiv, B, Kpad, eid, E, q, sqe, sqn, sc, sse, ssn, ssg, zr, sze, szn, szg, N, G, y, sym);
+      moe_rows_kernel<IMQ_DT_FP16, OUT_F32><<<grid, dim3(256), 0, st>>>(x, sxm, xdiv, xk, B, Kpad, eid, E, q, sqe, sqn, sc, sse, ssn, ssg, zr, sze, szn, szg, N, G, y, sym);
       break;
     case IMQ_DT_FP32:
-      moe_rows_kernel<IMQ_DT_FP32, OUT_F32><<<grid, dim3(256), 0, st>>>(x, sxm, xdiv, B, Kpad, eid, E, q, sqe, sqn, sc, sse, ssn, ssg, zr, sze, szn, szg, N, G, y, sym);
+      moe_rows_kernel<IMQ_DT_FP32, OUT_F32><<<grid, dim3(256), 0, st>>>(x, sxm, xdiv, xk, B, Kpad, eid, E, q, sqe, sqn, sc, sse, ssn, ssg, zr, sze, szn, szg, N, G, y, sym);
       break;
     default:
       return IMQ_ERR_INVALID;
@@ -578,7 +596,7 @@ extern "C" int imq_moe_rows_w4(const void* x, int64_t x_row_stride, int64_t B, i
   if (q_row_stride < K_pad / 2 || x_row_stride < K_pad || y_row_stride < N) return IMQ_ERR_INVALID;
   if (!aligned(qweight, 4) || (q_row_stride % 4) || (q_stride_e % 4) || !aligned(x, 16) || (x_row_stride % 8))
     return IMQ_ERR_ALIGN;
-  return launch_rows<false>((const uint16_t*)x, x_row_stride, 1, B, K_pad, eid, E, (const uint8_t*)qweight,
+  return launch_rows<false>((const uint16_t*)x, x_row_stride, 1, K_pad, B, K_pad, eid, E, (const uint8_t*)qweight,
                             q_stride_e, q_row_stride, scale, s_stride_e, s_stride_n, s_stride_g, zero,
                             z_stride_e, z_stride_n, z_stride_g, sz_dtype, N, group_size, y, y_row_stride,
                             (hipStream_t)stream);
@@ -640,6 +658,7 @@ struct MoeCall {
   float alpha, limit;
   uint16_t* out;
   int64_t os;
+  int64_t xk;            // valid hidden columns: gu_K_pad for padded rows, else H (H % 8 == 0)
 };
 
 // Token-sorted grouped path; IMQ_ERR_UNSUPPORTED when the shape or layout does not qualify.
@@ -664,18 +683,20 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit);
   IMQ_LAUNCH_CHECK();
   MoeLineArgs g{c.hidden, c.hs, (int)c.gK, (int)c.k, off, perm, hit, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn,
-                (int)c.E, 0, (int)c.I, h, L.hw, c.gb, c.gbe, c.bdt, c.alpha, c.limit};
+                (int)c.E, 0, (int)c.I, h, L.hw, c.gb, c.gbe, c.bdt, c.alpha, c.limit, (int)c.xk};
   int rc = c.act == IMQ_ACT_GPTOSS ? moe_line_sdt<2>(g, (int)(2 * c.I), c.sdt, st)
                                    : moe_line_sdt<0>(g, (int)(2 * c.I), c.sdt, st);
   if (rc != IMQ_OK) return rc;
-  if (c.dK > c.I) {
+  // h's columns past I read as zero when I % 8 == 0; otherwise the partial last 8 is zeroed here
+  const int64_t hxk = c.I % 8 == 0 ? c.I : c.dK;
+  if (hxk > c.I) {
     const int64_t total = B * (c.dK - c.I);
     const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
     moe_zero_pad_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(h, B, c.I, c.dK, L.hw);
     IMQ_LAUNCH_CHECK();
   }
   MoeLineArgs d{h, L.hw, (int)c.dK, (int)c.k, off, perm, hit, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn,
-                (int)c.E, 0, 0, yr, c.H, c.db, c.dbe, c.bdt, 0.f, 0.f};
+                (int)c.E, 0, 0, yr, c.H, c.db, c.dbe, c.bdt, 0.f, 0.f, (int)hxk};
   rc = moe_line_sdt<1>(d, (int)c.H, c.sdt, st);
   if (rc != IMQ_OK) return rc;
   const int64_t total = c.T * (c.H / 8);
@@ -691,7 +712,7 @@ int moe_per_row(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   float* gu = (float*)(ws + L.gu);
   uint16_t* h = (uint16_t*)(ws + L.h);
   float* z = (float*)(ws + L.z);
-  int rc = launch_rows<true>(c.hidden, c.hs, c.k, B, c.gK, c.idx, c.E, c.gq, c.gqe, c.gqn, c.gs, c.gse, c.gsn, 1,
+  int rc = launch_rows<true>(c.hidden, c.hs, c.k, c.xk, B, c.gK, c.idx, c.E, c.gq, c.gqe, c.gqn, c.gs, c.gse, c.gsn, 1,
                              c.gz, c.gse, c.gsn, 1, c.sdt, 2 * c.I, c.G, gu, 2 * c.I, st);
   if (rc != IMQ_OK) return rc;
   {
@@ -705,7 +726,7 @@ int moe_per_row(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
                                                                    c.bdt, c.alpha, c.limit, h);
     IMQ_LAUNCH_CHECK();
   }
-  rc = launch_rows<true>(h, L.hw, 1, B, c.dK, c.idx, c.E, c.dq, c.dqe, c.dqn, c.ds, c.dse, c.dsn, 1, c.dz, c.dse,
+  rc = launch_rows<true>(h, L.hw, 1, c.dK, B, c.dK, c.idx, c.E, c.dq, c.dqe, c.dqn, c.ds, c.dse, c.dsn, 1, c.dz, c.dse,
                          c.dsn, 1, c.sdt, c.H, c.G, z, c.H, st);
   if (rc != IMQ_OK) return rc;
   const int64_t total = c.T * c.H;
@@ -742,7 +763,9 @@ extern "C" int imq_moe_experts_w4_ex(
   if (gu_sz_stride_n < gu_K_pad / G || dn_sz_stride_n < dn_K_pad / G) return IMQ_ERR_INVALID;
   if (T == 0) return IMQ_OK;
   if (!workspace || workspace_bytes < L.total) return IMQ_ERR_INVALID;
-  if (h_row_stride < gu_K_pad || out_row_stride < H) return IMQ_ERR_INVALID;
+  // hidden rows either cover gu_K_pad (zero past H), or just H with H % 8 == 0: the kernels then
+  // clamp their reads to the first H columns
+  if (out_row_stride < H || h_row_stride < H || (h_row_stride < gu_K_pad && H % 8 != 0)) return IMQ_ERR_INVALID;
   if (!aligned(gu_q, 4) || !aligned(dn_q, 4) || (gu_q_row_stride % 4) || (dn_q_row_stride % 4) ||
       (gu_q_stride_e % 4) || (dn_q_stride_e % 4) || !aligned(hidden, 16) || (h_row_stride % 8) ||
       !aligned(workspace, 256))
@@ -751,7 +774,8 @@ extern "C" int imq_moe_experts_w4_ex(
                   (const uint8_t*)gu_q, gu_q_stride_e, gu_q_row_stride, gu_K_pad, gu_s, gu_z, gu_sz_stride_e,
                   gu_sz_stride_n, I, (const uint8_t*)dn_q, dn_q_stride_e, dn_q_row_stride, dn_K_pad, dn_s, dn_z,
                   dn_sz_stride_e, dn_sz_stride_n, sz_dtype, G, gu_bias, gu_bias_stride_e, dn_bias, dn_bias_stride_e,
-                  bias_dtype, act, alpha, limit, (uint16_t*)out, out_row_stride};
+                  bias_dtype, act, alpha, limit, (uint16_t*)out, out_row_stride,
+                  h_row_stride >= gu_K_pad ? gu_K_pad : H};
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   const int rs = moe_sorted(c, ws, L, st);

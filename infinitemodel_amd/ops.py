@@ -297,8 +297,10 @@ def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=
     gb, db = biases
     gK, dK = gq.shape[2] * 2, dq.shape[2] * 2
     x = _rows2d(hidden)
-    if x.shape[1] != gK:
-        x = torch.nn.functional.pad(x, (0, gK - x.shape[1])).contiguous()
+    if x.shape[1] != gK and (x.shape[1] != H or H % 8 or T > 16):
+        # rows of exactly H columns (H % 8 == 0) are read as zero past H by the kernels; past 16
+        # tokens every row is re-read by many passes and one zero-padded copy is cheaper
+        x = torch.nn.functional.pad(x[:, :H], (0, gK - H)).contiguous()
     idx = topk_idx.to(torch.int32).contiguous()
     w = topk_w.to(torch.bfloat16).contiguous()
     need = moe_workspace_bytes(T, k, E, H, I, group_size)

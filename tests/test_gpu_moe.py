@@ -221,3 +221,46 @@ def test_gptoss_module_install(dev):
         y = C.t2np(mod(C.to_torch(x, "bf16", dev), torch.from_numpy(idx).to(dev), C.to_torch(w, "bf16", dev)))
     exact = om.gptoss_exact(x, idx, w, Dgu, bgu, Ddn, bdn)
     assert oq.max_rel(y, exact) <= MAX_REL and oq.mean_rel(y, exact) <= MEAN_REL
+
+
+@pytest.mark.parametrize("kernel_layout", [False, True])
+def test_moe_unpadded_hidden_and_pad_codes(dev, kernel_layout):
+    """Hidden rows of exactly H columns (H % 8 == 0 < K_pad) give bit-identical results to
+    zero-padded rows, on the per-row path (K_pad 384) and the token-sorted path (kernel layout
+    512); arbitrary codes in the packed pad columns change nothing (they meet zero activations,
+    as in the reference's zero-padded x)."""
+    import torch
+    from infinitemodel_amd import ops
+    E, H, I, k, T, G = 6, 320, 160, 2, 7, 128
+    gu, dn, Dgu, Ddn = _layer(E, H, I, G, 17)
+    t = lambda a: C.to_torch(a, "bf16", dev)  # noqa: E731
+
+    def hold(p, junk):
+        q, s, z = C.u8(p[0], dev).clone(), t(p[1]), t(p[2])
+        if kernel_layout:
+            k2 = -(-q.shape[2] * 2 // 256) * 256
+            q2 = torch.zeros((*q.shape[:2], k2 // 2), dtype=torch.uint8, device=dev)
+            q2[:, :, :q.shape[2]] = q
+            s2 = torch.zeros((*s.shape[:2], k2 // G), dtype=s.dtype, device=dev)
+            z2 = torch.zeros_like(s2)
+            s2[:, :, :s.shape[2]], z2[:, :, :z.shape[2]] = s, z
+            q, s, z = q2, s2, z2
+        if junk is not None:
+            q[:, :, junk // 2:] = torch.randint(0, 256, q[:, :, junk // 2:].shape, dtype=torch.uint8,
+                                                 generator=torch.Generator(device=dev).manual_seed(5), device=dev)
+        return q, s, z
+
+    r = C.rng(18)
+    idx, w = om.route_topk(r.standard_normal((T, E)).astype(np.float32), k)
+    x = t(C.bf16_normal(r, (T, H)))
+    ti = torch.from_numpy(idx).to(dev)
+    a = (*hold(gu, None), H)
+    b = (*hold(dn, None), I)
+    y_un = ops.moe_experts_w4(x, ti, t(w), a, b, G)
+    xp = torch.nn.functional.pad(x, (0, a[0].shape[2] * 2 - H))
+    y_pad = ops.moe_experts_w4(xp, ti, t(w), a, b, G)
+    assert torch.equal(y_un, y_pad)
+    y_junk = ops.moe_experts_w4(x, ti, t(w), (*hold(gu, H), H), (*hold(dn, I), I), G)
+    assert torch.equal(y_un, y_junk)
+    exact = om.moe_exact_grouped(C.t2np(x), idx, w, Dgu, Ddn)
+    assert oq.max_rel(C.t2np(y_un), exact) <= MAX_REL
