@@ -232,6 +232,10 @@ struct MoeLineArgs {
   int bdt;
   float alpha, limit;    // MODE 2 activation
   int xk;                // valid x columns (a multiple of 8): columns past them read as zero
+  // direct decode form (no sort): an item is (routed row b, row block), expert idx[b], one row
+  const int32_t* idx;
+  int nrows;             // routed rows B
+  int direct;
 };
 
 IMQ_DEV float moe_row_swap8(float v) {
@@ -252,14 +256,25 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   const bool lo8 = c < 8;
   const int KL = a.Kpad / kMoeLine;
   const int ls0 = wave * S2;
-  const int items = a.hit[a.E] * a.NB;              // (hit expert, row block) work items
+  // (hit expert, row block) work items, or (routed row, row block) in the direct form
+  const int items = a.direct ? a.nrows * a.NB : a.hit[a.E] * a.NB;
 
   uint32_t* szl = (uint32_t*)smem + wave * (2 * NTL * 16 * DPR);
   float* red = (float*)(smem + (size_t)W * (2 * NTL * 16 * DPR) * 4);   // [W][NTL][16][16]
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
-  const int e = a.hit[item / a.NB];
   const int blk = item - (item / a.NB) * a.NB;
-  const int beg = a.off[e], end = a.off[e + 1];
+  int e, beg, end;
+  if (a.direct) {
+    beg = item / a.NB;
+    end = beg + 1;
+    e = a.idx[beg];
+    e = (e >= 0 && e < a.E) ? e : 0;   // ids outside [0, E) are clamped, as in the sort
+  } else {
+    e = a.hit[item / a.NB];
+    beg = a.off[e];
+    end = a.off[e + 1];
+  }
+  auto perm_at = [&](int p) -> int { return a.direct ? p : a.perm[p]; };
 
   auto rbase = [&](int t) -> int {
     if constexpr (MODE == 0) return (t < HALF) ? 16 * HALF * blk + 16 * t : a.I + 16 * HALF * blk + 16 * (t - HALF);
@@ -342,7 +357,7 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
     const int nrow = (end - p0) < 16 ? end - p0 : 16;
     const int pr = p0 + (c < nrow ? c : nrow - 1);    // A row of this lane (rows >= nrow repeat the last)
     const uint16_t* xr;
-    if constexpr (MODE != 1) xr = a.x + (int64_t)(a.perm[pr] / a.k) * a.sxm;   // gate_up: gather hidden rows
+    if constexpr (MODE != 1) xr = a.x + (int64_t)(perm_at(pr) / a.k) * a.sxm;   // gate_up: gather hidden rows
     else xr = a.x + (int64_t)pr * a.sxm;
     f32x4_t y0[NTL], y1[NTL];
 #pragma unroll
@@ -450,7 +465,7 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
           float v = 0.f;
           for (int w = 0; w < W; ++w) v += red[((w * NTL + t) * 16 + m) * 16 + n];
           v += bias_at(16 * NTL * blk + j);
-          ((float*)a.out)[(int64_t)a.perm[p0 + m] * a.som + 16 * NTL * blk + j] = v;
+          ((float*)a.out)[(int64_t)perm_at(p0 + m) * a.som + 16 * NTL * blk + j] = v;
         }
       }
     }
@@ -529,13 +544,11 @@ bool moe_line_shape(int64_t Kpad, int* S2, int* W) {
 // exit after reading its length. Measured on MI355X at the OLMoE shape against persistent grids
 // of 2-4 workgroups per CU and 32-row blocks: 64-row blocks with two line-steps per wave were
 // fastest at T = 1, 16 and 256.
-template <int SDT, int MODE>
-int moe_line_dispatch(MoeLineArgs a, int rows, hipStream_t st) {
-  constexpr int NTL = 4;
-  int S2, W;
-  if (!moe_line_shape(a.Kpad, &S2, &W)) return IMQ_ERR_UNSUPPORTED;
+template <int NTL, int SDT, int MODE>
+int moe_line_go(MoeLineArgs a, int rows, int64_t maxhit, int S2, int W, hipStream_t st) {
   a.NB = rows / (16 * NTL);
-  const int64_t items = (int64_t)a.E * a.NB;
+  // at most min(E, routed rows) experts are hit: no workgroups for items that cannot exist
+  const int64_t items = (maxhit < a.E ? maxhit : (int64_t)a.E) * a.NB;
   if (items > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   if (a.xk < a.Kpad) {
     if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, true>(a, W, (int)items, st);
@@ -545,12 +558,31 @@ int moe_line_dispatch(MoeLineArgs a, int rows, hipStream_t st) {
   return moe_line_launch<2, NTL, SDT, MODE, false>(a, W, (int)items, st);
 }
 
+template <int SDT, int MODE>
+int moe_line_dispatch(MoeLineArgs a, int rows, int64_t maxhit, hipStream_t st) {
+  int S2, W;
+  if (!moe_line_shape(a.Kpad, &S2, &W)) return IMQ_ERR_UNSUPPORTED;
+  const int KL = a.Kpad / kMoeLine;
+  if (a.direct && KL <= 8) {
+    // decode rows of a short K: 32-row blocks, and one line-step per wave below 8 line-steps,
+    // so a hit expert's rows spread over twice the workgroups, several of them per CU (measured
+    // on MI355X: OLMoE T=1 1189 -> 1258 GB/s; at gpt-oss's 12 line-steps 64-row blocks stay
+    // faster)
+    if (KL < 8) {
+      S2 = 1;
+      W = KL;
+    }
+    return moe_line_go<2, SDT, MODE>(a, rows, maxhit, S2, W, st);
+  }
+  return moe_line_go<4, SDT, MODE>(a, rows, maxhit, S2, W, st);
+}
+
 template <int MODE>
-int moe_line_sdt(const MoeLineArgs& a, int rows, int sdt, hipStream_t st) {
+int moe_line_sdt(const MoeLineArgs& a, int rows, int64_t maxhit, int sdt, hipStream_t st) {
   switch (sdt) {
-    case IMQ_DT_BF16: return moe_line_dispatch<IMQ_DT_BF16, MODE>(a, rows, st);
-    case IMQ_DT_FP16: return moe_line_dispatch<IMQ_DT_FP16, MODE>(a, rows, st);
-    case IMQ_DT_FP32: return moe_line_dispatch<IMQ_DT_FP32, MODE>(a, rows, st);
+    case IMQ_DT_BF16: return moe_line_dispatch<IMQ_DT_BF16, MODE>(a, rows, maxhit, st);
+    case IMQ_DT_FP16: return moe_line_dispatch<IMQ_DT_FP16, MODE>(a, rows, maxhit, st);
+    case IMQ_DT_FP32: return moe_line_dispatch<IMQ_DT_FP32, MODE>(a, rows, maxhit, st);
   }
   return IMQ_ERR_INVALID;
 }
@@ -680,12 +712,19 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   int32_t* hit = (int32_t*)(ws + L.hit);
   uint16_t* h = (uint16_t*)(ws + L.h);
   float* yr = (float*)(ws + L.z);
-  moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit);
-  IMQ_LAUNCH_CHECK();
+  // Decode: with few routed rows per expert there is little weight reuse to win by grouping, and
+  // the sort plus the off -> perm -> x dependent loads dominate; rows then run directly
+  // (routed order, one row per item, expert idx[b]).
+  const bool direct = B * 4 <= c.E;
+  if (!direct) {
+    moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit);
+    IMQ_LAUNCH_CHECK();
+  }
   MoeLineArgs g{c.hidden, c.hs, (int)c.gK, (int)c.k, off, perm, hit, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn,
-                (int)c.E, 0, (int)c.I, h, L.hw, c.gb, c.gbe, c.bdt, c.alpha, c.limit, (int)c.xk};
-  int rc = c.act == IMQ_ACT_GPTOSS ? moe_line_sdt<2>(g, (int)(2 * c.I), c.sdt, st)
-                                   : moe_line_sdt<0>(g, (int)(2 * c.I), c.sdt, st);
+                (int)c.E, 0, (int)c.I, h, L.hw, c.gb, c.gbe, c.bdt, c.alpha, c.limit, (int)c.xk,
+                c.idx, (int)B, direct ? 1 : 0};
+  int rc = c.act == IMQ_ACT_GPTOSS ? moe_line_sdt<2>(g, (int)(2 * c.I), B, c.sdt, st)
+                                   : moe_line_sdt<0>(g, (int)(2 * c.I), B, c.sdt, st);
   if (rc != IMQ_OK) return rc;
   // h's columns past I read as zero when I % 8 == 0; otherwise the partial last 8 is zeroed here
   const int64_t hxk = c.I % 8 == 0 ? c.I : c.dK;
@@ -696,8 +735,8 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
     IMQ_LAUNCH_CHECK();
   }
   MoeLineArgs d{h, L.hw, (int)c.dK, (int)c.k, off, perm, hit, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn,
-                (int)c.E, 0, 0, yr, c.H, c.db, c.dbe, c.bdt, 0.f, 0.f, (int)hxk};
-  rc = moe_line_sdt<1>(d, (int)c.H, c.sdt, st);
+                (int)c.E, 0, 0, yr, c.H, c.db, c.dbe, c.bdt, 0.f, 0.f, (int)hxk, c.idx, (int)B, direct ? 1 : 0};
+  rc = moe_line_sdt<1>(d, (int)c.H, B, c.sdt, st);
   if (rc != IMQ_OK) return rc;
   const int64_t total = c.T * (c.H / 8);
   const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
