@@ -1589,6 +1589,143 @@ __global__ __launch_bounds__(64 * MAXW) void w8_skinny_kernel(SkinnyArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// int8 decode line kernel (M <= 4): the int4 line kernel's structure for per-row int8. A
+// line-step is 128 bytes of a row = 128 codes. One workgroup owns a 16-row tile and all of K; W
+// waves split K in S2 line-steps each and issue all of their loads up front:
+//   * two 16-byte loads per line-step cover 8 rows x a whole 128-byte line each: lane (c, ar)
+//     keeps 16 codes of its own row c in the first half (K offset 16 ar) and 16 codes of row c ^ 8
+//     in the second half (K offset 64 + 16 ar), so every lane of one MFMA reads the same K;
+//   * operands are (q + 128) as bf16 (exact) against activations in natural order, staged in the
+//     wave's LDS with per-64-code row sums; a line-step contributes acc - 128 * sum(x) per half;
+//   * rows c ^ 8 are folded back with a row swap, partials reduce across waves in LDS, and the
+//     per-row scale multiplies the sum: y = s * sum_k x * q, the kernel form of `_ksk8`.
+// ---------------------------------------------------------------------------------------------
+constexpr int kLine8 = 128;   // codes per int8 line-step (128 bytes of a row)
+
+IMQ_HOST_DEV inline int line8_wave_lds(int M, int S2) { return M * (S2 * kLine8 + 8) * 2 + 2 * S2 * 16 * 4; }
+
+template <int S2, int MC, int SDT, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void w8_line_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int RC = MC < 4 ? MC : 4;                 // D registers that can hold a real row
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int c = lane & 15, ar = lane >> 4;
+  const bool lo8 = c < 8;
+  const int M = MC <= 2 ? MC : a.M;                 // MC 1 and 2 launch exactly that M
+  const int KL = a.Kpad / kLine8;                   // a.Kpad carries K (a multiple of 128)
+  const int ls0 = wave * S2;
+  const int row0 = blockIdx.x * 16;
+  const int rlast = a.N - 1 - row0;                  // last valid row within the tile
+
+  const int xrow = S2 * kLine8 + 8;
+  const int wbytes = line8_wave_lds(M, S2);
+  unsigned char* wl = smem + (size_t)wave * wbytes;
+  uint16_t* xw = (uint16_t*)wl;                      // [M][xrow], natural order
+  float* xs = (float*)(wl + M * xrow * 2);          // [2 * S2 half line-steps][16 rows]
+  float* red = (float*)(smem + (size_t)W * wbytes);
+
+  // 1) x: M rows x 16*S2 16-byte blocks of this wave's K range (clamped into the row)
+  constexpr int XB = 16 * S2;
+  constexpr int XU = (MC * XB + 63) / 64;
+  const int xtot = M * XB;
+  const uint16_t* xbase = a.x + (int64_t)ls0 * kLine8;
+  const int xlim = a.Kpad - ls0 * kLine8 - 8;        // last valid block start in the range
+  u32x4_t xv[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    int idx = lane + 64 * u;
+    idx = idx < xtot ? idx : xtot - 1;
+    const int m = idx / XB, b = idx - m * XB;
+    int kb = 8 * b;
+    kb = kb < xlim ? kb : xlim;
+    xv[u] = *(const u32x4_t*)(xbase + m * (int)a.sxm + kb);
+  }
+  // 2) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
+  const int8_t* qt = a.q8 + (int64_t)row0 * a.sqn;
+  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
+  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
+  const int8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
+  const int8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  u32x4_t wb[2 * S2];
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    int l = ls0 + i;
+    l = l < KL ? l : KL - 1;
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + kLine8 * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + kLine8 * l));
+  }
+  // 3) stage x with its per-64-code row sums
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int idx = lane + 64 * u;
+    const bool ok = idx < xtot;
+    const int m = (ok ? idx : 0) / XB, b = (ok ? idx : 0) - m * XB;
+    float sum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
+    // the 8 blocks of one half line-step are 8 consecutive idx (XB is a multiple of 8)
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 8);
+    if (ok) {
+      *(u32x4_t*)(xw + m * xrow + 8 * b) = xv[u];
+      if ((b & 7) == 0) xs[(b >> 3) * 16 + m] = sum;
+    }
+  }
+  // LDS is written and read by this wave only; its LDS operations execute in order
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+  const uint16_t* xa = xw + (c < M ? c : M - 1) * xrow + 16 * ar;
+  float y0[4] = {0.f, 0.f, 0.f, 0.f}, y1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    // a line-step past K (its loads re-read the last one) contributes nothing
+    const float v = ls0 + i < KL ? 1.f : 0.f;
+    const f32x4_t xs0 = *(const f32x4_t*)(xs + (2 * i) * 16 + 4 * ar);
+    const f32x4_t xs1 = *(const f32x4_t*)(xs + (2 * i + 1) * 16 + 4 * ar);
+    const bf16x8_t a00 = *(const bf16x8_t*)(xa + i * kLine8);
+    const bf16x8_t a01 = *(const bf16x8_t*)(xa + i * kLine8 + 8);
+    const bf16x8_t a10 = *(const bf16x8_t*)(xa + i * kLine8 + 64);
+    const bf16x8_t a11 = *(const bf16x8_t*)(xa + i * kLine8 + 72);
+    const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
+    u32x4_t gA, gB;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      gA[d] = lo8 ? w0[d] : w1[d];                   // own row c, first half
+      gB[d] = lo8 ? w1[d] : w0[d];                   // row c ^ 8, second half
+    }
+    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    acc0 = mfma16x16x32(a00, biased_i8x8_bf16(gA[0], gA[1]), acc0);
+    acc1 = mfma16x16x32(a10, biased_i8x8_bf16(gB[0], gB[1]), acc1);
+    acc0 = mfma16x16x32(a01, biased_i8x8_bf16(gA[2], gA[3]), acc0);
+    acc1 = mfma16x16x32(a11, biased_i8x8_bf16(gB[2], gB[3]), acc1);
+#pragma unroll
+    for (int r = 0; r < RC; ++r) {
+      y0[r] = fmaf(v, fmaf(-128.f, xs0[r], acc0[r]), y0[r]);
+      y1[r] = fmaf(v, fmaf(-128.f, xs1[r], acc1[r]), y1[r]);
+    }
+  }
+  // D row m = 4*ar + r; rows m < M <= 4 live in lanes ar == 0
+  float* rb = red + wave * (RC * 16);
+#pragma unroll
+  for (int r = 0; r < RC; ++r) {
+    const float vv = y0[r] + row_swap8(y1[r]);
+    if (ar == 0) rb[r * 16 + c] = vv;
+  }
+  lds_barrier();
+  for (int e = threadIdx.x; e < 16 * M; e += blockDim.x) {
+    const int m = e >> 4, n = e & 15;
+    float sum = 0.f;
+    for (int w = 0; w < W; ++w) sum += red[w * (RC * 16) + m * 16 + n];
+    if (n <= rlast) {
+      const float sc = load_as_f32<SDT>(a.sc, (int64_t)(row0 + n) * a.ssn);
+      a.y[(int64_t)m * a.sym + row0 + n] = (uint16_t)f32_to_bf16_bits(sc * sum);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Generic fallback: any bit width (2/4/8), any group size, any stride/alignment, M <= 16.
 // One wave per output row; every weight is dequantized in fp32 as (q - bf16(z)) * bf16(s), the
 // same un-rounded weight the fast kernels accumulate with, and accumulated in fp32. Slow but
@@ -2202,6 +2339,40 @@ int w8_dispatch(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
   return w8_launch_mw<SDT, 16>(a, lds, grid, W, st);
 }
 
+// int8 line kernel plan (M <= 4, K a multiple of 128; restated by the CPU bounds model in the
+// tests): S2 = 4 line-steps per wave (8 when K needs more than 16 waves of 4), W <= 16 waves.
+bool line8_plan(int64_t M, int64_t K, int64_t N, int64_t sqn, int64_t sxm, int max_lds, int* S2o, int* Wo,
+                size_t* ldso) {
+  if (M < 1 || M > 4 || K <= 0 || K % kLine8 != 0 || N < 1) return false;
+  if (16 * sqn >= (int64_t(1) << 31) || M * sxm * 2 >= (int64_t(1) << 31)) return false;
+  const int64_t KL = K / kLine8;
+  int S2 = 4;
+  if ((KL + S2 - 1) / S2 > 16) S2 = 8;
+  const int64_t W = (KL + S2 - 1) / S2;
+  if (W > 16) return false;
+  const int rc = M <= 2 ? (int)M : 4;
+  const size_t lds = (size_t)W * line8_wave_lds((int)M, S2) + (size_t)W * rc * 16 * 4;
+  if (lds > (size_t)max_lds) return false;
+  *S2o = S2;
+  *Wo = (int)W;
+  *ldso = lds;
+  return true;
+}
+
+template <int S2, int SDT>
+int line8_launch(const SkinnyArgs& a, int W, size_t lds, hipStream_t st) {
+  const dim3 g((unsigned)((a.N + 15) / 16)), b(64 * W);
+  if (a.M == 1) return launch_with_lds(w8_line_kernel<S2, 1, SDT, 16>, g, b, lds, st, a);
+  if (a.M == 2) return launch_with_lds(w8_line_kernel<S2, 2, SDT, 16>, g, b, lds, st, a);
+  return launch_with_lds(w8_line_kernel<S2, 4, SDT, 16>, g, b, lds, st, a);
+}
+
+template <int SDT>
+int line8_dispatch(const SkinnyArgs& a, int S2, int W, size_t lds, hipStream_t st) {
+  if (S2 == 8) return line8_launch<8, SDT>(a, W, lds, st);
+  return line8_launch<4, SDT>(a, W, lds, st);
+}
+
 int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st) {
   if (M < 1 || M > 16 || K <= 0 || K % kStep8 != 0) return IMQ_ERR_UNSUPPORTED;
@@ -2210,6 +2381,18 @@ int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t
   const DevInfo di = device_info();
   SkinnyArgs a{x, sxm, (int)M, (int)K, nullptr, sqn, sc, ssn, 0, nullptr, 0, 0, (int)N, 0, y, sym, 0};
   a.q8 = q;
+  {
+    int S2, W;
+    size_t lds;
+    if (line8_plan(M, K, N, sqn, sxm, di.max_lds, &S2, &W, &lds)) {
+      switch (sdt) {
+        case IMQ_DT_BF16: return line8_dispatch<IMQ_DT_BF16>(a, S2, W, lds, st);
+        case IMQ_DT_FP16: return line8_dispatch<IMQ_DT_FP16>(a, S2, W, lds, st);
+        case IMQ_DT_FP32: return line8_dispatch<IMQ_DT_FP32>(a, S2, W, lds, st);
+      }
+      return IMQ_ERR_INVALID;
+    }
+  }
   switch (sdt) {
     case IMQ_DT_BF16: return w8_dispatch<IMQ_DT_BF16>(a, di, st);
     case IMQ_DT_FP16: return w8_dispatch<IMQ_DT_FP16>(a, di, st);

@@ -384,6 +384,21 @@ def test_linear_w8_decode_kernel(dev, N, K, M, sdt):
     _int8_check(dev, N, K, M, sdt, seed=N + M)
 
 
+@pytest.mark.parametrize("N,K", [(37, 128), (100, 384), (512, 3584), (272, 14336), (152064 // 64, 3584)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_linear_w8_line_kernel(dev, N, K, M):
+    """Decode rows M <= 4 with K % 128 == 0 take the int8 line kernel: a ragged last tile, one
+    line-step (K 128), waves with unused line-steps (K 384 = 3 of S2 = 4), the Qwen2.5-7B head's
+    K 3584 (7 waves) and K 14336 (8 line-steps per wave, 14 waves)."""
+    _int8_check(dev, N, K, M, "bf16", seed=3 * N + M)
+
+
+@pytest.mark.parametrize("sdt", ["fp16", "fp32"])
+def test_linear_w8_line_kernel_scale_dtypes(dev, sdt):
+    for M in (1, 4):
+        _int8_check(dev, 200, 1024, M, sdt, seed=M + 90)
+
+
 def test_linear_w8_c4_shape_rows(dev):
     _int8_check(dev, 14336 // 8, 4096, 16, "fp16", seed=77)
 

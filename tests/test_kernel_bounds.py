@@ -698,6 +698,95 @@ def test_line2_plan_declines():
     assert line2_plan(1, 30720, 64, 64, 7680, 30720, 480, 4) is not None
 
 
+# ---- int8 line kernel (csrc/gemv.hip w8_line_kernel / line8_plan) -----------------------------
+LINE8 = 128
+
+
+def line8_plan(M, K, N, sqn, sxm, max_lds=160 * 1024):
+    """line8_plan in csrc/gemv.hip: (S2, W, LDS bytes) or None when the int8 line kernel declines."""
+    if not (1 <= M <= 4) or K <= 0 or K % LINE8 or N < 1:
+        return None
+    if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31:
+        return None
+    KL = K // LINE8
+    S2 = 4 if -(-KL // 4) <= 16 else 8
+    W = -(-KL // S2)
+    if W > 16:
+        return None
+    rc = M if M <= 2 else 4
+    lds = W * (M * (S2 * LINE8 + 8) * 2 + 2 * S2 * 16 * 4) + W * rc * 16 * 4
+    if lds > max_lds:
+        return None
+    return S2, W, lds
+
+
+def line8_ranges(M, K, N, sqn, sxm, S2, W):
+    """Max exclusive offsets the int8 line kernel reads (qweight bytes, x elements, scale rows)
+    and the LDS bytes its wave areas touch, from its per-lane arithmetic and clamps."""
+    KL = K // LINE8
+    XB = 16 * S2
+    xrow = S2 * LINE8 + 8
+    wave_lds = M * xrow * 2 + 2 * S2 * 16 * 4
+    r = dict(q=0, x=0, s=0, lds=0)
+    NT = -(-N // 16)
+    for tile in sorted({0, NT - 1}):
+        row0 = tile * 16
+        rlast = N - 1 - row0
+        for wave in range(W):
+            ls0 = wave * S2
+            base = wave * wave_lds
+            xlim = K - ls0 * LINE8 - 8
+            assert xlim >= 0
+            for idx in range(M * XB):
+                m, b = divmod(idx, XB)
+                kb = min(8 * b, xlim)
+                r["x"] = max(r["x"], ls0 * LINE8 + m * sxm + kb + 8)
+                r["lds"] = max(r["lds"], base + (m * xrow + 8 * b + 8) * 2)
+                if b % 8 == 0:
+                    r["lds"] = max(r["lds"], base + M * xrow * 2 + ((b >> 3) * 16 + m + 1) * 4)
+            for c in range(16):
+                lo8 = c < 8
+                rr0 = min(c & 7, rlast)
+                rr1 = min(8 + (c & 7), rlast)
+                mrow = c if c < M else M - 1
+                for ar in range(4):
+                    for i in range(S2):
+                        l = min(ls0 + i, KL - 1)
+                        r["q"] = max(r["q"], (row0 + rr0) * sqn + 16 * ar + (0 if lo8 else 64) + LINE8 * l + 16)
+                        r["q"] = max(r["q"], (row0 + rr1) * sqn + 16 * ar + (64 if lo8 else 0) + LINE8 * l + 16)
+                        r["lds"] = max(r["lds"], base + (mrow * xrow + 16 * ar + i * LINE8 + 72 + 8) * 2)
+                        r["lds"] = max(r["lds"], base + M * xrow * 2 + ((2 * i + 1) * 16 + 4 * ar + 4) * 4)
+        for n in range(16):
+            if n <= rlast:
+                r["s"] = max(r["s"], row0 + n + 1)
+    return r
+
+
+@pytest.mark.parametrize("N,K", [(152064, 3584), (4096, 14336), (14336, 4096), (37, 128), (100, 384), (17, 1280),
+                                 (64, 16384)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("pad", [0, 64])
+def test_line8_reads_in_bounds(N, K, M, pad):
+    sqn = K + pad
+    plan = line8_plan(M, K, N, sqn, K)
+    assert plan is not None
+    S2, W, lds = plan
+    assert W * S2 * LINE8 >= K and (W - 1) * S2 * LINE8 < K
+    r = line8_ranges(M, K, N, sqn, K, S2, W)
+    assert r["q"] <= (N - 1) * sqn + K
+    assert r["x"] <= (M - 1) * K + K
+    assert r["s"] <= N
+    rc = M if M <= 2 else 4
+    assert r["lds"] <= lds - W * rc * 16 * 4          # wave areas end where the reduction area starts
+
+
+def test_line8_plan_declines():
+    assert line8_plan(5, 4096, 64, 4096, 4096) is None         # M > 4: the skinny int8 kernel
+    assert line8_plan(1, 4032, 64, 4032, 4032) is None         # K % 128
+    assert line8_plan(1, 8 * 16 * 128 + 128, 64, 20000, 20000) is None   # more than 16 waves of 8
+    assert line8_plan(4, 16384, 64, 16384, 16384) is not None
+
+
 # ---- int2 K-split decode kernel (csrc/gemv.hip w2_ksplit_kernel / ksplit2_plan) --------------
 KS2_S2 = 2
 
