@@ -514,6 +514,322 @@ __global__ __launch_bounds__(256) void moe_zero_pad_kernel(uint16_t* __restrict_
   }
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// Decode form on the dense line kernel's structure (routed rows B with 4 B <= E, about one row
+// per hit expert): two launches, no sort and no combine launch.
+//   moe_gu_line_kernel  workgroup (routed row b, unit u) streams 16-row tiles of expert idx[b]'s
+//                       gate_up rows against hidden[b / k]: waves split K in S2 line-steps of
+//                       256 codes with every load issued up front (two full-line loads per
+//                       line-step, MFMA 16x16x32 with the +128 bias fold). ACT 0 pairs gate tile
+//                       u with up tile u + I/16 (two wave groups) and writes 16 h columns; ACT 1
+//                       (gpt-oss) takes 16 interleaved rows and writes 8. Row biases and the
+//                       activation run in the epilogue.
+//   moe_dn_line_kernel  workgroup (token t, 16 output rows) with one wave group per routed slot
+//                       j: group j streams expert idx[t k + j]'s down rows against h[t k + j],
+//                       scales its partial by w[t, j] (the down bias added once per slot), and
+//                       the fixed-order cross-wave LDS reduction is the weighted combine:
+//                       out[t] = bf16(sum_j w[t, j] (down_j + b_j)).
+// ---------------------------------------------------------------------------------------------
+constexpr int kDLine = 256;   // int4 codes per line-step (128 bytes of a row, 2 groups of 128)
+
+struct MoeDecArgs {
+  const uint16_t* x;       // gu: hidden (row b / k); dn: h (row b)
+  int64_t sxm;
+  int xk;                  // valid x columns (a multiple of 8): columns past them read as zero
+  int Kpad;                // kernel K (a multiple of 256)
+  int k;                   // top_k
+  const int32_t* idx;      // [B] expert of each routed row
+  const uint16_t* topk_w;  // [B] routing weights, bf16 (dn)
+  int E;
+  const uint8_t* q;
+  int64_t sqe, sqn;
+  const void* sc;
+  const void* zr;
+  int64_t sse, ssn;        // scale and zero share strides (expert, row); unit group stride
+  int I;                   // gu: intermediate size
+  int NR;                  // gu: units per routed row; dn: 16-row tiles per token
+  int Wk;                  // waves per tile (gu) or per routed slot (dn)
+  const void* bias;        // per-expert row bias [E][rows] or null
+  int64_t sbe;
+  int bdt;
+  float alpha, limit;      // gpt-oss activation
+  uint16_t* out;           // gu: h [B][som]; dn: out [T][som]
+  int64_t som;
+};
+
+IMQ_HOST_DEV inline int dec_wave_lds(int S2, int vb) { return (S2 * kDLine + 8) * 2 + 2 * S2 * 4 + 2 * 16 * (S2 * vb / 2) * 4; }
+
+// One wave's share of a 16-row tile (rows rbase.. of expert e, line-steps [ls0, ls0 + S2)) against
+// one activation row: returns the wave's partial dot of row c in lanes with ar == 0.
+template <int S2, int SDT, bool XCL>
+IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint16_t* xrow, int ls0, int KL,
+                               unsigned char* wl, int lane) {
+  constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
+  constexpr int DPR = S2 * VB / 2;                   // scale dwords per row per array
+  const int c = lane & 15, ar = lane >> 4;
+  const bool lo8 = c < 8;
+  const int xrowl = S2 * kDLine + 8;
+  uint16_t* xw = (uint16_t*)wl;                      // [xrowl], unpack order
+  float* xs = (float*)(wl + xrowl * 2);              // [2 * S2] group sums
+  uint32_t* szl = (uint32_t*)(xs + 2 * S2);          // [2 arrays][16 rows][DPR]
+
+  // 1) x: 32*S2 blocks of 8 of this wave's K range
+  constexpr int XB = 32 * S2;
+  constexpr int XU = XB / 64;
+  u32x4_t xv[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int bidx = lane + 64 * u;
+    const int col = ls0 * kDLine + 8 * bidx;
+    if constexpr (XCL) {
+      const bool in = col < a.xk;
+      xv[u] = *(const u32x4_t*)(xrow + (in ? col : a.xk - 8));
+      if (!in) xv[u] = u32x4_t{0u, 0u, 0u, 0u};
+    } else {
+      xv[u] = *(const u32x4_t*)(xrow + (col < a.Kpad ? col : a.Kpad - 8));
+    }
+  }
+  // 2) scale / zero words of groups [2*ls0, 2*ls0 + 2*S2) of the 16 rows
+  constexpr int ZU = (32 * DPR + 63) / 64;
+  const int ngd = a.Kpad / 128 * VB / 4;
+  const unsigned char* sbase = (const unsigned char*)a.sc + ((int64_t)e * a.sse + (int64_t)rbase * a.ssn) * VB;
+  const unsigned char* zbase = (const unsigned char*)a.zr + ((int64_t)e * a.sse + (int64_t)rbase * a.ssn) * VB;
+  uint32_t zv[ZU];
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    int d = lane + 64 * u;
+    d = d < 32 * DPR ? d : 32 * DPR - 1;
+    const int arr = d / (16 * DPR);
+    const int rem = d - arr * (16 * DPR);
+    const int r = rem / DPR;
+    const int dw = rem - r * DPR;
+    int gd = ls0 * (VB / 2) + dw;
+    gd = gd < ngd ? gd : ngd - 1;
+    zv[u] = *(const uint32_t*)((arr ? zbase : sbase) + (int64_t)r * a.ssn * VB + 4 * gd);
+  }
+  // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
+  const uint8_t* qt = a.q + (int64_t)e * a.sqe + (int64_t)rbase * a.sqn;
+  const uint8_t* q0 = qt + (int64_t)(c & 7) * a.sqn + 16 * ar + (lo8 ? 0 : 64);
+  const uint8_t* q1 = qt + (int64_t)(8 + (c & 7)) * a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  u32x4_t wb[2 * S2];
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    int l = ls0 + i;
+    l = l < KL ? l : KL - 1;
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+  }
+  // 4) stage x (unpack order) with its per-group sums, and the scale / zero words
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int bidx = lane + 64 * u;
+    float sum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    *(u32x4_t*)(xw + 8 * bidx) = permute_x8(xv[u]);
+    if ((bidx & 15) == 0) xs[bidx >> 4] = sum;
+  }
+#pragma unroll
+  for (int u = 0; u < ZU; ++u) {
+    const int d = lane + 64 * u;
+    if (d < 32 * DPR) szl[d] = zv[u];
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // wave-private LDS, in-order
+
+  const uint32_t magic = magic_bf16_128x2();
+  const uint16_t* xa = xw + 32 * ar;
+  const uint32_t* sc_c = szl + c * DPR;
+  const uint32_t* sc_x = szl + (c ^ 8) * DPR;
+  const uint32_t* zr_c = szl + 16 * DPR + c * DPR;
+  const uint32_t* zr_x = szl + 16 * DPR + (c ^ 8) * DPR;
+  auto val = [&](const uint32_t* p, int g) -> float {
+    if constexpr (VB == 4) return round_bf16_hw(__uint_as_float(p[g]));
+    else return raw_to_bf16_f32<SDT>((g & 1) ? (p[g >> 1] >> 16) : (p[g >> 1] & 0xffffu));
+  };
+  float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < S2; ++i) {
+    const bool v = ls0 + i < KL;
+    const float xs0 = xs[2 * i], xs1 = xs[2 * i + 1];
+    bf16x8_t A0[4], A1[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      A0[kk] = *(const bf16x8_t*)(xa + i * kDLine + 8 * kk);
+      A1[kk] = *(const bf16x8_t*)(xa + i * kDLine + 128 + 8 * kk);
+    }
+    float s0 = val(sc_c, 2 * i), s1 = val(sc_x, 2 * i + 1);   // read, then select
+    s0 = v ? s0 : 0.f;
+    s1 = v ? s1 : 0.f;
+    const float cz0 = -(128.f + val(zr_c, 2 * i)) * s0;
+    const float cz1 = -(128.f + val(zr_x, 2 * i + 1)) * s1;
+    const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
+    u32x4_t gA, gB;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      gA[d] = lo8 ? w0[d] : w1[d];
+      gB[d] = lo8 ? w1[d] : w0[d];
+    }
+    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      acc0 = mfma16x16x32(A0[kk], unpack_nib8_bf16(gA[kk], magic), acc0);
+      acc1 = mfma16x16x32(A1[kk], unpack_nib8_bf16(gB[kk], magic), acc1);
+    }
+    y0 = fmaf(cz0, xs0, y0);
+    y1 = fmaf(cz1, xs1, y1);
+    y0 = fmaf(s0, acc0[0], y0);
+    y1 = fmaf(s1, acc1[0], y1);
+  }
+  return y0 + moe_row_swap8(y1);                     // D row 0 (the activation row) in lanes ar == 0
+}
+
+template <int S2, int SDT, int ACT, bool XCL>
+__global__ __launch_bounds__(1024) void moe_gu_line_kernel(MoeDecArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int wbytes = dec_wave_lds(S2, VB);
+  const int b = blockIdx.x / a.NR, u = blockIdx.x - b * a.NR;
+  int e = a.idx[b];
+  e = (e >= 0 && e < a.E) ? e : 0;   // ids outside [0, E) are clamped, as in the sort
+  const int tile = ACT == 0 ? wave / a.Wk : 0;
+  const int wk = wave - tile * a.Wk;
+  const int rbase = ACT == 0 ? (tile == 0 ? 16 * u : a.I + 16 * u) : 16 * u;
+  const float v = dec_tile_partial<S2, SDT, XCL>(a, e, rbase, a.x + (int64_t)(b / a.k) * a.sxm, wk * S2,
+                                                 a.Kpad / kDLine, smem + (size_t)wave * wbytes, lane);
+  float* red = (float*)(smem + (size_t)W * wbytes);  // [W][16]
+  if ((lane >> 4) == 0) red[wave * 16 + (lane & 15)] = v;
+  lds_barrier();
+  auto bias_at = [&](int row) -> float {
+    return a.bias != nullptr ? load_bias(a.bias, a.bdt, (int64_t)e * a.sbe + row) : 0.f;
+  };
+  const int n = threadIdx.x;
+  if constexpr (ACT == 0) {
+    if (n < 16) {
+      float g = 0.f, up = 0.f;
+      for (int w = 0; w < a.Wk; ++w) {
+        g += red[w * 16 + n];
+        up += red[(a.Wk + w) * 16 + n];
+      }
+      g += bias_at(16 * u + n);
+      up += bias_at(a.I + 16 * u + n);
+      a.out[(int64_t)b * a.som + 16 * u + n] = (uint16_t)f32_to_bf16_bits(g / (1.f + __expf(-g)) * up);
+    }
+  } else {
+    if (n < 8) {
+      float g = 0.f, up = 0.f;
+      for (int w = 0; w < a.Wk; ++w) {
+        g += red[w * 16 + 2 * n];
+        up += red[w * 16 + 2 * n + 1];
+      }
+      g += bias_at(16 * u + 2 * n);
+      up += bias_at(16 * u + 2 * n + 1);
+      a.out[(int64_t)b * a.som + 8 * u + n] = (uint16_t)f32_to_bf16_bits(gptoss_glu(g, up, a.alpha, a.limit));
+    }
+  }
+}
+
+template <int S2, int SDT, bool XCL>
+__global__ __launch_bounds__(1024) void moe_dn_line_kernel(MoeDecArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int wbytes = dec_wave_lds(S2, VB);
+  const int t = blockIdx.x / a.NR, rt = blockIdx.x - t * a.NR;
+  const int j = wave / a.Wk, wk = wave - j * a.Wk;
+  const int b = t * a.k + j;
+  int e = a.idx[b];
+  e = (e >= 0 && e < a.E) ? e : 0;
+  float v = dec_tile_partial<S2, SDT, XCL>(a, e, 16 * rt, a.x + (int64_t)b * a.sxm, wk * S2, a.Kpad / kDLine,
+                                           smem + (size_t)wave * wbytes, lane);
+  const int c = lane & 15;
+  if (wk == 0 && a.bias != nullptr) v += load_bias(a.bias, a.bdt, (int64_t)e * a.sbe + 16 * rt + c);
+  v *= bf16_bits_to_f32(a.topk_w[b]);
+  float* red = (float*)(smem + (size_t)W * wbytes);  // [W][16]
+  if ((lane >> 4) == 0) red[wave * 16 + c] = v;
+  lds_barrier();
+  const int n = threadIdx.x;
+  if (n < 16) {
+    float sum = 0.f;
+    for (int w = 0; w < W; ++w) sum += red[w * 16 + n];   // slot order, then K order
+    a.out[(int64_t)t * a.som + 16 * rt + n] = (uint16_t)f32_to_bf16_bits(sum);
+  }
+}
+
+template <class KERN>
+int dec_launch(KERN kern, int grid, int W, size_t lds, hipStream_t st, const MoeDecArgs& a) {
+  if (lds > 65536) {
+    hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (err != hipSuccess) return (int)err;
+  }
+  kern<<<dim3((unsigned)grid), dim3(64 * W), lds, st>>>(a);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+// S2 line-steps per wave (2, or 4 when K needs more waves than the workgroup has room for):
+// Wk waves per tile or slot, at most 16 waves per workgroup in all.
+bool dec_shape(int64_t Kpad, int groups, int* S2, int* Wk) {
+  if (Kpad % kDLine) return false;
+  const int64_t KL = Kpad / kDLine;
+  for (int s = 2; s <= 4; s += 2) {
+    const int64_t w = (KL + s - 1) / s;
+    if (w * groups <= 16) {
+      *S2 = s;
+      *Wk = (int)w;
+      return true;
+    }
+  }
+  return false;
+}
+
+template <int SDT>
+int dec_gu(const MoeDecArgs& a0, int act, int64_t B, int max_lds, hipStream_t st) {
+  MoeDecArgs a = a0;
+  int S2, Wk;
+  const int groups = act == IMQ_ACT_GPTOSS ? 1 : 2;
+  if (!dec_shape(a.Kpad, groups, &S2, &Wk)) return IMQ_ERR_UNSUPPORTED;
+  a.Wk = Wk;
+  a.NR = act == IMQ_ACT_GPTOSS ? 2 * a.I / 16 : a.I / 16;
+  const int W = groups * Wk;
+  const size_t lds = (size_t)W * dec_wave_lds(S2, SDT == IMQ_DT_FP32 ? 4 : 2) + (size_t)W * 16 * 4;
+  if (lds > (size_t)max_lds || B * a.NR > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  const int grid = (int)(B * a.NR);
+  const bool xcl = a.xk < a.Kpad;
+#define IMQ_GU(S, A, X) dec_launch(moe_gu_line_kernel<S, SDT, A, X>, grid, W, lds, st, a)
+  if (act == IMQ_ACT_GPTOSS) {
+    if (S2 == 2) return xcl ? IMQ_GU(2, 1, true) : IMQ_GU(2, 1, false);
+    return xcl ? IMQ_GU(4, 1, true) : IMQ_GU(4, 1, false);
+  }
+  if (S2 == 2) return xcl ? IMQ_GU(2, 0, true) : IMQ_GU(2, 0, false);
+  return xcl ? IMQ_GU(4, 0, true) : IMQ_GU(4, 0, false);
+#undef IMQ_GU
+}
+
+template <int SDT>
+int dec_dn(const MoeDecArgs& a0, int64_t T, int max_lds, hipStream_t st) {
+  MoeDecArgs a = a0;
+  int S2, Wk;
+  if (!dec_shape(a.Kpad, a.k, &S2, &Wk)) return IMQ_ERR_UNSUPPORTED;
+  a.Wk = Wk;
+  const int W = a.k * Wk;
+  const size_t lds = (size_t)W * dec_wave_lds(S2, SDT == IMQ_DT_FP32 ? 4 : 2) + (size_t)W * 16 * 4;
+  if (lds > (size_t)max_lds || T * a.NR > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  const int grid = (int)(T * a.NR);
+  const bool xcl = a.xk < a.Kpad;
+  if (S2 == 2) return xcl ? dec_launch(moe_dn_line_kernel<2, SDT, true>, grid, W, lds, st, a)
+                          : dec_launch(moe_dn_line_kernel<2, SDT, false>, grid, W, lds, st, a);
+  return xcl ? dec_launch(moe_dn_line_kernel<4, SDT, true>, grid, W, lds, st, a)
+             : dec_launch(moe_dn_line_kernel<4, SDT, false>, grid, W, lds, st, a);
+}
+
 template <int S2, int NTL, int SDT, int MODE, bool XCL>
 int moe_line_launch(const MoeLineArgs& a, int W, int grid, hipStream_t st) {
   const size_t lds = (size_t)W * 2 * NTL * 16 * (S2 * ((SDT == IMQ_DT_FP32) ? 4 : 2) / 2) * 4 +
@@ -716,6 +1032,31 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   // the sort plus the off -> perm -> x dependent loads dominate; rows then run directly
   // (routed order, one row per item, expert idx[b]).
   const bool direct = B * 4 <= c.E;
+  if (direct && c.I % 16 == 0 && c.H % 16 == 0) {
+    // two line-kernel launches: gate_up with the activation, down with the weighted combine
+    MoeDecArgs gu{c.hidden, c.hs, (int)c.xk, (int)c.gK, (int)c.k, c.idx, c.topk_w, (int)c.E, c.gq, c.gqe, c.gqn,
+                  c.gs, c.gz, c.gse, c.gsn, (int)c.I, 0, 0, c.gb, c.gbe, c.bdt, c.alpha, c.limit, h, L.hw};
+    MoeDecArgs dn{h, L.hw, (int)c.I, (int)c.dK, (int)c.k, c.idx, c.topk_w, (int)c.E, c.dq, c.dqe, c.dqn,
+                  c.ds, c.dz, c.dse, c.dsn, (int)c.I, (int)(c.H / 16), 0, c.db, c.dbe, c.bdt, 0.f, 0.f, c.out, c.os};
+    int gs, dshape, dwk;
+    const int groups = c.act == IMQ_ACT_GPTOSS ? 1 : 2;
+    if (dec_shape(c.gK, groups, &gs, &dwk) && dec_shape(c.dK, (int)c.k, &dshape, &dwk)) {
+      int rc = IMQ_ERR_UNSUPPORTED;
+      switch (c.sdt) {
+        case IMQ_DT_BF16: rc = dec_gu<IMQ_DT_BF16>(gu, c.act, B, 65536, st); break;
+        case IMQ_DT_FP16: rc = dec_gu<IMQ_DT_FP16>(gu, c.act, B, 65536, st); break;
+        case IMQ_DT_FP32: rc = dec_gu<IMQ_DT_FP32>(gu, c.act, B, 65536, st); break;
+      }
+      if (rc == IMQ_OK) {
+        switch (c.sdt) {
+          case IMQ_DT_BF16: return dec_dn<IMQ_DT_BF16>(dn, c.T, 65536, st);
+          case IMQ_DT_FP16: return dec_dn<IMQ_DT_FP16>(dn, c.T, 65536, st);
+          case IMQ_DT_FP32: return dec_dn<IMQ_DT_FP32>(dn, c.T, 65536, st);
+        }
+      }
+      if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+    }
+  }
   if (!direct) {
     moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit);
     IMQ_LAUNCH_CHECK();

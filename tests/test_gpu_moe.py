@@ -264,3 +264,18 @@ def test_moe_unpadded_hidden_and_pad_codes(dev, kernel_layout):
     assert torch.equal(y_un, y_junk)
     exact = om.moe_exact_grouped(C.t2np(x), idx, w, Dgu, Ddn)
     assert oq.max_rel(C.t2np(y_un), exact) <= MAX_REL
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_gptoss_decode_gpt20b_widths(dev, T):
+    """Decode rows (4 B <= E) at gpt-oss-20b widths in the kernel layout (K 2880 padded to 3072):
+    the two-launch line path with unpadded hidden rows and h read as zero past I."""
+    _run_gptoss(dev, E=16, H=2880, I=2880, k=2, T=T, seed=95 + T, pad_to_256=True)
+
+
+@pytest.mark.parametrize("sdt", ["bf16", "fp16", "fp32"])
+def test_moe_decode_line_path(dev, sdt):
+    """SiLU-GLU decode through the two-launch line path: one token, 4 of 32 experts, kernel
+    layout K (H 320 -> 512), scale / zero dtypes."""
+    _run(dev, E=32, H=512, I=256, k=4, T=1, seed=97, sdt=sdt)
+    _run(dev, E=32, H=1024, I=512, k=8, T=1, seed=98, sdt=sdt)
