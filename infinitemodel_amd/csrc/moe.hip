@@ -345,6 +345,7 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
     }
 
   const uint32_t magic = magic_bf16_128x2();
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
   for (int p0 = beg; p0 < end; p0 += 16) {
     if constexpr (S2 > 1) {
       // keep the unpack inside the token loop: hoisting the unpacked operands of all tiles out of
@@ -370,10 +371,8 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
       int l = ls0 + i;
       l = l < KL ? l : KL - 1;
       bf16x8_t A[2][4];
-      float gs[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        float sum = 0.f;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
           const int col = kMoeLine * l + 128 * h + 32 * ar + 8 * kk;
@@ -385,20 +384,16 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
           } else {
             v = *(const u32x4_t*)(xr + col);
           }
-#pragma unroll
-          for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
           A[h][kk] = __builtin_bit_cast(bf16x8_t, permute_x8(v));
         }
-        sum += __shfl_xor(sum, 16, 64);
-        sum += __shfl_xor(sum, 32, 64);
-        gs[h] = sum;                                  // group sum of A row c
       }
-      // D rows of this lane: m = 4*ar + r
-      f32x4_t xs0, xs1;
+      // group row sums straight into the D layout (row m = 4*ar + r of every lane): MFMAs against
+      // a B of ones, in place of per-lane sums and cross-lane shuffles
+      f32x4_t xs0 = {0.f, 0.f, 0.f, 0.f}, xs1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        xs0[r] = __shfl(gs[0], 4 * ar + r, 64);
-        xs1[r] = __shfl(gs[1], 4 * ar + r, 64);
+      for (int kk = 0; kk < 4; ++kk) {
+        xs0 = mfma16x16x32(A[0][kk], ones, xs0);
+        xs1 = mfma16x16x32(A[1][kk], ones, xs1);
       }
 #pragma unroll
       for (int t = 0; t < NTL; ++t) {
