@@ -279,3 +279,11 @@ def test_moe_decode_line_path(dev, sdt):
     layout K (H 320 -> 512), scale / zero dtypes."""
     _run(dev, E=32, H=512, I=256, k=4, T=1, seed=97, sdt=sdt)
     _run(dev, E=32, H=1024, I=512, k=8, T=1, seed=98, sdt=sdt)
+
+
+@pytest.mark.parametrize("T", [64, 80])
+def test_moe_many_rows_per_expert(dev, T):
+    """16+ routed rows per expert on average: 32-row blocks with passes of 32 rows (a partial last
+    pass at T 80); SiLU-GLU and gpt-oss."""
+    _run(dev, E=8, H=512, I=256, k=2, T=T, seed=140 + T)
+    _run_gptoss(dev, E=8, H=512, I=256, k=2, T=T, seed=150 + T)
