@@ -66,7 +66,27 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int splits, kps;     // split-K: K steps [split * kps, +kps) per workgroup; 1 = no split
   float* part;         // split-K partials [splits][M][N] fp32
+  // grouped MoE form (the kernel's MOE != 0): a tile is (row block mt, column tile tn);
+  // mtl[2 mt] = expert, mtl[2 mt + 1] = first sorted row of the block, *nmt blocks in all
+  const int32_t* mtl = nullptr;
+  const int32_t* nmt = nullptr;
+  const int32_t* off = nullptr;       // [E + 1] sorted offsets
+  const int32_t* perm = nullptr;      // sorted position -> routed row
+  int64_t sqe = 0, sse = 0;           // expert strides: packed bytes, scale / zero elements
+  int k = 1, I = 0;                   // top_k; intermediate size (gate_up)
+  const void* bias = nullptr;         // per-expert row bias [E][rows] or null
+  int64_t sbe = 0;
+  int bdt = 0;
+  float alpha = 0.f, limit = 0.f;     // gpt-oss activation
+  float* yr = nullptr;                // MOE 3: fp32 rows [B][N] in routed order
 };
+
+// Element i of a per-expert bias row in the bias dtype.
+IMQ_DEV float gemm_bias(const void* p, int dt, int64_t i) {
+  if (dt == IMQ_DT_FP32) return ((const float*)p)[i];
+  if (dt == IMQ_DT_FP16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+  return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
 
 // LDS element offset of 16-byte chunk c of row `row`: the chunk index is XOR-ed with the row's
 // position inside a 256-byte bank period, so 8 consecutive rows read at one chunk hit 8 bank groups.
@@ -156,7 +176,12 @@ IMQ_DEV u32x4_t weight_chunk(const WRegs<BITS, WC>& r, int c, float s, float nzs
   }
 }
 
-template <class C, int BITS, int SDT, int ZDT>
+// MOE 0: the dense GEMM. Grouped MoE forms (int4, rows of one hit expert per block, gathered):
+// MOE 1 gate_up with SiLU-GLU (the tile's first BN/2 weight rows are gate rows, the rest the
+// matching up rows; h = silu(gate) * up written as bf16 in sorted order), MOE 2 gpt-oss gate_up
+// (consecutive interleaved rows, its clamped GLU), MOE 3 down (fp32 rows plus the row bias, in
+// routed order, for the combine).
+template <class C, int BITS, int SDT, int ZDT, int MOE = 0>
 __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, XC = C::XC, WC = C::WC;
   constexpr int BK = C::BK, CH = C::CH, KS = C::KS;
@@ -170,19 +195,34 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
   const int wave = tid >> 6;
 
   // ---- tile mapping: XCD-aware, grouped by GROUP_M tile-rows; split-K index outermost ---------
-  const int T = a.tiles_m * a.tiles_n;
-  const int split = blockIdx.x / T;                 // the splits of one tile run the same XCD
-  const int tile_id = blockIdx.x - split * T;
-  int L = tile_id;
-  if ((T & 7) == 0) L = (L & 7) * (T >> 3) + (L >> 3);
-  const int per_group = GROUP_M * a.tiles_n;
-  const int grp = L / per_group;
-  const int first_m = grp * GROUP_M;
-  const int gm = (a.tiles_m - first_m) < GROUP_M ? (a.tiles_m - first_m) : GROUP_M;
-  const int in_grp = L - grp * per_group;
-  const int tm = first_m + in_grp % gm;
-  const int tn = in_grp / gm;
-  const int m0 = tm * BM, n0 = tn * BN;
+  int split = 0, tn, m0, n0;
+  int e = 0, prow0 = 0, cnt = 0;                    // MOE: expert, first sorted row, rows of the block
+  if constexpr (MOE == 0) {
+    const int T = a.tiles_m * a.tiles_n;
+    split = blockIdx.x / T;                         // the splits of one tile run the same XCD
+    const int tile_id = blockIdx.x - split * T;
+    int L = tile_id;
+    if ((T & 7) == 0) L = (L & 7) * (T >> 3) + (L >> 3);
+    const int per_group = GROUP_M * a.tiles_n;
+    const int grp = L / per_group;
+    const int first_m = grp * GROUP_M;
+    const int gm = (a.tiles_m - first_m) < GROUP_M ? (a.tiles_m - first_m) : GROUP_M;
+    const int in_grp = L - grp * per_group;
+    const int tm = first_m + in_grp % gm;
+    tn = in_grp / gm;
+    m0 = tm * BM;
+    n0 = tn * BN;
+  } else {
+    const int mt = blockIdx.x / a.tiles_n;
+    tn = blockIdx.x - mt * a.tiles_n;
+    if (mt >= *a.nmt) return;                       // uniform over the workgroup
+    e = a.mtl[2 * mt];
+    prow0 = a.mtl[2 * mt + 1];
+    cnt = a.off[e + 1] - prow0;
+    cnt = cnt < BM ? cnt : BM;
+    m0 = 0;
+    n0 = tn * BN;
+  }
 
   // ---- global -> register load plan ----------------------------------------------------------
   // per-thread element offsets from the tile's first row (32-bit) + a uniform per-step base, so
@@ -195,21 +235,28 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
     const int id = tid + NTHR * j;
     const int row = id / CH, c = id % CH;
     int r = row;
-    if (m0 + r >= a.M) r = a.M - 1 - m0;
+    if constexpr (MOE == 0) {
+      if (m0 + r >= a.M) r = a.M - 1 - m0;
+    } else {
+      const int p = prow0 + (r < cnt ? r : cnt - 1);                  // sorted position
+      r = MOE == 3 ? p : a.perm[p] / a.k;           // down reads h in sorted order, gate_up gathers
+    }
     xo[j] = (int)(r * a.sxm) + c * 8;
     xl[j] = swz<C>(row, c);
   }
   constexpr int PARTS = BK / WC;                    // threads per weight row per step
   const int wrow = tid / PARTS, part = tid % PARTS;
   int gn = n0 + wrow;
+  if constexpr (MOE == 1)   // gate rows then the matching up rows
+    gn = wrow < BN / 2 ? tn * (BN / 2) + wrow : a.I + tn * (BN / 2) + (wrow - BN / 2);
   gn = gn < a.N ? gn : a.N - 1;
   constexpr int BYTES_STEP = BK * BITS / 8;
-  const uint8_t* wtile = a.q + (int64_t)n0 * a.sqn;
-  const int wo = (int)((gn - n0) * a.sqn) + part * (WC * BITS / 8);
+  const uint8_t* wtile = MOE == 0 ? a.q + (int64_t)n0 * a.sqn : a.q + (int64_t)e * a.sqe;
+  const int wo = (int)((gn - (MOE == 0 ? n0 : 0)) * a.sqn) + part * (WC * BITS / 8);
   int bl[WC / 8];
 #pragma unroll
   for (int c = 0; c < WC / 8; ++c) bl[c] = swz<C>(wrow, (WC / 8) * part + c);
-  const int64_t sbase = (int64_t)gn * a.ssn, zbase = (int64_t)gn * a.szn;
+  const int64_t sbase = (int64_t)gn * a.ssn + (int64_t)e * a.sse, zbase = (int64_t)gn * a.szn + (int64_t)e * a.sse;
   const int ssg = (int)a.ssg, szg = (int)a.szg;
 
   u32x4_t xr[PD][XC];
@@ -350,6 +397,87 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
     iter(kt + 1, std::integral_constant<int, 1>{});
   }
   if (kt < KT) iter(kt, std::integral_constant<int, 0>{});
+
+  // ---- grouped MoE epilogues --------------------------------------------------------------------
+  if constexpr (MOE != 0) {
+    auto bias_at = [&](int row) -> float {
+      return a.bias != nullptr ? gemm_bias(a.bias, a.bdt, (int64_t)e * a.sbe + row) : 0.f;
+    };
+    if constexpr (MOE == 3) {
+#pragma unroll
+      for (int j = 0; j < JB; ++j) {
+        const int n = n0 + wn * WN + j * 32 + (lane & 31);
+        if (n >= a.N) continue;
+        const float b = bias_at(n);
+#pragma unroll
+        for (int i = 0; i < IB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < cnt) a.yr[(int64_t)a.perm[prow0 + m] * a.N + n] = acc[i][j][r] + b;
+          }
+      }
+    } else if constexpr (MOE == 2) {
+      // interleaved (gate, up) columns sit in adjacent lanes
+#pragma unroll
+      for (int j = 0; j < JB; ++j) {
+        const int n = n0 + wn * WN + j * 32 + (lane & 31);   // even lanes: gate rows
+        const float bg = n < a.N ? bias_at(n) : 0.f, bu = n + 1 < a.N ? bias_at(n + 1) : 0.f;
+#pragma unroll
+        for (int i = 0; i < IB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float v = acc[i][j][r];
+            const float up = __shfl_xor(v, 1, 64);
+            const int m = wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if ((lane & 1) == 0 && m < cnt && n < a.N) {
+              float g = v + bg, u = up + bu;
+              g = g > a.limit ? a.limit : g;
+              u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
+              const float hv = (u + 1.f) * (g / (1.f + __expf(-a.alpha * g)));
+              a.y[(int64_t)(prow0 + m) * a.sym + (n >> 1)] = (uint16_t)cvt_pk_bf16(hv, 0.f);
+            }
+          }
+      }
+    } else {
+      // gate columns live in the waves of the left column half, up columns in the right half:
+      // the up sums go through LDS
+      constexpr int HW = C::WAVES_N / 2;
+      static_assert(C::WAVES_N % 2 == 0 && BM * (BN / 2) * 4 <= C::LDS, "MOE 1 pairs the tile's column halves");
+      float* U = (float*)lds;                        // [BM][BN/2], the K-loop buffers are done
+      const int wcol = (wn % HW) * WN;
+#pragma unroll
+      for (int j = 0; j < JB; ++j)
+#pragma unroll
+        for (int i = 0; i < IB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int col = wcol + j * 32 + (lane & 31);
+            if (wn >= HW) U[m * (BN / 2) + col] = acc[i][j][r];
+          }
+      __syncthreads();
+      if (wn < HW) {
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+          const int col = wcol + j * 32 + (lane & 31);
+          const int hc = tn * (BN / 2) + col;        // h column = gate row
+          const float bg = bias_at(hc), bu = bias_at(a.I + hc);
+#pragma unroll
+          for (int i = 0; i < IB; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int m = wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+              if (m < cnt) {
+                const float g = acc[i][j][r] + bg, u = U[m * (BN / 2) + col] + bu;
+                a.y[(int64_t)(prow0 + m) * a.sym + hc] = (uint16_t)cvt_pk_bf16(g / (1.f + __expf(-g)) * u, 0.f);
+              }
+            }
+        }
+      }
+    }
+    return;
+  }
 
   // ---- split-K: each split stores its fp32 partial tile into [split][M][N]; splitk_reduce_kernel
   // sums the splits in order (deterministic) and writes y. A second launch instead of arrival
@@ -523,6 +651,74 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 16 || N <= 0 || K % 64 != 0) return 0;
   const int cus = device_info().cus;
   return use_big(M) ? split_bytes<CfgBig>(M, N, K, cus) : split_bytes<CfgSmall>(M, N, K, cus);
+}
+
+namespace {
+// Grouped MoE GEMM (int4, G = 128): BM x BN tiles of one hit expert's sorted rows; see the
+// kernel's MOE forms. Tiles past the device-side block count exit at once.
+#ifndef IMQ_MOE_GEMM_CFG
+#define IMQ_MOE_GEMM_CFG 64, 128, 64, 2, 2, 2
+#endif
+using CfgMoe = Cfg<IMQ_MOE_GEMM_CFG>;
+template <int SDT, int MOE>
+int moe_gemm_launch(const GemmArgs& a, int64_t max_mt, hipStream_t st) {
+  const int64_t grid = max_mt * a.tiles_n;
+  if (grid > 0x7fffffff || grid <= 0) return grid <= 0 ? IMQ_OK : IMQ_ERR_UNSUPPORTED;
+  auto kern = gemm_wq_kernel<CfgMoe, 4, SDT, SDT, MOE>;
+  if (CfgMoe::LDS > 65536) {
+    static int attr_set = 0;   // benign race: every caller sets the same attribute value
+    if (!__atomic_load_n(&attr_set, __ATOMIC_ACQUIRE)) {
+      hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, CfgMoe::LDS);
+      if (e != hipSuccess) return (int)e;
+      __atomic_store_n(&attr_set, 1, __ATOMIC_RELEASE);
+    }
+  }
+  kern<<<dim3((unsigned)grid), dim3(CfgMoe::NTHR), CfgMoe::LDS, st>>>(a);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+}  // namespace
+
+int moe_gemm_bm() { return CfgMoe::BM; }
+int moe_gemm_bn() { return CfgMoe::BN; }
+
+// mode 1: gate_up SiLU-GLU (N = 2I, I a multiple of BN / 2), 2: gate_up gpt-oss (N = 2I), 3: down (N = H).
+// x rows: hidden (modes 1, 2: row perm[p] / k) or h (mode 3: row p), stride sxm, K columns.
+int moe_gemm_w4(int mode, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t K, const uint8_t* q, int64_t sqe,
+                int64_t sqn,
+                const void* sc, const void* zr, int64_t sse, int64_t ssn, int sdt, int64_t N, int64_t I,
+                const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off, const int32_t* perm, int k,
+                const void* bias, int64_t sbe, int bdt, float alpha, float limit, uint16_t* h, int64_t hs,
+                float* yr, hipStream_t st) {
+  if (K % CfgMoe::BK != 0 || K <= 0 || N <= 0 || (mode == 1 && I % (CfgMoe::BN / 2) != 0)) return IMQ_ERR_UNSUPPORTED;
+  if (((uintptr_t)x & 15) || (sxm & 7) || ((uintptr_t)q & 15) || (sqn & 15) || (sqe & 15)) return IMQ_ERR_UNSUPPORTED;
+  if (128 * sqn > 0x7fffffff || N * sqn > 0x7fffffff || xrows * sxm > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  GemmArgs a{x, sxm, 0, (int)K, q, sqn, sc, ssn, 1, zr, ssn, 1, (int)N, 7, h, hs, 0, 0, 1, 0, nullptr};
+  a.tiles_n = mode == 1 ? (int)(I / (CfgMoe::BN / 2)) : (int)((N + CfgMoe::BN - 1) / CfgMoe::BN);
+  a.kps = (int)(K / CfgMoe::BK);
+  a.mtl = mtl;
+  a.nmt = nmt;
+  a.off = off;
+  a.perm = perm;
+  a.sqe = sqe;
+  a.sse = sse;
+  a.k = k;
+  a.I = (int)I;
+  a.bias = bias;
+  a.sbe = sbe;
+  a.bdt = bdt;
+  a.alpha = alpha;
+  a.limit = limit;
+  a.yr = yr;
+#define IMQ_MG(S) (mode == 1 ? moe_gemm_launch<S, 1>(a, max_mt, st) : mode == 2 ? moe_gemm_launch<S, 2>(a, max_mt, st) \
+                                                                              : moe_gemm_launch<S, 3>(a, max_mt, st))
+  switch (sdt) {
+    case IMQ_DT_BF16: return IMQ_MG(IMQ_DT_BF16);
+    case IMQ_DT_FP16: return IMQ_MG(IMQ_DT_FP16);
+    case IMQ_DT_FP32: return IMQ_MG(IMQ_DT_FP32);
+  }
+#undef IMQ_MG
+  return IMQ_ERR_INVALID;
 }
 
 // Prefill GEMM entry used by imq_linear_w4 / _w2 / _w8 for M > 16. Returns IMQ_ERR_UNSUPPORTED

@@ -18,6 +18,19 @@
 //                    to both projections' outputs).
 #include "imq_common.h"
 
+namespace imq {
+int moe_gemm_bm();
+int moe_gemm_bn();
+int moe_gemm_w4(int mode, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t K, const uint8_t* q, int64_t sqe,
+                int64_t sqn, const void* sc, const void* zr, int64_t sse, int64_t ssn, int sdt, int64_t N, int64_t I,
+                const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off, const int32_t* perm, int k,
+                const void* bias, int64_t sbe, int bdt, float alpha, float limit, uint16_t* h, int64_t hs,
+                float* yr, hipStream_t st);
+}  // namespace imq
+using imq::moe_gemm_bm;
+using imq::moe_gemm_bn;
+using imq::moe_gemm_w4;
+
 namespace {
 
 constexpr int64_t kAlign = 256;
@@ -156,9 +169,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 //   moe_combine_kernel out[t] = bf16(sum_j w[t, j] * yr[t*k + j]), slot order.
 constexpr int kMoeLine = 256;
 
+// mtl (optional): the grouped GEMM's row blocks, mtl[0] = their number, then (expert, first sorted
+// row) pairs from mtl[2], bm sorted rows per block -- at most ceil(B / bm) + (hit experts) blocks.
 __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restrict__ idx, int B, int E,
                                                         int32_t* __restrict__ off, int32_t* __restrict__ perm,
-                                                        int32_t* __restrict__ hit) {
+                                                        int32_t* __restrict__ hit, int32_t* __restrict__ mtl,
+                                                        int bm) {
   extern __shared__ int32_t cnt[];     // [E]: counts, then scatter cursors
   const int tid = threadIdx.x, nt = blockDim.x;
   for (int e = tid; e < E; e += nt) cnt[e] = 0;
@@ -174,31 +190,39 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
     // the hit flags give the sorted offsets and the ascending list of hit experts
     const int per = (E + 63) / 64;
     const int e0 = tid * per, e1 = (e0 + per < E) ? e0 + per : E;
-    int rows = 0, hits = 0;
+    int rows = 0, hits = 0, blks = 0;
     for (int e = e0; e < e1; ++e) {
       rows += cnt[e];
       hits += cnt[e] > 0;
+      blks += (cnt[e] + bm - 1) / bm;
     }
-    int rs = rows, hs = hits;
+    int rs = rows, hs = hits, bs = blks;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-      const int r = __shfl_up(rs, d, 64), h = __shfl_up(hs, d, 64);
+      const int r = __shfl_up(rs, d, 64), h = __shfl_up(hs, d, 64), b = __shfl_up(bs, d, 64);
       if (tid >= d) {
         rs += r;
         hs += h;
+        bs += b;
       }
     }
-    int run = rs - rows, hrun = hs - hits;
+    int run = rs - rows, hrun = hs - hits, brun = bs - blks;
     for (int e = e0; e < e1; ++e) {
       const int c = cnt[e];
       off[e] = run;
       if (c > 0) hit[hrun++] = e;
+      if (mtl != nullptr)
+        for (int r0 = 0; r0 < c; r0 += bm, ++brun) {
+          mtl[2 + 2 * brun] = e;
+          mtl[3 + 2 * brun] = run + r0;
+        }
       cnt[e] = run;
       run += c;
     }
     if (tid == 63) {
       off[E] = rs;
       hit[E] = hs;                        // number of hit experts
+      if (mtl != nullptr) mtl[0] = bs;
     }
   }
   __syncthreads();
@@ -1004,6 +1028,51 @@ struct MoeCall {
   int64_t xk;            // valid hidden columns: gu_K_pad for padded rows, else H (H % 8 == 0)
 };
 
+// Grouped GEMM path for many routed rows per expert (prefill): the sort also lists the 64-row
+// blocks of each hit expert; gate_up and down then run as tiled dequant-GEMMs over those blocks
+// (the prefill GEMM kernel's grouped forms), the activation in gate_up's epilogue, the row bias
+// and the scatter to routed order in down's; the combine is moe_combine_kernel's. Measured on
+// MI355X (us per layer, line kernels -> GEMM): OLMoE T=128 (16 rows per expert) 107 -> 147,
+// T=256 148 -> 155; gpt-oss-20b T=256 (32 rows per expert) 368 -> 255: from 32 rows per expert.
+#ifndef IMQ_MOE_GEMM_ROWS
+#define IMQ_MOE_GEMM_ROWS 32
+#endif
+constexpr int64_t kMoeGemmRows = IMQ_MOE_GEMM_ROWS;   // routed rows per expert (B / E) from which the GEMM runs
+int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
+  const int64_t B = c.T * c.k;
+  const int bm = moe_gemm_bm();
+  const int64_t hits = c.E < B ? c.E : B;
+  const int64_t max_mt = imq_cdiv(B, bm) + hits;
+  if ((2 + 2 * max_mt) * 4 > L.h - L.gu) return IMQ_ERR_UNSUPPORTED;   // the list lives in gu's room
+  int32_t* off = (int32_t*)(ws + L.off);
+  int32_t* perm = (int32_t*)(ws + L.perm);
+  int32_t* hit = (int32_t*)(ws + L.hit);
+  int32_t* mtl = (int32_t*)(ws + L.gu);
+  uint16_t* h = (uint16_t*)(ws + L.h);
+  float* yr = (float*)(ws + L.z);
+  moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit, mtl, bm);
+  IMQ_LAUNCH_CHECK();
+  const int gmode = c.act == IMQ_ACT_GPTOSS ? 2 : 1;
+  int rc = moe_gemm_w4(gmode, c.hidden, c.hs, c.T, c.gK, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
+                       2 * c.I, c.I, mtl + 2, mtl, max_mt, off, perm, (int)c.k, c.gb, c.gbe, c.bdt, c.alpha, c.limit,
+                       h, L.hw, nullptr, st);
+  if (rc != IMQ_OK) return rc;
+  if (c.dK > c.I) {   // h's columns past I are read by down's K steps: zero them
+    const int64_t total = B * (c.dK - c.I);
+    const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
+    moe_zero_pad_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(h, B, c.I, c.dK, L.hw);
+    IMQ_LAUNCH_CHECK();
+  }
+  rc = moe_gemm_w4(3, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2, mtl,
+                   max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, st);
+  if (rc != IMQ_OK) return rc;
+  const int64_t total = c.T * (c.H / 8);
+  const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
+  moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, c.topk_w, c.T, c.k, c.H, c.out, c.os);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
 // Token-sorted grouped path; IMQ_ERR_UNSUPPORTED when the shape or layout does not qualify.
 int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   const int64_t B = c.T * c.k;
@@ -1052,8 +1121,14 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
       if (rc != IMQ_ERR_UNSUPPORTED) return rc;
     }
   }
+  const bool gemm_shape = c.act == IMQ_ACT_GPTOSS || c.I % (moe_gemm_bn() / 2) == 0;
+  if (!direct && B >= kMoeGemmRows * c.E && c.xk == c.gK && gemm_shape) {
+    const int rc = moe_gemm(c, ws, L, st);
+    if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+  }
   if (!direct) {
-    moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit);
+    moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit, nullptr,
+                                                                   1);
     IMQ_LAUNCH_CHECK();
   }
   MoeLineArgs g{c.hidden, c.hs, (int)c.gK, (int)c.k, off, perm, hit, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn,

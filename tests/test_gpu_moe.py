@@ -287,3 +287,26 @@ def test_moe_many_rows_per_expert(dev, T):
     pass at T 80); SiLU-GLU and gpt-oss."""
     _run(dev, E=8, H=512, I=256, k=2, T=T, seed=140 + T)
     _run_gptoss(dev, E=8, H=512, I=256, k=2, T=T, seed=150 + T)
+
+
+@pytest.mark.parametrize("E,H,I,k,T,sdt", [
+    (4, 512, 256, 2, 300, "bf16"),     # ~150 rows per expert: several 64-row blocks, partial last ones
+    (4, 512, 192, 2, 64, "bf16"),      # I_pad 256 > I: h's pad columns zeroed before down
+    (6, 768, 320, 3, 96, "fp16"),
+    (6, 512, 256, 2, 100, "fp32"),
+])
+def test_moe_grouped_gemm_path(dev, E, H, I, k, T, sdt):
+    """Prefill rows (B >= 32 E): the grouped dequant-GEMM over 64-row blocks of each hit expert,
+    SwiGLU in gate_up's epilogue, the scatter to routed order in down's."""
+    _run(dev, E=E, H=H, I=I, k=k, T=T, seed=160 + T, sdt=sdt)
+
+
+@pytest.mark.parametrize("E,H,I,k,T,bias_std,pad", [
+    (4, 512, 256, 2, 200, 0.02, False),
+    (6, 256, 128, 2, 100, 6.0, False),      # clamps active
+    (4, 2880, 2880, 2, 64, 0.02, True),     # gpt-oss-20b widths, K padded to 3072
+])
+def test_gptoss_grouped_gemm_path(dev, E, H, I, k, T, bias_std, pad):
+    """gpt-oss prefill rows through the grouped GEMM: interleaved (gate, up) columns in adjacent
+    lanes of the epilogue, its clamped GLU, both biases."""
+    _run_gptoss(dev, E=E, H=H, I=I, k=k, T=T, seed=170 + T, bias_std=bias_std, pad_to_256=pad)

@@ -937,3 +937,116 @@ def test_gemm_split_k_ranges(M, N, K):
     if S > 1:
         # stores are masked to m < M, n < N: the last partial element is ((S-1)*M + M-1)*N + N-1
         assert (((S - 1) * M + M - 1) * N + N - 1 + 1) * 4 == S * M * N * 4
+
+
+# ---- grouped MoE GEMM (csrc/gemm.hip gemm_wq_kernel MOE 1-3, csrc/moe.hip moe_sort_kernel) ----
+MOE_BM, MOE_BN, MOE_BK = 64, 128, 64
+
+
+def moe_blocks(idx, E, bm=MOE_BM):
+    """moe_sort_kernel's sorted offsets and its block list: wave 0's lanes own ceil(E / 64)
+    experts each; exclusive scans of the per-lane row and block counts place each lane's blocks."""
+    import numpy as np
+    e_of = np.where((idx >= 0) & (idx < E), idx, 0)
+    cnt = np.bincount(e_of, minlength=E)
+    per = -(-E // 64)
+    rows_l, blks_l = [], []
+    for lane in range(64):
+        e0, e1 = lane * per, min(lane * per + per, E)
+        rows_l.append(int(cnt[e0:e1].sum()) if e0 < E else 0)
+        blks_l.append(sum(-(-int(c) // bm) for c in cnt[e0:e1]) if e0 < E else 0)
+    run, brun = 0, 0
+    off = [0] * (E + 1)
+    mtl = {}
+    for lane in range(64):
+        e0, e1 = lane * per, min(lane * per + per, E)
+        b = brun
+        for e in range(e0, e1):
+            off[e] = run
+            for r0 in range(0, int(cnt[e]), bm):
+                mtl[b] = (e, run + r0)
+                b += 1
+            run += int(cnt[e])
+        brun += blks_l[lane]
+        assert b == brun
+    off[E] = run
+    perm = np.argsort(e_of, kind="stable")
+    return off, perm, [mtl[i] for i in range(brun)]
+
+
+def moe_gemm_ranges(mode, idx, E, k, K, N, I, sxm, xrows, sqe, sqn, sse, ssn, hs):
+    """Max exclusive element / byte offsets of one grouped launch and the written cells."""
+    B = len(idx)
+    off, perm, blocks = moe_blocks(idx, E)
+    max_mt = -(-B // MOE_BM) + min(E, B)
+    assert len(blocks) <= max_mt
+    tiles_n = I // (MOE_BN // 2) if mode == 1 else -(-N // MOE_BN)
+    x_hi = q_hi = s_hi = 0
+    written = set()
+    for e, p0 in blocks:
+        cnt = min(off[e + 1] - p0, MOE_BM)
+        assert cnt >= 1
+        for row in range(MOE_BM):
+            p = p0 + min(row, cnt - 1)
+            r = p if mode == 3 else int(perm[p]) // k
+            assert 0 <= r < xrows
+            x_hi = max(x_hi, r * sxm + K)              # last step: chunk 7 of columns K-64 .. K
+        for tn in range(tiles_n):
+            for wrow in range(MOE_BN):
+                gn = tn * MOE_BN + wrow
+                if mode == 1:
+                    gn = tn * 64 + wrow if wrow < 64 else I + tn * 64 + wrow - 64
+                gn = min(gn, N - 1)
+                q_hi = max(q_hi, e * sqe + gn * sqn + 16 + (K // MOE_BK - 1) * 32 + 16)
+                s_hi = max(s_hi, e * sse + gn * ssn + (K - 1) // 128 + 1)
+            for m in range(cnt):
+                if mode == 1:
+                    for col in range(64):
+                        written.add(((p0 + m) * hs + tn * 64 + col))
+                elif mode == 2:
+                    for n in range(tn * MOE_BN, min(tn * MOE_BN + MOE_BN, N), 2):
+                        written.add((p0 + m) * hs + n // 2)
+                else:
+                    for n in range(tn * MOE_BN, min(tn * MOE_BN + MOE_BN, N)):
+                        written.add(int(perm[p0 + m]) * N + n)
+    return x_hi, q_hi, s_hi, written
+
+
+@pytest.mark.parametrize("mode,E,T,k,H,I", [
+    (1, 4, 150, 2, 512, 256), (1, 6, 96, 3, 768, 320), (2, 4, 40, 2, 3072, 2880), (3, 4, 150, 2, 512, 256),
+    (3, 70, 40, 8, 256, 128),
+])
+def test_moe_gemm_in_bounds_and_covering(mode, E, T, k, H, I):
+    """Every read of the grouped GEMM stays in its exact-fit buffer and the writes cover exactly
+    the sorted h cells (gate_up) or the routed fp32 rows (down), for routings with empty experts,
+    more than 64 rows per expert and E > 64 (several experts per lane of the sort's scan)."""
+    import numpy as np
+    rng = np.random.default_rng(mode * 100 + E)
+    B = T * k
+    idx = rng.integers(0, max(1, E - 1), size=B)         # expert E-1 never hit
+    Ip = -(-I // 128) * 128
+    hw = -(-Ip // 256) * 256
+    if mode == 3:
+        K, N, sxm, xrows = Ip, H, hw, B
+    else:
+        K, N, sxm, xrows = H, 2 * I, H, T
+    sqn, ssn = K // 2, K // 128
+    sqe, sse = N * sqn, N * ssn
+    x_hi, q_hi, s_hi, written = moe_gemm_ranges(mode, idx, E, k, K, N, I, sxm, xrows, sqe, sqn, sse, ssn, hw)
+    assert x_hi <= xrows * sxm
+    assert q_hi <= E * sqe
+    assert s_hi <= E * sse
+    if mode == 3:
+        assert written == {b * N + n for b in range(B) for n in range(N)}
+    else:
+        assert written == {p * hw + c for p in range(B) for c in range(I)}
+
+
+def test_moe_blocks_model_catches_block_overlap():
+    """A block list built with a wrong block size (rows of 64-row blocks counted as 32) overlaps."""
+    import numpy as np
+    idx = np.repeat(np.arange(3), 100)
+    off, _, blocks = moe_blocks(idx, 3, bm=32)
+    spans = [(p0, min(off[e + 1] - p0, MOE_BM)) for e, p0 in blocks]
+    cover = sorted(p for p0, c in spans for p in range(p0, p0 + c))
+    assert len(cover) != len(set(cover))
