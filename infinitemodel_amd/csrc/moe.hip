@@ -1031,13 +1031,17 @@ struct MoeCall {
 // Grouped GEMM path for many routed rows per expert (prefill): the sort also lists the 64-row
 // blocks of each hit expert; gate_up and down then run as tiled dequant-GEMMs over those blocks
 // (the prefill GEMM kernel's grouped forms), the activation in gate_up's epilogue, the row bias
-// and the scatter to routed order in down's; the combine is moe_combine_kernel's. Measured on
-// MI355X (us per layer, line kernels -> GEMM): OLMoE T=128 (16 rows per expert) 107 -> 147,
-// T=256 148 -> 155; gpt-oss-20b T=256 (32 rows per expert) 368 -> 255: from 32 rows per expert.
-#ifndef IMQ_MOE_GEMM_ROWS
-#define IMQ_MOE_GEMM_ROWS 32
+// and the scatter to routed order in down's; the combine is moe_combine_kernel's. It pays once
+// an expert's rows times K is large enough to amortize the per-block costs; measured on MI355X
+// (us per layer, line kernels -> GEMM; rows per expert = B / E):
+//   OLMoE (K 2048)   T=128 (16 rows) 107 -> 147, T=256 (32) 148 -> 155, T=384 (48) 191 -> 163,
+//                    T=512 (64) 222 -> 187, T=1024 (128) 385 -> 304
+//   gpt-oss (K 3072) T=128 (16 rows) 249 -> 249, T=256 (32) 368 -> 255, T=512 (64) 609 -> 380
+// so the GEMM runs from (B / E) * gate_up K >= 81920 (32 rows at K 2560, 40 at K 2048).
+#ifndef IMQ_MOE_GEMM_WORK
+#define IMQ_MOE_GEMM_WORK 81920
 #endif
-constexpr int64_t kMoeGemmRows = IMQ_MOE_GEMM_ROWS;   // routed rows per expert (B / E) from which the GEMM runs
+constexpr int64_t kMoeGemmWork = IMQ_MOE_GEMM_WORK;
 int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   const int64_t B = c.T * c.k;
   const int bm = moe_gemm_bm();
@@ -1122,7 +1126,7 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
     }
   }
   const bool gemm_shape = c.act == IMQ_ACT_GPTOSS || c.I % (moe_gemm_bn() / 2) == 0;
-  if (!direct && B >= kMoeGemmRows * c.E && c.xk == c.gK && gemm_shape) {
+  if (!direct && B * c.gK >= kMoeGemmWork * c.E && c.xk == c.gK && gemm_shape) {
     const int rc = moe_gemm(c, ws, L, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }

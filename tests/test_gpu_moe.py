@@ -95,9 +95,11 @@ def test_moe_token_sorted_scale_dtypes(dev, sdt):
     _run(dev, E=4, H=512, I=256, k=2, T=20, seed=9, sdt=sdt)
 
 
-def test_moe_olmoe_shape_prefill(dev):
-    """BASELINE C5 at T = 256 (every expert hit, ~32 rows each)."""
-    _run(dev, E=64, H=2048, I=1024, k=8, T=256, seed=3000)
+@pytest.mark.parametrize("T", [256, 384])
+def test_moe_olmoe_shape_prefill(dev, T):
+    """BASELINE C5 at T = 256 (every expert hit, ~32 rows each: the token-sorted line kernels) and
+    T = 384 (~48 rows: the grouped GEMM)."""
+    _run(dev, E=64, H=2048, I=1024, k=8, T=T, seed=3000)
 
 
 def test_moe_repeat_identical(dev):
@@ -290,20 +292,20 @@ def test_moe_many_rows_per_expert(dev, T):
 
 
 @pytest.mark.parametrize("E,H,I,k,T,sdt", [
-    (4, 512, 256, 2, 300, "bf16"),     # ~150 rows per expert: several 64-row blocks, partial last ones
-    (4, 512, 192, 2, 64, "bf16"),      # I_pad 256 > I: h's pad columns zeroed before down
-    (6, 768, 320, 3, 96, "fp16"),
-    (6, 512, 256, 2, 100, "fp32"),
+    (4, 512, 256, 2, 400, "bf16"),     # ~200 rows per expert: several 64-row blocks, partial last ones
+    (4, 512, 192, 2, 330, "bf16"),     # I_pad 256 > I: h's pad columns zeroed before down
+    (6, 768, 320, 3, 220, "fp16"),
+    (6, 512, 256, 2, 480, "fp32"),
 ])
 def test_moe_grouped_gemm_path(dev, E, H, I, k, T, sdt):
-    """Prefill rows (B >= 32 E): the grouped dequant-GEMM over 64-row blocks of each hit expert,
-    SwiGLU in gate_up's epilogue, the scatter to routed order in down's."""
+    """Prefill rows ((B / E) * K >= 81920): the grouped dequant-GEMM over 64-row blocks of each hit
+    expert, SwiGLU in gate_up's epilogue, the scatter to routed order in down's."""
     _run(dev, E=E, H=H, I=I, k=k, T=T, seed=160 + T, sdt=sdt)
 
 
 @pytest.mark.parametrize("E,H,I,k,T,bias_std,pad", [
-    (4, 512, 256, 2, 200, 0.02, False),
-    (6, 256, 128, 2, 100, 6.0, False),      # clamps active
+    (4, 512, 256, 2, 330, 0.02, False),
+    (6, 256, 128, 2, 960, 6.0, False),      # clamps active
     (4, 2880, 2880, 2, 64, 0.02, True),     # gpt-oss-20b widths, K padded to 3072
 ])
 def test_gptoss_grouped_gemm_path(dev, E, H, I, k, T, bias_std, pad):
