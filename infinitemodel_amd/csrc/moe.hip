@@ -1090,7 +1090,8 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
       (c.dsn * vb) % 4 || (c.gse * vb) % 4 || (c.dse * vb) % 4)
     return IMQ_ERR_UNSUPPORTED;
   int s2, w;
-  if (!moe_line_shape(c.gK, &s2, &w) || !moe_line_shape(c.dK, &s2, &w)) return IMQ_ERR_UNSUPPORTED;
+  // the line kernels take K up to 4096; the grouped GEMM any K
+  const bool line_ok = moe_line_shape(c.gK, &s2, &w) && moe_line_shape(c.dK, &s2, &w);
   int32_t* off = (int32_t*)(ws + L.off);
   int32_t* perm = (int32_t*)(ws + L.perm);
   int32_t* hit = (int32_t*)(ws + L.hit);
@@ -1100,7 +1101,7 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   // the sort plus the off -> perm -> x dependent loads dominate; rows then run directly
   // (routed order, one row per item, expert idx[b]).
   const bool direct = B * 4 <= c.E;
-  if (direct && c.I % 16 == 0 && c.H % 16 == 0) {
+  if (direct && line_ok && c.I % 16 == 0 && c.H % 16 == 0) {
     // two line-kernel launches: gate_up with the activation, down with the weighted combine
     MoeDecArgs gu{c.hidden, c.hs, (int)c.xk, (int)c.gK, (int)c.k, c.idx, c.topk_w, (int)c.E, c.gq, c.gqe, c.gqn,
                   c.gs, c.gz, c.gse, c.gsn, (int)c.I, 0, 0, c.gb, c.gbe, c.bdt, c.alpha, c.limit, h, L.hw};
@@ -1126,10 +1127,11 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
     }
   }
   const bool gemm_shape = c.act == IMQ_ACT_GPTOSS || c.I % (moe_gemm_bn() / 2) == 0;
-  if (!direct && B * c.gK >= kMoeGemmWork * c.E && c.xk == c.gK && gemm_shape) {
+  if (!direct && (!line_ok || B * c.gK >= kMoeGemmWork * c.E) && c.xk == c.gK && gemm_shape) {
     const int rc = moe_gemm(c, ws, L, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }
+  if (!line_ok) return IMQ_ERR_UNSUPPORTED;
   if (!direct) {
     moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit, nullptr,
                                                                    1);

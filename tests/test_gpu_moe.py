@@ -312,3 +312,10 @@ def test_gptoss_grouped_gemm_path(dev, E, H, I, k, T, bias_std, pad):
     """gpt-oss prefill rows through the grouped GEMM: interleaved (gate, up) columns in adjacent
     lanes of the epilogue, its clamped GLU, both biases."""
     _run_gptoss(dev, E=E, H=H, I=I, k=k, T=T, seed=170 + T, bias_std=bias_std, pad_to_256=pad)
+
+
+@pytest.mark.parametrize("E,H,I,k,T", [(4, 4608, 256, 2, 24), (4, 512, 4352, 2, 24)])
+def test_moe_grouped_gemm_wide_k(dev, E, H, I, k, T):
+    """K beyond the line kernels' 4096 (gate_up K 4608, down K 4352): prefill rows take the grouped
+    GEMM whatever their number per expert."""
+    _run(dev, E=E, H=H, I=I, k=k, T=T, seed=180 + H)

@@ -1014,7 +1014,7 @@ def moe_gemm_ranges(mode, idx, E, k, K, N, I, sxm, xrows, sqe, sqn, sse, ssn, hs
 
 @pytest.mark.parametrize("mode,E,T,k,H,I", [
     (1, 4, 150, 2, 512, 256), (1, 6, 96, 3, 768, 320), (2, 4, 40, 2, 3072, 2880), (3, 4, 150, 2, 512, 256),
-    (3, 70, 40, 8, 256, 128),
+    (3, 70, 40, 8, 256, 128), (1, 4, 24, 2, 4608, 256), (3, 4, 24, 2, 512, 4352),
 ])
 def test_moe_gemm_in_bounds_and_covering(mode, E, T, k, H, I):
     """Every read of the grouped GEMM stays in its exact-fit buffer and the writes cover exactly
