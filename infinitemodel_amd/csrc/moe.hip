@@ -179,9 +179,11 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
   const int tid = threadIdx.x, nt = blockDim.x;
   for (int e = tid; e < E; e += nt) cnt[e] = 0;
   __syncthreads();
-  for (int b = tid; b < B; b += nt) {
+  int ec[4];                           // the first 4 of this thread's ids stay in registers
+  for (int b = tid, i = 0; b < B; b += nt, ++i) {
     int e = idx[b];
     e = (e >= 0 && e < E) ? e : 0;   // ids outside [0, E) are clamped, so every access stays in bounds
+    if (i < 4) ec[i] = e;
     atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
@@ -226,8 +228,8 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
     }
   }
   __syncthreads();
-  for (int b = tid; b < B; b += nt) {
-    int e = idx[b];
+  for (int b = tid, i = 0; b < B; b += nt, ++i) {
+    int e = i < 4 ? ec[i] : idx[b];
     e = (e >= 0 && e < E) ? e : 0;
     perm[atomicAdd(&cnt[e], 1)] = b;
   }
@@ -497,27 +499,33 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ yr, const uint16_t* __restrict__ w,
                                                           int64_t T, int64_t k, int64_t H,
                                                           uint16_t* __restrict__ out, int64_t so) {
-  const int64_t H8 = H / 8;
-  const int64_t total = T * H8;
+  // 4 columns per thread; the slots' loads go out 8 at a time before their sums (slot order kept)
+  const int64_t H4 = H / 4;
+  const int64_t total = T * H4;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t tok = t / H8;
-    const int64_t n = 8 * (t - tok * H8);
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int64_t j = 0; j < k; ++j) {
-      const float wj = bf16_bits_to_f32(w[tok * k + j]);
-      const float* src = yr + (tok * k + j) * H + n;
-      const f32x4_t v0 = *(const f32x4_t*)src, v1 = *(const f32x4_t*)(src + 4);
+    const int64_t tok = t / H4;
+    const int64_t n = 4 * (t - tok * H4);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t j0 = 0; j0 < k; j0 += 8) {
+      f32x4_t v[8];
+      float wj[8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc[q] = fmaf(wj, v0[q], acc[q]);
-        acc[4 + q] = fmaf(wj, v1[q], acc[4 + q]);
+      for (int j = 0; j < 8; ++j) {
+        const int64_t jj = j0 + j < k ? j0 + j : k - 1;
+        v[j] = *(const f32x4_t*)(yr + (tok * k + jj) * H + n);
+        wj[j] = bf16_bits_to_f32(w[tok * k + jj]);
       }
-    }
-    u32x4_t o;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) o[q] = cvt_pk_bf16(acc[2 * q], acc[2 * q + 1]);
-    *(u32x4_t*)(out + tok * so + n) = o;
+      for (int j = 0; j < 8; ++j)
+        if (j0 + j < k)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[q] = fmaf(wj[j], v[j][q], acc[q]);
+    }
+    u32x2_t o;
+    o[0] = cvt_pk_bf16(acc[0], acc[1]);
+    o[1] = cvt_pk_bf16(acc[2], acc[3]);
+    *(u32x2_t*)(out + tok * so + n) = o;
   }
 }
 
@@ -1070,7 +1078,7 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   rc = moe_gemm_w4(3, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2, mtl,
                    max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, st);
   if (rc != IMQ_OK) return rc;
-  const int64_t total = c.T * (c.H / 8);
+  const int64_t total = c.T * (c.H / 4);
   const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
   moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, c.topk_w, c.T, c.k, c.H, c.out, c.os);
   IMQ_LAUNCH_CHECK();
@@ -1155,7 +1163,7 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
                 (int)c.E, 0, 0, yr, c.H, c.db, c.dbe, c.bdt, 0.f, 0.f, (int)hxk, c.idx, (int)B, direct ? 1 : 0};
   rc = moe_line_sdt<1>(d, (int)c.H, B, c.sdt, st);
   if (rc != IMQ_OK) return rc;
-  const int64_t total = c.T * (c.H / 8);
+  const int64_t total = c.T * (c.H / 4);
   const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
   moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, c.topk_w, c.T, c.k, c.H, c.out, c.os);
   IMQ_LAUNCH_CHECK();
