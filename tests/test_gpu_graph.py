@@ -1,0 +1,110 @@
+"""HIP graph replay of every kernel family, the way bench.py times them.
+
+An op captured in a graph and replayed several times -- with eager work of the library and of
+torch between the replays -- must give results bit-identical to its eager call on every replay:
+no memset nodes, no state carried from one call to the next, workspaces reused correctly. The
+eager result itself is checked against the oracle by the parity tests of each family."""
+import numpy as np
+import pytest
+
+from oracle import moe as om
+from oracle import quant as oq
+from tests import _cases as C
+
+pytestmark = pytest.mark.gpu
+
+
+def _replay_check(fn, between):
+    import torch
+    eager = fn().clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        between()
+        torch.cuda.synchronize()
+    return eager
+
+
+def _x(dev, M, K, seed):
+    return C.to_torch(C.bf16_normal(C.rng(seed), (M, K)), "bf16", dev)
+
+
+@pytest.mark.parametrize("M", [1, 8, 64, 512])
+def test_graph_linear_w4(dev, M):
+    """Line kernel (M 1), K-split kernel + reduce launch (M 8), prefill GEMM (M 64, 512)."""
+    from infinitemodel_amd import ops
+    c = C.int4_case(1024, 2048, 128, seed=31)
+    q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev), C.to_torch(c["z"], "bf16", dev)
+    x, x2 = _x(dev, M, 2048, 1), _x(dev, 16, 2048, 2)
+    _replay_check(lambda: ops.linear_w4(x, q, 128, (s, z)),
+                  lambda: (ops.linear_w4(x2, q, 128, (s, z)), x2.float().sum()))
+
+
+@pytest.mark.parametrize("M", [1, 8, 64])
+def test_graph_linear_w2(dev, M):
+    from infinitemodel_amd import ops
+    c = C.int2_case(512, 2048, 64, seed=32, dt="fp16")
+    q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "fp16", dev), C.to_torch(c["z"], "fp16", dev)
+    x, x2 = _x(dev, M, 2048, 3), _x(dev, 4, 2048, 4)
+    _replay_check(lambda: ops.linear_w2(x, q, 64, (s, z)),
+                  lambda: (ops.linear_w2(x2, q, 64, (s, z)), x2.float().sum()))
+
+
+@pytest.mark.parametrize("M", [1, 64])
+def test_graph_linear_w8(dev, M):
+    from infinitemodel_amd import ops
+    c = C.int8_case(768, 1024, seed=33)
+    q, s = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev)
+    x, x2 = _x(dev, M, 1024, 5), _x(dev, 3, 1024, 6)
+    _replay_check(lambda: ops.linear_w8(x, q, s), lambda: (ops.linear_w8(x2, q, s), x2.float().sum()))
+
+
+def test_graph_dequant_w4(dev):
+    from infinitemodel_amd import ops
+    c = C.int4_case(256, 1024, 128, seed=34)
+    q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev), C.to_torch(c["z"], "bf16", dev)
+    out = _replay_check(lambda: ops.dequant_w4(q, s, z, 1024, 128), lambda: None)
+    assert np.array_equal(C.t2np(out), c["Wd"])
+
+
+@pytest.mark.parametrize("E,H,I,k,T,act", [
+    (32, 512, 256, 4, 1, "silu_glu"),      # decode: the two-launch line path
+    (8, 512, 256, 2, 20, "silu_glu"),      # token-sorted line kernels, sort + combine launches
+    (4, 512, 256, 2, 400, "silu_glu"),     # grouped GEMM (block list built by the sort)
+    (4, 512, 256, 2, 400, "gptoss"),
+])
+def test_graph_moe_experts(dev, E, H, I, k, T, act):
+    import torch
+    from infinitemodel_amd import ops
+    r = C.rng(35 + T)
+    gu = oq.pack_linear_int4_3d(C.bf16_normal(r, (E, 2 * I, H), 0.02), 128, "bf16")
+    dn = oq.pack_linear_int4_3d(C.bf16_normal(r, (E, H, I), 0.02), 128, "bf16")
+    t = lambda a: C.to_torch(a, "bf16", dev)  # noqa: E731
+    gut = (C.u8(gu[0], dev), t(gu[1]), t(gu[2]), H)
+    dnt = (C.u8(dn[0], dev), t(dn[1]), t(dn[2]), I)
+    kw = {}
+    if act == "gptoss":
+        kw = dict(act="gptoss", gu_bias=t(C.bf16_normal(r, (E, 2 * I), 0.02)),
+                  dn_bias=t(C.bf16_normal(r, (E, H), 0.02)))
+
+    def routed(seed, n):
+        idx, w = om.route_topk(C.rng(seed).standard_normal((n, E)).astype(np.float32), k)
+        return torch.from_numpy(idx).to(dev), t(w), _x(dev, n, H, seed + 1)
+
+    idx, w, x = routed(36, T)
+    idx2, w2, x2 = routed(37, max(1, T // 2))
+    _replay_check(lambda: ops.moe_experts_w4(x, idx, w, gut, dnt, 128, **kw),
+                  lambda: (ops.moe_experts_w4(x2, idx2, w2, gut, dnt, 128, **kw), x2.float().sum()))
