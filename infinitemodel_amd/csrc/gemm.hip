@@ -684,15 +684,17 @@ int moe_gemm_bn() { return CfgMoe::BN; }
 
 // mode 1: gate_up SiLU-GLU (N = 2I, I a multiple of BN / 2), 2: gate_up gpt-oss (N = 2I), 3: down (N = H).
 // x rows: hidden (modes 1, 2: row perm[p] / k) or h (mode 3: row p), stride sxm, K columns.
+// check_only: validate the shape and layout, launch nothing.
 int moe_gemm_w4(int mode, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t K, const uint8_t* q, int64_t sqe,
                 int64_t sqn,
                 const void* sc, const void* zr, int64_t sse, int64_t ssn, int sdt, int64_t N, int64_t I,
                 const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off, const int32_t* perm, int k,
                 const void* bias, int64_t sbe, int bdt, float alpha, float limit, uint16_t* h, int64_t hs,
-                float* yr, hipStream_t st) {
+                float* yr, hipStream_t st, bool check_only) {
   if (K % CfgMoe::BK != 0 || K <= 0 || N <= 0 || (mode == 1 && I % (CfgMoe::BN / 2) != 0)) return IMQ_ERR_UNSUPPORTED;
   if (((uintptr_t)x & 15) || (sxm & 7) || ((uintptr_t)q & 15) || (sqn & 15) || (sqe & 15)) return IMQ_ERR_UNSUPPORTED;
   if (128 * sqn > 0x7fffffff || N * sqn > 0x7fffffff || xrows * sxm > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  if (check_only) return IMQ_OK;
   GemmArgs a{x, sxm, 0, (int)K, q, sqn, sc, ssn, 1, zr, ssn, 1, (int)N, 7, h, hs, 0, 0, 1, 0, nullptr};
   a.tiles_n = mode == 1 ? (int)(I / (CfgMoe::BN / 2)) : (int)((N + CfgMoe::BN - 1) / CfgMoe::BN);
   a.kps = (int)(K / CfgMoe::BK);

@@ -25,7 +25,7 @@ int moe_gemm_w4(int mode, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t
                 int64_t sqn, const void* sc, const void* zr, int64_t sse, int64_t ssn, int sdt, int64_t N, int64_t I,
                 const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off, const int32_t* perm, int k,
                 const void* bias, int64_t sbe, int bdt, float alpha, float limit, uint16_t* h, int64_t hs,
-                float* yr, hipStream_t st);
+                float* yr, hipStream_t st, bool check_only = false);
 }  // namespace imq
 using imq::moe_gemm_bm;
 using imq::moe_gemm_bn;
@@ -1062,12 +1062,23 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   int32_t* mtl = (int32_t*)(ws + L.gu);
   uint16_t* h = (uint16_t*)(ws + L.h);
   float* yr = (float*)(ws + L.z);
+  const int gmode = c.act == IMQ_ACT_GPTOSS ? 2 : 1;
+  auto gate_up = [&](bool check) {
+    return moe_gemm_w4(gmode, c.hidden, c.hs, c.T, c.gK, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
+                       2 * c.I, c.I, mtl + 2, mtl, max_mt, off, perm, (int)c.k, c.gb, c.gbe, c.bdt, c.alpha, c.limit,
+                       h, L.hw, nullptr, st, check);
+  };
+  auto down = [&](bool check) {
+    return moe_gemm_w4(3, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2, mtl,
+                       max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, st, check);
+  };
+  // both projections are validated before anything is launched
+  int rc = gate_up(true);
+  if (rc == IMQ_OK) rc = down(true);
+  if (rc != IMQ_OK) return rc;
   moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit, mtl, bm);
   IMQ_LAUNCH_CHECK();
-  const int gmode = c.act == IMQ_ACT_GPTOSS ? 2 : 1;
-  int rc = moe_gemm_w4(gmode, c.hidden, c.hs, c.T, c.gK, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
-                       2 * c.I, c.I, mtl + 2, mtl, max_mt, off, perm, (int)c.k, c.gb, c.gbe, c.bdt, c.alpha, c.limit,
-                       h, L.hw, nullptr, st);
+  rc = gate_up(false);
   if (rc != IMQ_OK) return rc;
   if (c.dK > c.I) {   // h's columns past I are read by down's K steps: zero them
     const int64_t total = B * (c.dK - c.I);
@@ -1075,8 +1086,7 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
     moe_zero_pad_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(h, B, c.I, c.dK, L.hw);
     IMQ_LAUNCH_CHECK();
   }
-  rc = moe_gemm_w4(3, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2, mtl,
-                   max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, st);
+  rc = down(false);
   if (rc != IMQ_OK) return rc;
   const int64_t total = c.T * (c.H / 4);
   const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
