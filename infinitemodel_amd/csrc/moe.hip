@@ -553,10 +553,13 @@ __global__ __launch_bounds__(256) void moe_zero_pad_kernel(uint16_t* __restrict_
 //                       (gpt-oss) takes 16 interleaved rows and writes 8. Row biases and the
 //                       activation run in the epilogue.
 //   moe_dn_line_kernel  workgroup (token t, 16 output rows) with one wave group per routed slot
-//                       j: group j streams expert idx[t k + j]'s down rows against h[t k + j],
-//                       scales its partial by w[t, j] (the down bias added once per slot), and
-//                       the fixed-order cross-wave LDS reduction is the weighted combine:
-//                       out[t] = bf16(sum_j w[t, j] (down_j + b_j)).
+//                       j streaming expert idx[t k + j]'s down rows against h[t k + j]; or
+//                       (PAIR, when 16-row tiles would leave CUs idle) workgroup (t, 8 output
+//                       rows) with one wave group per slot pair (2p, 2p + 1): one 16-row MFMA
+//                       tile holds the 8 rows of both slots' experts, A rows 0 and 1 their h
+//                       rows. Each partial is scaled by w[t, j] (the down bias added once per
+//                       slot), and the fixed-order cross-wave LDS reduction is the weighted
+//                       combine: out[t] = bf16(sum_j w[t, j] (down_j + b_j)).
 // ---------------------------------------------------------------------------------------------
 constexpr int kDLine = 256;   // int4 codes per line-step (128 bytes of a row, 2 groups of 128)
 
@@ -575,7 +578,7 @@ struct MoeDecArgs {
   const void* zr;
   int64_t sse, ssn;        // scale and zero share strides (expert, row); unit group stride
   int I;                   // gu: intermediate size
-  int NR;                  // gu: units per routed row; dn: 16-row tiles per token
+  int NR;                  // gu: units per routed row; dn: row tiles per token (set by dec_dn)
   int Wk;                  // waves per tile (gu) or per routed slot (dn)
   const void* bias;        // per-expert row bias [E][rows] or null
   int64_t sbe;
@@ -585,43 +588,55 @@ struct MoeDecArgs {
   int64_t som;
 };
 
-IMQ_HOST_DEV inline int dec_wave_lds(int S2, int vb) { return (S2 * kDLine + 8) * 2 + 2 * S2 * 4 + 2 * 16 * (S2 * vb / 2) * 4; }
+// LDS of one wave: staged activation row(s) (two in the paired form), their group sums, the
+// scale / zero words of the 16 weight rows.
+IMQ_HOST_DEV inline int dec_wave_lds(int S2, int vb, bool pair) {
+  const int nx = pair ? 2 : 1;
+  return nx * (S2 * kDLine + 8) * 2 + nx * 2 * S2 * 4 + 2 * 16 * (S2 * vb / 2) * 4;
+}
 
-// One wave's share of a 16-row tile (rows rbase.. of expert e, line-steps [ls0, ls0 + S2)) against
-// one activation row: returns the wave's partial dot of row c in lanes with ar == 0.
-template <int S2, int SDT, bool XCL>
+// One wave's share of a 16-row tile (line-steps [ls0, ls0 + S2)): returns the wave's partial dot
+// for column c in lanes with ar == 0.
+//   PAIR false: rows rbase.. rbase+15 of expert e against the activation row xrow (the MFMA's A
+//               rows all hold it; D row 0 is used).
+//   PAIR true:  rows rbase.. rbase+7 of expert e (columns 0-7) against xrow and the same rows of
+//               expert e2 (columns 8-15) against xrow2: A row 1 holds xrow2, so D row 0 gives
+//               columns 0-7 and D row 1 columns 8-15 -- two routed slots share one 16-row MFMA.
+template <int S2, int SDT, bool XCL, bool PAIR>
 IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint16_t* xrow, int ls0, int KL,
-                               unsigned char* wl, int lane) {
+                               unsigned char* wl, int lane, int e2, const uint16_t* xrow2) {
   constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
   constexpr int DPR = S2 * VB / 2;                   // scale dwords per row per array
   const int c = lane & 15, ar = lane >> 4;
   const bool lo8 = c < 8;
+  constexpr int NX = PAIR ? 2 : 1;
   const int xrowl = S2 * kDLine + 8;
-  uint16_t* xw = (uint16_t*)wl;                      // [xrowl], unpack order
-  float* xs = (float*)(wl + xrowl * 2);              // [2 * S2] group sums
-  uint32_t* szl = (uint32_t*)(xs + 2 * S2);          // [2 arrays][16 rows][DPR]
+  uint16_t* xw = (uint16_t*)wl;                      // [NX][xrowl], unpack order
+  float* xs = (float*)(wl + NX * xrowl * 2);         // [NX][2 * S2] group sums
+  uint32_t* szl = (uint32_t*)(xs + NX * 2 * S2);     // [2 arrays][16 rows][DPR]
 
-  // 1) x: 32*S2 blocks of 8 of this wave's K range
+  // 1) x: 32*S2 blocks of 8 of this wave's K range (of each activation row)
   constexpr int XB = 32 * S2;
   constexpr int XU = XB / 64;
-  u32x4_t xv[XU];
+  u32x4_t xv[NX][XU];
 #pragma unroll
-  for (int u = 0; u < XU; ++u) {
-    const int bidx = lane + 64 * u;
-    const int col = ls0 * kDLine + 8 * bidx;
-    if constexpr (XCL) {
-      const bool in = col < a.xk;
-      xv[u] = *(const u32x4_t*)(xrow + (in ? col : a.xk - 8));
-      if (!in) xv[u] = u32x4_t{0u, 0u, 0u, 0u};
-    } else {
-      xv[u] = *(const u32x4_t*)(xrow + (col < a.Kpad ? col : a.Kpad - 8));
+  for (int h = 0; h < NX; ++h)
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+      const uint16_t* xr = h ? xrow2 : xrow;
+      const int bidx = lane + 64 * u;
+      const int col = ls0 * kDLine + 8 * bidx;
+      if constexpr (XCL) {
+        const bool in = col < a.xk;
+        xv[h][u] = *(const u32x4_t*)(xr + (in ? col : a.xk - 8));
+        if (!in) xv[h][u] = u32x4_t{0u, 0u, 0u, 0u};
+      } else {
+        xv[h][u] = *(const u32x4_t*)(xr + (col < a.Kpad ? col : a.Kpad - 8));
+      }
     }
-  }
   // 2) scale / zero words of groups [2*ls0, 2*ls0 + 2*S2) of the 16 rows
   constexpr int ZU = (32 * DPR + 63) / 64;
   const int ngd = a.Kpad / 128 * VB / 4;
-  const unsigned char* sbase = (const unsigned char*)a.sc + ((int64_t)e * a.sse + (int64_t)rbase * a.ssn) * VB;
-  const unsigned char* zbase = (const unsigned char*)a.zr + ((int64_t)e * a.sse + (int64_t)rbase * a.ssn) * VB;
   uint32_t zv[ZU];
 #pragma unroll
   for (int u = 0; u < ZU; ++u) {
@@ -633,12 +648,15 @@ IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint
     const int dw = rem - r * DPR;
     int gd = ls0 * (VB / 2) + dw;
     gd = gd < ngd ? gd : ngd - 1;
-    zv[u] = *(const uint32_t*)((arr ? zbase : sbase) + (int64_t)r * a.ssn * VB + 4 * gd);
+    const bool second = PAIR && r >= 8;             // rows 8-15: expert e2's rows rbase..
+    const int64_t el = (int64_t)(second ? e2 : e) * a.sse + (int64_t)(rbase + (second ? r - 8 : r)) * a.ssn;
+    zv[u] = *(const uint32_t*)((const unsigned char*)(arr ? a.zr : a.sc) + el * VB + 4 * gd);
   }
   // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
   const uint8_t* qt = a.q + (int64_t)e * a.sqe + (int64_t)rbase * a.sqn;
+  const uint8_t* qt2 = PAIR ? a.q + (int64_t)e2 * a.sqe + (int64_t)rbase * a.sqn : qt + 8 * a.sqn;
   const uint8_t* q0 = qt + (int64_t)(c & 7) * a.sqn + 16 * ar + (lo8 ? 0 : 64);
-  const uint8_t* q1 = qt + (int64_t)(8 + (c & 7)) * a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  const uint8_t* q1 = qt2 + (int64_t)(c & 7) * a.sqn + 16 * ar + (lo8 ? 64 : 0);
   u32x4_t wb[2 * S2];
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
@@ -649,16 +667,19 @@ IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint
   }
   // 4) stage x (unpack order) with its per-group sums, and the scale / zero words
 #pragma unroll
-  for (int u = 0; u < XU; ++u) {
-    const int bidx = lane + 64 * u;
-    float sum = 0.f;
+  for (int h = 0; h < NX; ++h)
 #pragma unroll
-    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
+    for (int u = 0; u < XU; ++u) {
+      const int bidx = lane + 64 * u;
+      float sum = 0.f;
 #pragma unroll
-    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
-    *(u32x4_t*)(xw + 8 * bidx) = permute_x8(xv[u]);
-    if ((bidx & 15) == 0) xs[bidx >> 4] = sum;
-  }
+      for (int d = 0; d < 4; ++d)
+        sum += __uint_as_float(xv[h][u][d] << 16) + __uint_as_float(xv[h][u][d] & 0xffff0000u);
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+      *(u32x4_t*)(xw + h * xrowl + 8 * bidx) = permute_x8(xv[h][u]);
+      if ((bidx & 15) == 0) xs[h * 2 * S2 + (bidx >> 4)] = sum;
+    }
 #pragma unroll
   for (int u = 0; u < ZU; ++u) {
     const int d = lane + 64 * u;
@@ -667,7 +688,11 @@ IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // wave-private LDS, in-order
 
   const uint32_t magic = magic_bf16_128x2();
-  const uint16_t* xa = xw + 32 * ar;
+  const uint16_t* xa = xw + ((PAIR && c == 1) ? xrowl : 0) + 32 * ar;   // A row 1: the second activation
+  // group sums of the activation each lane's column meets: y0 columns 0-7 / 8-15 are expert e / e2,
+  // y1 (read across the row swap) the other way round
+  const float* xs0p = xs + ((PAIR && !lo8) ? 2 * S2 : 0);
+  const float* xs1p = xs + ((PAIR && lo8) ? 2 * S2 : 0);
   const uint32_t* sc_c = szl + c * DPR;
   const uint32_t* sc_x = szl + (c ^ 8) * DPR;
   const uint32_t* zr_c = szl + 16 * DPR + c * DPR;
@@ -680,7 +705,7 @@ IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
     const bool v = ls0 + i < KL;
-    const float xs0 = xs[2 * i], xs1 = xs[2 * i + 1];
+    const float xs0 = xs0p[2 * i], xs1 = xs1p[2 * i + 1];
     bf16x8_t A0[4], A1[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -707,10 +732,11 @@ IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint
     }
     y0 = fmaf(cz0, xs0, y0);
     y1 = fmaf(cz1, xs1, y1);
-    y0 = fmaf(s0, acc0[0], y0);
-    y1 = fmaf(s1, acc1[0], y1);
+    // D row 0 (xrow) in lanes ar == 0; PAIR: row 1 (xrow2) for expert e2's columns
+    y0 = fmaf(s0, (PAIR && !lo8) ? acc0[1] : acc0[0], y0);
+    y1 = fmaf(s1, (PAIR && lo8) ? acc1[1] : acc1[0], y1);
   }
-  return y0 + moe_row_swap8(y1);                     // D row 0 (the activation row) in lanes ar == 0
+  return y0 + moe_row_swap8(y1);
 }
 
 template <int S2, int SDT, int ACT, bool XCL>
@@ -720,15 +746,16 @@ __global__ __launch_bounds__(1024) void moe_gu_line_kernel(MoeDecArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
-  const int wbytes = dec_wave_lds(S2, VB);
+  const int wbytes = dec_wave_lds(S2, VB, false);
   const int b = blockIdx.x / a.NR, u = blockIdx.x - b * a.NR;
   int e = a.idx[b];
   e = (e >= 0 && e < a.E) ? e : 0;   // ids outside [0, E) are clamped, as in the sort
   const int tile = ACT == 0 ? wave / a.Wk : 0;
   const int wk = wave - tile * a.Wk;
   const int rbase = ACT == 0 ? (tile == 0 ? 16 * u : a.I + 16 * u) : 16 * u;
-  const float v = dec_tile_partial<S2, SDT, XCL>(a, e, rbase, a.x + (int64_t)(b / a.k) * a.sxm, wk * S2,
-                                                 a.Kpad / kDLine, smem + (size_t)wave * wbytes, lane);
+  const uint16_t* xrow = a.x + (int64_t)(b / a.k) * a.sxm;
+  const float v = dec_tile_partial<S2, SDT, XCL, false>(a, e, rbase, xrow, wk * S2, a.Kpad / kDLine,
+                                                        smem + (size_t)wave * wbytes, lane, e, xrow);
   float* red = (float*)(smem + (size_t)W * wbytes);  // [W][16]
   if ((lane >> 4) == 0) red[wave * 16 + (lane & 15)] = v;
   lds_barrier();
@@ -761,32 +788,39 @@ __global__ __launch_bounds__(1024) void moe_gu_line_kernel(MoeDecArgs a) {
   }
 }
 
-template <int S2, int SDT, bool XCL>
+template <int S2, int SDT, bool XCL, bool PAIR>
 __global__ __launch_bounds__(1024) void moe_dn_line_kernel(MoeDecArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
-  const int wbytes = dec_wave_lds(S2, VB);
+  constexpr int ROWS = PAIR ? 8 : 16;               // output rows per workgroup
+  const int wbytes = dec_wave_lds(S2, VB, PAIR);
   const int t = blockIdx.x / a.NR, rt = blockIdx.x - t * a.NR;
-  const int j = wave / a.Wk, wk = wave - j * a.Wk;
-  const int b = t * a.k + j;
-  int e = a.idx[b];
+  const int grp = wave / a.Wk, wk = wave - grp * a.Wk;            // group: slot pair or slot
+  const int j = PAIR ? 2 * grp : grp;
+  const bool has2 = PAIR && j + 1 < a.k;                           // odd k: the last pair is one slot
+  const int b = t * a.k + j, b2 = has2 ? b + 1 : b;
+  int e = a.idx[b], e2 = a.idx[b2];
   e = (e >= 0 && e < a.E) ? e : 0;
-  float v = dec_tile_partial<S2, SDT, XCL>(a, e, 16 * rt, a.x + (int64_t)b * a.sxm, wk * S2, a.Kpad / kDLine,
-                                           smem + (size_t)wave * wbytes, lane);
+  e2 = (e2 >= 0 && e2 < a.E) ? e2 : 0;
+  float v = dec_tile_partial<S2, SDT, XCL, PAIR>(a, e, ROWS * rt, a.x + (int64_t)b * a.sxm, wk * S2,
+                                                 a.Kpad / kDLine, smem + (size_t)wave * wbytes, lane, e2,
+                                                 a.x + (int64_t)b2 * a.sxm);
   const int c = lane & 15;
-  if (wk == 0 && a.bias != nullptr) v += load_bias(a.bias, a.bdt, (int64_t)e * a.sbe + 16 * rt + c);
-  v *= bf16_bits_to_f32(a.topk_w[b]);
+  const bool hi = PAIR && c >= 8;                                  // PAIR columns 8-15: slot b2
+  const int row = PAIR ? 8 * rt + (c & 7) : 16 * rt + c;
+  if (wk == 0 && a.bias != nullptr) v += load_bias(a.bias, a.bdt, (int64_t)(hi ? e2 : e) * a.sbe + row);
+  v *= hi ? (has2 ? bf16_bits_to_f32(a.topk_w[b2]) : 0.f) : bf16_bits_to_f32(a.topk_w[b]);
   float* red = (float*)(smem + (size_t)W * wbytes);  // [W][16]
   if ((lane >> 4) == 0) red[wave * 16 + c] = v;
   lds_barrier();
   const int n = threadIdx.x;
-  if (n < 16) {
+  if (n < ROWS) {
     float sum = 0.f;
-    for (int w = 0; w < W; ++w) sum += red[w * 16 + n];   // slot order, then K order
-    a.out[(int64_t)t * a.som + 16 * rt + n] = (uint16_t)f32_to_bf16_bits(sum);
+    for (int w = 0; w < W; ++w) sum += PAIR ? red[w * 16 + n] + red[w * 16 + 8 + n] : red[w * 16 + n];
+    a.out[(int64_t)t * a.som + ROWS * rt + n] = (uint16_t)f32_to_bf16_bits(sum);
   }
 }
 
@@ -826,7 +860,7 @@ int dec_gu(const MoeDecArgs& a0, int act, int64_t B, int max_lds, hipStream_t st
   a.Wk = Wk;
   a.NR = act == IMQ_ACT_GPTOSS ? 2 * a.I / 16 : a.I / 16;
   const int W = groups * Wk;
-  const size_t lds = (size_t)W * dec_wave_lds(S2, SDT == IMQ_DT_FP32 ? 4 : 2) + (size_t)W * 16 * 4;
+  const size_t lds = (size_t)W * dec_wave_lds(S2, SDT == IMQ_DT_FP32 ? 4 : 2, false) + (size_t)W * 16 * 4;
   if (lds > (size_t)max_lds || B * a.NR > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   const int grid = (int)(B * a.NR);
   const bool xcl = a.xk < a.Kpad;
@@ -840,21 +874,38 @@ int dec_gu(const MoeDecArgs& a0, int act, int64_t B, int max_lds, hipStream_t st
 #undef IMQ_GU
 }
 
+// Slot pairs (8 output rows per workgroup) while the T * H / 8 workgroups fit the CUs in one
+// round -- measured on MI355X: OLMoE T=1 (H 2048: 256 workgroups) 1741 -> 1823 GB/s, gpt-oss T=1
+// (H 2880: 360) 2631 -> 2543 -- else one slot per wave group and 16 rows per workgroup.
+// Returns true when the pair form is taken; `groups` gets the wave groups per workgroup.
+inline bool dec_dn_pairs(int64_t T, int64_t H, int k, int* groups) {
+  const bool pair = H % 8 == 0 && T * (H / 8) <= device_info().cus;
+  *groups = pair ? (k + 1) / 2 : k;
+  return pair;
+}
+
 template <int SDT>
-int dec_dn(const MoeDecArgs& a0, int64_t T, int max_lds, hipStream_t st) {
+int dec_dn(const MoeDecArgs& a0, int64_t T, int64_t H, int max_lds, hipStream_t st) {
   MoeDecArgs a = a0;
-  int S2, Wk;
-  if (!dec_shape(a.Kpad, a.k, &S2, &Wk)) return IMQ_ERR_UNSUPPORTED;
+  int S2, Wk, groups;
+  const bool pair = dec_dn_pairs(T, H, a.k, &groups);
+  if (!pair && H % 16 != 0) return IMQ_ERR_UNSUPPORTED;
+  if (!dec_shape(a.Kpad, groups, &S2, &Wk)) return IMQ_ERR_UNSUPPORTED;
   a.Wk = Wk;
-  const int W = a.k * Wk;
-  const size_t lds = (size_t)W * dec_wave_lds(S2, SDT == IMQ_DT_FP32 ? 4 : 2) + (size_t)W * 16 * 4;
+  a.NR = (int)(pair ? H / 8 : H / 16);
+  const int W = groups * Wk;
+  const size_t lds = (size_t)W * dec_wave_lds(S2, SDT == IMQ_DT_FP32 ? 4 : 2, pair) + (size_t)W * 16 * 4;
   if (lds > (size_t)max_lds || T * a.NR > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   const int grid = (int)(T * a.NR);
   const bool xcl = a.xk < a.Kpad;
-  if (S2 == 2) return xcl ? dec_launch(moe_dn_line_kernel<2, SDT, true>, grid, W, lds, st, a)
-                          : dec_launch(moe_dn_line_kernel<2, SDT, false>, grid, W, lds, st, a);
-  return xcl ? dec_launch(moe_dn_line_kernel<4, SDT, true>, grid, W, lds, st, a)
-             : dec_launch(moe_dn_line_kernel<4, SDT, false>, grid, W, lds, st, a);
+#define IMQ_DN(S, X, P) dec_launch(moe_dn_line_kernel<S, SDT, X, P>, grid, W, lds, st, a)
+  if (pair) {
+    if (S2 == 2) return xcl ? IMQ_DN(2, true, true) : IMQ_DN(2, false, true);
+    return xcl ? IMQ_DN(4, true, true) : IMQ_DN(4, false, true);
+  }
+  if (S2 == 2) return xcl ? IMQ_DN(2, true, false) : IMQ_DN(2, false, false);
+  return xcl ? IMQ_DN(4, true, false) : IMQ_DN(4, false, false);
+#undef IMQ_DN
 }
 
 template <int S2, int NTL, int SDT, int MODE, bool XCL>
@@ -1124,10 +1175,12 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
     MoeDecArgs gu{c.hidden, c.hs, (int)c.xk, (int)c.gK, (int)c.k, c.idx, c.topk_w, (int)c.E, c.gq, c.gqe, c.gqn,
                   c.gs, c.gz, c.gse, c.gsn, (int)c.I, 0, 0, c.gb, c.gbe, c.bdt, c.alpha, c.limit, h, L.hw};
     MoeDecArgs dn{h, L.hw, (int)c.I, (int)c.dK, (int)c.k, c.idx, c.topk_w, (int)c.E, c.dq, c.dqe, c.dqn,
-                  c.ds, c.dz, c.dse, c.dsn, (int)c.I, (int)(c.H / 16), 0, c.db, c.dbe, c.bdt, 0.f, 0.f, c.out, c.os};
+                  c.ds, c.dz, c.dse, c.dsn, (int)c.I, 0, 0, c.db, c.dbe, c.bdt, 0.f, 0.f, c.out, c.os};
     int gs, dshape, dwk;
     const int groups = c.act == IMQ_ACT_GPTOSS ? 1 : 2;
-    if (dec_shape(c.gK, groups, &gs, &dwk) && dec_shape(c.dK, (int)c.k, &dshape, &dwk)) {
+    int dgroups;
+    dec_dn_pairs(c.T, c.H, (int)c.k, &dgroups);
+    if (dec_shape(c.gK, groups, &gs, &dwk) && dec_shape(c.dK, dgroups, &dshape, &dwk)) {
       int rc = IMQ_ERR_UNSUPPORTED;
       switch (c.sdt) {
         case IMQ_DT_BF16: rc = dec_gu<IMQ_DT_BF16>(gu, c.act, B, 65536, st); break;
@@ -1136,9 +1189,9 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
       }
       if (rc == IMQ_OK) {
         switch (c.sdt) {
-          case IMQ_DT_BF16: return dec_dn<IMQ_DT_BF16>(dn, c.T, 65536, st);
-          case IMQ_DT_FP16: return dec_dn<IMQ_DT_FP16>(dn, c.T, 65536, st);
-          case IMQ_DT_FP32: return dec_dn<IMQ_DT_FP32>(dn, c.T, 65536, st);
+          case IMQ_DT_BF16: return dec_dn<IMQ_DT_BF16>(dn, c.T, c.H, 65536, st);
+          case IMQ_DT_FP16: return dec_dn<IMQ_DT_FP16>(dn, c.T, c.H, 65536, st);
+          case IMQ_DT_FP32: return dec_dn<IMQ_DT_FP32>(dn, c.T, c.H, 65536, st);
         }
       }
       if (rc != IMQ_ERR_UNSUPPORTED) return rc;

@@ -319,3 +319,10 @@ def test_moe_grouped_gemm_wide_k(dev, E, H, I, k, T):
     """K beyond the line kernels' 4096 (gate_up K 4608, down K 4352): prefill rows take the grouped
     GEMM whatever their number per expert."""
     _run(dev, E=E, H=H, I=I, k=k, T=T, seed=180 + H)
+
+
+@pytest.mark.parametrize("k,T", [(3, 1), (5, 2), (2, 4)])
+def test_moe_decode_slot_pairs(dev, k, T):
+    """Decode down with two routed slots per 16-row MFMA tile (8 output rows per workgroup while
+    T * H / 8 fits the CUs): odd k leaves the last pair one slot; T 4 at H 1024 takes 16-row tiles."""
+    _run(dev, E=64, H=1024 if T == 4 else 512, I=256, k=k, T=T, seed=190 + 10 * k + T)

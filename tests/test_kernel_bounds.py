@@ -1050,3 +1050,80 @@ def test_moe_blocks_model_catches_block_overlap():
     spans = [(p0, min(off[e + 1] - p0, MOE_BM)) for e, p0 in blocks]
     cover = sorted(p for p0, c in spans for p in range(p0, p0 + c))
     assert len(cover) != len(set(cover))
+
+
+# ---- MoE decode line kernels (csrc/moe.hip dec_tile_partial, moe_dn_line_kernel) -------------
+DLINE = 256
+
+
+def dec_shape(Kpad, groups):
+    """dec_shape in csrc/moe.hip."""
+    if Kpad % DLINE:
+        return None
+    KL = Kpad // DLINE
+    for s in (2, 4):
+        w = -(-KL // s)
+        if w * groups <= 16:
+            return s, w
+    return None
+
+
+def dec_ranges(pair, E, H, Kpad, vb, sqe, sqn, sse, ssn, e_list, rbase_rows, scale_index=None):
+    """Max exclusive byte offsets of the weight and scale reads of every wave, and the largest
+    output row, for a down launch (pair) or a 16-row tile form; `scale_index` overrides the scale
+    element formula (for the negative control)."""
+    S2, Wk = dec_shape(Kpad, 1)
+    KL = Kpad // DLINE
+    DPR = S2 * vb // 2
+    ngd = Kpad // 128 * vb // 4
+    q_hi = s_hi = 0
+    idx = scale_index or (lambda ex, row: ex * sse + row * ssn)
+    for e, e2 in e_list:
+        for rbase in rbase_rows:
+            for wk in range(-(-KL // S2)):
+                ls0 = wk * S2
+                for lane in range(64):
+                    c, ar = lane & 15, lane >> 4
+                    lo8 = c < 8
+                    r0 = rbase + (c & 7)
+                    r1 = rbase + (c & 7) if pair else rbase + 8 + (c & 7)
+                    e1 = e2 if pair else e
+                    for i in range(S2):
+                        l = min(ls0 + i, KL - 1)
+                        q_hi = max(q_hi, e * sqe + r0 * sqn + 16 * ar + (0 if lo8 else 64) + 128 * l + 16,
+                                   e1 * sqe + r1 * sqn + 16 * ar + (64 if lo8 else 0) + 128 * l + 16)
+                    for u in range(-(-(32 * DPR) // 64)):
+                        d = min(lane + 64 * u, 32 * DPR - 1)
+                        rem = d % (16 * DPR)
+                        r, dw = rem // DPR, rem % DPR
+                        gd = min(ls0 * (vb // 2) + dw, ngd - 1)
+                        second = pair and r >= 8
+                        el = idx(e2 if second else e, rbase + (r - 8 if second else r))
+                        s_hi = max(s_hi, el * vb + 4 * gd + 4)
+    return q_hi, s_hi
+
+
+@pytest.mark.parametrize("pair,H,Kpad,vb", [(True, 2048, 1024, 2), (True, 2880, 3072, 2), (True, 512, 512, 4),
+                                             (False, 2048, 2048, 2)])
+def test_dec_reads_in_bounds(pair, H, Kpad, vb):
+    """Both forms read inside exact-fit weight and scale buffers of E experts, for the first and
+    last experts and row tiles (every other tile lies between them)."""
+    E = 5
+    sqn, ssn = Kpad // 2, Kpad // 128
+    sqe, sse = H * sqn, H * ssn
+    step = 8 if pair else 16
+    rows = [0, H - step]
+    q_hi, s_hi = dec_ranges(pair, E, H, Kpad, vb, sqe, sqn, sse, ssn, [(0, E - 1), (E - 1, 0), (E - 1, E - 1)], rows)
+    assert q_hi <= E * sqe
+    assert s_hi <= E * sse * vb
+
+
+def test_dec_model_catches_expert_stride_times_row_stride():
+    """The scale element (e sse + row) ssn -- the expert stride scaled by the row stride -- is
+    caught: it runs past the buffer."""
+    E, H, Kpad, vb = 5, 2048, 1024, 2
+    sqn, ssn = Kpad // 2, Kpad // 128
+    sqe, sse = H * sqn, H * ssn
+    _, s_hi = dec_ranges(True, E, H, Kpad, vb, sqe, sqn, sse, ssn, [(E - 1, E - 1)], [H - 8],
+                         scale_index=lambda ex, row: (ex * sse + row) * ssn)
+    assert s_hi > E * sse * vb
