@@ -980,7 +980,8 @@ def moe_gemm_ranges(mode, idx, E, k, K, N, I, sxm, xrows, sqe, sqn, sse, ssn, hs
     off, perm, blocks = moe_blocks(idx, E)
     max_mt = -(-B // MOE_BM) + min(E, B)
     assert len(blocks) <= max_mt
-    tiles_n = I // (MOE_BN // 2) if mode == 1 else -(-N // MOE_BN)
+    half = MOE_BN // 2                                  # mode 1: gate rows per tile (then as many up rows)
+    tiles_n = I // half if mode == 1 else -(-N // MOE_BN)
     x_hi = q_hi = s_hi = 0
     written = set()
     for e, p0 in blocks:
@@ -995,14 +996,14 @@ def moe_gemm_ranges(mode, idx, E, k, K, N, I, sxm, xrows, sqe, sqn, sse, ssn, hs
             for wrow in range(MOE_BN):
                 gn = tn * MOE_BN + wrow
                 if mode == 1:
-                    gn = tn * 64 + wrow if wrow < 64 else I + tn * 64 + wrow - 64
+                    gn = tn * half + wrow if wrow < half else I + tn * half + wrow - half
                 gn = min(gn, N - 1)
                 q_hi = max(q_hi, e * sqe + gn * sqn + 16 + (K // MOE_BK - 1) * 32 + 16)
                 s_hi = max(s_hi, e * sse + gn * ssn + (K - 1) // 128 + 1)
             for m in range(cnt):
                 if mode == 1:
-                    for col in range(64):
-                        written.add(((p0 + m) * hs + tn * 64 + col))
+                    for col in range(half):
+                        written.add(((p0 + m) * hs + tn * half + col))
                 elif mode == 2:
                     for n in range(tn * MOE_BN, min(tn * MOE_BN + MOE_BN, N), 2):
                         written.add((p0 + m) * hs + n // 2)
