@@ -14,8 +14,10 @@
  *   - `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream).
  *   - Return 0 on success, IMQ_ERR_* (< 0) for rejected arguments, or a positive hipError_t
  *     when a launch fails. No call allocates, frees or synchronizes; all are re-entrant and
- *     keep no state between calls except a per-device immutable attribute cache. Scratch memory
- *     (split-K partials, MoE intermediates) is a caller-provided workspace argument.
+ *     keep no state between calls except a per-device immutable attribute cache (and, for
+ *     imq_linear_w4_noalloc, the per-device address of its static scratch array). Scratch
+ *     memory (split-K partials, MoE intermediates) is a caller-provided workspace argument,
+ *     except in imq_linear_w4_noalloc.
  */
 #ifndef IMQ_H
 #define IMQ_H
@@ -26,7 +28,7 @@
 extern "C" {
 #endif
 
-#define IMQ_ABI_VERSION 3
+#define IMQ_ABI_VERSION 4
 
 #define IMQ_DT_BF16 0
 #define IMQ_DT_FP16 1
@@ -40,6 +42,7 @@ extern "C" {
 #define IMQ_ERR_INVALID (-1)     /* bad shape / stride / dtype / null pointer */
 #define IMQ_ERR_UNSUPPORTED (-2) /* valid for the reference but not for this kernel family */
 #define IMQ_ERR_ALIGN (-3)       /* pointer or stride not aligned as the kernel requires */
+#define IMQ_ERR_SCRATCH (-4)     /* workspace need exceeds IMQ_NOALLOC_SCRATCH_BYTES */
 
 int imq_abi_version(void);
 const char* imq_strerror(int status);
@@ -117,6 +120,25 @@ int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
 int imq_linear_w8(const void* x, int64_t x_row_stride, int64_t M, int64_t K, const void* qweight,
                   int64_t q_row_stride, const void* scale, int64_t s_stride_n, int s_dtype, int64_t N,
                   void* y, int64_t y_row_stride, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- allocation-free int4 linear -----------------------------------------------------------------
+ * No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same arguments,
+ * kernels and results as imq_linear_w4 without the workspace arguments. The K-split / split-K
+ * partials go to a static scratch array of IMQ_NOALLOC_SCRATCH_BYTES bytes that each GPU the
+ * library runs on holds from the first call on that GPU until the process ends; nothing is
+ * allocated or freed per call. Shapes whose workspace need (imq_linear_workspace_bytes) exceeds
+ * it return IMQ_ERR_SCRATCH before any launch. Every call on one GPU shares that GPU's array and
+ * it keeps the last call's partials (they need no clearing: each call writes every partial it
+ * reads), so calls that may overlap on one GPU (other streams, or unordered work) race: order
+ * them on one stream. */
+#define IMQ_NOALLOC_SCRATCH_BYTES (32ll << 20)
+
+int imq_linear_w4_noalloc(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
+                          const void* qweight, int64_t q_row_stride, const void* scale, int64_t s_stride_n,
+                          int64_t s_stride_g, int s_dtype, const void* zero, int64_t z_stride_n,
+                          int64_t z_stride_g, int z_dtype, int64_t N, int64_t group_size, void* y,
+                          int64_t y_row_stride, void* stream);
 
 /* ---- fused MoE experts (int4 g-wise, [E, N, K_pad/2] stacks) ----------------------------------
  * Per-row grouped GEMV: y[b, :] = x[b, :] @ dequant(W[eid[b]])^T for b < B (fp32 accumulate,

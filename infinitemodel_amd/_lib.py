@@ -19,7 +19,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("IMQ_LIB_PATH") or os.path.join(HERE, "_lib", "libimq.so")
 
 IMQ_DT_BF16, IMQ_DT_FP16, IMQ_DT_FP32 = 0, 1, 2
-IMQ_OK, IMQ_ERR_INVALID, IMQ_ERR_UNSUPPORTED, IMQ_ERR_ALIGN = 0, -1, -2, -3
+IMQ_OK, IMQ_ERR_INVALID, IMQ_ERR_UNSUPPORTED, IMQ_ERR_ALIGN, IMQ_ERR_SCRATCH = 0, -1, -2, -3, -4
+IMQ_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -45,6 +46,9 @@ SIGNATURES = {
     "imq_linear_w4": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_int,
                                _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
                                _c_vp]),
+    "imq_linear_w4_noalloc": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64,
+                                       _c_int, _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64,
+                                       _c_vp]),
     "imq_linear_w2": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_int,
                                _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
                                _c_vp]),

@@ -2,6 +2,12 @@
 // ABI metadata calls. Dispatch: decode rows (M <= 16) go to the MFMA skinny GEMV, prefill rows
 // to the LDS-dequant MFMA GEMM; shapes or alignments a fast kernel rejects fall back to the
 // generic dequantize-then-matmul kernel (never wrong, just slower).
+//
+// imq_linear_w4_noalloc is imq_linear_w4 with its workspace taken from a static per-device
+// scratch array instead of a caller buffer (for callers that cannot allocate device memory).
+#include <atomic>
+#include <mutex>
+
 #include "imq_common.h"
 
 namespace imq {
@@ -57,6 +63,9 @@ extern "C" const char* imq_strerror(int status) {
     case IMQ_ERR_INVALID: return "invalid argument (shape, stride, dtype or null pointer)";
     case IMQ_ERR_UNSUPPORTED: return "configuration not supported by this kernel family";
     case IMQ_ERR_ALIGN: return "pointer or stride misaligned for this kernel";
+    case IMQ_ERR_SCRATCH:
+      return "workspace need exceeds the static scratch of the allocation-free entry point "
+             "(IMQ_NOALLOC_SCRATCH_BYTES)";
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
   return "unknown status";
@@ -89,6 +98,63 @@ extern "C" int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int
   return imq::generic_gemv<4>(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
                               s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb,
                               y_row_stride, st);
+}
+
+// ---- allocation-free variant of imq_linear_w4 ----------------------------------------------------
+// The scratch array: each device the library runs on holds its own copy until the process ends.
+// Host code never uses the name `scratch` as an address (on the host it is only a stand-in for
+// the symbol): the device address comes from hipGetSymbolAddress, once per device, and only that
+// pointer is passed to kernels.
+static __device__ __align__(256) unsigned char scratch[IMQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's scratch array, resolved on the first call per device
+// (with that device current) and cached.
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return IMQ_ERR_UNSUPPORTED;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (!p) return IMQ_ERR_UNSUPPORTED;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return IMQ_OK;
+}
+
+}  // namespace
+
+extern "C" int imq_linear_w4_noalloc(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
+                                     const void* qweight, int64_t q_row_stride, const void* scale,
+                                     int64_t s_stride_n, int64_t s_stride_g, int s_dtype, const void* zero,
+                                     int64_t z_stride_n, int64_t z_stride_g, int z_dtype, int64_t N,
+                                     int64_t group_size, void* y, int64_t y_row_stride, void* stream) {
+  int rc = check_g(4, x, x_row_stride, M, K_pad, qweight, q_row_stride, scale, s_dtype, zero, z_dtype, N,
+                   group_size, y, y_row_stride);
+  if (rc != IMQ_OK) return rc;
+  if (M == 0 || N == 0) return IMQ_OK;
+  // The partials of the K-split / split-K launches need no initialisation (every element a
+  // reduction reads is written first by the same call), so the array is never cleared.
+  if (imq_linear_workspace_bytes(M, N, K_pad) > IMQ_NOALLOC_SCRATCH_BYTES) return IMQ_ERR_SCRATCH;
+  void* ws = nullptr;
+  rc = scratch_ptr(&ws);
+  if (rc != IMQ_OK) return rc;
+  return imq_linear_w4(x, x_row_stride, M, K_pad, qweight, q_row_stride, scale, s_stride_n, s_stride_g, s_dtype,
+                       zero, z_stride_n, z_stride_g, z_dtype, N, group_size, y, y_row_stride, ws,
+                       IMQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,

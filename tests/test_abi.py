@@ -81,9 +81,9 @@ def test_exports_are_c_linkage():
 
 
 def test_abi_version_and_strerror(L):
-    assert L.imq_abi_version() == 3
+    assert L.imq_abi_version() == 4
     assert L.imq_strerror(0) == b"ok"
-    for rc in (_lib.IMQ_ERR_INVALID, _lib.IMQ_ERR_UNSUPPORTED, _lib.IMQ_ERR_ALIGN):
+    for rc in (_lib.IMQ_ERR_INVALID, _lib.IMQ_ERR_UNSUPPORTED, _lib.IMQ_ERR_ALIGN, _lib.IMQ_ERR_SCRATCH):
         assert len(L.imq_strerror(rc)) > 5
 
 
@@ -126,3 +126,20 @@ def test_invalid_arguments_are_rejected_on_the_host(L):
     assert rc == _lib.IMQ_ERR_INVALID
     rc = L.imq_dequant_w4(one, 2048, one, 32, 1, 0, one, 32, 1, 0, 4096, 4096, 100, one, 4096, 0, nul)
     assert rc == _lib.IMQ_ERR_INVALID
+
+
+def test_noalloc_rejects_on_the_host(L):
+    """imq_linear_w4_noalloc validates like imq_linear_w4 and refuses, before any device call,
+    shapes whose workspace need exceeds its static scratch (IMQ_ERR_SCRATCH)."""
+    nul = None
+    rc = L.imq_linear_w4_noalloc(nul, 4096, 1, 4096, nul, 2048, nul, 32, 1, 0, nul, 32, 1, 0, 4096, 128, nul,
+                                 4096, nul)
+    assert rc == _lib.IMQ_ERR_INVALID
+    one = ctypes.c_void_p(16)   # never dereferenced: the size check fails first
+    M, N, K = 16, 1 << 20, 4096
+    need = L.imq_linear_workspace_bytes(M, N, K)
+    assert need > _lib.IMQ_NOALLOC_SCRATCH_BYTES
+    rc = L.imq_linear_w4_noalloc(one, K, M, K, one, K // 2, one, K // 128, 1, 0, one, K // 128, 1, 0, N, 128, one,
+                                 N, nul)
+    assert rc == _lib.IMQ_ERR_SCRATCH
+    assert b"scratch" in L.imq_strerror(rc)
