@@ -2,8 +2,9 @@
 
 Every function takes/returns torch tensors on a ROCm device, checks shapes/strides on the host,
 and launches on torch's current stream for that device. Outputs are allocated with torch (so
-they come from the caching allocator, and from the graph pool under stream capture); nothing
-here synchronizes, so these calls are capturable into HIP graphs.
+they come from the caching allocator, and from the graph pool under stream capture). Nothing
+here synchronizes except the MoE ops' routing-id check, which is skipped under stream capture,
+so these calls are capturable into HIP graphs.
 
 These are the product path: they never fall back to a CPU/torch computation. A missing library
 raises ``ImqUnavailable``, a rejected call raises ``ImqError``.
@@ -44,22 +45,48 @@ def _rows2d(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
-# Split-K workspaces of the fused linears, one per (device, stream): calls sharing one must be
-# stream-ordered. Its contents need no initialization, so a cached workspace is reusable (also
-# inside captured HIP graphs).
+# Workspaces (split-K / K-split partials of the fused linears, MoE intermediates), one per
+# (device, stream): calls sharing one are ordered by that stream, and their contents need no
+# initialization. A workspace is never freed once handed out, because a HIP graph captured with it
+# keeps its address: when a call needs more, the old buffer is retired (kept alive for the life of
+# the process) and one at least twice its size takes its place, so at most log2(largest need)
+# buffers are ever retired per stream.
 _WS: dict = {}
+_WS_RETIRED: list = []
 
 
-def _workspace(dev: torch.device, M: int, N: int, K: int):
-    need = int(_lib.lib().imq_linear_workspace_bytes(M, N, K))
+def _scratch(dev: torch.device, need: int):
+    """The (device, current stream) workspace of at least ``need`` bytes, or None if need <= 0."""
     if need <= 0:
-        return 0, 0
+        return None
     key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
     ws = _WS.get(key)
     if ws is None or ws.numel() < need:
-        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        size = need
+        if ws is not None:
+            _WS_RETIRED.append(ws)
+            size = max(need, 2 * ws.numel())
+        ws = torch.empty(size, dtype=torch.uint8, device=dev)
         _WS[key] = ws
+    return ws
+
+
+def _workspace(dev: torch.device, M: int, N: int, K: int):
+    ws = _scratch(dev, int(_lib.lib().imq_linear_workspace_bytes(M, N, K)))
+    if ws is None:
+        return 0, 0
     return ws.data_ptr(), ws.numel()
+
+
+def _check_expert_ids(idx: torch.Tensor, E: int) -> None:
+    """Refuse routing ids outside [0, E), as the reference's eager experts loop does (its
+    ``one_hot(num_classes=E)`` raises). One device-to-host read, so it is skipped while a HIP graph
+    is being captured (the kernels then only keep out-of-range ids' loads in bounds)."""
+    if idx.numel() == 0 or (idx.is_cuda and torch.cuda.is_current_stream_capturing()):
+        return
+    lo, hi = (int(v) for v in torch.aminmax(idx))
+    if lo < 0 or hi >= E:
+        raise ValueError(f"expert ids must lie in [0, {E}); got ids in [{lo}, {hi}]")
 
 
 def _check_packed(q: torch.Tensor, dt=torch.uint8):
@@ -214,9 +241,10 @@ def linear_w8(x, qweight, scale, out=None):
 # ---------------------------------------------------------------------------------------------
 # fused MoE experts
 # ---------------------------------------------------------------------------------------------
-def moe_rows_w4(x, eid, q, scale, zero, group_size: int, in_features: int):
+def moe_rows_w4(x, eid, q, scale, zero, group_size: int, in_features: int, *, check_ids: bool = True):
     """``op(x[B,Kin], eid[B], q[E,N,Kpad/2], scale, zero, group, in_features) -> y[B,N] bf16``:
-    the op returned by the reference's _w4a16_moe_op (worker_quant.py:1452-1487)."""
+    the op returned by the reference's _w4a16_moe_op (worker_quant.py:1452-1487). Expert ids
+    outside [0, E) raise ValueError (``check_ids``; not checked under graph capture)."""
     dev = _check_dev(x, eid, q, scale, zero)
     _check_packed(q)
     if scale.dtype != zero.dtype:
@@ -228,6 +256,8 @@ def moe_rows_w4(x, eid, q, scale, zero, group_size: int, in_features: int):
     eid = eid.to(torch.int32).contiguous()
     B = x.shape[0]
     E, N = q.shape[0], q.shape[1]
+    if check_ids:
+        _check_expert_ids(eid, E)
     ng = Kpad // group_size
     if tuple(scale.shape) != (E, N, ng) or tuple(zero.shape) != (E, N, ng) or eid.numel() != B:
         raise ValueError("scale/zero must be [E, N, K_pad/group] and eid [B]")
@@ -248,7 +278,7 @@ _ACT = {"silu_glu": 0, "gptoss": 1}
 
 
 def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=None, *, act: str = "silu_glu",
-                   gu_bias=None, dn_bias=None, alpha: float = 1.702, limit: float = 7.0):
+                   gu_bias=None, dn_bias=None, alpha: float = 1.702, limit: float = 7.0, check_ids: bool = True):
     """One MoE layer's experts forward: ``out[t] = sum_j w[t,j] * (down_e(act(gate_up_e(x_t))) + b_dn[e])``.
 
     ``gu`` / ``dn`` are (qweight, scale, zero, in_features) of the gate_up [E, 2I, K1/2] and down
@@ -258,7 +288,11 @@ def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=
     ``act="silu_glu"``: rows [gate | up], h = silu(gate) * up -- the transformers eager experts
     loop (modeling_olmoe.py:301-325) as fused by worker_quant.py:2167-2191. ``act="gptoss"``:
     rows interleaved (gate 2i, up 2i+1) with per-expert biases ``gu_bias`` [E, 2I] and ``dn_bias``
-    [E, H] and gpt-oss's clamped GLU (worker_quant.py:2280-2314)."""
+    [E, H] and gpt-oss's clamped GLU (worker_quant.py:2280-2314).
+
+    Routing ids outside [0, E) raise ValueError, as the reference's eager loop does
+    (``check_ids``: one device-to-host read per call, skipped under graph capture). Without a
+    ``workspace`` the call uses the cached per-(device, stream) workspace."""
     gq, gs, gz, H = gu
     dq, ds, dz, I = dn
     dev = _check_dev(hidden, topk_idx, topk_w, gq, gs, gz, dq, ds, dz)
@@ -302,10 +336,12 @@ def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=
         # tokens every row is re-read by many passes and one zero-padded copy is cheaper
         x = torch.nn.functional.pad(x[:, :H], (0, gK - H)).contiguous()
     idx = topk_idx.to(torch.int32).contiguous()
+    if check_ids:
+        _check_expert_ids(idx, E)
     w = topk_w.to(torch.bfloat16).contiguous()
     need = moe_workspace_bytes(T, k, E, H, I, group_size)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        workspace = _scratch(dev, max(need, 1))
     out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
         call("imq_moe_experts_w4_ex", _ptr(x), x.stride(0), T, H, k, _ptr(idx), _ptr(w), E,

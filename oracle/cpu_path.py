@@ -11,6 +11,11 @@
 The tinygemm dequant is (q - 8) * S + bf16((8 - z) * S), not (q - z) * S: third-party op, parity
 unpinned beyond the reference's own rel < 0.05 self-check (worker_quant.py:760-767); it is only a
 timing comparator here.
+
+Pins (tests/test_oracle.py): ``dequant_g`` is bit-identical to oracle.quant's dequant for int4 /
+int2 in bf16 / fp16 / fp32; ``naive_linear`` (both row branches), ``naive_linear_int8`` and
+``moe_eager_cpu`` agree with the oracle's pinned products and eager MoE loop within their bf16
+roundings.
 """
 from __future__ import annotations
 

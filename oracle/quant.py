@@ -19,6 +19,12 @@ Pins (independent checks, see tests/test_oracle.py):
                                bf16-division quirk KAT.
   * dequant-then-matmul     -> torch tinygemm CPU (independent ATen int4 consumer with its own
                                (q-8)*S + (8-z)*S dequant), one-hot column extraction.
+  * int8_gemm_ref           -> hand-computed KAT; torch float64 dequantize-then-F.linear (the
+                               scale applied per weight row), with a wrong-axis negative control.
+  * dequant_exact           -> hand-computed KATs (integer and non-integer zeros); torch float64
+                               over torch's own bf16 casts; rounded once to bf16 it equals the
+                               reference dequant for integer zeros; within one rounding of it for
+                               C3's non-integer zeros.
 """
 from __future__ import annotations
 

@@ -108,3 +108,50 @@ def test_graph_moe_experts(dev, E, H, I, k, T, act):
     idx2, w2, x2 = routed(37, max(1, T // 2))
     _replay_check(lambda: ops.moe_experts_w4(x, idx, w, gut, dnt, 128, **kw),
                   lambda: (ops.moe_experts_w4(x2, idx2, w2, gut, dnt, 128, **kw), x2.float().sum()))
+
+
+def test_graph_survives_workspace_growth(dev):
+    """A graph captured with the cached K-split workspace of its capture stream keeps replaying
+    correctly after eager calls on that same stream need a larger workspace: the old buffer is
+    retired, never freed, so the graph's baked-in address stays valid and no later allocation can
+    land on it."""
+    import torch
+    from infinitemodel_amd import _lib, ops
+    c = C.int4_case(1024, 2048, 128, seed=38)
+    q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev), C.to_torch(c["z"], "bf16", dev)
+    x = _x(dev, 8, 2048, 7)
+    g = torch.Generator(device=dev)
+    g.manual_seed(39)
+    N2, K2 = 8192, 8192
+    q2 = torch.randint(0, 256, (N2, K2 // 2), dtype=torch.uint8, device=dev, generator=g)
+    s2 = (torch.rand((N2, K2 // 128), device=dev, generator=g) * 0.004 + 0.001).to(torch.bfloat16)
+    z2 = torch.randint(0, 16, (N2, K2 // 128), device=dev, generator=g).to(torch.bfloat16)
+    x2 = _x(dev, 16, K2, 8)
+    L = _lib.lib()
+    assert L.imq_linear_workspace_bytes(16, N2, K2) > 4 * L.imq_linear_workspace_bytes(8, 1024, 2048) > 0
+
+    eager = ops.linear_w4(x, q, 128, (s, z)).clone()
+    cs = torch.cuda.Stream(dev)
+    cs.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(cs):
+        ops.linear_w4(x, q, 128, (s, z))           # warm-up: the capture stream's workspace exists
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cs):
+        out = ops.linear_w4(x, q, 128, (s, z))
+    torch.cuda.synchronize(dev)
+    ref2 = None
+    for i in range(3):
+        with torch.cuda.stream(cs):
+            out.zero_()
+            graph.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(out, eager), i
+        with torch.cuda.stream(cs):
+            y2 = ops.linear_w4(x2, q2, 128, (s2, z2))   # grows this stream's workspace
+            junk = torch.full((1 << 22,), 7.0, device=dev)
+            junk.add_(1.0)
+        torch.cuda.synchronize(dev)
+        if ref2 is None:
+            ref2 = y2.clone()
+        assert torch.equal(y2, ref2), i

@@ -326,3 +326,26 @@ def test_moe_decode_slot_pairs(dev, k, T):
     """Decode down with two routed slots per 16-row MFMA tile (8 output rows per workgroup while
     T * H / 8 fits the CUs): odd k leaves the last pair one slot; T 4 at H 1024 takes 16-row tiles."""
     _run(dev, E=64, H=1024 if T == 4 else 512, I=256, k=k, T=T, seed=190 + 10 * k + T)
+
+
+@pytest.mark.parametrize("bad", [8, -1])
+def test_moe_out_of_range_expert_ids_raise(dev, bad):
+    """Routing ids outside [0, E) raise ValueError (the reference's eager loop raises in
+    one_hot(num_classes=E)) in both MoE ops, before any launch."""
+    import torch
+    from infinitemodel_amd import ops
+    E, H, I, k, G = 8, 256, 128, 2, 128
+    gu, dn, _, _ = _layer(E, H, I, G, 77)
+    t = lambda a: C.to_torch(a, "bf16", dev)  # noqa: E731
+    gut = (C.u8(gu[0], dev), t(gu[1]), t(gu[2]), H)
+    dnt = (C.u8(dn[0], dev), t(dn[1]), t(dn[2]), I)
+    x = t(C.bf16_normal(C.rng(78), (3, H)))
+    idx = torch.tensor([[0, 1], [2, bad], [4, 5]], dtype=torch.int32, device=dev)
+    w = torch.full((3, k), 0.5, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="expert ids"):
+        ops.moe_experts_w4(x, idx, w, gut, dnt, G)
+    with pytest.raises(ValueError, match="expert ids"):
+        ops.moe_rows_w4(x[:1].expand(6, H).contiguous(), idx.reshape(-1), gut[0], gut[1], gut[2], G, H)
+    ok = ops.moe_experts_w4(x, idx.clamp(0, E - 1), w, gut, dnt, G)
+    torch.cuda.synchronize()
+    assert torch.isfinite(ok.float()).all()

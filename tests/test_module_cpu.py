@@ -143,3 +143,15 @@ def test_experts_walker_packs_3d_params():
     w = torch.rand(3, 2).to(torch.bfloat16)
     y = ex(x, idx, w)
     assert tuple(y.shape) == (3, 128) and torch.isfinite(y.float()).all()
+
+
+def test_expert_ids_outside_range_are_refused():
+    """The MoE ops refuse routing ids outside [0, E) as the reference's eager loop does
+    (one_hot(num_classes=E) raises) instead of routing them to some expert."""
+    import torch
+    from infinitemodel_amd import ops
+    ops._check_expert_ids(torch.tensor([[0, 63], [5, 7]], dtype=torch.int32), 64)
+    ops._check_expert_ids(torch.zeros((0, 8), dtype=torch.int32), 64)
+    for bad in ([[0, 64]], [[-1, 3]]):
+        with pytest.raises(ValueError, match=r"\[0, 64\)"):
+            ops._check_expert_ids(torch.tensor(bad, dtype=torch.int32), 64)

@@ -360,3 +360,153 @@ def test_gptoss_glu_hand_cases():
              (-9.0, 20.0, 8.0 * -9.0 * sig(-a * 9.0)), (1.0, -8.0, -6.0 * 1.0 * sig(a)), (0.0, 3.0, 0.0)]
     for g, u, want in cases:
         assert om.gptoss_glu64(g, u, a, L) == pytest.approx(want, rel=1e-15, abs=1e-300)
+
+
+# ---------------------------------------------------------------------------------------------
+# int8_gemm_ref: the kernel form s * (x @ q.T) (worker_quant.py:977-980, 1019-1020)
+# ---------------------------------------------------------------------------------------------
+def test_int8_gemm_ref_known_answer():
+    """Hand-computed: x = [1, 2], rows q0 = [3, -4] (s 0.5), q1 = [127, -127] (s 2)."""
+    x = np.array([[1.0, 2.0]], np.float32)
+    q = np.array([[3, -4], [127, -127]], np.int8)
+    s = np.array([[0.5], [2.0]], np.float32)
+    assert np.array_equal(oq.int8_gemm_ref(x, q, s), np.array([[-2.5, -254.0]]))
+
+
+@pytest.mark.parametrize("sdt", ["bf16", "fp16"])
+def test_int8_gemm_ref_matches_torch_dequant_then_linear(sdt):
+    """The scale factored out of K equals torch's dequantize-then-matmul in float64 (the
+    reference's naive path, worker_quant.py:411-417, without its final rounding): the weight
+    q.double() * s.double() per row, then F.linear. A scale applied per input column instead of
+    per output row (wrong axis) must not match."""
+    import torch
+    import torch.nn.functional as F
+    c = C.int8_case(48, 96, seed=21, dt=sdt)
+    x = C.bf16_normal(C.rng(22), (5, 96))
+    ref = F.linear(torch.from_numpy(x).double(),
+                   torch.from_numpy(c["q"]).double() * torch.from_numpy(c["s"]).double()).numpy()
+    got = oq.int8_gemm_ref(x, c["q"], c["s"])
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    # oracle's own int8 dequant (pinned by the promotion tests) then linear_ref: same product
+    Wd, res = oq.dequant_int8(c["q"], c["s"], sdt, "bf16")
+    assert np.allclose(oq.linear_ref(x, Wd), got, rtol=1e-12, atol=1e-12) or res != "fp32"
+    # negative control: scale broadcast over K instead of N
+    x2 = C.bf16_normal(C.rng(23), (5, 48))
+    q2 = np.ascontiguousarray(c["q"][:, :48])
+    wrong = F.linear(torch.from_numpy(x2).double(),
+                     torch.from_numpy(q2).double() * torch.from_numpy(c["s"]).double().reshape(1, -1)).numpy()
+    assert not np.allclose(oq.int8_gemm_ref(x2, q2, c["s"]), wrong, rtol=1e-3, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------------------------
+# dequant_exact: un-rounded (q - bf16(z)) * bf16(s) (worker_quant.py:1176-1177, 646-647)
+# ---------------------------------------------------------------------------------------------
+def test_dequant_exact_known_answer():
+    """Codes 15 / 0 with zero 8 and scale 0.1 (bf16(0.1) = 0.10009765625): (15-8)*0.10009765625 and
+    (0-8)*0.10009765625, exactly; a non-integer fp16 zero 1.3 is first taken to bf16 (1.296875)."""
+    codes = np.array([[15, 0]], np.uint8)
+    s = np.array([[0.1]], np.float32)
+    z = np.array([[8.0]], np.float32)
+    got = oq.dequant_exact(codes, s, z, 2, 2)
+    assert np.array_equal(got, np.array([[7 * 0.10009765625, -8 * 0.10009765625]]))
+    z2 = np.array([[1.3]], np.float32)
+    got2 = oq.dequant_exact(np.array([[3, 1]], np.uint8), s, z2, 2, 2)
+    assert np.array_equal(got2, np.array([[(3 - 1.296875) * 0.10009765625, (1 - 1.296875) * 0.10009765625]]))
+
+
+@pytest.mark.parametrize("bits,G", [(4, 128), (2, 64)])
+def test_dequant_exact_matches_torch_and_rounds_to_reference(bits, G):
+    """Against torch float64 over torch's own bf16 casts of scale/zero (independent of the oracle's
+    bf16 emulation); rounded once to bf16 it is bit-identical to the reference dequant for the
+    integer zeros every reference packer writes; the K tail past in_features is dropped."""
+    import torch
+    mk = C.int4_case if bits == 4 else C.int2_case
+    c = mk(40, 2 * G + 24, G, seed=24)
+    codes = oq.unpack_int4(c["q"]) if bits == 4 else oq.unpack_int2(c["q"])
+    N, Kp = codes.shape
+    zt = torch.from_numpy(c["z"]).to(torch.bfloat16).double()
+    st = torch.from_numpy(c["s"]).to(torch.bfloat16).double()
+    want = ((torch.from_numpy(codes.astype(np.int64)).double().reshape(N, -1, G) - zt[:, :, None])
+            * st[:, :, None]).reshape(N, Kp)[:, :c["in_f"]].numpy()
+    got = oq.dequant_exact(codes, c["s"], c["z"], G, c["in_f"])
+    assert got.shape == (N, c["in_f"]) and np.array_equal(got, want)
+    assert np.array_equal(oq.round_to(got.astype(np.float32), "bf16"), c["Wd"])
+
+
+def test_dequant_exact_non_integer_zero_within_one_rounding():
+    """C3's fp16 non-integer zeros: the reference rounds (q - z) before the product; the exact
+    form differs from it by at most that one bf16 rounding of (q - z) times s plus the final one."""
+    c = C.int2_random_case(32, 256, 64, seed=2000, dt="fp16")
+    codes = oq.unpack_int2(c["q"])
+    ex = oq.dequant_exact(codes, c["s"], c["z"], 64, 256)
+    s_b = np.repeat(oq.round_to(c["s"], "bf16"), 64, axis=1).astype(np.float64)
+    err = np.abs(c["Wd"].astype(np.float64) - ex)
+    assert (err <= 2.0 ** -8 * 4.0 * s_b + 2.0 ** -9 * np.abs(ex)).all()
+    assert (err > 0).any()     # the two roundings are visible (not the integer-zero case)
+
+
+# ---------------------------------------------------------------------------------------------
+# cpu_path helpers (the timed CPU comparator) against the pinned oracle
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("bits,G,dt", [(4, 128, "bf16"), (4, 128, "fp16"), (4, 64, "fp32"), (2, 64, "bf16"),
+                                       (2, 64, "fp16")])
+def test_cpu_path_dequant_g_is_the_reference_dequant(bits, G, dt):
+    import torch
+    from oracle import cpu_path as cp
+    c = (C.int4_case if bits == 4 else C.int2_case)(24, 3 * G - 8, G, seed=25)
+    tdt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dt]
+    w = cp.dequant_g(torch.from_numpy(c["q"]), torch.from_numpy(c["s"]).to(torch.bfloat16),
+                     torch.from_numpy(c["z"]).to(torch.bfloat16), c["in_f"], G, tdt, bits)
+    ref = (oq.dequant_int4 if bits == 4 else oq.dequant_int2)(c["q"], c["s"], c["z"], c["in_f"], G, dt)
+    assert w.dtype == tdt and np.array_equal(w.float().numpy(), ref)
+
+
+@pytest.mark.parametrize("rows", [1, 15, 16, 40])
+def test_cpu_path_naive_linear_rows_rule(rows):
+    """rows < 16: bf16 F.linear over the bf16 dequant; rows >= 16: fp32 dequant + fp32 GEMM, then
+    bf16 (worker_quant.py:847-853). Each within one bf16 rounding (+ fp32 accumulation) of the
+    exact product over its own dequant: the bf16 dequant below 16 rows, the un-rounded fp32
+    dequant ``(q - z) * s`` from 16 rows."""
+    import torch
+    from oracle import cpu_path as cp
+    c = C.int4_case(64, 256, 128, seed=26)
+    x = C.bf16_normal(C.rng(27), (rows, 256))
+    y = cp.naive_linear(torch.from_numpy(x).to(torch.bfloat16), torch.from_numpy(c["q"]),
+                        torch.from_numpy(c["s"]).to(torch.bfloat16), torch.from_numpy(c["z"]).to(torch.bfloat16),
+                        c["in_f"], 128, 4)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (rows, 64)
+    Wd = c["Wd"] if rows < 16 else oq.dequant_int4(c["q"], c["s"], c["z"], c["in_f"], 128, "fp32")
+    assert oq.max_rel(y.float().numpy(), oq.linear_ref(x, Wd)) <= 2.0 ** -8 + 1e-6
+
+
+@pytest.mark.parametrize("rows,sdt", [(2, "bf16"), (16, "fp16"), (24, "bf16")])
+def test_cpu_path_naive_linear_int8(rows, sdt):
+    import torch
+    from oracle import cpu_path as cp
+    c = C.int8_case(32, 128, seed=28, dt=sdt)
+    x = C.bf16_normal(C.rng(29), (rows, 128))
+    tdt = torch.bfloat16 if sdt == "bf16" else torch.float16
+    y = cp.naive_linear_int8(torch.from_numpy(x).to(torch.bfloat16), torch.from_numpy(c["q"]),
+                             torch.from_numpy(c["s"]).to(tdt))
+    assert y.dtype == torch.bfloat16
+    assert oq.max_rel(y.float().numpy(), oq.int8_gemm_ref(x, c["q"], c["s"])) <= 2.0 ** -7
+
+
+def test_cpu_path_moe_eager_matches_oracle_loop():
+    """The torch eager experts loop against the oracle's bf16 eager loop (pinned against
+    transformers' OlmoeExperts) and the exact MoE."""
+    import torch
+    from oracle import cpu_path as cp
+    E, H, I, k, T, G = 8, 256, 128, 2, 6, 128
+    r = C.rng(30)
+    gu = oq.pack_linear_int4_3d(C.bf16_normal(r, (E, 2 * I, H), 0.02), G, "bf16")
+    dn = oq.pack_linear_int4_3d(C.bf16_normal(r, (E, H, I), 0.02), G, "bf16")
+    Dgu = np.stack([oq.dequant_int4_3d(gu[0], gu[1], gu[2], e, H, G) for e in range(E)])
+    Ddn = np.stack([oq.dequant_int4_3d(dn[0], dn[1], dn[2], e, I, G) for e in range(E)])
+    idx, w = om.route_topk(r.standard_normal((T, E)).astype(np.float32), k)
+    x = C.bf16_normal(r, (T, H))
+    b = lambda a: torch.from_numpy(a).to(torch.bfloat16)  # noqa: E731
+    y = cp.moe_eager_cpu(b(x), torch.from_numpy(idx), b(w), (torch.from_numpy(gu[0]), b(gu[1]), b(gu[2]), H),
+                         (torch.from_numpy(dn[0]), b(dn[1]), b(dn[2]), I), G).float().numpy()
+    assert oq.max_rel(y, om.moe_eager_bf16(x, idx, w, Dgu, Ddn)) <= 2e-2
+    assert oq.max_rel(y, om.moe_exact_grouped(x, idx, w, Dgu, Ddn)) <= 3e-2
