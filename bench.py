@@ -102,14 +102,24 @@ def _cpu_time(fn, seconds: float, min_runs: int = 3) -> tuple:
 
 
 def _cpu_model() -> str:
+    """Host CPU model, sockets and physical cores (from /proc/cpuinfo)."""
+    model, sockets, cores = "unknown", set(), set()
     try:
         with open("/proc/cpuinfo") as f:
+            phys = None
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                    sockets.add(v)
+                elif k == "core id":
+                    cores.add((phys, v))
     except Exception:
         pass
-    return "unknown"
+    return f"{model}, {max(1, len(sockets))} socket(s), {len(cores) or '?'} physical cores"
 
 
 def _traffic(key: str):
@@ -164,15 +174,22 @@ def bench_c2(args, dev):
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
     total = sum(L.algorithmic_bytes(M) for L in lins)
     per_launch_us = ms * 1e3 / len(lins)
-    roof = _hbm_roofline("w4_skinny_kernel (imq_linear_w4, M<=16)", total / len(lins), per_launch_us,
-                         _traffic(f"c2_m{M}"))
+    roof = _hbm_roofline(_w4_decode_kernel(M), total / len(lins), per_launch_us, _traffic(f"c2_m{M}"))
     cfg = {"workload": f"C2 llama-3-8b int4 g128 decode stack, 32 layers x (qkv, o, gate_up, down), M={M}",
            "layers": 32, "M": M, "launches_per_step": len(lins), "graph": not args.no_graph,
-           "bytes_per_step": total, "weights": "int4 g128 asymmetric, bf16 scale/zero"}
+           "bytes_per_step": total, "distinct_bytes_per_step": total,
+           "weights": "int4 g128 asymmetric, bf16 scale/zero"}
     del lins
     torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_c2(args, M)
     return _line(round(total / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
+
+
+def _w4_decode_kernel(M: int) -> str:
+    """The kernel imq_linear_w4 runs for M decode rows at the C1 / C2 shapes (gemv.hip)."""
+    if M <= 4:
+        return f"w4_line_kernel (imq_linear_w4, M={M})"
+    return f"w4_ksplit_kernel + splitk_rows_reduce_kernel (imq_linear_w4, M={M})"
 
 
 def _cpu_int4_random(N, K, seed, G=128):
@@ -216,13 +233,13 @@ def cpu_c2(args, M: int, layers: int = 8):
 
 
 # ---------------------------------------------------------------------------------------------
-# C1: one int4 linear 1 x 4096 -> 4096 (rotated over 32 distinct copies)
+# C1: one int4 linear 1 x 4096 -> 4096 (rotated over 64 distinct copies, 571 MB)
 # ---------------------------------------------------------------------------------------------
 def bench_c1(args, dev):
     import torch
     from infinitemodel_amd import ops, workloads as wl
     M = args.m or 1
-    lins = [wl.rtn_int4_linear(4096, 4096, i, dev, name=f"c1.{i}") for i in range(32)]
+    lins = [wl.rtn_int4_linear(4096, 4096, i, dev, name=f"c1.{i}") for i in range(64)]
     x = wl.activations(M, 4096, 0, dev)
     y = torch.empty((M, 4096), dtype=torch.bfloat16, device=dev)
 
@@ -233,9 +250,9 @@ def bench_c1(args, dev):
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
     b = lins[0].algorithmic_bytes(M)
     us = ms * 1e3 / len(lins)
-    roof = _hbm_roofline("w4_skinny_kernel (imq_linear_w4, M<=16)", b, us, _traffic(f"c1_m{M}"))
-    cfg = {"workload": f"C1 single int4 g128 linear {M}x4096->4096, 32 distinct copies per step", "M": M,
-           "launches_per_step": len(lins)}
+    roof = _hbm_roofline(_w4_decode_kernel(M), b, us, _traffic(f"c1_m{M}"))
+    cfg = {"workload": f"C1 single int4 g128 linear {M}x4096->4096, {len(lins)} distinct copies per step",
+           "M": M, "launches_per_step": len(lins), "distinct_bytes_per_step": b * len(lins)}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path
@@ -277,9 +294,12 @@ def bench_c3(args, dev):
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
     nbytes = sum(q.numel() + s.numel() * 2 + z.numel() * 2 + M * K * 2 + M * N * 2 for N, K, q, s, z in sets)
     us = ms * 1e3 / len(sets)
-    roof = _hbm_roofline("imq_linear_w2 decode kernel", nbytes / len(sets), us, _traffic(f"c3_m{M}"))
+    kern = ("w2_line_kernel" if M <= 2 else "w2_ksplit_kernel + splitk_rows_reduce_kernel" if M <= 16
+            else "gemm_wq_kernel<2>")
+    roof = _hbm_roofline(f"{kern} (imq_linear_w2, M={M})", nbytes / len(sets), us, _traffic(f"c3_m{M}"))
     cfg = {"workload": f"C3 int2 g64 70B shapes 8192->28672 and 28672->8192, M={M}, 8 copies each", "M": M,
-           "launches_per_step": len(sets), "weights": "int2 g64, fp16 scale ~U(0.005,0.05), zero ~U(0,3)"}
+           "launches_per_step": len(sets), "distinct_bytes_per_step": nbytes,
+           "weights": "int2 g64, fp16 scale ~U(0.005,0.05), zero ~U(0,3)"}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path
@@ -311,7 +331,7 @@ def bench_c4(args, dev):
     M = args.m or 2048
     shapes = [(14336, 4096), (4096, 14336)]
     sets = []
-    for i in range(2):
+    for i in range(6):        # 6 copies of each shape: 374 MB (int4) / 705 MB (int8), past the MALL
         for j, (N, K) in enumerate(shapes):
             if args.quant == "int4":
                 L = wl.rtn_int4_linear(N, K, 5000 + 2 * i + j, dev)
@@ -331,10 +351,12 @@ def bench_c4(args, dev):
     tf = flops / (ms * 1e-3)
     roof = {"bound": "mfma", "achieved": round(tf / 1e12, 2), "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s",
             "frac": round(tf / BF16_PEAK, 4), "traffic": _traffic(f"c4_{args.quant}_m{M}"),
-            "kernel": f"imq_linear_{'w4' if args.quant == 'int4' else 'w8'} prefill path",
+            "kernel": f"gemm_wq_kernel<{4 if args.quant == 'int4' else 8}> (imq_linear_"
+                      f"{'w4' if args.quant == 'int4' else 'w8'} prefill GEMM)",
             "avg_launch_us": round(ms * 1e3 / len(sets), 3), "flops_per_launch": flops / len(sets)}
+    wbytes = sum(N * K * (0.53125 if args.quant == "int4" else 1.0) for N, K, _ in sets)
     cfg = {"workload": f"C4 prefill {args.quant} 4096->14336 and 14336->4096, M={M}", "M": M,
-           "quant": args.quant, "launches_per_step": len(sets)}
+           "quant": args.quant, "launches_per_step": len(sets), "distinct_bytes_per_step": int(wbytes)}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path
@@ -364,41 +386,61 @@ def bench_c4(args, dev):
 
 
 # ---------------------------------------------------------------------------------------------
-# C5: OLMoE fused MoE experts (E=64, top-8, H=2048, I=1024), 4 distinct layers
+# C5: OLMoE fused MoE experts (E=64, top-8, H=2048, I=1024), 16 layers routed independently
 # ---------------------------------------------------------------------------------------------
+MOE_LAYERS = 16     # C5 T=1: 16 x 8 hit experts x 3.34 MB = 428 MB of distinct weights, past the MALL
+
+
+def _moe_layer_bytes(idx, per_expert: int, act_bytes: int) -> tuple:
+    """(algorithmic bytes, distinct experts) of one MoE layer: each hit expert's weights once, the
+    activations in and out, and the routing ids and weights."""
+    import torch
+    U = int(torch.unique(idx).numel())
+    return U * per_expert + act_bytes + idx.numel() * 6, U
+
+
 def bench_c5(args, dev):
     import torch
     from infinitemodel_amd import ops, workloads as wl
     T = args.m or 1
-    layers = [wl.olmoe_layer(dev, seed=3000 + l) for l in range(4)]
-    idx, w = wl.olmoe_routing(T, dev)
+    layers = [wl.olmoe_layer(dev, seed=3000 + l) for l in range(MOE_LAYERS)]
+    routes = [wl.olmoe_routing(T, dev, seed=4 + l) for l in range(MOE_LAYERS)]
     x = wl.activations(T, 2048, 11, dev)
 
     def step():
-        for gu, dn in layers:
+        for (gu, dn), (idx, w) in zip(layers, routes):
             ops.moe_experts_w4(x, idx, w, gu, dn, 128)
 
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
-    U = int(torch.unique(idx).numel())
     per_expert = 3342336
-    nbytes = U * per_expert + T * 2048 * 2 * 2 + idx.numel() * 6
+    per_layer = [_moe_layer_bytes(idx, per_expert, T * 2048 * 2 * 2) for idx, _ in routes]
+    nbytes = sum(b for b, _ in per_layer)
     us = ms * 1e3 / len(layers)
-    roof = _hbm_roofline("imq_moe_experts_w4 (one MoE layer)", nbytes, us, _traffic(f"c5_t{T}"))
-    cfg = {"workload": f"C5 OLMoE fused MoE experts, T={T}, top-8 of 64, H=2048, I=1024, 4 layers", "T": T,
-           "distinct_experts": U, "bytes_per_layer": nbytes, "layers_per_step": len(layers)}
+    B = T * 8       # routed rows; the dispatch rule of moe.hip: direct decode when 4 B <= E, the
+    #                 grouped GEMM when B K_gate_up >= 81920 E, token-sorted line kernels between
+    kern = ("moe_gu_line_kernel + moe_dn_line_kernel" if 4 * B <= 64 else
+            "moe_sort_kernel + gemm_wq_kernel MOE forms + moe_combine_kernel" if B * 2048 >= 81920 * 64 else
+            "moe_sort_kernel + moe_line_kernel (x2) + moe_combine_kernel")
+    roof = _hbm_roofline(f"imq_moe_experts_w4: {kern} (one MoE layer)", nbytes / len(layers), us,
+                         _traffic(f"c5_t{T}"))
+    cfg = {"workload": f"C5 OLMoE fused MoE experts, T={T}, top-8 of 64, H=2048, I=1024, {len(layers)} layers "
+                       f"routed independently", "T": T,
+           "distinct_experts_per_layer": [u for _, u in per_layer], "layers_per_step": len(layers),
+           "distinct_bytes_per_step": nbytes}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path
         n = cpu_path.tune_cpu_threads()
         cl = wl.olmoe_layer(torch.device("cpu"), seed=3000)
+        idx, w = routes[0]
         xc, ic, wc = x.cpu(), idx.cpu(), w.cpu()
         med, runs = _cpu_time(lambda: cpu_path.moe_eager_cpu(xc, ic, wc, cl[0], cl[1], 128), args.cpu_seconds,
                               min_runs=2)
-        cpu = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
+        cpu = {"value": round(per_layer[0][0] / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
                "sample": f"C5 one layer at T={T}: the eager per-expert loop over bf16 dequantized experts "
                          f"(modeling_olmoe.py:301-325 over Packed4Tensor3D), median of {runs}",
                "cpu": _cpu_model()}
-    return _line(round(nbytes * len(layers) / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
+    return _line(round(nbytes / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -409,26 +451,29 @@ def bench_gptoss(args, dev):
     from infinitemodel_amd import ops, workloads as wl
     T = args.m or 1
     E, k, H, I = 32, 4, 2880, 2880
-    layers = [wl.gptoss_layer(dev, seed=5000 + 7 * l) for l in range(4)]
-    idx, w = wl.olmoe_routing(T, dev, E=E, k=k)
+    layers = [wl.gptoss_layer(dev, seed=5000 + 7 * l) for l in range(MOE_LAYERS)]
+    routes = [wl.olmoe_routing(T, dev, E=E, k=k, seed=40 + l) for l in range(MOE_LAYERS)]
     x = wl.activations(T, H, 13, dev)
 
     def step():
-        for gu, dn, bgu, bdn in layers:
+        for (gu, dn, bgu, bdn), (idx, w) in zip(layers, routes):
             ops.moe_experts_w4(x, idx, w, gu, dn, 128, act="gptoss", gu_bias=bgu, dn_bias=bdn)
 
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
-    U = int(torch.unique(idx).numel())
     ng = -(-H // 128)                      # 23 groups: the reference's packed K_pad 2944
     per_expert = (2 * I + H) * (ng * 64 + ng * 2 * 2) + (2 * I + H) * 2     # codes + s/z + biases
-    nbytes = U * per_expert + T * H * 2 * 2 + idx.numel() * 6
+    per_layer = [_moe_layer_bytes(idx, per_expert, T * H * 2 * 2) for idx, _ in routes]
+    nbytes = sum(b for b, _ in per_layer)
     us = ms * 1e3 / len(layers)
-    roof = _hbm_roofline("imq_moe_experts_w4_ex gptoss (one MoE layer)", nbytes, us, _traffic(f"gptoss_t{T}"))
-    cfg = {"workload": f"gpt-oss-20b fused experts, T={T}, top-{k} of {E}, H=I={H}, 4 layers", "T": T,
-           "distinct_experts": U, "bytes_per_layer": nbytes, "layers_per_step": len(layers),
+    roof = _hbm_roofline("imq_moe_experts_w4_ex gptoss (one MoE layer)", nbytes / len(layers), us,
+                         _traffic(f"gptoss_t{T}"))
+    cfg = {"workload": f"gpt-oss-20b fused experts, T={T}, top-{k} of {E}, H=I={H}, {len(layers)} layers routed "
+                       f"independently", "T": T,
+           "distinct_experts_per_layer": [u for _, u in per_layer], "layers_per_step": len(layers),
+           "distinct_bytes_per_step": nbytes,
            "note": "algorithmic bytes count the reference's K_pad 2944 packing; the kernel layout "
                    "reads rows padded to 3072"}
-    return _line(round(nbytes * len(layers) / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, None)
+    return _line(round(nbytes / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, None)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -447,7 +492,7 @@ def bench_head(args, dev):
     nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
     roof = _hbm_roofline("imq_linear_w8 decode kernel", nbytes, ms * 1e3, _traffic(f"head_m{M}"))
     cfg = {"workload": f"int8 lm_head 3584 -> 152064 (Qwen2.5-7B), M={M}", "M": M,
-           "weights": "int8 per-row symmetric, bf16 scale"}
+           "weights": "int8 per-row symmetric, bf16 scale", "distinct_bytes_per_step": nbytes}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path

@@ -88,23 +88,15 @@ def pack_linear_int2(W, group_size: int = INT2_GROUP):
 
 
 def pack_linear_int4_3d(W3, group_size: int = INT4_GROUP, in_major: bool = False):
-    """Per-expert int4 stack (shard_compile.py:97-140): returns
+    """Per-expert int4 stack (shard_compile.py:97-140): each expert ``[out, in]`` (the transpose of
+    ``W3[e]`` when ``in_major``) through pack_linear_int4 -- group quantization never crosses an
+    expert -- stacked on a leading expert axis. Returns
     (qweight [E, out, in_pad/2], scale [E, out, ng], zero [E, out, ng], in_features, ng)."""
     import torch
-
-    def _expert(i):
-        return W3[i].t().contiguous() if in_major else W3[i]
-
-    E = int(W3.shape[0])
-    q0, s0, z0, in_f = pack_linear_int4(_expert(0), group_size)
-    qpacked = torch.empty((E,) + tuple(q0.shape), dtype=q0.dtype, device=q0.device)
-    scale = torch.empty((E,) + tuple(s0.shape), dtype=s0.dtype, device=s0.device)
-    zero = torch.empty((E,) + tuple(z0.shape), dtype=z0.dtype, device=z0.device)
-    qpacked[0], scale[0], zero[0] = q0, s0, z0
-    for e in range(1, E):
-        qe, se, ze, _ = pack_linear_int4(_expert(e), group_size)
-        qpacked[e], scale[e], zero[e] = qe, se, ze
-    return qpacked, scale, zero, in_f, int(scale.shape[2])
+    packs = [pack_linear_int4(W3[e].t().contiguous() if in_major else W3[e], group_size)
+             for e in range(int(W3.shape[0]))]
+    q, scale, zero = (torch.stack([p[i] for p in packs]) for i in range(3))
+    return q, scale, zero, packs[0][3], int(scale.shape[2])
 
 
 def pack_linear_int8(W):
@@ -127,10 +119,16 @@ def _shard_cache_root(model_dir: str) -> str:
 
 
 def _sha256_file(path: str) -> str:
+    """Hex sha256 of a file, read through one reused 4 MiB buffer."""
     h = hashlib.sha256()
-    with open(path, "rb") as f:
-        for chunk in iter(lambda: f.read(1 << 20), b""):
-            h.update(chunk)
+    buf = bytearray(4 << 20)
+    view = memoryview(buf)
+    with open(path, "rb", buffering=0) as f:
+        while True:
+            n = f.readinto(buf)
+            if not n:
+                break
+            h.update(view[:n])
     return h.hexdigest()
 
 
@@ -173,55 +171,67 @@ def _in_major_expert_names(raw: dict) -> set:
     return {n for n, W in raw.items() if W.dim() == 3 and (n + "_bias") in raw}
 
 
+def _unit_tensor_kind(name: str, W, quant: str, lin2d, in_major: set) -> str:
+    """How the cache stores one tensor of a unit: "experts" (fused 3D experts, int4 per-expert
+    packs), "linear" (a packed 2D Linear weight: a decoder-layer Linear, or the lm_head at int8)
+    or "plain" (written as is). Refuses what the serve side could not install correctly."""
+    fused_expert = (W.dim() == 3 and ".experts." in name
+                    and (name.endswith(".gate_up_proj") or name.endswith(".down_proj")))
+    if fused_expert:
+        if quant != "int4":
+            raise ValueError(f"{name}: fused 3D MoE experts are only cacheable at int4 (got {quant})")
+        if name in in_major:
+            # the serve side cannot install transpose-packed gpt-oss experts from a cache, so
+            # the compiler refuses instead of writing one (shard_compile.py:315-330)
+            raise ValueError(f"{name}: in-major fused MoE experts (gpt-oss, [E, in, out]) are not "
+                             "shard-cacheable; load gpt-oss at int4 without a shard cache, or at quant=none")
+        return "experts"
+    if W.dim() == 3 and ".experts." in name and quant != "int4":
+        raise ValueError(f"{name}: fused 3D MoE experts cannot be packed at {quant}")
+    if W.dim() == 2:
+        in_layer = name in lin2d if lin2d is not None else (name.endswith(".weight") and ".layers." in name)
+        if in_layer or (quant == "int8" and name == "lm_head.weight"):
+            return "linear"
+    return "plain"
+
+
 def pack_unit_tensors(raw: dict, lin2d: Optional[set] = None, quant: str = "int4",
                       group_size: int = INT4_GROUP):
-    """Pack one unit's tensors (logical 'model.*' names) into the cache dict + manifest fragments,
-    for dense units and already-fused 3D experts (shard_compile.py:262-355, without the meta-
-    skeleton MoE fuse). 2D layer Linears in ``lin2d`` (or, when None, every 2D '.weight' under
-    '.layers.') are packed; 3D '.experts.*.gate_up_proj/down_proj' are int4-packed per expert;
-    int8 also packs 'lm_head.weight'; everything else passes through."""
+    """Pack one unit's tensors (logical 'model.*' names) into the cache dict + per-tensor manifest
+    entries (shard_compile.py:262-355, for dense units and already-fused 3D experts). Decoder-layer
+    Linears (those in ``lin2d``, or when None every 2D '.weight' under '.layers.') are packed at
+    ``quant``, fused 3D experts per expert at int4, the lm_head at int8; the rest passes through."""
     if quant not in ("int4", "int8", "int2"):
         raise ValueError(f"shard pack supports quant int4|int8|int2 (got {quant!r})")
     group_size = _default_group(quant, group_size)
     in_major = _in_major_expert_names(raw) if quant == "int4" else set()
+    packers = {"int4": pack_linear_int4, "int2": pack_linear_int2}
     out_sd: dict = {}
-    mt: dict = {}
+    meta: dict = {}
     for name, W in raw.items():
-        is_expert3d = (quant == "int4" and W.dim() == 3 and ".experts." in name
-                       and (name.endswith(".gate_up_proj") or name.endswith(".down_proj")))
-        if is_expert3d and name in in_major:
-            # shard_compile.py:315-330: the serve side cannot install transpose-packed gpt-oss
-            # experts from a cache, so the compile refuses rather than writing one
-            raise ValueError(f"{name}: in-major fused MoE experts (gpt-oss, [E, in, out]) are not "
-                             "shard-cacheable; load gpt-oss at int4 without a shard cache, or at "
-                             "quant=none")
-        if lin2d is not None:
-            is_lin = W.dim() == 2 and name in lin2d
-        else:
-            is_lin = W.dim() == 2 and name.endswith(".weight") and ".layers." in name
-        is_int8_head = quant == "int8" and name == "lm_head.weight" and W.dim() == 2
-        if W.dim() == 3 and quant != "int4" and ".experts." in name:
-            raise ValueError(f"fused 3D MoE experts cannot be packed at {quant}")
-        if is_expert3d:
-            qw, sc, ze, in_f, ng = pack_linear_int4_3d(W, group_size)
-            out_sd[name + ".qweight"], out_sd[name + ".scale"], out_sd[name + ".zero"] = qw, sc, ze
-            mt[name] = {"q": True, "is_3d": True, "num_experts": int(W.shape[0]), "out": int(W.shape[1]),
-                        "in_features": in_f, "ng": ng, "group_size": group_size,
-                        "shape": [int(x) for x in W.shape]}
-        elif is_lin or is_int8_head:
-            if quant in ("int4", "int2"):
-                pk = pack_linear_int4 if quant == "int4" else pack_linear_int2
-                qw, sc, ze, in_f = pk(W, group_size)
-                out_sd[name + ".qweight"], out_sd[name + ".scale"], out_sd[name + ".zero"] = qw, sc, ze
-                mt[name] = {"q": True, "in_features": in_f, "shape": [int(x) for x in W.shape]}
-            else:
-                qw, sc = pack_linear_int8(W)
-                out_sd[name + ".qweight"], out_sd[name + ".scale"] = qw, sc
-                mt[name] = {"q": True, "shape": [int(x) for x in W.shape]}
+        kind = _unit_tensor_kind(name, W, quant, lin2d, in_major)
+        shape = [int(d) for d in W.shape]
+        if kind == "experts":
+            q, s, z, in_f, ng = pack_linear_int4_3d(W, group_size)
+            parts = {"qweight": q, "scale": s, "zero": z}
+            info = {"q": True, "is_3d": True, "num_experts": shape[0], "out": shape[1], "in_features": in_f,
+                    "ng": ng, "group_size": group_size}
+        elif kind == "linear" and quant == "int8":
+            q, s = pack_linear_int8(W)
+            parts = {"qweight": q, "scale": s}
+            info = {"q": True}
+        elif kind == "linear":
+            q, s, z, in_f = packers[quant](W, group_size)
+            parts = {"qweight": q, "scale": s, "zero": z}
+            info = {"q": True, "in_features": in_f}
         else:
             out_sd[name] = W.contiguous()
-            mt[name] = {"q": False, "shape": [int(x) for x in W.shape]}
-    return out_sd, mt
+            meta[name] = {"q": False, "shape": shape}
+            continue
+        for leaf, t in parts.items():
+            out_sd[f"{name}.{leaf}"] = t
+        meta[name] = {**info, "shape": shape}
+    return out_sd, meta
 
 
 def write_cache(model_dir: str, units: dict, quant: str, group_size: int, num_layers: int,
@@ -249,51 +259,67 @@ def write_cache(model_dir: str, units: dict, quant: str, group_size: int, num_la
     return manifest
 
 
-def verify_shard_cache(model_dir: str, quant: str) -> tuple:
-    """(ok, problems) -- manifest present, every file's size and sha256, file count, packer_hash
-    (shard_compile.py:701-736; a missing packer_hash is accepted as legacy)."""
-    d = os.path.join(_shard_cache_root(model_dir), quant)
-    mf = os.path.join(d, "manifest.json")
-    if not os.path.isfile(mf):
-        return False, ["manifest.json missing"]
+def _read_manifest(d: str):
+    """(manifest dict, None) or (None, problem) for the cache directory ``d``."""
+    path = os.path.join(d, "manifest.json")
+    if not os.path.isfile(path):
+        return None, "no manifest.json"
     try:
-        with open(mf, encoding="utf-8") as fh:
-            man = json.load(fh)
+        with open(path, encoding="utf-8") as f:
+            return json.load(f), None
     except Exception as exc:
-        return False, [f"manifest.json unreadable: {exc}"]
-    problems = []
-    files = man.get("files", {})
-    for fname, meta in files.items():
-        p = os.path.join(d, fname)
-        if not os.path.isfile(p):
-            problems.append(f"missing file {fname}")
-            continue
-        if os.path.getsize(p) != meta.get("bytes"):
-            problems.append(f"size mismatch {fname}")
-            continue
-        if _sha256_file(p) != meta.get("sha256"):
-            problems.append(f"sha256 mismatch {fname} (corrupt)")
-    exp = int(man.get("num_layers", 0)) + 2
-    if len(files) != exp:
-        problems.append(f"incomplete: {len(files)} files, expected {exp}")
-    ph = man.get("packer_hash")
-    if ph is not None:
+        return None, f"manifest.json cannot be read ({exc})"
+
+
+def _unit_file_problem(d: str, fname: str, entry: dict):
+    """The first way cached unit ``fname`` disagrees with its manifest entry, or None."""
+    path = os.path.join(d, fname)
+    if not os.path.isfile(path):
+        return f"{fname}: listed in the manifest but absent"
+    size = os.path.getsize(path)
+    if size != entry.get("bytes"):
+        return f"{fname}: {size} bytes on disk, {entry.get('bytes')} in the manifest"
+    if _sha256_file(path) != entry.get("sha256"):
+        return f"{fname}: sha256 differs from the manifest (corrupt unit)"
+    return None
+
+
+def verify_shard_cache(model_dir: str, quant: str) -> tuple:
+    """(ok, problems) of ``_shards/<quant>/`` (shard_compile.py:701-736): a readable manifest, each
+    listed unit present with the manifest's size and sha256, one unit per layer plus embed and
+    head, and -- when the manifest records one (older caches do not) -- this packer's tag."""
+    d = os.path.join(_shard_cache_root(model_dir), quant)
+    man, err = _read_manifest(d)
+    if err is not None:
+        return False, [err]
+    units = man.get("files", {})
+    problems = [p for p in (_unit_file_problem(d, f, e) for f, e in units.items()) if p is not None]
+    layers = int(man.get("num_layers", 0))
+    if len(units) != layers + 2:
+        problems.append(f"manifest lists {len(units)} units; {layers} layers need {layers + 2} "
+                        "(embed, layers, head) -- incomplete cache")
+    tag = man.get("packer_hash")
+    if tag is not None:
         want = _packer_tag(man.get("quant", quant), int(man.get("group_size", INT4_GROUP)))
-        if ph != want:
-            problems.append(f"packer_hash mismatch ({ph} != {want}) — recompile")
-    return (len(problems) == 0), problems
+        if tag != want:
+            problems.append(f"packer tag {tag!r} is not this packer's {want!r}: recompile the cache")
+    return not problems, problems
+
+
+def _unit_file_name(start: int, end: int, embed: bool, head: bool):
+    """File name of a cached unit: the embedding, the head, or one decoder layer L%04d; None for
+    a span of several layers (the cache stores layers one per file)."""
+    if embed:
+        return "embed.safetensors"
+    if head:
+        return "head.safetensors"
+    return f"L{start:04d}.safetensors" if end == start + 1 else None
 
 
 def cache_unit_path(model_dir: str, quant: str, start: int, end: int, embed: bool, head: bool):
-    """Path of one cached unit or None (shard_compile.py:768-787)."""
-    d = os.path.join(_shard_cache_root(model_dir), quant)
-    if embed:
-        name = "embed.safetensors"
-    elif head:
-        name = "head.safetensors"
-    elif end - start == 1:
-        name = f"L{start:04d}.safetensors"
-    else:
+    """Path of one cached unit when it exists, else None (shard_compile.py:768-787)."""
+    name = _unit_file_name(start, end, embed, head)
+    if name is None:
         return None
-    p = os.path.join(d, name)
-    return p if os.path.isfile(p) else None
+    path = os.path.join(_shard_cache_root(model_dir), quant, name)
+    return path if os.path.isfile(path) else None

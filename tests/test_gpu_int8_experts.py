@@ -45,7 +45,7 @@ def test_int8_experts_eager_loop(dev, T):
     Dd = np.stack([oq.dequant_int8(*oq.pack_linear_int8(Wd[e], "bf16"), "bf16")[0] for e in range(E)])
     ex.to(dev)
     w0 = ex.gate_up_proj[0]
-    assert type(w0).__name__ == "_W8A16Weight" and ex.gate_up_proj._expert_triton
+    assert type(w0).__name__ == "_W8A16Weight" and ex.gate_up_proj._expert_kernel
     r = C.rng(12 + T)
     idx, w = om.route_topk(r.standard_normal((T, E)).astype(np.float32), k)
     x = C.bf16_normal(r, (T, H))

@@ -113,7 +113,7 @@ def test_packed4_expert_weight_subclass(dev):
     W3 = C.bf16_normal(r, (4, 128, 256), 0.02)
     p = wq._pack4_3d(C.to_torch(W3, "bf16", dev))
     w1 = p[1]
-    assert p._expert_triton is True and type(w1).__name__ == "_W4A16Weight"
+    assert p._expert_kernel is True and type(w1).__name__ == "_W4A16Weight"
     x = C.bf16_normal(r, (3, 256))
     y = F.linear(C.to_torch(x, "bf16", dev), w1)
     ref = oq.linear_ref(x, oq.dequant_int4_3d(C.t2np(p.qweight).astype(np.uint8), C.t2np(p.scale),

@@ -1,6 +1,7 @@
 """The reference module API on a CPU device (no GPU): construction, state_dict keys, the
 reference dequant, the forward dispatch rules (bf16 below 16 rows, fp32 GEMM at >= 16 rows, bias
-after the op), prepare_fused as a no-op that never raises, and the router-excluding walkers."""
+after the op), prepare_fused binding torch's CPU int4 GEMM (and nothing for int2 / int8), and the
+router-excluding walkers."""
 import numpy as np
 import pytest
 import torch
@@ -67,11 +68,31 @@ def test_forward_large_rows_takes_fp32_gemm():
     assert torch.equal(y, ref)
 
 
-def test_prepare_fused_on_cpu_is_a_noop():
-    m, _ = _mod4()
+@pytest.mark.parametrize("rows", [1, 4, 20])
+def test_prepare_fused_on_cpu_binds_the_cpu_int4_gemm(rows):
+    """worker_quant.py:725-815: on a CPU device the int4 module binds torch's CPU int4 GEMM over
+    the same codes (no re-quantization), releases qweight / scale / zero, and serves every row
+    count from it; its results stay within the binding's self-check bar of the exact product."""
+    m, c = _mod4(bias=True)
     m.prepare_fused()
+    m.prepare_fused()                                    # idempotent
+    assert m._fused_tried and m._fused is not None
+    assert m._fused[2] is torch.ops.aten._weight_int4pack_mm_for_cpu and m._fused[3] == 384
+    assert m.qweight is None and m.scale is None and m.zero is None
+    x = torch.randn(rows, 300).to(torch.bfloat16)
+    y = m(x)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (rows, 48)
+    exact = oq.linear_ref(x.float().numpy(), c["Wd"]) + m.bias.detach().float().numpy()
+    yn = y.detach().float().numpy()
+    assert oq.mean_rel(yn, exact) < 0.05 and oq.max_rel(yn, exact) < 2e-2
+
+
+def test_prepare_fused_on_cpu_int2_stays_naive():
+    c = C.int2_random_case(40, 256, 64, 2000, "fp16")
+    m = wq._quant2_linear_cls()(C.u8(c["q"], "cpu"), C.to_torch(c["s"], "fp16", "cpu"),
+                                C.to_torch(c["z"], "fp16", "cpu"), None, 256, 64)
     m.prepare_fused()
-    assert getattr(m, "_fused", None) is None and m._fused_tried
+    assert getattr(m, "_fused", None) is None and m._fused_tried and m.qweight is not None
 
 
 def test_int8_module_cpu():

@@ -135,11 +135,13 @@ def test_verify_catches_corrupt_missing_and_foreign_units(tmp_path):
     data[-5] ^= 0xFF                                         # same size, different bytes
     open(p, "wb").write(bytes(data))
     ok, probs = sc.verify_shard_cache(str(tmp_path), "int4")
-    assert not ok and any("sha256 mismatch L0000" in s for s in probs)
+    assert not ok and any(s.startswith("L0000.safetensors: sha256 differs") for s in probs)
     open(p, "wb").write(bytes(data[:-1]))                    # truncated
-    assert any("size mismatch L0000" in s for s in sc.verify_shard_cache(str(tmp_path), "int4")[1])
+    assert any(s.startswith("L0000.safetensors: ") and "bytes on disk" in s
+               for s in sc.verify_shard_cache(str(tmp_path), "int4")[1])
     os.remove(os.path.join(d, "head.safetensors"))
-    assert any("missing file head" in s for s in sc.verify_shard_cache(str(tmp_path), "int4")[1])
+    assert any(s.startswith("head.safetensors: ") and "absent" in s
+               for s in sc.verify_shard_cache(str(tmp_path), "int4")[1])
     import json
     mf = os.path.join(d, "manifest.json")
     man = json.load(open(mf))
@@ -147,9 +149,9 @@ def test_verify_catches_corrupt_missing_and_foreign_units(tmp_path):
     man["files"].pop("head.safetensors")
     json.dump(man, open(mf, "w"))
     probs = sc.verify_shard_cache(str(tmp_path), "int4")[1]
-    assert any("packer_hash mismatch" in s for s in probs) and any("incomplete" in s for s in probs)
+    assert any("packer tag" in s for s in probs) and any("incomplete" in s for s in probs)
     os.remove(mf)
-    assert sc.verify_shard_cache(str(tmp_path), "int4") == (False, ["manifest.json missing"])
+    assert sc.verify_shard_cache(str(tmp_path), "int4") == (False, ["no manifest.json"])
 
 
 def test_install_refusals():
