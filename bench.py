@@ -349,6 +349,26 @@ def bench_c4(args, dev):
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
     flops = sum(2.0 * M * N * K for N, K, _ in sets)
     tf = flops / (ms * 1e-3)
+    # the module's naive prefill path on the same weights: the bit-exact HIP dequant to bf16, then
+    # the bf16 GEMM (hipBLASLt, as F.linear) -- what _bench_large_m_naive weighs the fused kernel
+    # against
+    naive_sets = []
+    for i, (N, K, _fn) in enumerate(sets[:2]):
+        if args.quant == "int4":
+            L = wl.rtn_int4_linear(N, K, 5000 + i, dev)
+            naive_sets.append((N, K, lambda x, y, L=L, K=K: torch.mm(
+                x, ops.dequant_w4(L.q, L.s, L.z, K, 128, torch.bfloat16).t(), out=y)))
+        else:
+            q, s_ = wl.int8_linear(N, K, 5000 + i, dev)
+            naive_sets.append((N, K, lambda x, y, q=q, s_=s_: torch.mm(
+                x, ops.dequant_w8(q, s_, torch.bfloat16).to(torch.bfloat16).t(), out=y)))
+
+    def naive_step():
+        for N, K, fn in naive_sets:
+            fn(xs[K], ys[N])
+
+    ms_naive = _time_steps(naive_step, max(3, args.steps // 4), 2)
+    tf_naive = sum(2.0 * M * N * K for N, K, _ in naive_sets) / (ms_naive * 1e-3)
     roof = {"bound": "mfma", "achieved": round(tf / 1e12, 2), "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s",
             "frac": round(tf / BF16_PEAK, 4), "traffic": _traffic(f"c4_{args.quant}_m{M}"),
             "kernel": f"gemm_wq_kernel<{4 if args.quant == 'int4' else 8}> (imq_linear_"
@@ -356,7 +376,10 @@ def bench_c4(args, dev):
             "avg_launch_us": round(ms * 1e3 / len(sets), 3), "flops_per_launch": flops / len(sets)}
     wbytes = sum(N * K * (0.53125 if args.quant == "int4" else 1.0) for N, K, _ in sets)
     cfg = {"workload": f"C4 prefill {args.quant} 4096->14336 and 14336->4096, M={M}", "M": M,
-           "quant": args.quant, "launches_per_step": len(sets), "distinct_bytes_per_step": int(wbytes)}
+           "quant": args.quant, "launches_per_step": len(sets), "distinct_bytes_per_step": int(wbytes),
+           "naive": {"value": round(tf_naive / 1e12, 3), "unit": "TFLOP/s",
+                     "path": "imq dequant to bf16 + F.linear (hipBLASLt), both shapes, eager",
+                     "fused_speedup": round(tf / tf_naive, 3)}}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path

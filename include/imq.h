@@ -132,7 +132,7 @@ int imq_linear_w8(const void* x, int64_t x_row_stride, int64_t M, int64_t K, con
  * it keeps the last call's partials (they need no clearing: each call writes every partial it
  * reads), so calls that may overlap on one GPU (other streams, or unordered work) race: order
  * them on one stream. */
-#define IMQ_NOALLOC_SCRATCH_BYTES (32ll << 20)
+#define IMQ_NOALLOC_SCRATCH_BYTES (64ll << 20)
 
 int imq_linear_w4_noalloc(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
                           const void* qweight, int64_t q_row_stride, const void* scale, int64_t s_stride_n,

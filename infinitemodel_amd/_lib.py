@@ -20,7 +20,7 @@ LIB_PATH = os.environ.get("IMQ_LIB_PATH") or os.path.join(HERE, "_lib", "libimq.
 
 IMQ_DT_BF16, IMQ_DT_FP16, IMQ_DT_FP32 = 0, 1, 2
 IMQ_OK, IMQ_ERR_INVALID, IMQ_ERR_UNSUPPORTED, IMQ_ERR_ALIGN, IMQ_ERR_SCRATCH = 0, -1, -2, -3, -4
-IMQ_NOALLOC_SCRATCH_BYTES = 32 << 20
+IMQ_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int

@@ -26,6 +26,12 @@
 
 namespace imq {
 
+bool rb_takes(int bits, int64_t M, int64_t N, int64_t K, int64_t G);
+int64_t rb_workspace_bytes(int bits, int64_t M, int64_t N, int64_t K, int cus);
+int gemm_rb(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
+            const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg, int zdt,
+            int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
+
 namespace {
 
 constexpr int GROUP_M = 8;
@@ -646,11 +652,14 @@ int gemm_bits(const GemmArgs& a, int sdt, int zdt, void* ws, int64_t wsb, hipStr
 
 }  // namespace
 
-// Workspace bytes a split-K launch of this shape uses (0: the launch does not split K).
+// Workspace bytes a split-K launch of this shape may use (0: no launch splits K): the larger of
+// the register-B GEMM's plan (int4 / int8) and the LDS-dequant GEMM's (int2, other layouts).
 int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 16 || N <= 0 || K % 64 != 0) return 0;
   const int cus = device_info().cus;
-  return use_big(M) ? split_bytes<CfgBig>(M, N, K, cus) : split_bytes<CfgSmall>(M, N, K, cus);
+  const int64_t lds = use_big(M) ? split_bytes<CfgBig>(M, N, K, cus) : split_bytes<CfgSmall>(M, N, K, cus);
+  const int64_t rb = rb_workspace_bytes(4, M, N, K, cus);
+  return lds > rb ? lds : rb;
 }
 
 namespace {
@@ -744,6 +753,10 @@ int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, cons
   // widest weight load of either tile configuration: 16 B (int4, int8 as 2 x 16 B), 8 B (int2)
   const int wbytes = bits == 2 ? 8 : 16;
   if (((uintptr_t)q % wbytes) || (sqn % wbytes)) return IMQ_ERR_UNSUPPORTED;
+  if (rb_takes(bits, M, N, K, G)) {
+    const int rc = gemm_rb(bits, x, sxm, M, K, q, sqn, sc, ssn, ssg, sdt, zr, szn, szg, zdt, N, G, y, sym, ws, wsb, st);
+    if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+  }
   GemmArgs a{x, sxm, (int)M, (int)K, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, gsh, y, sym, 0, 0, 1, 0,
              nullptr};
   switch (bits) {

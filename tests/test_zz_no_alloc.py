@@ -49,7 +49,7 @@ def _run_pair(dev, M, N, K, seed):
 
 
 @pytest.mark.parametrize("first,second", [
-    # prefill split-K: C4 14336 -> 4096 at M=512 (16 MiB of partials), then a smaller split-K shape
+    # prefill split-K: C4 14336 -> 4096 at M=512 (32 MiB of partials), then a smaller split-K shape
     ((512, 4096, 14336), (64, 4096, 4096)),
     # decode K-split: C2 gate_up at M=16 (7.3 MB of partials), then down at M=8
     ((16, 28672, 4096), (8, 4096, 14336)),
@@ -71,7 +71,7 @@ def test_noalloc_rejects_oversize_on_gpu(dev):
     nothing (the output keeps its contents)."""
     import torch
     L = _lib.lib()
-    M, N, K = 16, 1 << 18, 4096      # 4 splits x 16 x 262144 x 4 B = 64 MiB of partials
+    M, N, K = 16, 1 << 19, 4096      # 4 splits x 16 x 524288 x 4 B = 128 MiB of partials
     assert L.imq_linear_workspace_bytes(M, N, K) > _lib.IMQ_NOALLOC_SCRATCH_BYTES
     x, q, s, z = _case(dev, M, N, K, seed=15)
     y = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
