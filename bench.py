@@ -19,8 +19,9 @@ linears, launched back to back on one stream and replayed as a HIP graph.
 Other configs print lines of the same shape: --config c1 (single 1x4096->4096 linear), c3 (int2
 g64 70B shapes), c4 (prefill, --quant int4|int8, --m 512|2048), c5 (OLMoE fused MoE, --m = T),
 gptoss (gpt-oss-20b fused experts, --m = T), head (int8 lm_head decode at the Qwen2.5-7B head,
-152064 x 3584, --m rows) and ``copy`` (the plain device copy used to calibrate the PMC byte
-counters).
+152064 x 3584, --m rows), ``ceiling`` (the C2 weights read by a read-only streaming kernel, one
+launch per linear and one persistent launch, beside the decode kernels) and ``copy`` (the plain
+device copy used to calibrate the PMC byte counters).
 """
 from __future__ import annotations
 
@@ -42,7 +43,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "gptoss", "head", "copy"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "gptoss", "head", "copy", "ceiling"])
     ap.add_argument("--m", type=int, default=None, help="rows: C2/C3/C4 M, C5 tokens T")
     ap.add_argument("--quant", default="int4", choices=["int4", "int8"], help="C4 weight format")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -532,6 +533,68 @@ def bench_head(args, dev):
 
 
 # ---------------------------------------------------------------------------------------------
+# Read-only ceiling of the C2 decode pass (the measurement probes of libimq)
+# ---------------------------------------------------------------------------------------------
+def bench_ceiling(args, dev):
+    """The C2 stack's weight bytes (codes + scale + zero of all 128 linears, 3.7 GB) read by a
+    read-only streaming kernel: (a) one launch per linear, the ceiling of any one-launch-per-linear
+    design; (b) one persistent launch over all of them, the ceiling with no launch boundaries;
+    (c) the decode kernels themselves on the same weights at M=1. value = (a)."""
+    import torch
+    from infinitemodel_amd import _lib, ops, workloads as wl
+    L = _lib.lib()
+    lins = wl.llama8b_stack(dev)
+    st = lambda: torch.cuda.current_stream(dev).cuda_stream   # noqa: E731
+    sink = torch.empty(int(L.imq_probe_sink_bytes()) // 4 + 1, dtype=torch.int32, device=dev)
+    per_linear = []
+    allp, alln = [], []
+    for lin in lins:
+        bufs = [lin.q, lin.s, lin.z]
+        for b in bufs:
+            assert b.is_contiguous() and (b.numel() * b.element_size()) % 16 == 0 and b.data_ptr() % 16 == 0
+        ptrs = torch.tensor([b.data_ptr() for b in bufs], dtype=torch.int64, device=dev)
+        n16 = torch.tensor([b.numel() * b.element_size() // 16 for b in bufs], dtype=torch.int64, device=dev)
+        per_linear.append((ptrs, n16, int(n16.max())))
+        allp += [b.data_ptr() for b in bufs]
+        alln += [b.numel() * b.element_size() // 16 for b in bufs]
+    all_ptrs = torch.tensor(allp, dtype=torch.int64, device=dev)
+    all_n16 = torch.tensor(alln, dtype=torch.int64, device=dev)
+    weight_bytes = 16 * sum(alln)
+
+    def per_launch():
+        for ptrs, n16, mx in per_linear:
+            _lib.call("imq_probe_read_seq", ptrs.data_ptr(), n16.data_ptr(), 3, mx, sink.data_ptr(),
+                      sink.numel() * 4, st())
+
+    def persistent():
+        _lib.call("imq_probe_read_seq", all_ptrs.data_ptr(), all_n16.data_ptr(), len(alln), max(alln),
+                  sink.data_ptr(), sink.numel() * 4, st())
+
+    x_in = wl.activations(1, 4096, 1, dev)
+    x_dn = wl.activations(1, 14336, 2, dev)
+    ys = {n: torch.empty((1, N), dtype=torch.bfloat16, device=dev) for n, _, N in wl.LLAMA8B_PROJ}
+
+    def decode():
+        for lin in lins:
+            kind = lin.name.split(".")[1]
+            ops.linear_w4(x_dn if kind == "down" else x_in, lin.q, lin.G, (lin.s, lin.z), out=ys[kind])
+
+    g = not args.no_graph
+    ms_a = _time_steps(_graph_or_eager(per_launch, g), args.steps, args.warmup)
+    ms_b = _time_steps(_graph_or_eager(persistent, g), args.steps, args.warmup)
+    ms_c = _time_steps(_graph_or_eager(decode, g), args.steps, args.warmup)
+    gbs = lambda ms: round(weight_bytes / (ms * 1e-3) / 1e9, 2)   # noqa: E731
+    roof = _hbm_roofline("probe_read_seq_kernel (one launch per linear)", weight_bytes / len(lins),
+                         ms_a * 1e3 / len(lins), None)
+    cfg = {"workload": "C2 llama-3-8b int4 weights (128 linears, codes + scale + zero), read-only ceilings",
+           "weight_bytes_per_step": weight_bytes, "distinct_bytes_per_step": weight_bytes,
+           "per_linear_launch_gbs": gbs(ms_a), "persistent_launch_gbs": gbs(ms_b),
+           "decode_kernels_gbs": gbs(ms_c), "persistent_ms": round(ms_b, 5), "decode_ms": round(ms_c, 5),
+           "note": "GB/s over the weight bytes only (the decode line adds x and y, 0.1%)"}
+    return _line(gbs(ms_a), "GB/s", ms_a, args, cfg, roof, None, data="synthetic: the C2 stack's RTN-packed weights")
+
+
+# ---------------------------------------------------------------------------------------------
 def bench_copy(args, dev):
     """Plain device copy of 1 GiB (read 1 GiB + write 1 GiB per launch): calibrates the PMC
     FETCH_SIZE / WRITE_SIZE counters against known bytes."""
@@ -546,7 +609,7 @@ def bench_copy(args, dev):
 
 
 BENCH = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "gptoss": bench_gptoss,
-         "head": bench_head, "copy": bench_copy}
+         "head": bench_head, "copy": bench_copy, "ceiling": bench_ceiling}
 
 
 def main():

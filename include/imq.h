@@ -197,6 +197,19 @@ int imq_moe_experts_w4_ex(const void* hidden, int64_t h_row_stride, int64_t T, i
                           void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
                           void* stream);
 
+/* ---- measurement probes ---------------------------------------------------------------------
+ * No counterpart in the reference: read-only HBM streaming kernels that set the practical ceiling
+ * the decode kernels are measured against (bench.py --config ceiling). Nothing is written.
+ *   imq_probe_read: one launch reads `bytes` (a multiple of 16, 16-byte aligned) of `buf`.
+ *   imq_probe_read_seq: one launch reads nbuf buffers in order; `ptrs` is a device array of nbuf
+ *     uint64 addresses (16-byte aligned), `n16s` a device array of nbuf int64 sizes in 16-byte
+ *     units, max_n16 the largest of them (sizes the grid).
+ *   `sink`: device memory of at least imq_probe_sink_bytes() bytes (never written in practice). */
+int64_t imq_probe_sink_bytes(void);
+int imq_probe_read(const void* buf, int64_t bytes, void* sink, int64_t sink_bytes, void* stream);
+int imq_probe_read_seq(const void* ptrs, const void* n16s, int nbuf, int64_t max_n16, void* sink,
+                       int64_t sink_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,6 +67,9 @@ SIGNATURES = {
                                        _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64,
                                        _c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int,
                                        _c_float, _c_float, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
+    "imq_probe_sink_bytes": (_c_i64, []),
+    "imq_probe_read": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
+    "imq_probe_read_seq": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_vp, _c_i64, _c_vp]),
 }
 
 
