@@ -33,9 +33,15 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libimq.so)")
 
 
+# Per-source extra flags. moe_rb.hip: MFMA results in VGPRs (LLVM's VGPR form of the MFMA
+# instructions), so the folded MoE kernels' per-group fold reads them without AGPR copies and two
+# waves fit per SIMD; the option is scoped to that file's kernels.
+EXTRA = {"moe_rb.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc(), *COMMON, "-c", src, "-o", obj]
+    cmd = [hipcc(), *COMMON, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

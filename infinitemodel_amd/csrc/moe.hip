@@ -26,10 +26,19 @@ int moe_gemm_w4(int mode, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t
                 const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off, const int32_t* perm, int k,
                 const void* bias, int64_t sbe, int bdt, float alpha, float limit, uint16_t* h, int64_t hs,
                 float* yr, hipStream_t st, bool check_only = false);
+int moe_rb(int mode, int ib, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t K, const uint8_t* q,
+           int64_t sqe, int64_t sqn, const void* sc, const void* zr, int64_t sse, int64_t ssn, int sdt, int64_t N,
+           int64_t I, const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off,
+           const int32_t* perm, int k, const void* bias, int64_t sbe, int bdt, float alpha, float limit,
+           uint16_t* h, int64_t hs, float* yr, const float* rs, int rs_stride, int rs_groups, float* hrs,
+           int hrs_stride, hipStream_t st, bool check_only);
+bool moe_rb_folded();
 }  // namespace imq
 using imq::moe_gemm_bm;
 using imq::moe_gemm_bn;
 using imq::moe_gemm_w4;
+using imq::moe_rb;
+using imq::moe_rb_folded;
 
 namespace {
 
@@ -1034,8 +1043,24 @@ namespace {
 // down K_pad a kernel layout may use. The token-sorted path uses h, z, off, perm and hit; the
 // per-row path gu, h and z.
 struct MoeWs {
-  int64_t gu, h, z, off, perm, hit, total, hw;
+  int64_t gu, h, z, off, perm, hit, rsx, rsh, total, hw;
 };
+
+// rs[t][g] = the fp32 sum of row t's bf16 values over columns [128 g, 128 g + 128), g < ng: one
+// wave per (row, group), a fixed-order wave reduction.
+__global__ __launch_bounds__(256) void moe_rowsum_kernel(const uint16_t* __restrict__ x, int64_t sxm, int64_t T,
+                                                         int ng, float* __restrict__ rs) {
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wid >= T * ng) return;
+  const int64_t t = wid / ng;
+  const int g = (int)(wid - t * ng);
+  const uint32_t v = *(const uint32_t*)(x + t * sxm + 128 * g + 2 * lane);
+  float sum = __uint_as_float(v << 16) + __uint_as_float(v & 0xffff0000u);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  if (lane == 0) rs[t * ng + g] = sum;
+}
 
 MoeWs moe_ws(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t G) {
   const int64_t B = T * top_k;
@@ -1048,7 +1073,10 @@ MoeWs moe_ws(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t 
   w.off = w.z + align_up(B * H * 4, kAlign);
   w.perm = w.off + align_up((E + 1) * 4, kAlign);
   w.hit = w.perm + align_up(B * 4, kAlign);
-  w.total = w.hit + align_up((E + 1) * 4, kAlign);
+  // the register-B grouped GEMM's row group sums (groups of 128): hidden rows, then h rows
+  w.rsx = w.hit + align_up((E + 1) * 4, kAlign);
+  w.rsh = w.rsx + align_up(T * imq_cdiv(H, 128) * 4, kAlign);
+  w.total = w.rsh + align_up(B * imq_cdiv(I, 128) * 4, kAlign);
   return w;
 }
 }  // namespace
@@ -1087,26 +1115,30 @@ struct MoeCall {
   int64_t xk;            // valid hidden columns: gu_K_pad for padded rows, else H (H % 8 == 0)
 };
 
-// Grouped GEMM path for many routed rows per expert (prefill): the sort also lists the 64-row
-// blocks of each hit expert; gate_up and down then run as tiled dequant-GEMMs over those blocks
-// (the prefill GEMM kernel's grouped forms), the activation in gate_up's epilogue, the row bias
-// and the scatter to routed order in down's; the combine is moe_combine_kernel's. It pays once
-// an expert's rows times K is large enough to amortize the per-block costs; measured on MI355X
-// (us per layer, line kernels -> GEMM; rows per expert = B / E):
-//   OLMoE (K 2048)   T=128 (16 rows) 107 -> 147, T=256 (32) 148 -> 155, T=384 (48) 191 -> 163,
-//                    T=512 (64) 222 -> 187, T=1024 (128) 385 -> 304
-//   gpt-oss (K 3072) T=128 (16 rows) 249 -> 249, T=256 (32) 368 -> 255, T=512 (64) 609 -> 380
-// so the GEMM runs from (B / E) * gate_up K >= 81920 (32 rows at K 2560, 40 at K 2048).
+// Grouped GEMM path for many routed rows per expert (prefill): the sort also lists the row
+// blocks of each hit expert; gate_up and down then run as grouped GEMMs over those blocks --
+// the register-B kernel's MoE forms where they apply (int4 groups of 128, K a multiple of 128 up
+// to 5120, I a multiple of 128 or the gpt-oss layout), else the LDS-dequant GEMM's -- the
+// activation in gate_up's epilogue, the row bias and the scatter to routed order in down's; the
+// combine is moe_combine_kernel's. It pays once an expert's rows times K is large enough to
+// amortize the per-block costs; measured on MI355X (us per layer, line kernels -> register-B
+// GEMM; rows per expert = B / E):
+//   OLMoE (K 2048)   T=64 (8 rows) 81 -> 84, T=128 (16) 101 -> 88, T=256 (32) 146 -> 94,
+//                    T=512 (64) 256 -> 147, T=1024 (128) 400 -> 230
+//   gpt-oss (K 3072) T=64 (8 rows) 191 -> 223, T=128 (16) 241 -> 228, T=256 (32) 370 -> 234
+// so the register-B forms run from (B / E) * gate_up K >= 32768 (16 rows at K 2048); the
+// LDS-dequant GEMM, slower at these sizes, from 81920 (its crossover with the line kernels).
+#ifndef IMQ_MOE_RB_WORK
+#define IMQ_MOE_RB_WORK 32768
+#endif
 #ifndef IMQ_MOE_GEMM_WORK
 #define IMQ_MOE_GEMM_WORK 81920
 #endif
+constexpr int64_t kMoeRbWork = IMQ_MOE_RB_WORK;
 constexpr int64_t kMoeGemmWork = IMQ_MOE_GEMM_WORK;
-int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
+int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream_t st) {
   const int64_t B = c.T * c.k;
-  const int bm = moe_gemm_bm();
   const int64_t hits = c.E < B ? c.E : B;
-  const int64_t max_mt = imq_cdiv(B, bm) + hits;
-  if ((2 + 2 * max_mt) * 4 > L.h - L.gu) return IMQ_ERR_UNSUPPORTED;   // the list lives in gu's room
   int32_t* off = (int32_t*)(ws + L.off);
   int32_t* perm = (int32_t*)(ws + L.perm);
   int32_t* hit = (int32_t*)(ws + L.hit);
@@ -1114,19 +1146,51 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   uint16_t* h = (uint16_t*)(ws + L.h);
   float* yr = (float*)(ws + L.z);
   const int gmode = c.act == IMQ_ACT_GPTOSS ? 2 : 1;
+  const int ib = 2;
+  // the register-B form (weights dequantized into MFMA operands) where it takes both
+  // projections, else the LDS-dequant GEMM; the block size of the sort's list follows the form
+  bool rb = true;
+  int bm = 32 * ib;
+  int64_t max_mt = imq_cdiv(B, bm) + hits;
+  // the folded form's row group sums: hidden rows (a launch of their own), h rows (gate_up's epilogue)
+  float* rsx = (float*)(ws + L.rsx);
+  float* rsh = (float*)(ws + L.rsh);
+  const int ngx = (int)imq_cdiv(c.H, 128), ngh = (int)imq_cdiv(c.I, 128);
   auto gate_up = [&](bool check) {
+    if (rb)
+      return moe_rb(gmode, ib, c.hidden, c.hs, c.T, c.gK, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
+                    2 * c.I, c.I, mtl + 2, mtl, max_mt, off, perm, (int)c.k, c.gb, c.gbe, c.bdt, c.alpha, c.limit, h,
+                    L.hw, nullptr, rsx, ngx, ngx, rsh, ngh, st, check);
     return moe_gemm_w4(gmode, c.hidden, c.hs, c.T, c.gK, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
                        2 * c.I, c.I, mtl + 2, mtl, max_mt, off, perm, (int)c.k, c.gb, c.gbe, c.bdt, c.alpha, c.limit,
                        h, L.hw, nullptr, st, check);
   };
   auto down = [&](bool check) {
+    if (rb)
+      return moe_rb(3, ib, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2,
+                    mtl, max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, rsh, ngh, ngh,
+                    nullptr, 0, st, check);
     return moe_gemm_w4(3, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2, mtl,
                        max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, st, check);
   };
   // both projections are validated before anything is launched
-  int rc = gate_up(true);
-  if (rc == IMQ_OK) rc = down(true);
-  if (rc != IMQ_OK) return rc;
+  if (gate_up(true) != IMQ_OK || down(true) != IMQ_OK) {
+    // the LDS-dequant GEMM only above its own crossover, while the line kernels take the shape
+    if (line_ok && B * c.gK < kMoeGemmWork * c.E) return IMQ_ERR_UNSUPPORTED;
+    rb = false;
+    bm = moe_gemm_bm();
+    max_mt = imq_cdiv(B, bm) + hits;
+    int rc = gate_up(true);
+    if (rc == IMQ_OK) rc = down(true);
+    if (rc != IMQ_OK) return rc;
+  }
+  if ((2 + 2 * max_mt) * 4 > L.h - L.gu) return IMQ_ERR_UNSUPPORTED;   // the list lives in gu's room
+  int rc;
+  if (rb && moe_rb_folded()) {
+    const int64_t waves = c.T * ngx;
+    moe_rowsum_kernel<<<dim3((unsigned)imq_cdiv(waves, 4)), dim3(256), 0, st>>>(c.hidden, c.hs, c.T, ngx, rsx);
+    IMQ_LAUNCH_CHECK();
+  }
   moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit, mtl, bm);
   IMQ_LAUNCH_CHECK();
   rc = gate_up(false);
@@ -1150,17 +1214,20 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
 int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   const int64_t B = c.T * c.k;
   const int vb = c.sdt == IMQ_DT_FP32 ? 4 : 2;
-  if (c.G != 128 || c.gK % kMoeLine || c.dK % kMoeLine || c.I % 32 || c.H % 64) return IMQ_ERR_UNSUPPORTED;
+  // (K padded to a multiple of the line, 256, is the line kernels' condition -- moe_line_shape /
+  // dec_shape; the grouped GEMMs take K_pad multiples of 128)
+  if (c.G != 128 || c.I % 32 || c.H % 64) return IMQ_ERR_UNSUPPORTED;
   if (!aligned(c.out, 16) || (c.os % 8)) return IMQ_ERR_UNSUPPORTED;
   if (c.E > 16384 || B > 0x7fffffff || c.T * c.hs > 0x7fffffffLL * 8) return IMQ_ERR_UNSUPPORTED;
   if (!aligned(c.gq, 16) || !aligned(c.dq, 16) || (c.gqn % 16) || (c.dqn % 16) || (c.gqe % 16) || (c.dqe % 16))
     return IMQ_ERR_UNSUPPORTED;
-  if (!aligned(c.gs, 4) || !aligned(c.gz, 4) || !aligned(c.ds, 4) || !aligned(c.dz, 4) || (c.gsn * vb) % 4 ||
-      (c.dsn * vb) % 4 || (c.gse * vb) % 4 || (c.dse * vb) % 4)
-    return IMQ_ERR_UNSUPPORTED;
+  // the line kernels read scale / zero pairs as 4-byte words and take K up to 4096; the grouped
+  // GEMMs read them element-wise and take any K
+  const bool sz_words = aligned(c.gs, 4) && aligned(c.gz, 4) && aligned(c.ds, 4) && aligned(c.dz, 4) &&
+                        (c.gsn * vb) % 4 == 0 && (c.dsn * vb) % 4 == 0 && (c.gse * vb) % 4 == 0 &&
+                        (c.dse * vb) % 4 == 0;
   int s2, w;
-  // the line kernels take K up to 4096; the grouped GEMM any K
-  const bool line_ok = moe_line_shape(c.gK, &s2, &w) && moe_line_shape(c.dK, &s2, &w);
+  const bool line_ok = sz_words && moe_line_shape(c.gK, &s2, &w) && moe_line_shape(c.dK, &s2, &w);
   int32_t* off = (int32_t*)(ws + L.off);
   int32_t* perm = (int32_t*)(ws + L.perm);
   int32_t* hit = (int32_t*)(ws + L.hit);
@@ -1198,8 +1265,8 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
     }
   }
   const bool gemm_shape = c.act == IMQ_ACT_GPTOSS || c.I % (moe_gemm_bn() / 2) == 0;
-  if (!direct && (!line_ok || B * c.gK >= kMoeGemmWork * c.E) && c.xk == c.gK && gemm_shape) {
-    const int rc = moe_gemm(c, ws, L, st);
+  if (!direct && (!line_ok || B * c.gK >= kMoeRbWork * c.E) && c.xk == c.gK && gemm_shape) {
+    const int rc = moe_gemm(c, ws, L, line_ok, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }
   if (!line_ok) return IMQ_ERR_UNSUPPORTED;

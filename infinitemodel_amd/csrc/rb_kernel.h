@@ -1,0 +1,652 @@
+// The register-B GEMM kernel (weights dequantized straight into MFMA B operands) for int4
+// group-wise and int8 per-row weights on gfx950, shared by the dense launchers (gemm_rb.hip)
+// and the grouped MoE launchers (moe_rb.hip).
+//
+// y[M, N] = x[M, K] . dequant(W[N, K])^T, bf16 activations, fp32 accumulation, bf16 output: the
+// contract of the reference's `_k` / `_k8` GEMM kernels (worker_quant.py:1098-1126, 953-980).
+//
+// Structure. A workgroup of NW waves computes a BM x (64 NW) output tile; wave w owns all BM rows
+// of columns [64 w, 64 w + 64), as IB x 2 blocks of v_mfma_f32_32x32x16_bf16 (BM = 32 IB).
+//   * Activations: the workgroup stages the BM x 64 tile of each K step in LDS (three buffers,
+//     XOR-swizzled 16-byte chunks, one barrier per step), loaded from global two steps ahead;
+//     every wave reads all BM rows from LDS, one MFMA slice ahead of use.
+//   * Weights never touch LDS: each wave loads its own 64 columns' packed bytes from global memory
+//     (one 16-byte load per lane per 32-column block per step for int4, two for int8, two steps
+//     ahead) and converts them in registers into the MFMA B fragments -- every weight is
+//     dequantized exactly once per workgroup and the LDS carries only the activations, so LDS
+//     bytes per flop are 1 / 64 (against 1 / 32 for a 64 x 64 wave tile with both operands in LDS).
+//   * K order inside a step is permuted consistently for A and B: MFMA slice s of half h
+//     (lanes 32 h .. 32 h + 31) covers K [32 h + 8 s, +8), so a lane's B codes for the whole step
+//     are 32 consecutive columns of its row (one contiguous load) and its A chunks are LDS chunks
+//     4 h + s. The sum over K is unchanged.
+//   * int4: w = bf16((q - z) s) with z, s taken to bf16 first -- the exact product rounded once,
+//     the reference GEMM's weight tile (worker_quant.py:1121-1122). int8: the exact integer, the
+//     per-row scale applied to the fp32 accumulator in the epilogue.
+//   * Tiles are dealt XCD-aware and in groups of 8 tile-rows (as the LDS-dequant GEMM); when the
+//     tiles do not fill the CUs K is split across workgroups into fp32 partials [split][M][N]
+//     that a second launch sums in split order.
+#pragma once
+#include "imq_common.h"
+
+#include <type_traits>
+
+namespace imq {
+namespace {
+
+constexpr int RB_GROUP_M = 8;
+constexpr int RB_BK = 64;
+// VALU instructions the scheduler places after each MFMA (int4 dequant / int8 conversion work):
+// chosen per format as the pattern that keeps the 256-row variants within the register file.
+#ifndef RB_VALU_PER_MFMA_4
+#define RB_VALU_PER_MFMA_4 5
+#endif
+#ifndef RB_VALU_PER_MFMA_8
+#define RB_VALU_PER_MFMA_8 3
+#endif
+
+struct RbArgs {
+  const uint16_t* x;
+  int64_t sxm;
+  int M, K;
+  const uint8_t* q;
+  int64_t sqn;
+  const void* sc;
+  int64_t ssn, ssg;
+  const void* zr;
+  int64_t szn, szg;
+  int N, gsh;
+  uint16_t* y;
+  int64_t sym;
+  int tiles_m, tiles_n;
+  int splits, kps;
+  float* part;
+  // grouped MoE forms (MOE != 0): a tile is (row block, column tile); mtl[2 b] = expert and
+  // mtl[2 b + 1] = first sorted row of block b, *nmt blocks in all; off = [E + 1] sorted offsets,
+  // perm = sorted position -> routed row
+  const int32_t* mtl = nullptr;
+  const int32_t* nmt = nullptr;
+  const int32_t* off = nullptr;
+  const int32_t* perm = nullptr;
+  int64_t sqe = 0, sse = 0;           // expert strides: packed bytes, scale / zero elements
+  int k = 1, I = 0;                   // top_k; intermediate size (gate_up)
+  const void* bias = nullptr;         // per-expert row bias [E][rows] or null
+  int64_t sbe = 0;
+  int bdt = 0;
+  float alpha = 0.f, limit = 0.f;     // gpt-oss activation
+  float* yr = nullptr;                // MOE 3: fp32 rows [B][N] in routed order
+  // scale-folded form (FOLD): per-row sums of the activations over each group of 128 K,
+  // rs[row][g] (row = token for gate_up, sorted position for down), groups >= rs_groups read 0;
+  // gate_up also writes the group sums of its bf16 h rows into hrs[p][tn] (down's rs)
+  const float* rs = nullptr;
+  int rs_stride = 0, rs_groups = 0;
+  float* hrs = nullptr;
+  int hrs_stride = 0;
+};
+
+IMQ_DEV float rb_bias(const void* p, int dt, int64_t i) {
+  if (dt == IMQ_DT_FP32) return ((const float*)p)[i];
+  if (dt == IMQ_DT_FP16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+  return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+IMQ_DEV int rb_swz(int row, int c) { return (row * 8 + (c ^ ((row >> 1) & 7))) * 8; }
+
+// w & m computed in a register the compiler cannot see through, so the byte extractions below
+// stay single v_cvt_f32_ubyteN instructions instead of being re-folded into per-nibble bit-field
+// extracts (the result only feeds VALU conversions, never an MFMA operand directly).
+IMQ_DEV uint32_t rb_and(uint32_t w, uint32_t m) {
+  uint32_t r;
+  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(w), "v"(m));
+  return r;
+}
+
+// 8 int4 codes of one dword (code i at bits 4i) -> 4 dwords of bf16 (c - z) s in K order: the
+// even codes sit in the bytes of lo, the odd ones in the bytes of hi, each one v_cvt_f32_ubyteN
+// from fp32; fma(c, s, -z s) is the exact (c - z) s, rounded once by the pack.
+IMQ_DEV u32x4_t rb_dequant4(uint32_t w, float s, float nzs) {
+  const uint32_t lo = rb_and(w, 0x0F0F0F0Fu), hi = rb_and(w >> 4, 0x0F0F0F0Fu);
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float c0 = (float)((lo >> (8 * i)) & 0xffu);
+    const float c1 = (float)((hi >> (8 * i)) & 0xffu);
+    r[i] = cvt_pk_bf16(fmaf(c0, s, nzs), fmaf(c1, s, nzs));
+  }
+  return r;
+}
+
+// 8 int8 codes (two dwords) -> 4 dwords of bf16, exact.
+IMQ_DEV u32x4_t rb_convert8(uint32_t lo, uint32_t hi) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t w = i ? hi : lo;
+    r[2 * i] = cvt_pk_bf16((float)(int8_t)(w & 0xff), (float)(int8_t)((w >> 8) & 0xff));
+    r[2 * i + 1] = cvt_pk_bf16((float)(int8_t)((w >> 16) & 0xff), (float)(int8_t)(w >> 24));
+  }
+  return r;
+}
+
+// MOE 0: the dense GEMM. Grouped MoE forms (int4; one hit expert's sorted rows per row block,
+// gathered): MOE 1 gate_up with SiLU-GLU -- wave w's first column block holds gate rows, its
+// second the matching up rows, so h = silu(gate) * up is formed in registers and written as bf16
+// in sorted order; MOE 2 gpt-oss gate_up (interleaved gate / up rows in adjacent lanes, its
+// clamped GLU); MOE 3 down (fp32 rows plus the row bias, scattered to routed order).
+//
+// PD: register sets of the global -> register pipeline; B(kt) is loaded PD steps ahead and A(kt)
+// PD + 1 steps ahead (the dense GEMM's long steps need 2, the MoE forms' short ones more).
+//
+// FOLD (MoE forms, int4, groups of 128 = two K steps): the B operand is the exact bf16 128 + q
+// (the code dropped into the mantissa of 0x4300: 7 integer ops per 8 codes instead of 23 for
+// the dequantized bf16 (q - z) s), the MFMAs of one group accumulate into fresh registers which
+// are folded into the total with the group's scale s -- sum_g s_g sum_{k in g} x_k (128 + q_k) --
+// and the remaining -s_g (128 + z_g) sum_{k in g} x_k terms are one fp32 32x32x2 MFMA chain per
+// block over the groups, from the rows' group sums rs. The activations' K order inside each
+// 8-element chunk is permuted to the order the magic unpack produces. Every product is exact
+// and no weight is rounded to bf16, so the sums are within fp32 accumulation error of the exact
+// (q - z) s products (the dequantizing form rounds each weight to bf16 first).
+template <int BITS, int SDT, int ZDT, int IB, int NW, int MOE = 0, int PD = 2, bool FOLD = false>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
+  static_assert(!FOLD || (MOE != 0 && BITS == 4 && PD % 2 == 0), "the folded form: int4 MoE, even pipeline depth");
+  constexpr int BM = 32 * IB, BN = 64 * NW, BK = RB_BK, NTHR = 64 * NW;
+  constexpr int A_EL = BM * BK;                    // bf16 elements of one LDS buffer
+  constexpr int XC = BM * 8 / NTHR;                // 16-byte activation chunks per thread per step
+  constexpr int QV = BITS == 8 ? 2 : 1;            // 16-byte weight loads per lane per column block
+  static_assert((BM * 8) % NTHR == 0, "activation chunks must divide evenly");
+  extern __shared__ __align__(16) uint16_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, c = lane & 31;
+
+  // ---- tile mapping ------------------------------------------------------------------------------
+  int split = 0, m0 = 0, n0, tn = 0;
+  int e = 0, prow0 = 0, cnt = 0;                    // MOE: expert, first sorted row, rows of the block
+  if constexpr (MOE == 0) {
+    // XCD-aware, grouped by RB_GROUP_M tile-rows; split-K index outermost
+    const int T = a.tiles_m * a.tiles_n;
+    split = blockIdx.x / T;
+    int L = blockIdx.x - split * T;
+    if ((T & 7) == 0) L = (L & 7) * (T >> 3) + (L >> 3);
+    const int per_group = RB_GROUP_M * a.tiles_n;
+    const int grp = L / per_group;
+    const int first_m = grp * RB_GROUP_M;
+    const int gm = (a.tiles_m - first_m) < RB_GROUP_M ? (a.tiles_m - first_m) : RB_GROUP_M;
+    const int in_grp = L - grp * per_group;
+    m0 = (first_m + in_grp % gm) * BM;
+    n0 = (in_grp / gm) * BN;
+  } else {
+    // The grid covers the most blocks the routing can produce; the Tr tiles that exist are dealt
+    // so that dispatch index b (which runs on XCD b % 8) gets a contiguous run of tiles per XCD,
+    // column tiles fastest: the tiles reading one block's gathered rows share an L2.
+    const int Tr = *a.nmt * a.tiles_n;
+    const int b = blockIdx.x;
+    if (b >= Tr) return;                            // uniform over the workgroup
+    const int x8 = b & 7, q8 = Tr >> 3, r8 = Tr & 7;
+    const int lid = x8 * q8 + (x8 < r8 ? x8 : r8) + (b >> 3);
+    const int mt = lid / a.tiles_n;
+    tn = lid - mt * a.tiles_n;
+    e = a.mtl[2 * mt];
+    prow0 = a.mtl[2 * mt + 1];
+    cnt = a.off[e + 1] - prow0;
+    cnt = cnt < BM ? cnt : BM;
+    n0 = tn * BN;
+  }
+
+  // ---- activation load plan (32-bit offsets from the tile's first row) -------------------------
+  const uint16_t* xtile = a.x + (int64_t)m0 * a.sxm;
+  int xo[XC], xl[XC];
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int id = tid + NTHR * j;
+    const int row = id >> 3, ch = id & 7;
+    int r;
+    if constexpr (MOE == 0) {
+      r = m0 + row < a.M ? row : a.M - 1 - m0;
+    } else {
+      const int p = prow0 + (row < cnt ? row : cnt - 1);                // sorted position
+      r = MOE == 3 ? p : a.perm[p] / a.k;           // down reads h in sorted order, gate_up gathers
+    }
+    xo[j] = (int)(r * a.sxm) + ch * 8;
+    xl[j] = rb_swz(row, ch);
+  }
+
+  // ---- weight load plan: columns n0 + 64 wave + 32 j + c (MOE 1: gate column tn 32 NW + 32 wave
+  // + c for j = 0, the matching up column I + that for j = 1), K bytes [32 h, +32) codes per step --
+  const uint8_t* qb[2];
+  int64_t sb[2], zb[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    int n = MOE == 1 ? (j ? a.I : 0) + tn * (32 * NW) + 32 * wave + c : n0 + 64 * wave + 32 * j + c;
+    n = n < a.N ? n : a.N - 1;
+    qb[j] = a.q + (int64_t)e * a.sqe + (int64_t)n * a.sqn + (BITS == 8 ? 32 : 16) * h;
+    sb[j] = (int64_t)e * a.sse + (int64_t)n * a.ssn;
+    zb[j] = (int64_t)e * a.sse + (int64_t)n * a.szn;
+  }
+
+  // MoE forms: the tile's scale / zero pairs for all K groups are staged in LDS once, as
+  // [group][tile column] dwords (bf16 scale | bf16 zero << 16, both rounded to bf16 as the
+  // dequantization uses them); each step then reads one dword per column block from LDS instead
+  // of two strided global loads per column block -- those loads touch a separate cache line per
+  // lane and, issued every step, kept the texture unit busier than the weight stream itself.
+  uint32_t* SZ = (uint32_t*)(lds + 3 * A_EL);
+  if constexpr (MOE != 0) {
+    // batches of 8 elements per thread, all loads of a batch issued before any is consumed;
+    // consecutive threads take consecutive groups of one column (one scale row segment)
+    constexpr int SB = 8;
+    const int ng = a.K >> a.gsh, total = ng * BN;
+    for (int base = 0; base < total; base += SB * NTHR) {
+      uint32_t sv[SB], zv[SB];
+      int at[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int idx = base + u * NTHR + tid;
+        const int id = idx < total ? idx : total - 1;
+        const int tc = id / ng, g = id - tc * ng;
+        const int w_ = tc >> 6, j_ = (tc >> 5) & 1, c_ = tc & 31;
+        int n = MOE == 1 ? (j_ ? a.I : 0) + tn * (32 * NW) + 32 * w_ + c_ : n0 + tc;
+        n = n < a.N ? n : a.N - 1;
+        const int64_t gb = (int64_t)e * a.sse + (int64_t)g * a.ssg;
+        sv[u] = load_raw_bits<SDT>(a.sc, gb + (int64_t)n * a.ssn);
+        zv[u] = load_raw_bits<ZDT>(a.zr, gb + (int64_t)n * a.szn);
+        at[u] = idx < total ? g * BN + tc : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const float s_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<SDT>(sv[u]));
+        const float z_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<ZDT>(zv[u]));
+        if (at[u] >= 0) SZ[at[u]] = (__float_as_uint(s_) >> 16) | (__float_as_uint(z_) & 0xffff0000u);
+      }
+    }
+    __syncthreads();   // the prologue's weight-set loads read pairs other threads staged
+  }
+
+  static_assert(PD >= 2 && PD <= 4, "pipeline depth 2..4");
+  u32x4_t xr[PD][XC];
+  u32x4_t qr[PD][2][QV];
+  uint32_t sr[PD][2], zr[PD][2];
+  const int kt0 = split * a.kps;
+  const int KT = (a.K / BK - kt0) < a.kps ? (a.K / BK - kt0) : a.kps;
+
+  auto load_a = [&](auto setc, int ktl) {
+    constexpr int set = decltype(setc)::value;
+    const int kt = kt0 + (ktl < KT ? ktl : KT - 1);
+#pragma unroll
+    for (int j = 0; j < XC; ++j) xr[set][j] = *(const u32x4_t*)(xtile + kt * BK + xo[j]);
+  };
+  auto load_b = [&](auto setc, int ktl) {
+    constexpr int set = decltype(setc)::value;
+    const int kt = kt0 + (ktl < KT ? ktl : KT - 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int v = 0; v < QV; ++v) qr[set][j][v] = *(const u32x4_t*)(qb[j] + kt * (BK * BITS / 8) + 16 * v);
+      if constexpr (MOE != 0) {
+        const int g = (kt * BK + 32 * h) >> a.gsh;
+        sr[set][j] = SZ[g * BN + 64 * wave + 32 * j + c];
+      } else if constexpr (BITS != 8) {
+        const int g = (kt * BK + 32 * h) >> a.gsh;
+        sr[set][j] = load_raw_bits<SDT>(a.sc, sb[j] + (int64_t)g * a.ssg);
+        zr[set][j] = load_raw_bits<ZDT>(a.zr, zb[j] + (int64_t)g * a.szg);
+      }
+    }
+  };
+  auto store_a = [&](auto setc, uint16_t* A) {
+    constexpr int set = decltype(setc)::value;
+#pragma unroll
+    for (int j = 0; j < XC; ++j) *(u32x4_t*)(A + xl[j]) = FOLD ? permute_x8(xr[set][j]) : xr[set][j];
+  };
+
+  // acc: the running sums (FOLD: the current group's sums of x (128 + q)); tot: FOLD's total
+  f32x16_t acc[IB][2];
+  f32x16_t tot[FOLD ? IB : 1][2];
+#pragma unroll
+  for (int i = 0; i < IB; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.f;
+        if constexpr (FOLD) tot[i][j][r] = 0.f;
+      }
+  const uint32_t magic = FOLD ? magic_bf16_128x2() : 0u;
+  float sfold[2] = {0.f, 0.f};   // FOLD: scale of the group whose sums acc holds
+  int aoff[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) aoff[s] = rb_swz(c, 4 * h + s);   // + 32 rows (2048 elements) per i
+
+  bf16x8_t af[2][IB];        // A fragments of slice s live in af[s & 1], B fragments in bq[s & 1]
+  bf16x8_t bq[2][2];         // (4 slices: the parity pattern repeats every step)
+  auto read_frags = [&](auto pc, const uint16_t* A, int s) {
+    constexpr int p = decltype(pc)::value;
+#pragma unroll
+    for (int i = 0; i < IB; ++i) af[p][i] = *(const bf16x8_t*)(A + aoff[s] + i * 32 * BK);
+  };
+
+  // The scale / zero of a B register set as (s, -z s), both taken to bf16 first.
+  auto scale_pair = [&](auto bsc, float* sv, float* nz) {
+    constexpr int bs = decltype(bsc)::value;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if constexpr (MOE != 0) {
+        const float s_ = __uint_as_float(sr[bs][j] << 16), z_ = __uint_as_float(sr[bs][j] & 0xffff0000u);
+        sv[j] = s_;
+        nz[j] = -z_ * s_;
+      } else if constexpr (BITS != 8) {
+        float s_ = raw_bits_to_f32<SDT>(sr[bs][j]);
+        float z_ = raw_bits_to_f32<ZDT>(zr[bs][j]);
+        if constexpr (SDT != IMQ_DT_BF16) s_ = round_to<IMQ_DT_BF16>(s_);
+        if constexpr (ZDT != IMQ_DT_BF16) z_ = round_to<IMQ_DT_BF16>(z_);
+        sv[j] = s_;
+        nz[j] = -z_ * s_;
+      } else {
+        sv[j] = nz[j] = 0.f;
+      }
+    }
+  };
+  auto b_frag = [&](auto bsc, int s, int j, float sv, float nz) -> bf16x8_t {
+    constexpr int bs = decltype(bsc)::value;
+    if constexpr (FOLD) return unpack_nib8_bf16(qr[bs][j][0][s], magic);
+    u32x4_t d;
+    if constexpr (BITS == 8) d = rb_convert8(qr[bs][j][s >> 1][2 * (s & 1)], qr[bs][j][s >> 1][2 * (s & 1) + 1]);
+    else d = rb_dequant4(qr[bs][j][0][s], sv, nz);
+    return __builtin_bit_cast(bf16x8_t, d);
+  };
+
+  // LDS: three buffers of BM x 64 activations; step kt reads buffer kt % 3 and writes A(kt+1) into
+  // buffer (kt+1) % 3, whose last reads (steps kt-2 and the slice-0 prefetch at the end of kt-3)
+  // all precede the barrier of step kt-1 -- so one barrier per step suffices, placed after
+  // slice 1 once its MFMAs are queued.
+  //
+  // Step kt (B register set kt % PD, A register set (kt+1) % PD holding A(kt+1)):
+  //   slice s: dequantize B(kt) slice s; read the A fragments of slice s+1 (slice 0 of step
+  //            kt+1 from the new buffer at s = 3, dequantized from B(kt+1)); MFMAs of slice s on
+  //            the fragments read one slice earlier;
+  //   slice 0: also write A(kt+1) into the next buffer;
+  //   slice 1: then wait for the LDS writes, barrier, and load A(kt+1+PD) into the freed A set;
+  //   after slice 3: load B(kt+PD) into the freed B set.
+  auto step = [&](int kt, int rb, int wb, auto bsc) {
+    constexpr int bs = decltype(bsc)::value;     // kt % PD
+    constexpr int as = (bs + 1) % PD;            // A(kt+1) and B(kt+1) live in set (kt+1) % PD
+    const uint16_t* Ar = lds + rb * A_EL;
+    uint16_t* Aw = lds + wb * A_EL;
+    float sv[2], nz[2];
+    scale_pair(bsc, sv, nz);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      // operands of the next slice (slice 0 of step kt+1 at s = 3) into the other register pair,
+      // while this slice's MFMAs read the pair filled one slice earlier
+      if (s < 3) {
+        if ((s & 1) == 0) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) bq[1][j] = b_frag(bsc, s + 1, j, sv[j], nz[j]);
+          read_frags(std::integral_constant<int, 1>{}, Ar, s + 1);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) bq[0][j] = b_frag(bsc, s + 1, j, sv[j], nz[j]);
+          read_frags(std::integral_constant<int, 0>{}, Ar, s + 1);
+        }
+      } else {
+        float sv2[2], nz2[2];
+        scale_pair(std::integral_constant<int, as>{}, sv2, nz2);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) bq[0][j] = b_frag(std::integral_constant<int, as>{}, 0, j, sv2[j], nz2[j]);
+        read_frags(std::integral_constant<int, 0>{}, Aw, 0);
+      }
+      if ((s & 1) == 0) {
+        // FOLD, first slice of a group (even step): fold the previous group's sums into the
+        // total with its scale, then start the group's sums from zero
+        constexpr bool group_start = FOLD && bs % 2 == 0;
+#pragma unroll
+        for (int i = 0; i < IB; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            if (group_start && s == 0) {
+              if constexpr (FOLD) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) tot[i][j][r] = fmaf(sfold[j], acc[i][j][r], tot[i][j][r]);
+              }
+              acc[i][j] = mfma32x32x16(af[0][i], bq[0][j], f32x16_t{});
+            } else {
+              acc[i][j] = mfma32x32x16(af[0][i], bq[0][j], acc[i][j]);
+            }
+          }
+        if (group_start && s == 0) {
+          sfold[0] = sv[0];
+          sfold[1] = sv[1];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < IB; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[1][i], bq[1][j], acc[i][j]);
+      }
+      if (s == 0) store_a(std::integral_constant<int, as>{}, Aw);
+      if (s == 1) {
+        lds_barrier();
+        load_a(std::integral_constant<int, as>{}, kt + 1 + PD);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // one MFMA, then a few VALU and one LDS read, repeated: keeps the dequant and the fragment
+      // reads between MFMAs instead of bunched before them
+#pragma unroll
+      for (int k = 0; k < 2 * IB; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, BITS == 8 ? RB_VALU_PER_MFMA_8 : RB_VALU_PER_MFMA_4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(bsc, kt + PD);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue, in the loop's steady-state load order (A(kt+1), B(kt), ..., A(kt+PD), B(kt+PD-1)
+  // outstanding at the top of step kt) so the waits the compiler places at the loop head match
+  // the loop's: A(0) is loaded first, then A(1), B(0), ..., with A(0) written to buffer 0 just
+  // before A(PD) takes its register set.
+  load_a(std::integral_constant<int, 0>{}, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  auto prologue_pair = [&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if constexpr (j + 1 == PD) {
+      store_a(std::integral_constant<int, 0>{}, lds);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    load_a(std::integral_constant<int, (j + 1) % PD>{}, j + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(jc, j);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  prologue_pair(std::integral_constant<int, 0>{});
+  prologue_pair(std::integral_constant<int, 1>{});
+  if constexpr (PD > 2) prologue_pair(std::integral_constant<int, 2>{});
+  if constexpr (PD > 3) prologue_pair(std::integral_constant<int, 3>{});
+  lds_barrier();
+  read_frags(std::integral_constant<int, 0>{}, lds, 0);
+  {
+    float sv0[2], nz0[2];
+    scale_pair(std::integral_constant<int, 0>{}, sv0, nz0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) bq[0][j] = b_frag(std::integral_constant<int, 0>{}, 0, j, sv0[j], nz0[j]);
+  }
+
+  // main loop unrolled by PD so every register set index is a compile-time constant
+  int rb = 0;
+  int kt = 0;
+  auto run_step = [&](auto uc) {
+    const int wb = rb == 2 ? 0 : rb + 1;
+    step(kt + decltype(uc)::value, rb, wb, uc);
+    rb = wb;
+  };
+  for (; kt + PD - 1 < KT; kt += PD) {
+    run_step(std::integral_constant<int, 0>{});
+    run_step(std::integral_constant<int, 1>{});
+    if constexpr (PD > 2) run_step(std::integral_constant<int, 2>{});
+    if constexpr (PD > 3) run_step(std::integral_constant<int, 3>{});
+  }
+  if (kt < KT) run_step(std::integral_constant<int, 0>{});
+  if constexpr (PD > 2)
+    if (kt + 1 < KT) run_step(std::integral_constant<int, 1>{});
+  if constexpr (PD > 3)
+    if (kt + 2 < KT) run_step(std::integral_constant<int, 2>{});
+
+  if constexpr (FOLD) {
+    // the last group's fold, then the -s_g (128 + z_g) sum_{k in g} x_k terms: one fp32
+    // 32x32x2 MFMA per pair of groups, A = the rows' group sums (lane: row c, group g0 + h),
+    // B = -s (128 + z) of the lane's column and group g0 + h
+#pragma unroll
+    for (int i = 0; i < IB; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tot[i][j][r] = fmaf(sfold[j], acc[i][j][r], tot[i][j][r]);
+    const int ng = a.K >> a.gsh;
+    const float* rsr[IB];
+#pragma unroll
+    for (int i = 0; i < IB; ++i) {
+      const int row = 32 * i + c;
+      const int p = prow0 + (row < cnt ? row : cnt - 1);
+      const int rid = MOE == 3 ? p : a.perm[p] / a.k;
+      rsr[i] = a.rs + (int64_t)rid * a.rs_stride;
+    }
+    for (int g0 = 0; g0 < ng; g0 += 2) {
+      const int g = g0 + h;
+      float av[IB], bv[2];
+#pragma unroll
+      for (int i = 0; i < IB; ++i) av[i] = g < a.rs_groups ? rsr[i][g] : 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t pr = g < ng ? SZ[g * BN + 64 * wave + 32 * j + c] : 0u;
+        bv[j] = -(128.f + __uint_as_float(pr & 0xffff0000u)) * __uint_as_float(pr << 16);
+      }
+#pragma unroll
+      for (int i = 0; i < IB; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) tot[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], tot[i][j], 0, 0, 0);
+    }
+  }
+  // the finished sums of block (i, j)
+  auto res = [&](int i, int j) -> const f32x16_t& {
+    if constexpr (FOLD) return tot[i][j];
+    else return acc[i][j];
+  };
+
+  // ---- epilogue: D lane l holds column l % 32, element r at row 8 (r / 4) + 4 (l / 32) + r % 4 ---
+  if constexpr (MOE != 0) {
+    auto bias_at = [&](int row) -> float {
+      return a.bias != nullptr ? rb_bias(a.bias, a.bdt, (int64_t)e * a.sbe + row) : 0.f;
+    };
+    if constexpr (MOE == 1 || MOE == 2) {
+      // h through LDS as [BM][HS] bf16 (rows padded against bank conflicts): the tile's 128 h
+      // columns then leave as 16-byte row segments, and their sum per row (the bf16 values down
+      // reads) is the group sum hrs[p][tn] of down's folded form
+      constexpr int HS = 136;
+      uint16_t* Ht = lds;              // the activation buffers: every wave is past its last step
+      __syncthreads();
+      if constexpr (MOE == 1) {
+        const int hc = 32 * wave + c;                   // tile-local h column; I % 128 == 0
+        const int g = tn * (32 * NW) + hc;
+        const float bg = bias_at(g), bu = bias_at(a.I + g);
+#pragma unroll
+        for (int i = 0; i < IB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+            const float gv = res(i, 0)[r] + bg, uv = res(i, 1)[r] + bu;
+            Ht[m * HS + hc] = (uint16_t)cvt_pk_bf16(gv / (1.f + __expf(-gv)) * uv, 0.f);
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + 64 * wave + 32 * j + c;    // even lanes: gate rows, odd: the up rows
+          const int hc = (64 * wave + 32 * j + c) >> 1;
+          const float bg = n < a.N ? bias_at(n) : 0.f, bu = n + 1 < a.N ? bias_at(n + 1) : 0.f;
+#pragma unroll
+          for (int i = 0; i < IB; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float v = res(i, j)[r];
+              const float up = __shfl_xor(v, 1, 64);
+              const int m = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+              if ((c & 1) == 0) {
+                float gv = v + bg, uv = up + bu;
+                gv = gv > a.limit ? a.limit : gv;
+                uv = uv > a.limit ? a.limit : (uv < -a.limit ? -a.limit : uv);
+                const float hv = (uv + 1.f) * (gv / (1.f + __expf(-a.alpha * gv)));
+                Ht[m * HS + hc] = n < a.N ? (uint16_t)cvt_pk_bf16(hv, 0.f) : (uint16_t)0;   // past I: zero
+              }
+            }
+        }
+      }
+      __syncthreads();
+      // four threads per row, 32 columns (64 bytes) each
+      const int q = tid & 3;
+#pragma unroll
+      for (int row = tid >> 2; row < BM; row += NTHR / 4) {
+        u32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = *(const u32x4_t*)(Ht + row * HS + 32 * q + 8 * u);
+        float sum = 0.f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[u][d] << 16) + __uint_as_float(v[u][d] & 0xffff0000u);
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if (row < cnt) {
+          uint16_t* dst = a.y + (int64_t)(prow0 + row) * a.sym + tn * 128 + 32 * q;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) *(u32x4_t*)(dst + 8 * u) = v[u];
+          if (a.hrs != nullptr && q == 0) a.hrs[(int64_t)(prow0 + row) * a.hrs_stride + tn] = sum;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + 64 * wave + 32 * j + c;
+        if (n >= a.N) continue;
+        const float bn = bias_at(n);
+#pragma unroll
+        for (int i = 0; i < IB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (m < cnt) a.yr[(int64_t)a.perm[prow0 + m] * a.N + n] = res(i, j)[r] + bn;
+          }
+      }
+    }
+    return;
+  }
+  if (a.splits > 1) {
+    float* pbase = a.part + (size_t)split * a.M * a.N;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 64 * wave + 32 * j + c;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int i = 0; i < IB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (m < a.M) pbase[(size_t)m * a.N + n] = acc[i][j][r];
+        }
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + 64 * wave + 32 * j + c;
+    if (n >= a.N) continue;
+    float sc8 = 1.f;
+    if constexpr (BITS == 8) sc8 = load_as_f32<SDT>(a.sc, (int64_t)n * a.ssn);
+#pragma unroll
+    for (int i = 0; i < IB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (m < a.M) a.y[(int64_t)m * a.sym + n] = (uint16_t)cvt_pk_bf16(acc[i][j][r] * sc8, 0.f);
+      }
+  }
+}
+
+}  // namespace
+}  // namespace imq

@@ -314,6 +314,17 @@ def test_gptoss_grouped_gemm_path(dev, E, H, I, k, T, bias_std, pad):
     _run_gptoss(dev, E=E, H=H, I=I, k=k, T=T, seed=170 + T, bias_std=bias_std, pad_to_256=pad)
 
 
+@pytest.mark.parametrize("gpt,E,H,I,k,T", [(True, 4, 2880, 2880, 2, 64), (False, 4, 640, 384, 2, 64)])
+def test_grouped_gemm_k_pad_128(dev, gpt, E, H, I, k, T):
+    """K_pad a multiple of 128 but not of the line kernels' 256 (gpt-oss-20b's 2944, a 640 x 384
+    SiLU layer): the grouped register-B GEMM; at I = 2880 the last gate_up tile holds half a
+    group of h columns, the rest of that group reading as zeros in down's group sums."""
+    if gpt:
+        _run_gptoss(dev, E=E, H=H, I=I, k=k, T=T, seed=185)
+    else:
+        _run(dev, E=E, H=H, I=I, k=k, T=T, seed=186)
+
+
 @pytest.mark.parametrize("E,H,I,k,T", [(4, 4608, 256, 2, 24), (4, 512, 4352, 2, 24)])
 def test_moe_grouped_gemm_wide_k(dev, E, H, I, k, T):
     """K beyond the line kernels' 4096 (gate_up K 4608, down K 4352): prefill rows take the grouped
