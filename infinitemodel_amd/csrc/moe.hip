@@ -30,8 +30,8 @@ int moe_rb(int mode, int ib, const uint16_t* x, int64_t sxm, int64_t xrows, int6
            int64_t sqe, int64_t sqn, const void* sc, const void* zr, int64_t sse, int64_t ssn, int sdt, int64_t N,
            int64_t I, const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off,
            const int32_t* perm, int k, const void* bias, int64_t sbe, int bdt, float alpha, float limit,
-           uint16_t* h, int64_t hs, float* yr, const float* rs, int rs_stride, int rs_groups, float* hrs,
-           int hrs_stride, hipStream_t st, bool check_only);
+           uint16_t* h, int64_t hs, float* yr, bool yr_bf16, const float* rs, int rs_stride, int rs_groups,
+           float* hrs, int hrs_stride, hipStream_t st, bool check_only);
 bool moe_rb_folded();
 }  // namespace imq
 using imq::moe_gemm_bm;
@@ -180,12 +180,30 @@ constexpr int kMoeLine = 256;
 
 // mtl (optional): the grouped GEMM's row blocks, mtl[0] = their number, then (expert, first sorted
 // row) pairs from mtl[2], bm sorted rows per block -- at most ceil(B / bm) + (hit experts) blocks.
+// Workgroups past the first (rs != nullptr): rs[t][g] = the fp32 sum of row t of x over columns
+// [128 g, 128 g + 128), g < ng -- one wave per (row, group), a fixed-order wave reduction; they
+// run beside the sort in the same launch.
 __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restrict__ idx, int B, int E,
                                                         int32_t* __restrict__ off, int32_t* __restrict__ perm,
                                                         int32_t* __restrict__ hit, int32_t* __restrict__ mtl,
-                                                        int bm) {
+                                                        int bm, const uint16_t* __restrict__ x = nullptr,
+                                                        int64_t sxm = 0, int64_t T = 0, int ng = 0,
+                                                        float* __restrict__ rs = nullptr) {
   extern __shared__ int32_t cnt[];     // [E]: counts, then scatter cursors
   const int tid = threadIdx.x, nt = blockDim.x;
+  if (blockIdx.x > 0) {
+    const int64_t wid = (int64_t)(blockIdx.x - 1) * (nt >> 6) + (tid >> 6);
+    const int lane = tid & 63;
+    if (rs == nullptr || wid >= T * ng) return;
+    const int64_t t = wid / ng;
+    const int g = (int)(wid - t * ng);
+    const uint32_t v = *(const uint32_t*)(x + t * sxm + 128 * g + 2 * lane);
+    float sum = __uint_as_float(v << 16) + __uint_as_float(v & 0xffff0000u);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if (lane == 0) rs[t * ng + g] = sum;
+    return;
+  }
   for (int e = tid; e < E; e += nt) cnt[e] = 0;
   __syncthreads();
   int ec[4];                           // the first 4 of this thread's ids stay in registers
@@ -504,7 +522,44 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   }
 }
 
-// out[t][n .. n+7] = bf16(sum_j w[t][j] * yr[t*k + j][n .. n+7]), slot order; H % 8 == 0.
+// out[t][n .. n+7] = bf16(sum_j w[t][j] * yr[t*k + j][n .. n+7]) for bf16 rows yr (the register-B
+// grouped down's output), slot order, fp32 sums; H % 8 == 0. 16-byte loads, 8 slots in flight.
+__global__ __launch_bounds__(256) void moe_combine_bf16_kernel(const uint16_t* __restrict__ yr,
+                                                               const uint16_t* __restrict__ w, int64_t T, int64_t k,
+                                                               int64_t H, uint16_t* __restrict__ out, int64_t so) {
+  const int64_t H8 = H / 8;
+  const int64_t total = T * H8;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t tok = t / H8;
+    const int64_t n = 8 * (t - tok * H8);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int64_t j0 = 0; j0 < k; j0 += 8) {
+      u32x4_t v[8];
+      float wj[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t jj = j0 + j < k ? j0 + j : k - 1;
+        v[j] = *(const u32x4_t*)(yr + (tok * k + jj) * H + n);
+        wj[j] = bf16_bits_to_f32(w[tok * k + jj]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j0 + j < k)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[2 * q] = fmaf(wj[j], __uint_as_float(v[j][q] << 16), acc[2 * q]);
+            acc[2 * q + 1] = fmaf(wj[j], __uint_as_float(v[j][q] & 0xffff0000u), acc[2 * q + 1]);
+          }
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = cvt_pk_bf16(acc[2 * q], acc[2 * q + 1]);
+    *(u32x4_t*)(out + tok * so + n) = o;
+  }
+}
+
+// out[t][n .. n+3] = bf16(sum_j w[t][j] * yr[t*k + j][n .. n+3]), slot order, fp32 sums; H % 4 == 0.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ yr, const uint16_t* __restrict__ w,
                                                           int64_t T, int64_t k, int64_t H,
                                                           uint16_t* __restrict__ out, int64_t so) {
@@ -1046,22 +1101,6 @@ struct MoeWs {
   int64_t gu, h, z, off, perm, hit, rsx, rsh, total, hw;
 };
 
-// rs[t][g] = the fp32 sum of row t's bf16 values over columns [128 g, 128 g + 128), g < ng: one
-// wave per (row, group), a fixed-order wave reduction.
-__global__ __launch_bounds__(256) void moe_rowsum_kernel(const uint16_t* __restrict__ x, int64_t sxm, int64_t T,
-                                                         int ng, float* __restrict__ rs) {
-  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (wid >= T * ng) return;
-  const int64_t t = wid / ng;
-  const int g = (int)(wid - t * ng);
-  const uint32_t v = *(const uint32_t*)(x + t * sxm + 128 * g + 2 * lane);
-  float sum = __uint_as_float(v << 16) + __uint_as_float(v & 0xffff0000u);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-  if (lane == 0) rs[t * ng + g] = sum;
-}
-
 MoeWs moe_ws(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t G) {
   const int64_t B = T * top_k;
   const int64_t I_pad = imq_cdiv(I, G) * G;
@@ -1160,7 +1199,7 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream
     if (rb)
       return moe_rb(gmode, ib, c.hidden, c.hs, c.T, c.gK, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
                     2 * c.I, c.I, mtl + 2, mtl, max_mt, off, perm, (int)c.k, c.gb, c.gbe, c.bdt, c.alpha, c.limit, h,
-                    L.hw, nullptr, rsx, ngx, ngx, rsh, ngh, st, check);
+                    L.hw, nullptr, false, rsx, ngx, ngx, rsh, ngh, st, check);
     return moe_gemm_w4(gmode, c.hidden, c.hs, c.T, c.gK, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
                        2 * c.I, c.I, mtl + 2, mtl, max_mt, off, perm, (int)c.k, c.gb, c.gbe, c.bdt, c.alpha, c.limit,
                        h, L.hw, nullptr, st, check);
@@ -1168,8 +1207,8 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream
   auto down = [&](bool check) {
     if (rb)
       return moe_rb(3, ib, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2,
-                    mtl, max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, rsh, ngh, ngh,
-                    nullptr, 0, st, check);
+                    mtl, max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, true, rsh, ngh,
+                    ngh, nullptr, 0, st, check);
     return moe_gemm_w4(3, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2, mtl,
                        max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, st, check);
   };
@@ -1186,12 +1225,13 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream
   }
   if ((2 + 2 * max_mt) * 4 > L.h - L.gu) return IMQ_ERR_UNSUPPORTED;   // the list lives in gu's room
   int rc;
-  if (rb && moe_rb_folded()) {
-    const int64_t waves = c.T * ngx;
-    moe_rowsum_kernel<<<dim3((unsigned)imq_cdiv(waves, 4)), dim3(256), 0, st>>>(c.hidden, c.hs, c.T, ngx, rsx);
-    IMQ_LAUNCH_CHECK();
-  }
-  moe_sort_kernel<<<dim3(1), dim3(1024), (size_t)c.E * 4, st>>>(c.idx, (int)B, (int)c.E, off, perm, hit, mtl, bm);
+  // the sort, and beside it (folded form) the hidden rows' group sums: 16 (row, group) waves per
+  // extra workgroup
+  const bool sums = rb && moe_rb_folded();
+  const int64_t rs_blocks = sums ? imq_cdiv(c.T * ngx, 16) : 0;
+  if (rs_blocks > 0x7ffffffe) return IMQ_ERR_UNSUPPORTED;
+  moe_sort_kernel<<<dim3((unsigned)(1 + rs_blocks)), dim3(1024), (size_t)c.E * 4, st>>>(
+      c.idx, (int)B, (int)c.E, off, perm, hit, mtl, bm, c.hidden, c.hs, c.T, ngx, sums ? rsx : nullptr);
   IMQ_LAUNCH_CHECK();
   rc = gate_up(false);
   if (rc != IMQ_OK) return rc;
@@ -1205,7 +1245,14 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream
   if (rc != IMQ_OK) return rc;
   const int64_t total = c.T * (c.H / 4);
   const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
-  moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, c.topk_w, c.T, c.k, c.H, c.out, c.os);
+  if (rb) {
+    const int64_t t8 = c.T * (c.H / 8);
+    const int64_t b8 = imq_cdiv(t8, 256) < 4096 ? imq_cdiv(t8, 256) : 4096;
+    moe_combine_bf16_kernel<<<dim3((unsigned)b8), dim3(256), 0, st>>>((const uint16_t*)yr, c.topk_w, c.T, c.k, c.H,
+                                                                       c.out, c.os);
+  } else {
+    moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(yr, c.topk_w, c.T, c.k, c.H, c.out, c.os);
+  }
   IMQ_LAUNCH_CHECK();
   return IMQ_OK;
 }

@@ -43,6 +43,13 @@ constexpr int RB_BK = 64;
 #ifndef RB_VALU_PER_MFMA_8
 #define RB_VALU_PER_MFMA_8 3
 #endif
+#ifndef RB_VALU_PER_MFMA_FOLD
+#define RB_VALU_PER_MFMA_FOLD 4
+#endif
+// FOLD: 1 unpacks a step's four B slices at its top (step_fold), 0 one slice ahead (step)
+#ifndef RB_FOLD_EARLY_UNPACK
+#define RB_FOLD_EARLY_UNPACK 1
+#endif
 
 struct RbArgs {
   const uint16_t* x;
@@ -74,6 +81,7 @@ struct RbArgs {
   int bdt = 0;
   float alpha = 0.f, limit = 0.f;     // gpt-oss activation
   float* yr = nullptr;                // MOE 3: fp32 rows [B][N] in routed order
+  uint16_t* yrb = nullptr;            // MOE 3, instead: bf16 rows [B][N] in routed order
   // scale-folded form (FOLD): per-row sums of the activations over each group of 128 K,
   // rs[row][g] (row = token for gate_up, sorted position for down), groups >= rs_groups read 0;
   // gate_up also writes the group sums of its bf16 h rows into hrs[p][tn] (down's rs)
@@ -228,34 +236,108 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   // of two strided global loads per column block -- those loads touch a separate cache line per
   // lane and, issued every step, kept the texture unit busier than the weight stream itself.
   uint32_t* SZ = (uint32_t*)(lds + 3 * A_EL);
-  if constexpr (MOE != 0) {
-    // batches of 8 elements per thread, all loads of a batch issued before any is consumed;
-    // consecutive threads take consecutive groups of one column (one scale row segment)
-    constexpr int SB = 8;
-    const int ng = a.K >> a.gsh, total = ng * BN;
-    for (int base = 0; base < total; base += SB * NTHR) {
-      uint32_t sv[SB], zv[SB];
-      int at[SB];
+  // FOLD's step unpacks all of a step's weights at its top (step_fold); else one slice ahead
+  constexpr bool EARLY = FOLD && RB_FOLD_EARLY_UNPACK;
+  // The MoE forms' staging into LDS (the caller places the barrier after it).
+  auto stage_moe = [&]() {
+    if constexpr (MOE != 0) {
+      // FOLD: the block rows' group sums too, as [group][BM rows] floats after the pairs -- read by
+      // the final correction's MFMA operands (lane: row c of block i, group g0 + h)
+      if constexpr (FOLD) {
+        float* RS = (float*)(SZ + (a.K >> a.gsh) * BN);
+        const int ng = a.K >> a.gsh, total = ng * BM;
+        for (int base = 0; base < total; base += 8 * NTHR) {
+          float v[8];
+          int at[8];
 #pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        const int idx = base + u * NTHR + tid;
-        const int id = idx < total ? idx : total - 1;
-        const int tc = id / ng, g = id - tc * ng;
-        const int w_ = tc >> 6, j_ = (tc >> 5) & 1, c_ = tc & 31;
-        int n = MOE == 1 ? (j_ ? a.I : 0) + tn * (32 * NW) + 32 * w_ + c_ : n0 + tc;
-        n = n < a.N ? n : a.N - 1;
-        const int64_t gb = (int64_t)e * a.sse + (int64_t)g * a.ssg;
-        sv[u] = load_raw_bits<SDT>(a.sc, gb + (int64_t)n * a.ssn);
-        zv[u] = load_raw_bits<ZDT>(a.zr, gb + (int64_t)n * a.szn);
-        at[u] = idx < total ? g * BN + tc : -1;
+          for (int u = 0; u < 8; ++u) {
+            const int idx = base + u * NTHR + tid;
+            const int id = idx < total ? idx : total - 1;
+            const int row = id / ng, g = id - row * ng;   // consecutive threads: consecutive groups of a row
+            const int p = prow0 + (row < cnt ? row : cnt - 1);
+            const int rid = MOE == 3 ? p : a.perm[p] / a.k;
+            v[u] = g < a.rs_groups ? a.rs[(int64_t)rid * a.rs_stride + g] : 0.f;
+            at[u] = idx < total ? g * BM + row : -1;
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (at[u] >= 0) RS[at[u]] = v[u];
+        }
       }
+      // scale / zero pairs: with 16-byte aligned scale rows (unit group stride), one 16-byte load
+      // covers 16 / sizeof(scale) groups of a column (the row's allocated stride covers the last
+      // chunk); else element by element
+      constexpr int ES = SDT == IMQ_DT_FP32 ? 4 : 2;
+      constexpr int VG = 16 / ES;
+      const int ngs = a.K >> a.gsh;
+      const bool vec = a.ssg == 1 && a.szg == 1 && ((a.ssn * ES) & 15) == 0 && ((a.szn * ES) & 15) == 0 &&
+                       ((a.sse * ES) & 15) == 0 && ((((uintptr_t)a.sc) | ((uintptr_t)a.zr)) & 15) == 0;
+      if (vec) {
+        const int nch = (ngs + VG - 1) / VG, items = BN * nch;
+        for (int base = 0; base < items; base += 4 * NTHR) {
+          u32x4_t sv4[4], zv4[4];
+          int tcs[4], g0s[4];
 #pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        const float s_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<SDT>(sv[u]));
-        const float z_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<ZDT>(zv[u]));
-        if (at[u] >= 0) SZ[at[u]] = (__float_as_uint(s_) >> 16) | (__float_as_uint(z_) & 0xffff0000u);
+          for (int u = 0; u < 4; ++u) {
+            const int it = base + u * NTHR + tid;
+            const int id = it < items ? it : items - 1;
+            const int tc = id / nch, ch = id - tc * nch;
+            const int w_ = tc >> 6, j_ = (tc >> 5) & 1, c_ = tc & 31;
+            int n = MOE == 1 ? (j_ ? a.I : 0) + tn * (32 * NW) + 32 * w_ + c_ : n0 + tc;
+            n = n < a.N ? n : a.N - 1;
+            const int64_t eb = (int64_t)e * a.sse + (int64_t)ch * VG;
+            sv4[u] = *(const u32x4_t*)((const char*)a.sc + (eb + (int64_t)n * a.ssn) * ES);
+            zv4[u] = *(const u32x4_t*)((const char*)a.zr + (eb + (int64_t)n * a.szn) * ES);
+            tcs[u] = it < items ? tc : -1;
+            g0s[u] = ch * VG;
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int v = 0; v < VG; ++v) {
+              const uint32_t sraw = ES == 4 ? sv4[u][v] : ((sv4[u][v >> 1] >> (16 * (v & 1))) & 0xffffu);
+              const uint32_t zraw = ES == 4 ? zv4[u][v] : ((zv4[u][v >> 1] >> (16 * (v & 1))) & 0xffffu);
+              const float s_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<SDT>(sraw));
+              const float z_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<ZDT>(zraw));
+              const int g = g0s[u] + v;
+              if (tcs[u] >= 0 && g < ngs)
+                SZ[g * BN + tcs[u]] = (__float_as_uint(s_) >> 16) | (__float_as_uint(z_) & 0xffff0000u);
+            }
+          }
+        }
+        return;
+      }
+      // batches of 16 elements per thread, all loads of a batch issued before any is consumed;
+      // consecutive threads take consecutive groups of one column (one scale row segment)
+      constexpr int SB = 16;
+      const int ng = a.K >> a.gsh, total = ng * BN;
+      for (int base = 0; base < total; base += SB * NTHR) {
+        uint32_t sv[SB], zv[SB];
+        int at[SB];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const int idx = base + u * NTHR + tid;
+          const int id = idx < total ? idx : total - 1;
+          const int tc = id / ng, g = id - tc * ng;
+          const int w_ = tc >> 6, j_ = (tc >> 5) & 1, c_ = tc & 31;
+          int n = MOE == 1 ? (j_ ? a.I : 0) + tn * (32 * NW) + 32 * w_ + c_ : n0 + tc;
+          n = n < a.N ? n : a.N - 1;
+          const int64_t gb = (int64_t)e * a.sse + (int64_t)g * a.ssg;
+          sv[u] = load_raw_bits<SDT>(a.sc, gb + (int64_t)n * a.ssn);
+          zv[u] = load_raw_bits<ZDT>(a.zr, gb + (int64_t)n * a.szn);
+          at[u] = idx < total ? g * BN + tc : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const float s_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<SDT>(sv[u]));
+          const float z_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<ZDT>(zv[u]));
+          if (at[u] >= 0) SZ[at[u]] = (__float_as_uint(s_) >> 16) | (__float_as_uint(z_) & 0xffff0000u);
+        }
       }
     }
+  };
+  if constexpr (MOE != 0 && !EARLY) {
+    stage_moe();
     __syncthreads();   // the prologue's weight-set loads read pairs other threads staged
   }
 
@@ -279,14 +361,21 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
       for (int v = 0; v < QV; ++v) qr[set][j][v] = *(const u32x4_t*)(qb[j] + kt * (BK * BITS / 8) + 16 * v);
-      if constexpr (MOE != 0) {
-        const int g = (kt * BK + 32 * h) >> a.gsh;
-        sr[set][j] = SZ[g * BN + 64 * wave + 32 * j + c];
-      } else if constexpr (BITS != 8) {
+      if constexpr (MOE == 0 && BITS != 8) {
         const int g = (kt * BK + 32 * h) >> a.gsh;
         sr[set][j] = load_raw_bits<SDT>(a.sc, sb[j] + (int64_t)g * a.ssg);
         zr[set][j] = load_raw_bits<ZDT>(a.zr, zb[j] + (int64_t)g * a.szg);
       }
+    }
+  };
+  // MoE forms: the scale / zero pair of a weight set, from the staged LDS copy
+  auto load_s = [&](auto setc, int ktl) {
+    if constexpr (MOE != 0) {
+      constexpr int set = decltype(setc)::value;
+      const int kt = kt0 + (ktl < KT ? ktl : KT - 1);
+      const int g = (kt * BK + 32 * h) >> a.gsh;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) sr[set][j] = SZ[g * BN + 64 * wave + 32 * j + c];
     }
   };
   auto store_a = [&](auto setc, uint16_t* A) {
@@ -430,12 +519,79 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
 #pragma unroll
       for (int k = 0; k < 2 * IB; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, BITS == 8 ? RB_VALU_PER_MFMA_8 : RB_VALU_PER_MFMA_4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, FOLD ? RB_VALU_PER_MFMA_FOLD : BITS == 8 ? RB_VALU_PER_MFMA_8 : RB_VALU_PER_MFMA_4, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
     load_b(bsc, kt + PD);
+    load_s(bsc, kt + PD);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // FOLD's step (PD 2). The magic unpack is cheap, so all four slices of B(kt) are unpacked at
+  // the top of the step and B(kt+2) is issued at once into the freed register set: a weight load
+  // has two full steps to arrive (the dequantizing step above unpacks the next step's first
+  // slice in its last one, so B(kt+1) must land within the step it was issued after). At the
+  // first slice of a group (even step) the previous group's sums are folded into the total with
+  // its scale and the group's sums restart from zero.
+  bf16x8_t bq4[FOLD ? 4 : 1][2];
+  auto step_fold = [&](int kt, int rb, int wb, auto bsc) {
+    constexpr int bs = decltype(bsc)::value;     // kt % 2
+    constexpr int as = (bs + 1) % PD;
+    constexpr bool group_start = bs % 2 == 0;
+    const uint16_t* Ar = lds + rb * A_EL;
+    uint16_t* Aw = lds + wb * A_EL;
+    float sv[2], nz[2];
+    scale_pair(bsc, sv, nz);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bq4[FOLD ? s : 0][j] = b_frag(bsc, s, j, sv[j], nz[j]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(bsc, kt + PD);
+    load_s(bsc, kt + PD);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s < 3) {
+        if ((s & 1) == 0) read_frags(std::integral_constant<int, 1>{}, Ar, s + 1);
+        else read_frags(std::integral_constant<int, 0>{}, Ar, s + 1);
+      } else {
+        read_frags(std::integral_constant<int, 0>{}, Aw, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < IB; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const bf16x8_t av = (s & 1) ? af[1][i] : af[0][i];
+          if (group_start && s == 0) {
+            if constexpr (FOLD) {
+#pragma unroll
+              for (int r = 0; r < 16; ++r) tot[i][j][r] = fmaf(sfold[j], acc[i][j][r], tot[i][j][r]);
+            }
+            acc[i][j] = mfma32x32x16(av, bq4[FOLD ? s : 0][j], f32x16_t{});
+          } else {
+            acc[i][j] = mfma32x32x16(av, bq4[FOLD ? s : 0][j], acc[i][j]);
+          }
+        }
+      if (group_start && s == 0) {
+        sfold[0] = sv[0];
+        sfold[1] = sv[1];
+      }
+      if (s == 0) store_a(std::integral_constant<int, as>{}, Aw);
+      if (s == 1) {
+        lds_barrier();
+        load_a(std::integral_constant<int, as>{}, kt + 1 + PD);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int k = 0; k < 2 * IB; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -443,30 +599,56 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   // outstanding at the top of step kt) so the waits the compiler places at the loop head match
   // the loop's: A(0) is loaded first, then A(1), B(0), ..., with A(0) written to buffer 0 just
   // before A(PD) takes its register set.
-  load_a(std::integral_constant<int, 0>{}, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  auto prologue_pair = [&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    if constexpr (j + 1 == PD) {
-      store_a(std::integral_constant<int, 0>{}, lds);
+  if constexpr (EARLY) {
+    // the fold step's steady-state order: B(kt), A(kt+1), B(kt+1), A(kt+2) outstanding at the
+    // top of step kt. The staging's loads go out right after the first weight and activation
+    // loads, so their latencies overlap.
+    static_assert(PD == 2, "the fold step keeps two register sets");
+    load_a(std::integral_constant<int, 0>{}, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(std::integral_constant<int, 0>{}, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(std::integral_constant<int, 1>{}, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(std::integral_constant<int, 1>{}, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_moe();
+    __syncthreads();
+    load_s(std::integral_constant<int, 0>{}, 0);
+    load_s(std::integral_constant<int, 1>{}, 1);
+    store_a(std::integral_constant<int, 0>{}, lds);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(std::integral_constant<int, 0>{}, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    read_frags(std::integral_constant<int, 0>{}, lds, 0);
+  } else {
+    load_a(std::integral_constant<int, 0>{}, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    auto prologue_pair = [&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      if constexpr (j + 1 == PD) {
+        store_a(std::integral_constant<int, 0>{}, lds);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      load_a(std::integral_constant<int, (j + 1) % PD>{}, j + 1);
       __builtin_amdgcn_sched_barrier(0);
-    }
-    load_a(std::integral_constant<int, (j + 1) % PD>{}, j + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    load_b(jc, j);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  prologue_pair(std::integral_constant<int, 0>{});
-  prologue_pair(std::integral_constant<int, 1>{});
-  if constexpr (PD > 2) prologue_pair(std::integral_constant<int, 2>{});
-  if constexpr (PD > 3) prologue_pair(std::integral_constant<int, 3>{});
-  lds_barrier();
-  read_frags(std::integral_constant<int, 0>{}, lds, 0);
-  {
-    float sv0[2], nz0[2];
-    scale_pair(std::integral_constant<int, 0>{}, sv0, nz0);
+      load_b(jc, j);
+      load_s(jc, j);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    prologue_pair(std::integral_constant<int, 0>{});
+    prologue_pair(std::integral_constant<int, 1>{});
+    if constexpr (PD > 2) prologue_pair(std::integral_constant<int, 2>{});
+    if constexpr (PD > 3) prologue_pair(std::integral_constant<int, 3>{});
+    lds_barrier();
+    read_frags(std::integral_constant<int, 0>{}, lds, 0);
+    {
+      float sv0[2], nz0[2];
+      scale_pair(std::integral_constant<int, 0>{}, sv0, nz0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) bq[0][j] = b_frag(std::integral_constant<int, 0>{}, 0, j, sv0[j], nz0[j]);
+      for (int j = 0; j < 2; ++j) bq[0][j] = b_frag(std::integral_constant<int, 0>{}, 0, j, sv0[j], nz0[j]);
+    }
   }
 
   // main loop unrolled by PD so every register set index is a compile-time constant
@@ -474,7 +656,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   int kt = 0;
   auto run_step = [&](auto uc) {
     const int wb = rb == 2 ? 0 : rb + 1;
-    step(kt + decltype(uc)::value, rb, wb, uc);
+    if constexpr (EARLY) step_fold(kt + decltype(uc)::value, rb, wb, uc);
+    else step(kt + decltype(uc)::value, rb, wb, uc);
     rb = wb;
   };
   for (; kt + PD - 1 < KT; kt += PD) {
@@ -500,19 +683,12 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) tot[i][j][r] = fmaf(sfold[j], acc[i][j][r], tot[i][j][r]);
     const int ng = a.K >> a.gsh;
-    const float* rsr[IB];
-#pragma unroll
-    for (int i = 0; i < IB; ++i) {
-      const int row = 32 * i + c;
-      const int p = prow0 + (row < cnt ? row : cnt - 1);
-      const int rid = MOE == 3 ? p : a.perm[p] / a.k;
-      rsr[i] = a.rs + (int64_t)rid * a.rs_stride;
-    }
+    const float* RS = (const float*)(SZ + ng * BN);   // staged [group][BM rows] (zero past rs_groups)
     for (int g0 = 0; g0 < ng; g0 += 2) {
       const int g = g0 + h;
       float av[IB], bv[2];
 #pragma unroll
-      for (int i = 0; i < IB; ++i) av[i] = g < a.rs_groups ? rsr[i][g] : 0.f;
+      for (int i = 0; i < IB; ++i) av[i] = g < ng ? RS[g * BM + 32 * i + c] : 0.f;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const uint32_t pr = g < ng ? SZ[g * BN + 64 * wave + 32 * j + c] : 0u;
@@ -598,6 +774,31 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
           for (int u = 0; u < 4; ++u) *(u32x4_t*)(dst + 8 * u) = v[u];
           if (a.hrs != nullptr && q == 0) a.hrs[(int64_t)(prow0 + row) * a.hrs_stride + tn] = sum;
         }
+      }
+    } else if (a.yrb != nullptr) {
+      // bf16 rows through LDS as [BM][YS] (rows padded against bank conflicts): 16-byte row
+      // segments to the routed rows (N % 64 == 0, so a segment lies wholly inside or past N)
+      constexpr int YS = BN + 8;
+      uint16_t* Yt = lds;              // every wave is past its last step and the correction
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = 64 * wave + 32 * j + c;
+        const float bn = n0 + col < a.N ? bias_at(n0 + col) : 0.f;
+#pragma unroll
+        for (int i = 0; i < IB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+            Yt[m * YS + col] = (uint16_t)cvt_pk_bf16(res(i, j)[r] + bn, 0.f);
+          }
+      }
+      __syncthreads();
+      for (int it = tid; it < BM * (BN / 8); it += NTHR) {
+        const int row = it / (BN / 8), ch = it - row * (BN / 8);
+        const int n = n0 + 8 * ch;
+        if (row < cnt && n < a.N)
+          *(u32x4_t*)(a.yrb + (int64_t)a.perm[prow0 + row] * a.N + n) = *(const u32x4_t*)(Yt + row * YS + 8 * ch);
       }
     } else {
 #pragma unroll
