@@ -222,10 +222,10 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
     const int mt = blockIdx.x / a.tiles_n;
     tn = blockIdx.x - mt * a.tiles_n;
     if (mt >= *a.nmt) return;                       // uniform over the workgroup
-    e = a.mtl[2 * mt];
+    const int ec = a.mtl[2 * mt];                   // expert | rows of the block (<= BM) << 16
+    e = ec & 0xffff;
+    cnt = ec >> 16;
     prow0 = a.mtl[2 * mt + 1];
-    cnt = a.off[e + 1] - prow0;
-    cnt = cnt < BM ? cnt : BM;
     m0 = 0;
     n0 = tn * BN;
   }

@@ -178,8 +178,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 //   moe_combine_kernel out[t] = bf16(sum_j w[t, j] * yr[t*k + j]), slot order.
 constexpr int kMoeLine = 256;
 
-// mtl (optional): the grouped GEMM's row blocks, mtl[0] = their number, then (expert, first sorted
-// row) pairs from mtl[2], bm sorted rows per block -- at most ceil(B / bm) + (hit experts) blocks.
+// mtl (optional): the grouped GEMM's row blocks, mtl[0] = their number, then from mtl[2] one pair
+// per block: (expert | rows of the block << 16, first sorted row), bm sorted rows per block -- at
+// most ceil(B / bm) + (hit experts) blocks.
 // Workgroups past the first (rs != nullptr): rs[t][g] = the fp32 sum of row t of x over columns
 // [128 g, 128 g + 128), g < ng -- one wave per (row, group), a fixed-order wave reduction; they
 // run beside the sort in the same launch.
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
       if (c > 0) hit[hrun++] = e;
       if (mtl != nullptr)
         for (int r0 = 0; r0 < c; r0 += bm, ++brun) {
-          mtl[2 + 2 * brun] = e;
+          mtl[2 + 2 * brun] = e | ((c - r0 < bm ? c - r0 : bm) << 16);   // E <= 16384, bm <= 128
           mtl[3 + 2 * brun] = run + r0;
         }
       cnt[e] = run;

@@ -192,31 +192,33 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
     const int lid = x8 * q8 + (x8 < r8 ? x8 : r8) + (b >> 3);
     const int mt = lid / a.tiles_n;
     tn = lid - mt * a.tiles_n;
-    e = a.mtl[2 * mt];
+    const int ec = a.mtl[2 * mt];                   // expert | rows of the block (<= BM) << 16
+    e = ec & 0xffff;
+    cnt = ec >> 16;
     prow0 = a.mtl[2 * mt + 1];
-    cnt = a.off[e + 1] - prow0;
-    cnt = cnt < BM ? cnt : BM;
     n0 = tn * BN;
   }
 
-  // ---- activation load plan (32-bit offsets from the tile's first row) -------------------------
+  // ---- activation load plan (32-bit offsets from the tile's first row); the MoE forms gather
+  // rows through perm, so the folded form runs it after its first weight loads are out ------
   const uint16_t* xtile = a.x + (int64_t)m0 * a.sxm;
   int xo[XC], xl[XC];
+  auto plan_a = [&]() {
 #pragma unroll
-  for (int j = 0; j < XC; ++j) {
-    const int id = tid + NTHR * j;
-    const int row = id >> 3, ch = id & 7;
-    int r;
-    if constexpr (MOE == 0) {
-      r = m0 + row < a.M ? row : a.M - 1 - m0;
-    } else {
-      const int p = prow0 + (row < cnt ? row : cnt - 1);                // sorted position
-      r = MOE == 3 ? p : a.perm[p] / a.k;           // down reads h in sorted order, gate_up gathers
+    for (int j = 0; j < XC; ++j) {
+      const int id = tid + NTHR * j;
+      const int row = id >> 3, ch = id & 7;
+      int r;
+      if constexpr (MOE == 0) {
+        r = m0 + row < a.M ? row : a.M - 1 - m0;
+      } else {
+        const int p = prow0 + (row < cnt ? row : cnt - 1);                // sorted position
+        r = MOE == 3 ? p : a.perm[p] / a.k;           // down reads h in sorted order, gate_up gathers
+      }
+      xo[j] = (int)(r * a.sxm) + ch * 8;
+      xl[j] = rb_swz(row, ch);
     }
-    xo[j] = (int)(r * a.sxm) + ch * 8;
-    xl[j] = rb_swz(row, ch);
-  }
-
+  };
   // ---- weight load plan: columns n0 + 64 wave + 32 j + c (MOE 1: gate column tn 32 NW + 32 wave
   // + c for j = 0, the matching up column I + that for j = 1), K bytes [32 h, +32) codes per step --
   const uint8_t* qb[2];
@@ -238,8 +240,12 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   uint32_t* SZ = (uint32_t*)(lds + 3 * A_EL);
   // FOLD's step unpacks all of a step's weights at its top (step_fold); else one slice ahead
   constexpr bool EARLY = FOLD && RB_FOLD_EARLY_UNPACK;
-  // The MoE forms' staging into LDS (the caller places the barrier after it).
-  auto stage_moe = [&]() {
+  // The MoE forms' staging into LDS (the caller places the barrier after it): the block rows'
+  // group sums (FOLD, needs the row plan), and the scale / zero pairs -- with 16-byte aligned
+  // scale rows (unit group stride) one 16-byte load covers 16 / sizeof(scale) groups of a column
+  // (the row's allocated stride covers the last chunk), issued apart from their LDS stores when
+  // a thread has at most four such loads; else element by element.
+  auto stage_rs = [&]() {
     if constexpr (MOE != 0) {
       // FOLD: the block rows' group sums too, as [group][BM rows] floats after the pairs -- read by
       // the final correction's MFMA operands (lane: row c of block i, group g0 + h)
@@ -264,49 +270,52 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
             if (at[u] >= 0) RS[at[u]] = v[u];
         }
       }
-      // scale / zero pairs: with 16-byte aligned scale rows (unit group stride), one 16-byte load
-      // covers 16 / sizeof(scale) groups of a column (the row's allocated stride covers the last
-      // chunk); else element by element
-      constexpr int ES = SDT == IMQ_DT_FP32 ? 4 : 2;
-      constexpr int VG = 16 / ES;
-      const int ngs = a.K >> a.gsh;
-      const bool vec = a.ssg == 1 && a.szg == 1 && ((a.ssn * ES) & 15) == 0 && ((a.szn * ES) & 15) == 0 &&
-                       ((a.sse * ES) & 15) == 0 && ((((uintptr_t)a.sc) | ((uintptr_t)a.zr)) & 15) == 0;
-      if (vec) {
-        const int nch = (ngs + VG - 1) / VG, items = BN * nch;
-        for (int base = 0; base < items; base += 4 * NTHR) {
-          u32x4_t sv4[4], zv4[4];
-          int tcs[4], g0s[4];
+    }
+  };
+  constexpr int ES = SDT == IMQ_DT_FP32 ? 4 : 2;
+  constexpr int VG = 16 / ES;
+  const int ngs = a.K >> a.gsh;
+  const int nch = (ngs + VG - 1) / VG;
+  const bool sz_vec = MOE != 0 && a.ssg == 1 && a.szg == 1 && ((a.ssn * ES) & 15) == 0 &&
+                      ((a.szn * ES) & 15) == 0 && ((a.sse * ES) & 15) == 0 &&
+                      ((((uintptr_t)a.sc) | ((uintptr_t)a.zr)) & 15) == 0 && BN * nch <= 4 * NTHR;
+  u32x4_t szs[4], szz[4];
+  auto sz_issue = [&]() {   // sz_vec: the loads
+    if constexpr (MOE != 0) {
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int it = base + u * NTHR + tid;
-            const int id = it < items ? it : items - 1;
-            const int tc = id / nch, ch = id - tc * nch;
-            const int w_ = tc >> 6, j_ = (tc >> 5) & 1, c_ = tc & 31;
-            int n = MOE == 1 ? (j_ ? a.I : 0) + tn * (32 * NW) + 32 * w_ + c_ : n0 + tc;
-            n = n < a.N ? n : a.N - 1;
-            const int64_t eb = (int64_t)e * a.sse + (int64_t)ch * VG;
-            sv4[u] = *(const u32x4_t*)((const char*)a.sc + (eb + (int64_t)n * a.ssn) * ES);
-            zv4[u] = *(const u32x4_t*)((const char*)a.zr + (eb + (int64_t)n * a.szn) * ES);
-            tcs[u] = it < items ? tc : -1;
-            g0s[u] = ch * VG;
-          }
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-#pragma unroll
-            for (int v = 0; v < VG; ++v) {
-              const uint32_t sraw = ES == 4 ? sv4[u][v] : ((sv4[u][v >> 1] >> (16 * (v & 1))) & 0xffffu);
-              const uint32_t zraw = ES == 4 ? zv4[u][v] : ((zv4[u][v >> 1] >> (16 * (v & 1))) & 0xffffu);
-              const float s_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<SDT>(sraw));
-              const float z_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<ZDT>(zraw));
-              const int g = g0s[u] + v;
-              if (tcs[u] >= 0 && g < ngs)
-                SZ[g * BN + tcs[u]] = (__float_as_uint(s_) >> 16) | (__float_as_uint(z_) & 0xffff0000u);
-            }
-          }
-        }
-        return;
+      for (int u = 0; u < 4; ++u) {
+        const int it = u * NTHR + tid;
+        const int id = it < BN * nch ? it : BN * nch - 1;
+        const int tc = id / nch, ch = id - tc * nch;
+        const int w_ = tc >> 6, j_ = (tc >> 5) & 1, c_ = tc & 31;
+        int n = MOE == 1 ? (j_ ? a.I : 0) + tn * (32 * NW) + 32 * w_ + c_ : n0 + tc;
+        n = n < a.N ? n : a.N - 1;
+        const int64_t eb = (int64_t)e * a.sse + (int64_t)ch * VG;
+        szs[u] = *(const u32x4_t*)((const char*)a.sc + (eb + (int64_t)n * a.ssn) * ES);
+        szz[u] = *(const u32x4_t*)((const char*)a.zr + (eb + (int64_t)n * a.szn) * ES);
       }
+    }
+  };
+  auto sz_store = [&]() {   // sz_vec: the LDS stores
+    if constexpr (MOE != 0) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int it = u * NTHR + tid;
+        const int tc = it / nch, ch = it - tc * nch;
+#pragma unroll
+        for (int v = 0; v < VG; ++v) {
+          const uint32_t sraw = ES == 4 ? szs[u][v] : ((szs[u][v >> 1] >> (16 * (v & 1))) & 0xffffu);
+          const uint32_t zraw = ES == 4 ? szz[u][v] : ((szz[u][v >> 1] >> (16 * (v & 1))) & 0xffffu);
+          const float s_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<SDT>(sraw));
+          const float z_ = round_to<IMQ_DT_BF16>(raw_bits_to_f32<ZDT>(zraw));
+          const int g = ch * VG + v;
+          if (it < BN * nch && g < ngs) SZ[g * BN + tc] = (__float_as_uint(s_) >> 16) | (__float_as_uint(z_) & 0xffff0000u);
+        }
+      }
+    }
+  };
+  auto sz_scalar = [&]() {   // !sz_vec
+    if constexpr (MOE != 0) {
       // batches of 16 elements per thread, all loads of a batch issued before any is consumed;
       // consecutive threads take consecutive groups of one column (one scale row segment)
       constexpr int SB = 16;
@@ -336,6 +345,16 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
       }
     }
   };
+  auto stage_moe = [&]() {
+    stage_rs();
+    if (sz_vec) {
+      sz_issue();
+      sz_store();
+    } else {
+      sz_scalar();
+    }
+  };
+  if constexpr (!EARLY) plan_a();
   if constexpr (MOE != 0 && !EARLY) {
     stage_moe();
     __syncthreads();   // the prologue's weight-set loads read pairs other threads staged
@@ -600,19 +619,25 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   // the loop's: A(0) is loaded first, then A(1), B(0), ..., with A(0) written to buffer 0 just
   // before A(PD) takes its register set.
   if constexpr (EARLY) {
-    // the fold step's steady-state order: B(kt), A(kt+1), B(kt+1), A(kt+2) outstanding at the
-    // top of step kt. The staging's loads go out right after the first weight and activation
-    // loads, so their latencies overlap.
+    // the fold step's steady state has B(kt), A(kt+1), B(kt+1), A(kt+2) outstanding at the top
+    // of step kt
     static_assert(PD == 2, "the fold step keeps two register sets");
-    load_a(std::integral_constant<int, 0>{}, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    // weights and scales need only the tile: their loads go out before the gathered rows' plan
+    // (a dependent load of perm), so the two latencies overlap
     load_b(std::integral_constant<int, 0>{}, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(std::integral_constant<int, 1>{}, 1);
     __builtin_amdgcn_sched_barrier(0);
     load_b(std::integral_constant<int, 1>{}, 1);
     __builtin_amdgcn_sched_barrier(0);
-    stage_moe();
+    if (sz_vec) sz_issue();
+    __builtin_amdgcn_sched_barrier(0);
+    plan_a();
+    load_a(std::integral_constant<int, 0>{}, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(std::integral_constant<int, 1>{}, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (sz_vec) sz_store();
+    else sz_scalar();
+    stage_rs();
     __syncthreads();
     load_s(std::integral_constant<int, 0>{}, 0);
     load_s(std::integral_constant<int, 1>{}, 1);
