@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define IMQ_ABI_VERSION 4
+#define IMQ_ABI_VERSION 5
 
 #define IMQ_DT_BF16 0
 #define IMQ_DT_FP16 1
@@ -209,6 +209,28 @@ int64_t imq_probe_sink_bytes(void);
 int imq_probe_read(const void* buf, int64_t bytes, void* sink, int64_t sink_bytes, void* stream);
 int imq_probe_read_seq(const void* ptrs, const void* n16s, int nbuf, int64_t max_n16, void* sink,
                        int64_t sink_bytes, void* stream);
+
+/* GPTQ int2 solver (the calibrated int2 packer's quantization, after its Cholesky stage).
+ *   imq_gptq_int2_params: the group search alone -- replaces gptq_pack.py:78-100 (_find_params):
+ *       scale[r], zero[r] of rows Wg[r][0:cols) (fp32, row stride ldw) on the asymmetric 0..3 grid,
+ *       the best of int(maxshrink * grid) range-shrink candidates by sum |dq - w|^2.4.
+ *   imq_gptq_int2_solve: replaces gptq_pack.py:141-180 (_GPTQ.solve from its block loop): W
+ *       [out][ldw] fp32 (dead columns zeroed; consumed: overwritten by the cross-block updates),
+ *       Hinv [in_f][ldh] fp32 the upper Cholesky factor of the damped H^-1, blocks of blocksize
+ *       (<= 128, a multiple of group_size, itself a multiple of 4) columns. Writes qweight
+ *       [out][ldq] crumbs (byte j of a row = columns 4j..4j+3, lowest bits first; in_pad =
+ *       ceil(in_f / group_size) * group_size, padded columns at the last group's rounded zero),
+ *       scale / zero [out][ldsz] fp32 and, when dq is non-null, the dequantized weight
+ *       dq [out][lddq] fp32. Workspace: imq_gptq_int2_workspace_bytes(out, blocksize).
+ * float32 throughout, every operation rounded on its own, sums in a fixed order: reproducible
+ * bit for bit on any device by a restatement with the same order. */
+int64_t imq_gptq_int2_workspace_bytes(int64_t out, int64_t blocksize);
+int imq_gptq_int2_params(const float* Wg, int64_t ldw, int64_t rows, int64_t cols, int grid, double maxshrink,
+                         float* scale, float* zero, void* stream);
+int imq_gptq_int2_solve(float* W, int64_t ldw, int64_t out, int64_t in_f, const float* Hinv, int64_t ldh,
+                        int64_t group_size, int grid, double maxshrink, int64_t blocksize, uint8_t* qweight,
+                        int64_t ldq, float* scale, float* zero, int64_t ldsz, float* dq, int64_t lddq,
+                        void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -70,6 +70,11 @@ SIGNATURES = {
     "imq_probe_sink_bytes": (_c_i64, []),
     "imq_probe_read": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
     "imq_probe_read_seq": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_vp, _c_i64, _c_vp]),
+    "imq_gptq_int2_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "imq_gptq_int2_params": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, ctypes.c_double, _c_vp, _c_vp, _c_vp]),
+    "imq_gptq_int2_solve": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_int, ctypes.c_double,
+                                     _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
+                                     _c_vp]),
 }
 
 

@@ -51,7 +51,7 @@ def _ctype(c: str):
     c = c.replace("const ", "").strip()
     if c.endswith("*"):
         return ctypes.c_char_p if c == "char*" or c == "char *" else ctypes.c_void_p
-    return {"int64_t": ctypes.c_int64, "int": ctypes.c_int, "float": ctypes.c_float,
+    return {"int64_t": ctypes.c_int64, "int": ctypes.c_int, "float": ctypes.c_float, "double": ctypes.c_double,
             "void": None}[c]
 
 
@@ -81,7 +81,7 @@ def test_exports_are_c_linkage():
 
 
 def test_abi_version_and_strerror(L):
-    assert L.imq_abi_version() == 4
+    assert L.imq_abi_version() == 5
     assert L.imq_strerror(0) == b"ok"
     for rc in (_lib.IMQ_ERR_INVALID, _lib.IMQ_ERR_UNSUPPORTED, _lib.IMQ_ERR_ALIGN, _lib.IMQ_ERR_SCRATCH):
         assert len(L.imq_strerror(rc)) > 5
