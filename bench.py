@@ -124,8 +124,8 @@ def _cpu_model() -> str:
 
 
 def _traffic(key: str):
-    """HBM bytes per launch of the dominant kernel for workload ``key`` from the committed PMC
-    summary (FETCH_SIZE + WRITE_SIZE per dispatch, copy-calibrated), or None."""
+    """HBM bytes per launch (one linear or one MoE layer, every hot-path kernel of it) for workload
+    ``key`` from the committed PMC summary (FETCH_SIZE x 2 + WRITE_SIZE, copy-calibrated), or None."""
     path = os.path.join(HERE, "profiles", "traffic.json")
     try:
         with open(path) as f:
@@ -415,6 +415,18 @@ def bench_c4(args, dev):
 MOE_LAYERS = 16     # C5 T=1: 16 x 8 hit experts x 3.34 MB = 428 MB of distinct weights, past the MALL
 
 
+def _moe_kernels(B: int, E: int, gK: int) -> str:
+    """The kernels one imq_moe_experts_w4 call launches for B routed rows, E experts and gate_up
+    K_pad gK (the dispatch rule of moe.hip): direct decode when 4 B <= E; the register-B grouped
+    GEMM when B gK >= 32768 E; the token-sorted line kernels between."""
+    if 4 * B <= E:
+        return "moe_gu_line_kernel + moe_dn_line_kernel (direct decode)"
+    if B * gK >= 32768 * E:
+        return ("moe_sort_kernel (with the hidden rows' group sums) + gemm_rb_kernel MoE forms "
+                "(gate_up, down; scale-folded) + moe_combine_bf16_kernel")
+    return "moe_sort_kernel + moe_line_kernel (gate_up, down) + moe_combine_kernel"
+
+
 def _moe_layer_bytes(idx, per_expert: int, act_bytes: int) -> tuple:
     """(algorithmic bytes, distinct experts) of one MoE layer: each hit expert's weights once, the
     activations in and out, and the routing ids and weights."""
@@ -440,11 +452,7 @@ def bench_c5(args, dev):
     per_layer = [_moe_layer_bytes(idx, per_expert, T * 2048 * 2 * 2) for idx, _ in routes]
     nbytes = sum(b for b, _ in per_layer)
     us = ms * 1e3 / len(layers)
-    B = T * 8       # routed rows; the dispatch rule of moe.hip: direct decode when 4 B <= E, the
-    #                 grouped GEMM when B K_gate_up >= 81920 E, token-sorted line kernels between
-    kern = ("moe_gu_line_kernel + moe_dn_line_kernel" if 4 * B <= 64 else
-            "moe_sort_kernel + gemm_wq_kernel MOE forms + moe_combine_kernel" if B * 2048 >= 81920 * 64 else
-            "moe_sort_kernel + moe_line_kernel (x2) + moe_combine_kernel")
+    kern = _moe_kernels(T * 8, 64, 2048)
     roof = _hbm_roofline(f"imq_moe_experts_w4: {kern} (one MoE layer)", nbytes / len(layers), us,
                          _traffic(f"c5_t{T}"))
     cfg = {"workload": f"C5 OLMoE fused MoE experts, T={T}, top-8 of 64, H=2048, I=1024, {len(layers)} layers "
@@ -489,7 +497,8 @@ def bench_gptoss(args, dev):
     per_layer = [_moe_layer_bytes(idx, per_expert, T * H * 2 * 2) for idx, _ in routes]
     nbytes = sum(b for b, _ in per_layer)
     us = ms * 1e3 / len(layers)
-    roof = _hbm_roofline("imq_moe_experts_w4_ex gptoss (one MoE layer)", nbytes / len(layers), us,
+    kern = _moe_kernels(T * k, E, 3072)
+    roof = _hbm_roofline(f"imq_moe_experts_w4_ex gptoss: {kern} (one MoE layer)", nbytes / len(layers), us,
                          _traffic(f"gptoss_t{T}"))
     cfg = {"workload": f"gpt-oss-20b fused experts, T={T}, top-{k} of {E}, H=I={H}, {len(layers)} layers routed "
                        f"independently", "T": T,
@@ -515,7 +524,7 @@ def bench_head(args, dev):
                      args.warmup)
     nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
     roof = _hbm_roofline("imq_linear_w8 decode kernel", nbytes, ms * 1e3, _traffic(f"head_m{M}"))
-    cfg = {"workload": f"int8 lm_head 3584 -> 152064 (Qwen2.5-7B), M={M}", "M": M,
+    cfg = {"workload": f"int8 lm_head 3584 -> 152064 (Qwen2.5-7B), M={M}", "M": M, "launches_per_step": 1,
            "weights": "int8 per-row symmetric, bf16 scale", "distinct_bytes_per_step": nbytes}
     cpu = None
     if not args.no_cpu:
