@@ -826,6 +826,232 @@ __global__ __launch_bounds__(256) void splitk_rows_reduce_kernel(const float* __
 }
 
 // ---------------------------------------------------------------------------------------------
+// int4 decode kernel for 4 < M <= 16 (G = 128) with K split across the waves of one workgroup.
+//
+// Wave w of the NW waves owns line-steps [w R, w R + R) of every row (K_pad = NW R 256). Its slice
+// of the activations is read once, one full row per load, arranged through wave-private LDS
+// (unpack order, per-group row sums) and kept in registers as the 16 A-operand rows (zero beyond
+// M) with the group sums in the D layout; it serves every row tile the workgroup streams (a
+// persistent grid over the N / 16 tiles, one workgroup per CU). Per tile a wave reads 16 rows x
+// R line-steps of packed weights with two full-line loads per line-step, PD tiles ahead, plus one
+// scale and one zero dword (two groups) per line-step and row. The per-group math is the K-split
+// kernel's: B = 128 + code, y += s acc - s (128 + z) sum(x). The waves' 16 x 16 fp32 partials meet
+// in LDS (double-buffered, one barrier per tile) and are summed in wave order (deterministic).
+// The bf16 results wait in LDS and are stored after the last tile (or every kWsYB tiles): a store
+// in flight would make each tile's wait for its weights drain every outstanding load (loads and
+// stores share one counter). No workspace and no second launch: no partial leaves the workgroup.
+// ---------------------------------------------------------------------------------------------
+constexpr int kWsYB = 8;   // tiles of bf16 results held in LDS between stores
+
+IMQ_HOST_DEV inline int wsplit_lds(int R, int NW) {
+  return NW * (16 * (R * kLine + 8) * 2 + 2 * R * 16 * 4) + 2 * NW * 256 * 4 + kWsYB * 256 * 2;
+}
+
+template <int R, int SDT, int NW, int PD>
+__global__ __launch_bounds__(64 * NW) void w4_wsplit_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int XROW = R * kLine + 8;                // staged row stride (bf16 elements)
+  constexpr int CPR = R * 32;                        // 16-byte chunks per row of the slice
+  constexpr int XU = 16 * CPR / 64;                  // row loads per lane (all 16 rows)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, ar = lane >> 4;
+  const bool lo8 = c < 8;
+  const int M = a.M;
+  const int T = (a.N + 15) / 16;
+  const int ls0 = wave * R;                          // first line-step of this wave
+  uint16_t* xw = (uint16_t*)(smem + (size_t)wave * (16 * XROW * 2 + 2 * R * 16 * 4));
+  float* xsum = (float*)(xw + 16 * XROW);            // [2 R groups][16 rows]
+  float (*red)[NW][256] = (float (*)[NW][256])(smem + (size_t)NW * (16 * XROW * 2 + 2 * R * 16 * 4));
+  uint16_t (*ybuf)[256] = (uint16_t (*)[256])((unsigned char*)red + 2 * NW * 256 * 4);
+
+  // 1) the activation slice, one row (or two) per load: chunk ch of row m is x[m, 256 ls0 + 8 ch).
+  //    Every load is unconditional (rows past M read row M - 1 and are not staged): a load under a
+  //    branch makes the compiler wait for all outstanding loads where the paths join.
+  u32x4_t xv[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int idx = 64 * u + lane;
+    const int m = idx / CPR, ch = idx - m * CPR;
+    xv[u] = *(const u32x4_t*)(a.x + (int64_t)(m < M ? m : M - 1) * a.sxm + ls0 * kLine + 8 * ch);
+  }
+
+  // 2) per tile: weights (two full-line loads per line-step) and scale / zero dwords of row c
+  struct Tile {
+    u32x4_t w[2 * R];
+    uint32_t sw[R * (SDT == IMQ_DT_FP32 ? 2 : 1)], zw[R * (SDT == IMQ_DT_FP32 ? 2 : 1)];
+  };
+  // A tile past the workgroup's last (t > tlast: the prefetch runs PD tiles ahead) loads one
+  // 16-byte word of the operands for every lane and row -- a single request per load, no branch.
+  auto load_tile = [&](int t, Tile& tl, int tlast) {
+    const bool live = t <= tlast;
+    const int row0 = t * 16;
+    const int rlast = a.N - 1 - row0;
+    const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
+    const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
+    const int64_t qo = (int64_t)row0 * a.sqn + ls0 * 128 + 16 * ar;
+    const uint8_t* q0 = a.q + (live ? qo + rr0 * a.sqn + (lo8 ? 0 : 64) : 0);
+    const uint8_t* q1 = a.q + (live ? qo + rr1 * a.sqn + (lo8 ? 64 : 0) : 0);
+    const int ist = live ? 128 : 0;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      tl.w[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + ist * i));
+      tl.w[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + ist * i));
+    }
+    const int rc = live ? row0 + (c < rlast ? c : rlast) : 0;
+    const int g0 = live ? 2 * ls0 : 0;
+    if constexpr (SDT == IMQ_DT_FP32) {
+      const uint32_t* sp = (const uint32_t*)a.sc + (int64_t)rc * a.ssn + g0;
+      const uint32_t* zp = (const uint32_t*)a.zr + (int64_t)rc * a.szn + g0;
+#pragma unroll
+      for (int j = 0; j < 2 * R; ++j) {
+        tl.sw[j] = sp[j];
+        tl.zw[j] = zp[j];
+      }
+    } else {
+      const uint32_t* sp = (const uint32_t*)((const uint16_t*)a.sc + (int64_t)rc * a.ssn + g0);
+      const uint32_t* zp = (const uint32_t*)((const uint16_t*)a.zr + (int64_t)rc * a.szn + g0);
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        tl.sw[j] = sp[j];
+        tl.zw[j] = zp[j];
+      }
+    }
+  };
+  // scale / zero of group 2 i (row c) and 2 i + 1 (row c ^ 8, from lane c ^ 8)
+  auto sz = [&](const Tile& tl, int i, float& s0, float& s1, float& z0, float& z1) {
+    if constexpr (SDT == IMQ_DT_FP32) {
+      s0 = round_bf16_hw(__uint_as_float(tl.sw[2 * i]));
+      z0 = round_bf16_hw(__uint_as_float(tl.zw[2 * i]));
+      s1 = round_bf16_hw(__uint_as_float((uint32_t)__shfl_xor((int)tl.sw[2 * i + 1], 8)));
+      z1 = round_bf16_hw(__uint_as_float((uint32_t)__shfl_xor((int)tl.zw[2 * i + 1], 8)));
+    } else {
+      const uint32_t sx = (uint32_t)__shfl_xor((int)tl.sw[i], 8), zx = (uint32_t)__shfl_xor((int)tl.zw[i], 8);
+      s0 = raw_to_bf16_f32<SDT>(tl.sw[i] & 0xffffu);
+      z0 = raw_to_bf16_f32<SDT>(tl.zw[i] & 0xffffu);
+      s1 = raw_to_bf16_f32<SDT>(sx >> 16);
+      z1 = raw_to_bf16_f32<SDT>(zx >> 16);
+    }
+  };
+  // the first PD tiles' loads, in flight while the activations are arranged
+  const int G = gridDim.x;
+  const int tlast = blockIdx.x + (T - 1 - (int)blockIdx.x) / G * G;
+  Tile ring[PD + 1];
+  int t = blockIdx.x;
+#pragma unroll
+  for (int j = 0; j < PD; ++j) load_tile(t + j * G, ring[j], tlast);
+
+  // 3) stage the slice permuted to the unpack order with per-group row sums (16 consecutive lanes
+  //    hold one group of one row), then read the A operands and the sums in the D layout
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int idx = 64 * u + lane;
+    const int m = idx / CPR, ch = idx - m * CPR;
+    float sum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    if (m < M) {
+      *(u32x4_t*)(xw + m * XROW + 8 * ch) = permute_x8(xv[u]);
+      if ((ch & 15) == 0) xsum[(ch >> 4) * 16 + m] = sum;
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // wave-private: the wave's own writes first
+  bf16x8_t A0[R][4], A1[R][4];
+  f32x4_t xs0[R], xs1[R];
+  {
+    const uint16_t* xa = xw + (c < M ? c : 0) * XROW + 32 * ar;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        A0[i][k] = *(const bf16x8_t*)(xa + i * kLine + 8 * k);
+        A1[i][k] = *(const bf16x8_t*)(xa + i * kLine + 128 + 8 * k);
+        if (c >= M) {
+          A0[i][k] = bf16x8_t{};
+          A1[i][k] = bf16x8_t{};
+        }
+      }
+      xs0[i] = *(const f32x4_t*)(xsum + (2 * i) * 16 + 4 * ar);
+      xs1[i] = *(const f32x4_t*)(xsum + (2 * i + 1) * 16 + 4 * ar);
+    }
+  }
+
+  const uint32_t magic = magic_bf16_128x2();
+  auto compute = [&](const Tile& tl, int buf, int slot) {
+    float y0[4] = {0.f, 0.f, 0.f, 0.f}, y1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      float s0, s1, z0, z1;
+      sz(tl, i, s0, s1, z0, z1);
+      const float cz0 = -(128.f + z0) * s0;
+      const float cz1 = -(128.f + z1) * s1;
+      const u32x4_t w0 = tl.w[2 * i], w1 = tl.w[2 * i + 1];
+      u32x4_t gA, gB;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        gA[d] = lo8 ? w0[d] : w1[d];
+        gB[d] = lo8 ? w1[d] : w0[d];
+      }
+      f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc0 = mfma16x16x32(A0[i][k], unpack_nib8_bf16(gA[k], magic), acc0);
+        acc1 = mfma16x16x32(A1[i][k], unpack_nib8_bf16(gB[k], magic), acc1);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        y0[r] = fmaf(cz0, xs0[i][r], y0[r]);
+        y1[r] = fmaf(cz1, xs1[i][r], y1[r]);
+        y0[r] = fmaf(s0, acc0[r], y0[r]);
+        y1[r] = fmaf(s1, acc1[r], y1[r]);
+      }
+    }
+    float* rw = red[buf][wave];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rw[(4 * ar + r) * 16 + c] = y0[r] + row_swap8(y1[r]);
+    lds_barrier();
+    const int e = threadIdx.x;
+    if (e < 256) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) sum += red[buf][w][e];
+      ybuf[slot][e] = (uint16_t)f32_to_bf16_bits(sum);
+    }
+  };
+  // thread e < 256 stores its own buffered results (element (e / 16, e % 16) of each tile)
+  auto flush = [&](int k0, int k1) {
+    const int e = threadIdx.x;
+    const int m = e >> 4, col = e & 15;
+    if (e < 256 && m < M) {
+      for (int k = k0; k < k1; ++k) {
+        const int row = (blockIdx.x + k * G) * 16 + col;
+        if (row < a.N) a.y[(int64_t)m * a.sym + row] = ybuf[k % kWsYB][e];
+      }
+    }
+  };
+
+  // 4) tile loop, PD tiles of loads ahead of the one computed, in a ring of PD + 1 register sets
+  int buf = 0, k = 0, kf = 0;
+  for (; t < T; t += (PD + 1) * G) {
+#pragma unroll
+    for (int j = 0; j <= PD; ++j) {
+      const int tj = t + j * G;
+      if (tj >= T) break;
+      load_tile(tj + PD * G, ring[(j + PD) % (PD + 1)], tlast);
+      compute(ring[j], buf, k % kWsYB);
+      buf ^= 1;
+      ++k;
+      if (k - kf == kWsYB || tj + G >= T) {
+        flush(kf, k);
+        kf = k;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // int2 decode kernel (M <= 16). A K-step is one 64-code group: 16 bytes of each packed row.
 // Lane (row nl, quarter jl) works on dword jl = codes [16*jl, 16*jl+16) of each step, which
 // feeds two v_mfma_f32_16x16x32_bf16: MFMA h takes codes {4h..4h+3} and {4h+8..4h+11} of each
@@ -1956,8 +2182,10 @@ int line_w4(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
 
 // K-split kernel plan (4 < M <= 16, G == 128, K_pad a multiple of 256, unit group strides, same
 // scale / zero dtype, N % 4 == 0 for the vector reduction; restated by the CPU bounds model in the
-// tests): S2 = 4 line-steps (1024 codes) per split, NW = 8 or 4 row tiles per workgroup. Returns
-// false when the kernel does not take the call.
+// tests): S2 = 4 line-steps (1024 codes) per split, NW = 8 row tiles per workgroup while that still
+// gives every CU a workgroup, else 4. Every workgroup restages its split's activations (M x 1024
+// bf16), so 8 tiles halve that traffic per weight byte (measured at M = 16: down_proj 4096 x 14336
+// 16.1 -> 14.8 us); below one workgroup per CU the 4-tile grid is faster.
 constexpr int kKsS2 = 4;
 bool ksplit_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
                  int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int cus, int* splitso,
@@ -1972,7 +2200,7 @@ bool ksplit_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int
   const int64_t splits = (Kpad / kLine + kKsS2 - 1) / kKsS2;
   // 8 row tiles per workgroup (half the activation staging per weight byte) while that still
   // yields two workgroups per CU, else 4
-  const int nw = splits * ((N + 127) / 128) >= 2 * (int64_t)cus ? 8 : 4;
+  const int nw = splits * ((N + 127) / 128) >= (int64_t)cus ? 8 : 4;
   const int64_t rbs = (N + 16 * nw - 1) / (16 * nw);
   if (splits * rbs > 0x7fffffff) return false;
   const size_t lds = (size_t)ksplit_lds((int)M, kKsS2, nw, vb);
@@ -2031,6 +2259,61 @@ int ksplit_w4(const SkinnyArgs& a0, int sdt, void* ws, int64_t wsb, const DevInf
   return IMQ_ERR_UNSUPPORTED;
 }
 
+// Wave-split plan (4 < M <= 16, G == 128, K_pad == 8 R 256 with R 1 or 2, unit group strides,
+// same scale / zero dtype, 4-byte aligned scale / zero rows, the LDS of wsplit_lds within the
+// device's, at least 4 row tiles per CU; restated by the CPU bounds model in the tests): NW = 8
+// waves, one workgroup per CU, the grid min(tiles, CUs). Returns R, or 0 when the kernel does not
+// take the call. Every workgroup reads all of x (M x K_pad bf16), which costs about as much as a
+// tile stream of the same bytes, and the first tile waits for it: the kernel pays off where a
+// workgroup streams many tiles (measured at M = 16: gate_up 4096 -> 28672, 7 tiles per CU, 20.8 us
+// against 24.0 us for K-split + reduction; qkv 4096 -> 6144 and o 4096 -> 4096, 1-2 tiles per
+// CU, 11.3 / 9.7 us against 10.3 / 8.2 us). PD = 2 tiles of prefetch measured best (3, 4: no gain
+// on gate_up, slower on short grids).
+constexpr int kWsNW = 8;
+#ifndef IMQ_WS_PD
+#define IMQ_WS_PD 2
+#endif
+int wsplit_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
+                int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int cus) {
+  if (M <= 4 || M > 16 || G != 128 || sdt != zdt || ssg != 1 || szg != 1) return 0;
+  if (Kpad != kWsNW * kLine && Kpad != 2 * kWsNW * kLine) return 0;
+  if (N < 1 || N > (1 << 30) || sxm % 8 != 0) return 0;
+  const int vb = sdt == IMQ_DT_FP32 ? 4 : 2;
+  if ((ssn * vb) % 4 != 0 || (szn * vb) % 4 != 0) return 0;
+  if (N * sqn >= (int64_t(1) << 46) || 16 * sqn >= (int64_t(1) << 31) || M * sxm * 2 >= (int64_t(1) << 31)) return 0;
+  const int R = (int)(Kpad / (kWsNW * kLine));
+  if (wsplit_lds(R, kWsNW) > max_lds || (N + 15) / 16 < 4 * (int64_t)cus) return 0;
+  return R;
+}
+
+template <int SDT>
+int wsplit_launch(const SkinnyArgs& a, int R, const DevInfo& di, hipStream_t st) {
+  const int64_t T = (a.N + 15) / 16;
+  const dim3 g((unsigned)(T < di.cus ? T : di.cus)), b(64 * kWsNW);
+  const size_t lds = (size_t)wsplit_lds(R, kWsNW);
+  auto kern = R == 1 ? w4_wsplit_kernel<1, SDT, kWsNW, IMQ_WS_PD> : w4_wsplit_kernel<2, SDT, kWsNW, IMQ_WS_PD>;
+  static int attr_set[2] = {0, 0};   // benign race: every caller sets the same value
+  if (lds > 65536 && !__atomic_load_n(&attr_set[R - 1], __ATOMIC_ACQUIRE)) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    __atomic_store_n(&attr_set[R - 1], 1, __ATOMIC_RELEASE);
+  }
+  kern<<<g, b, lds, st>>>(a);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+int wsplit_w4(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
+  const int R = wsplit_plan(a.M, a.Kpad, a.G, a.N, a.sqn, a.sxm, a.ssn, a.ssg, a.szn, a.szg, sdt, sdt, di.max_lds, di.cus);
+  if (!R) return IMQ_ERR_UNSUPPORTED;
+  switch (sdt) {
+    case IMQ_DT_BF16: return wsplit_launch<IMQ_DT_BF16>(a, R, di, st);
+    case IMQ_DT_FP16: return wsplit_launch<IMQ_DT_FP16>(a, R, di, st);
+    case IMQ_DT_FP32: return wsplit_launch<IMQ_DT_FP32>(a, R, di, st);
+  }
+  return IMQ_ERR_UNSUPPORTED;
+}
+
 // Fast path eligibility + launch. Returns IMQ_ERR_UNSUPPORTED when the caller must fall back.
 // ws / wsb: the caller's optional workspace (the K-split path of 4 < M <= 16 needs one).
 int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
@@ -2045,6 +2328,8 @@ int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
   SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, 0};
   if (((uintptr_t)sc & 3) == 0 && ((uintptr_t)zr & 3) == 0) {
     int rc = line_w4(a, sdt, di, st);
+    if (rc != IMQ_ERR_UNSUPPORTED) return rc;
+    rc = wsplit_w4(a, sdt, di, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
     rc = ksplit_w4(a, sdt, ws, wsb, di, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;

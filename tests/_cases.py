@@ -49,6 +49,19 @@ def int2_random_case(N, K, G=64, seed=2000, dt="fp16"):
     return dict(q=q, s=s, z=z, in_f=K, G=G, dt=dt, Wd=Wd)
 
 
+@functools.lru_cache(maxsize=4)
+def int4_random_case(N, K, G=128, seed=0, dt="bf16"):
+    """Large-N int4 cases without the RTN search: codes ~ U{0..15}, scale ~ U(0.0005, 0.005),
+    zero ~ U{0..15} (stored in dt). No bf16 oracle dequant (Wd None): the checks use the exact
+    dequant, which is fast at these sizes."""
+    r = rng(seed)
+    ng = -(-K // G)
+    q = r.integers(0, 256, size=(N, ng * G // 2), dtype=np.uint8)
+    s = oq.round_to(r.uniform(0.0005, 0.005, size=(N, ng)).astype(np.float32), dt)
+    z = r.integers(0, 16, size=(N, ng)).astype(np.float32)
+    return dict(q=q, s=s, z=z, in_f=K, G=G, dt=dt, Wd=None)
+
+
 @functools.lru_cache(maxsize=16)
 def int8_case(N, K, seed=0, dt="bf16", wstd=0.02):
     r = rng(seed)

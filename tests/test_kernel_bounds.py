@@ -432,7 +432,7 @@ def ksplit_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024, cus=256):
     if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31 or 16 * ssn * vb >= 2 ** 31:
         return None
     splits = -(-(Kpad // LINE) // KS_S2)
-    nw = 8 if splits * -(-N // 128) >= 2 * cus else 4
+    nw = 8 if splits * -(-N // 128) >= cus else 4
     lds = M * (KS_S2 * LINE + 8) * 2 + 2 * KS_S2 * 16 * 4 + nw * 2 * 16 * (KS_S2 * vb // 2) * 4
     if lds > max_lds:
         return None
@@ -553,6 +553,131 @@ def test_ksplit_plan_declines():
     assert ksplit_plan(8, 384, 128, 36, 192, 384, 3, 2) is None           # K_pad % 256
     assert ksplit_plan(8, 512, 128, 37, 256, 512, 4, 2) is None           # N % 4 (vector reduction)
     assert ksplit_plan(16, 14336, 128, 4096, 7168, 14336, 112, 2) is not None
+
+
+# ---- int4 wave-split decode kernel (csrc/gemv.hip w4_wsplit_kernel / wsplit_plan) --------------
+WS_NW = 8
+
+
+def wsplit_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, cus=256):
+    """wsplit_plan in csrc/gemv.hip: R (line-steps per wave) or None when the kernel declines."""
+    if not (4 < M <= 16) or G != 128 or Kpad not in (WS_NW * LINE, 2 * WS_NW * LINE):
+        return None
+    if N < 1 or sxm % 8 or (ssn * vb) % 4:
+        return None
+    if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31:
+        return None
+    if -(-N // 16) < 4 * cus:
+        return None
+    return Kpad // (WS_NW * LINE)
+
+
+def wsplit_ranges(M, Kpad, N, sqn, sxm, ssn, vb, cus=256, clamp=True):
+    """Max exclusive offsets the wave-split kernel reads (x elements, qweight bytes, scale
+    elements), its wave-private LDS offsets (staged x, A-operand reads, group sums), and the y
+    elements it writes (with multiplicity), from its index arithmetic: every lane of every wave
+    for the first and last tile of each workgroup (the prefetch past the last tile re-reads it),
+    and every tile for y."""
+    R = wsplit_plan(M, Kpad, 128, N, sqn, sxm, ssn, vb, cus)
+    T = -(-N // 16)
+    G = min(T, cus)
+    r = dict(x=0, q=0, s=0, red=0, lds_x=0, lds_xa=0, lds_sum=0)
+    ywrites = {}
+    CPR = 32 * R
+    XROW = R * LINE + 8
+    for wave in range(WS_NW):
+        ls0 = wave * R
+        for lane in range(64):
+            c, ar = lane & 15, lane >> 4
+            for u in range(16 * CPR // 64):
+                m, ch = divmod(64 * u + lane, CPR)
+                r["x"] = max(r["x"], min(m, M - 1) * sxm + ls0 * LINE + 8 * ch + 8)
+                if m < M:
+                    r["lds_x"] = max(r["lds_x"], m * XROW + 8 * ch + 8)
+                    if ch % 16 == 0:
+                        r["lds_sum"] = max(r["lds_sum"], (ch >> 4) * 16 + m + 1)
+            row = c if c < M else 0
+            for i in range(R):
+                for k in range(4):
+                    r["lds_xa"] = max(r["lds_xa"], row * XROW + 32 * ar + i * LINE + 128 + 8 * k + 8)
+                r["lds_sum"] = max(r["lds_sum"], (2 * i + 1) * 16 + 4 * ar + 4)
+    tiles = set()
+    for b in range(G):
+        ts = list(range(b, T, G))
+        tiles.update(ts)
+        for t in (ts[0], ts[-1]):
+            row0 = t * 16
+            rlast = N - 1 - row0
+            assert rlast >= 0
+            for wave in range(WS_NW):
+                ls0 = wave * R
+                for lane in range(64):
+                    c, ar = lane & 15, lane >> 4
+                    lo8 = c < 8
+                    rr0 = min(c & 7, rlast) if clamp else c & 7
+                    rr1 = min(8 + (c & 7), rlast) if clamp else 8 + (c & 7)
+                    rc = min(c, rlast) if clamp else c
+                    for i in range(R):
+                        r["q"] = max(r["q"], (row0 + rr0) * sqn + ls0 * 128 + 16 * ar + (0 if lo8 else 64) + 128 * i + 16)
+                        r["q"] = max(r["q"], (row0 + rr1) * sqn + ls0 * 128 + 16 * ar + (64 if lo8 else 0) + 128 * i + 16)
+                    nwords = 2 * R if vb == 4 else R
+                    per = 1 if vb == 4 else 2        # scale elements per dword
+                    r["s"] = max(r["s"], (row0 + rc) * ssn + 2 * ls0 + nwords * per)
+                    for rr in range(4):
+                        r["red"] = max(r["red"], (4 * ar + rr) * 16 + c + 1)
+    assert tiles == set(range(T))
+    for t in range(T):
+        for e in range(64 * WS_NW):
+            m, col = e >> 4, e & 15
+            if e < 256 and m < M and t * 16 + col < N:
+                key = (m, t * 16 + col)
+                ywrites[key] = ywrites.get(key, 0) + 1
+    return R, r, ywrites
+
+
+@pytest.mark.parametrize("N,K,cus", [(28672, 4096, 256), (16400, 2048, 256), (100, 2048, 1), (68, 4096, 1),
+                                     (4100, 2048, 64), (72, 2048, 1), (1000, 4096, 8)])
+@pytest.mark.parametrize("M", [5, 9, 16])
+@pytest.mark.parametrize("vb", [2, 4])
+@pytest.mark.parametrize("pad", [0, 64])
+def test_wsplit_in_bounds_and_covering(N, K, cus, M, vb, pad):
+    """Every wave-split read lies inside its operand (exact-fit allocations, the +64-byte row
+    view), the LDS partials stay inside one wave's 256 floats, the persistent grid visits every
+    tile once, and every y element is written exactly once. Small CU counts put short grids,
+    partial last tiles and uneven tiles per workgroup under the plan's 4-tiles-per-CU rule."""
+    Kpad, ng = K, K // 128
+    sqn = Kpad // 2 + pad
+    ssn = ng + (pad // 2 if vb == 2 else pad // 4)
+    R, r, yw = wsplit_ranges(M, Kpad, N, sqn, Kpad, ssn, vb, cus)
+    assert R in (1, 2)
+    assert r["x"] <= (M - 1) * Kpad + Kpad
+    assert r["q"] <= (N - 1) * sqn + Kpad // 2
+    assert r["s"] <= (N - 1) * ssn + ng
+    assert r["red"] <= 256
+    xrow = R * LINE + 8
+    assert r["lds_x"] <= 16 * xrow and r["lds_xa"] <= 16 * xrow and r["lds_sum"] <= 2 * R * 16
+    lds = WS_NW * (16 * xrow * 2 + 2 * R * 16 * 4) + 2 * WS_NW * 256 * 4 + 8 * 256 * 2
+    assert lds <= 160 * 1024
+    assert len(yw) == M * N and set(yw.values()) == {1}
+
+
+def test_wsplit_model_catches_missing_row_clamp():
+    """Negative control: without the row clamps a partial last tile (N % 16) would read weight and
+    scale rows past N."""
+    N, K, M = 100, 2048, 8
+    _, r, _ = wsplit_ranges(M, K, N, K // 2, K, K // 128, 2, cus=1, clamp=False)
+    assert r["q"] > (N - 1) * (K // 2) + K // 2 or r["s"] > (N - 1) * (K // 128) + K // 128
+
+
+def test_wsplit_plan_declines():
+    assert wsplit_plan(4, 4096, 128, 4096, 2048, 4096, 32, 2) is None     # M <= 4: line kernel
+    assert wsplit_plan(8, 14336, 128, 4096, 7168, 14336, 112, 2) is None  # K_pad not 2048 / 4096
+    assert wsplit_plan(8, 4096, 64, 4096, 2048, 4096, 64, 2) is None      # G != 128
+    assert wsplit_plan(8, 4096, 128, 4096, 2048, 4096, 33, 2) is None     # odd bf16 scale row stride
+    assert wsplit_plan(16, 4096, 128, 4096, 2048, 4096, 32, 2) is None    # 1 tile per CU: K-split
+    assert wsplit_plan(16, 4096, 128, 6144, 2048, 4096, 32, 2) is None    # qkv: 1.5 tiles per CU
+    assert wsplit_plan(16, 4096, 128, 28672, 2048, 4096, 32, 2) == 2      # gate_up: 7 tiles per CU
+    assert wsplit_plan(8, 2048, 128, 16384, 1024, 2048, 16, 2) == 1
 
 
 def test_ksplit_model_catches_missing_row_clamp():
