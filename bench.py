@@ -187,10 +187,11 @@ def bench_c2(args, dev):
 
 
 def _w4_decode_kernel(M: int) -> str:
-    """The kernel imq_linear_w4 runs for M decode rows at the C1 / C2 shapes (gemv.hip)."""
+    """The kernels imq_linear_w4 runs for M decode rows at the C1 / C2 shapes (gemv.hip)."""
     if M <= 4:
         return f"w4_line_kernel (imq_linear_w4, M={M})"
-    return f"w4_ksplit_kernel + splitk_rows_reduce_kernel (imq_linear_w4, M={M})"
+    return (f"w4_wsplit_kernel (gate_up) + w4_ksplit_kernel + splitk_rows_reduce_kernel (qkv, o, down) "
+            f"(imq_linear_w4, M={M})")
 
 
 def _cpu_int4_random(N, K, seed, G=128):
