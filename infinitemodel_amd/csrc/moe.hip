@@ -1291,11 +1291,16 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
                   c.gs, c.gz, c.gse, c.gsn, (int)c.I, 0, 0, c.gb, c.gbe, c.bdt, c.alpha, c.limit, h, L.hw};
     MoeDecArgs dn{h, L.hw, (int)c.I, (int)c.dK, (int)c.k, c.idx, c.topk_w, (int)c.E, c.dq, c.dqe, c.dqn,
                   c.ds, c.dz, c.dse, c.dsn, (int)c.I, 0, 0, c.db, c.dbe, c.bdt, 0.f, 0.f, c.out, c.os};
-    int gs, dshape, dwk;
+    int gs, gwk, dshape, dwk;
     const int groups = c.act == IMQ_ACT_GPTOSS ? 1 : 2;
     int dgroups;
-    dec_dn_pairs(c.T, c.H, (int)c.k, &dgroups);
-    if (dec_shape(c.gK, groups, &gs, &dwk) && dec_shape(c.dK, dgroups, &dshape, &dwk)) {
+    const bool dpair = dec_dn_pairs(c.T, c.H, (int)c.k, &dgroups);
+    const int vb = c.sdt == IMQ_DT_FP32 ? 4 : 2;
+    // both launches' shapes and LDS are checked before the first is issued, so a down that
+    // would decline never follows a gate_up already in flight
+    if (dec_shape(c.gK, groups, &gs, &gwk) && dec_shape(c.dK, dgroups, &dshape, &dwk) &&
+        (size_t)groups * gwk * (dec_wave_lds(gs, vb, false) + 64) <= 65536 &&
+        (size_t)dgroups * dwk * (dec_wave_lds(dshape, vb, dpair) + 64) <= 65536 && (dpair || c.H % 16 == 0)) {
       int rc = IMQ_ERR_UNSUPPORTED;
       switch (c.sdt) {
         case IMQ_DT_BF16: rc = dec_gu<IMQ_DT_BF16>(gu, c.act, B, 65536, st); break;

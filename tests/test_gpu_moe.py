@@ -283,6 +283,48 @@ def test_moe_decode_line_path(dev, sdt):
     _run(dev, E=32, H=1024, I=512, k=8, T=1, seed=98, sdt=sdt)
 
 
+class _LazyExact:
+    """[E, N, K] view of random-code experts, dequantized exactly per expert on access (only the
+    hit experts are ever read by moe_exact_grouped)."""
+
+    def __init__(self, q, s, z, K, G):
+        self.q, self.s, self.z, self.K, self.G = q, s, z, K, G
+        self.shape = (q.shape[0], q.shape[1], K)
+
+    def __getitem__(self, e):
+        return oq.dequant_exact(oq.unpack_int4(self.q[e]), self.s[e], self.z[e], self.G, self.K)
+
+
+def test_moe_decode_down_over_lds_declines_before_launch(dev):
+    """Top-8 decode (4 B <= E: the direct two-launch form) with the down projection's K 3584 at
+    H 512: the paired down form would need 16 waves x 4.7 KB > 64 KiB of LDS, so the plan checks
+    both launches' LDS before the first and the call runs on the token-sorted path instead of
+    launching a gate_up whose down then declines. Random codes (the RTN search at this size would
+    take minutes on the host); results against the exact oracle."""
+    import torch
+    from infinitemodel_amd import ops
+    E, H, I, k, T, G = 32, 512, 3584, 8, 1, 128
+    r = C.rng(99)
+    def experts(N, K):
+        q = r.integers(0, 256, size=(E, N, K // 2), dtype=np.uint8)
+        s = oq.round_to(r.uniform(0.0005, 0.005, size=(E, N, K // G)).astype(np.float32), "bf16")
+        z = r.integers(0, 16, size=(E, N, K // G)).astype(np.float32)
+        return q, s, z
+    gu, dn = experts(2 * I, H), experts(H, I)
+    logits = r.standard_normal((T, E)).astype(np.float32)
+    idx, w = om.route_topk(logits, k)
+    x = C.bf16_normal(r, (T, H))
+    t = lambda a: C.to_torch(a, "bf16", dev)  # noqa: E731
+    out = ops.moe_experts_w4(t(x), torch.from_numpy(idx).to(dev), t(w),
+                             (C.u8(gu[0], dev), t(gu[1]), t(gu[2]), H),
+                             (C.u8(dn[0], dev), t(dn[1]), t(dn[2]), I), G)
+    y = C.t2np(out)
+    exact = om.moe_exact_grouped(x, idx, w, _LazyExact(*gu, H, G), _LazyExact(*dn, I, G))
+    assert np.isfinite(y).all()
+    mr, me = oq.max_rel(y, exact), oq.mean_rel(y, exact)
+    assert mr <= MAX_REL and me <= MEAN_REL, (mr, me)
+
+
 @pytest.mark.parametrize("T", [64, 80])
 def test_moe_many_rows_per_expert(dev, T):
     """16+ routed rows per expert on average: 32-row blocks with passes of 32 rows (a partial last
