@@ -215,6 +215,27 @@ def test_linear_w4_wsplit_repeat_bit_identical_and_matches_skinny(dev):
     assert d <= 2 ** -7 * y1.float().abs().max().item()
 
 
+@pytest.mark.parametrize("N,K,M", [(16400, 4096, 16), (16400, 2048, 7), (4100, 4096, 12)])
+def test_linear_w4_decode_strided_rows_bit_identical(dev, N, K, M):
+    """Activation rows with a stride past K_pad and output rows with a stride past N (views of
+    wider buffers) give bit-identical y to the contiguous call: the wave-split kernel (N 16400)
+    and the K-split kernel (N 4100)."""
+    import torch
+    from infinitemodel_amd import ops
+    c = C.int4_random_case(N, K, 128, seed=31 + N + M)
+    q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev), C.to_torch(c["z"], "bf16", dev)
+    x = C.to_torch(C.bf16_normal(C.rng(32), (M, K)), "bf16", dev)
+    y0 = ops.linear_w4(x, q, 128, (s, z))
+    xb = torch.zeros((M, K + 64), dtype=torch.bfloat16, device=dev)
+    xb[:, :K].copy_(x)
+    yb = torch.full((M, N + 32), float("nan"), dtype=torch.bfloat16, device=dev)
+    y1 = ops.linear_w4(xb[:, :K], q, 128, (s, z), out=yb[:, :N])
+    torch.cuda.synchronize()
+    assert xb[:, :K].stride(0) == K + 64 and y1.stride(0) == N + 32
+    assert torch.equal(y1, y0)
+    assert torch.isnan(yb[:, N:].float()).all()          # nothing written past the row's N columns
+
+
 @pytest.mark.parametrize("sdt", ["fp16", "fp32"])
 def test_linear_w4_ksplit_scale_dtypes_dealias(dev, sdt):
     """The K-split kernel's fp16 / fp32 scale-zero words and the +64-byte de-alias row view."""
