@@ -7,11 +7,12 @@ stack, 32 layers x {qkv 4096->6144, o 4096->4096, gate_up 4096->28672, down 1433
 linears, launched back to back on one stream and replayed as a HIP graph.
 
   value        whole-pass algorithmic bytes (int4 codes + bf16 scale/zero + x + y) / step time
-  roofline     the dominant (here: only) kernel family, imq's w4 skinny GEMV: algorithmic bytes
-               per launch / average launch duration, both over the timed region (HIP events on
-               the stream the graph replays on); ``traffic`` = HBM bytes per launch from the
-               committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, scaled by a copy-kernel
-               calibration (profiles/), null when no summary matches the workload
+  roofline     the dominant (here: only) kernel, imq's w4 line kernel (the M=1 decode GEMV):
+               algorithmic bytes per launch / average launch duration, both over the timed
+               region (HIP events on the stream the graph replays on); ``traffic`` = HBM bytes
+               per launch (every kernel of one linear or MoE layer) from the committed
+               rocprofv3 FETCH_SIZE / WRITE_SIZE summary, scaled by a copy-kernel calibration
+               (profiles/traffic.json), null when no summary matches the workload
   cpu_baseline the reference's CPU int4 path (torch tinygemm, as worker_quant.py:732-759 binds
                it) on a bounded sample: 8 layers of the same shapes (0.93 GB, beyond host cache),
                median pass time on this host's cores
