@@ -2185,11 +2185,23 @@ int line_w4(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
 // tests): S2 = 4 line-steps (1024 codes) per split, NW = 8 row tiles per workgroup while that still
 // gives every CU a workgroup, else 4. Every workgroup restages its split's activations (M x 1024
 // bf16), so 8 tiles halve that traffic per weight byte (measured at M = 16: down_proj 4096 x 14336
-// 16.1 -> 14.8 us); below one workgroup per CU the 4-tile grid is faster.
+// 16.1 -> 14.8 us); below one workgroup per CU the 4-tile grid is faster. A 4-tile grid of at most
+// two workgroups per CU splits K in 512-code pieces instead (twice the workgroups, half the
+// activations each; measured at M = 16: qkv 4096 -> 6144 10.6 -> 9.9 us, o 4096 -> 4096 8.3 ->
+// 8.0 us).
 constexpr int kKsS2 = 4;
+
+// Line-steps per split (4, or 2 for short grids) and tiles per workgroup of the K-split plan.
+inline void ksplit_shape(int64_t Kpad, int64_t N, int cus, int* s2, int* nw) {
+  const int64_t KL = Kpad / kLine;
+  const int64_t splits4 = (KL + kKsS2 - 1) / kKsS2;
+  *nw = splits4 * ((N + 127) / 128) >= (int64_t)cus ? 8 : 4;
+  *s2 = *nw == 4 && splits4 * ((N + 63) / 64) <= 2 * (int64_t)cus ? 2 : kKsS2;
+}
+
 bool ksplit_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
                  int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int cus, int* splitso,
-                 int* nwo, size_t* ldso) {
+                 int* nwo, int* s2o, size_t* ldso) {
   if (M <= 4 || M > 16 || G != 128 || Kpad % kLine != 0 || Kpad <= 0 || sdt != zdt) return false;
   if (N % 4 != 0 || sxm % 8 != 0) return false;
   if (ssg != 1 || szg != 1 || N < 1 || N > (1 << 30) || Kpad > (1 << 28)) return false;
@@ -2197,33 +2209,36 @@ bool ksplit_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int
   if ((ssn * vb) % 4 != 0 || (szn * vb) % 4 != 0) return false;
   if (16 * sqn >= (int64_t(1) << 31) || M * sxm * 2 >= (int64_t(1) << 31)) return false;
   if (16 * ssn * vb >= (int64_t(1) << 31) || 16 * szn * vb >= (int64_t(1) << 31)) return false;
-  const int64_t splits = (Kpad / kLine + kKsS2 - 1) / kKsS2;
-  // 8 row tiles per workgroup (half the activation staging per weight byte) while that still
-  // yields two workgroups per CU, else 4
-  const int nw = splits * ((N + 127) / 128) >= (int64_t)cus ? 8 : 4;
+  int s2, nw;
+  ksplit_shape(Kpad, N, cus, &s2, &nw);
+  const int64_t splits = (Kpad / kLine + s2 - 1) / s2;
   const int64_t rbs = (N + 16 * nw - 1) / (16 * nw);
   if (splits * rbs > 0x7fffffff) return false;
-  const size_t lds = (size_t)ksplit_lds((int)M, kKsS2, nw, vb);
+  const size_t lds = (size_t)ksplit_lds((int)M, s2, nw, vb);
   if (lds > (size_t)max_lds) return false;
   *splitso = (int)splits;
   *nwo = nw;
+  *s2o = s2;
   *ldso = lds;
   return true;
 }
 
-// Workspace bytes of the K-split decode path for this shape (0: the shape does not use it).
+// Workspace bytes of the K-split decode path for this shape on the current device (0: the shape
+// does not use it).
 int64_t ksplit_workspace_bytes(int64_t M, int64_t N, int64_t Kpad) {
   if (M <= 4 || M > 16 || N <= 0 || Kpad <= 0 || Kpad % kLine != 0) return 0;
-  return (Kpad / kLine + kKsS2 - 1) / kKsS2 * M * N * 4;
+  int s2, nw;
+  ksplit_shape(Kpad, N, device_info().cus, &s2, &nw);
+  return (Kpad / kLine + s2 - 1) / s2 * M * N * 4;
 }
 
-template <int SDT, int NW>
+template <int SDT, int NW, int S2>
 int ksplit_launch(const SkinnyArgs& a, int splits, size_t lds, hipStream_t st) {
   const int rbs = (a.N + 16 * NW - 1) / (16 * NW);
   const dim3 g((unsigned)(splits * rbs)), b(64 * NW);
   int rc;
-  if (a.M <= 8) rc = launch_with_lds(w4_ksplit_kernel<kKsS2, 8, SDT, NW>, g, b, lds, st, a);
-  else rc = launch_with_lds(w4_ksplit_kernel<kKsS2, 16, SDT, NW>, g, b, lds, st, a);
+  if (a.M <= 8) rc = launch_with_lds(w4_ksplit_kernel<S2, 8, SDT, NW>, g, b, lds, st, a);
+  else rc = launch_with_lds(w4_ksplit_kernel<S2, 16, SDT, NW>, g, b, lds, st, a);
   if (rc != IMQ_OK) return rc;
   const int n4 = a.N / 4;
   splitk_rows_reduce_kernel<<<dim3((unsigned)((a.M * n4 + 255) / 256)), dim3(256), 0, st>>>(a.part, splits, a.M,
@@ -2232,29 +2247,28 @@ int ksplit_launch(const SkinnyArgs& a, int splits, size_t lds, hipStream_t st) {
   return IMQ_OK;
 }
 
+template <int SDT>
+int ksplit_dispatch(const SkinnyArgs& a, int nw, int s2, int splits, size_t lds, hipStream_t st) {
+  if (nw == 8) return ksplit_launch<SDT, 8, kKsS2>(a, splits, lds, st);
+  if (s2 == 2) return ksplit_launch<SDT, 4, 2>(a, splits, lds, st);
+  return ksplit_launch<SDT, 4, kKsS2>(a, splits, lds, st);
+}
+
 int ksplit_w4(const SkinnyArgs& a0, int sdt, void* ws, int64_t wsb, const DevInfo& di, hipStream_t st) {
-  int splits, nw;
+  int splits, nw, s2;
   size_t lds;
   if (!ksplit_plan(a0.M, a0.Kpad, a0.G, a0.N, a0.sqn, a0.sxm, a0.ssn, a0.ssg, a0.szn, a0.szg, sdt, sdt,
-                   di.max_lds, di.cus, &splits, &nw, &lds))
+                   di.max_lds, di.cus, &splits, &nw, &s2, &lds))
     return IMQ_ERR_UNSUPPORTED;
   const int64_t need = (int64_t)splits * a0.M * a0.N * 4;
   if (!ws || wsb < need || ((uintptr_t)ws & 15)) return IMQ_ERR_UNSUPPORTED;
   if (((uintptr_t)a0.y & 7) || (a0.sym & 3)) return IMQ_ERR_UNSUPPORTED;   // 8-byte y stores
   SkinnyArgs a = a0;
   a.part = (float*)ws;
-  if (nw == 8) {
-    switch (sdt) {
-      case IMQ_DT_BF16: return ksplit_launch<IMQ_DT_BF16, 8>(a, splits, lds, st);
-      case IMQ_DT_FP16: return ksplit_launch<IMQ_DT_FP16, 8>(a, splits, lds, st);
-      case IMQ_DT_FP32: return ksplit_launch<IMQ_DT_FP32, 8>(a, splits, lds, st);
-    }
-  } else {
-    switch (sdt) {
-      case IMQ_DT_BF16: return ksplit_launch<IMQ_DT_BF16, 4>(a, splits, lds, st);
-      case IMQ_DT_FP16: return ksplit_launch<IMQ_DT_FP16, 4>(a, splits, lds, st);
-      case IMQ_DT_FP32: return ksplit_launch<IMQ_DT_FP32, 4>(a, splits, lds, st);
-    }
+  switch (sdt) {
+    case IMQ_DT_BF16: return ksplit_dispatch<IMQ_DT_BF16>(a, nw, s2, splits, lds, st);
+    case IMQ_DT_FP16: return ksplit_dispatch<IMQ_DT_FP16>(a, nw, s2, splits, lds, st);
+    case IMQ_DT_FP32: return ksplit_dispatch<IMQ_DT_FP32>(a, nw, s2, splits, lds, st);
   }
   return IMQ_ERR_UNSUPPORTED;
 }

@@ -162,8 +162,12 @@ def test_linear_w4_ksplit_shapes(dev, N, K, M):
     others the K-split kernel (workspace from ops): a partial last row block (N % 64), splits with
     unused line-steps (K 768, 1280), Llama down_proj K 14336 (14 splits, 8-tile workgroups),
     both activation-row instantiations (M <= 8, <= 16)."""
+    import torch
     from infinitemodel_amd import _lib
-    assert _lib.lib().imq_linear_workspace_bytes(M, N, K) == -(-K // 1024) * M * N * 4
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    splits4 = -(-K // 1024)
+    short = splits4 * -(-N // 128) < cus and splits4 * -(-N // 64) <= 2 * cus   # 512-code splits
+    assert _lib.lib().imq_linear_workspace_bytes(M, N, K) == (-(-K // 512) if short else splits4) * M * N * 4
     c = C.int4_case(N, K, 128, seed=N + K + M)
     _linear_check(dev, c, M, seed=M)
 

@@ -423,20 +423,22 @@ KS_S2 = 4
 
 
 def ksplit_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024, cus=256):
-    """ksplit_plan in csrc/gemv.hip: (splits, NW, LDS bytes) or None when the K-split kernel
-    declines."""
+    """ksplit_plan in csrc/gemv.hip: (splits, NW, LDS bytes, line-steps per split) or None when
+    the K-split kernel declines."""
     if not (4 < M <= 16) or G != 128 or Kpad % LINE or Kpad <= 0 or N < 1:
         return None
     if N % 4 or sxm % 8 or (ssn * vb) % 4:
         return None
     if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31 or 16 * ssn * vb >= 2 ** 31:
         return None
-    splits = -(-(Kpad // LINE) // KS_S2)
-    nw = 8 if splits * -(-N // 128) >= cus else 4
-    lds = M * (KS_S2 * LINE + 8) * 2 + 2 * KS_S2 * 16 * 4 + nw * 2 * 16 * (KS_S2 * vb // 2) * 4
+    splits4 = -(-(Kpad // LINE) // KS_S2)
+    nw = 8 if splits4 * -(-N // 128) >= cus else 4
+    s2 = 2 if nw == 4 and splits4 * -(-N // 64) <= 2 * cus else KS_S2     # short grids: 512-code splits
+    splits = -(-(Kpad // LINE) // s2)
+    lds = M * (s2 * LINE + 8) * 2 + 2 * s2 * 16 * 4 + nw * 2 * 16 * (s2 * vb // 2) * 4
     if lds > max_lds:
         return None
-    return splits, nw, lds
+    return splits, nw, lds, s2
 
 
 def ksplit_ranges(M, Kpad, N, sqn, sxm, ssn, vb):
@@ -444,8 +446,7 @@ def ksplit_ranges(M, Kpad, N, sqn, sxm, ssn, vb):
     writes (partials, LDS x elements / xs floats / s-z dwords), per the kernel's index arithmetic
     and clamps, over the first and last split and row block; plus the set of (split, m, n) partial
     elements written over every workgroup."""
-    splits, NW, _ = ksplit_plan(M, Kpad, 128, N, sqn, sxm, ssn, vb)
-    S2 = KS_S2
+    splits, NW, _, S2 = ksplit_plan(M, Kpad, 128, N, sqn, sxm, ssn, vb)
     MC = 8 if M <= 8 else 16
     NT = 64 * NW
     KL = Kpad // LINE
@@ -528,21 +529,23 @@ def test_ksplit_in_bounds_and_covering(N, K, M, vb, pad):
     sqn = Kpad // 2 + pad
     plan = ksplit_plan(M, Kpad, 128, N, sqn, Kpad, ng, vb)
     assert plan is not None
-    splits, nw, lds = plan
+    splits, nw, lds, s2 = plan
     if N == 28672:
         assert nw == 8
-    assert splits * KS_S2 * LINE >= Kpad and (splits - 1) * KS_S2 * LINE < Kpad
+    if (N, K) in ((4096, 4096), (6144, 4096)):
+        assert nw == 4 and s2 == 2                    # short grids: 512-code splits
+    assert splits * s2 * LINE >= Kpad and (splits - 1) * s2 * LINE < Kpad
     _, r, written = ksplit_ranges(M, Kpad, N, sqn, Kpad, ng, vb)
     assert r["q"] <= (N - 1) * sqn + Kpad // 2
     assert r["s"] <= N * ng * vb
     assert r["x"] <= (M - 1) * Kpad + Kpad
     assert r["part"] <= splits * M * N
     assert len(written) == splits * M * N            # complete: the reduction reads no stale value
-    xrow = KS_S2 * LINE + 8
+    xrow = s2 * LINE + 8
     x_bytes = M * xrow * 2
     assert r["lds_x"] * 2 <= x_bytes and r["lds_xa"] * 2 <= x_bytes
-    assert r["lds_xs"] <= 2 * KS_S2 * 16
-    sz_off = x_bytes + 2 * KS_S2 * 16 * 4
+    assert r["lds_xs"] <= 2 * s2 * 16
+    sz_off = x_bytes + 2 * s2 * 16 * 4
     assert sz_off + r["lds_sz"] * 4 <= lds
 
 
@@ -684,7 +687,7 @@ def test_ksplit_model_catches_missing_row_clamp():
     """Negative control: without the idle-wave clamp (rowa = row0 for every wave), a partial last
     row block would address rows past N."""
     N, K, M = 100, 1024, 8
-    _, NW, _ = ksplit_plan(M, K, 128, N, K // 2, K, K // 128, 2)
+    _, NW, _, _ = ksplit_plan(M, K, 128, N, K // 2, K, K // 128, 2)
     RB = -(-N // (16 * NW))
     row0 = ((RB - 1) * NW + NW - 1) * 16
     assert row0 >= N and N - 1 - row0 < 0
