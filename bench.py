@@ -328,6 +328,36 @@ def bench_c3(args, dev):
 # ---------------------------------------------------------------------------------------------
 # C4: prefill dequant-GEMM (int4 g128 or int8 per-row), 4096->14336 and 14336->4096
 # ---------------------------------------------------------------------------------------------
+def _c4_module_path(quant: str, shapes, dev) -> dict:
+    """Which path the drop-in module itself keeps for prefill at each C4 shape: the QuantLinear4 /
+    int8 QuantLinear built over the same kind of weights, prepare_fused run (its self-check and
+    its measured naive-vs-fused rule at the production prefill chunk), the decision read back.
+    The module's log lines are kept out of stdout (one JSON line there)."""
+    import contextlib
+    import io
+    from infinitemodel_amd import workloads as wl, worker_quant as wq
+    out = {}
+    log = io.StringIO()
+    with contextlib.redirect_stdout(log):
+        for i, (N, K) in enumerate(shapes):
+            if quant == "int4":
+                L = wl.rtn_int4_linear(N, K, 5000 + i, dev)
+                mod = wq._quant4_linear_cls()(L.q, L.s, L.z, None, K, 128)
+                mod.prepare_fused()
+                thr = getattr(mod, "_naive_m_min", 0)
+                path = ("naive (fused op not bound)" if getattr(mod, "_fused", None) is None
+                        else f"naive from row bucket {thr}" if thr else "fused at every M")
+            else:
+                q, s = wl.int8_linear(N, K, 5000 + i, dev)
+                mod = wq._quant_linear_cls()(q, s, None)
+                mod.prepare_fused()
+                m_max = getattr(mod, "_w8_m_max", None)
+                path = ("naive (int8 op not bound)" if getattr(mod, "_w8", None) is None
+                        else "fused at every M" if not m_max else f"fused up to M={m_max}")
+            out[f"{K}->{N}"] = path
+    return out
+
+
 def bench_c4(args, dev):
     import torch
     from infinitemodel_amd import ops, workloads as wl
@@ -372,17 +402,20 @@ def bench_c4(args, dev):
 
     ms_naive = _time_steps(naive_step, max(3, args.steps // 4), 2)
     tf_naive = sum(2.0 * M * N * K for N, K, _ in naive_sets) / (ms_naive * 1e-3)
+    bits = 4 if args.quant == "int4" else 8
+    gemm = (f"gemm_rb_kernel<{bits}> + rb_reduce_kernel (register-B GEMM" if M > 512
+            else f"gemm_wq_kernel<{bits}> (LDS-dequant GEMM")
     roof = {"bound": "mfma", "achieved": round(tf / 1e12, 2), "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s",
             "frac": round(tf / BF16_PEAK, 4), "traffic": _traffic(f"c4_{args.quant}_m{M}"),
-            "kernel": f"gemm_wq_kernel<{4 if args.quant == 'int4' else 8}> (imq_linear_"
-                      f"{'w4' if args.quant == 'int4' else 'w8'} prefill GEMM)",
+            "kernel": f"{gemm}, imq_linear_{'w4' if bits == 4 else 'w8'} prefill)",
             "avg_launch_us": round(ms * 1e3 / len(sets), 3), "flops_per_launch": flops / len(sets)}
     wbytes = sum(N * K * (0.53125 if args.quant == "int4" else 1.0) for N, K, _ in sets)
     cfg = {"workload": f"C4 prefill {args.quant} 4096->14336 and 14336->4096, M={M}", "M": M,
            "quant": args.quant, "launches_per_step": len(sets), "distinct_bytes_per_step": int(wbytes),
            "naive": {"value": round(tf_naive / 1e12, 3), "unit": "TFLOP/s",
                      "path": "imq dequant to bf16 + F.linear (hipBLASLt), both shapes, eager",
-                     "fused_speedup": round(tf / tf_naive, 3)}}
+                     "fused_speedup": round(tf / tf_naive, 3)},
+           "module_path": _c4_module_path(args.quant, shapes, dev)}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path
