@@ -402,6 +402,25 @@ def bench_c4(args, dev):
 
     ms_naive = _time_steps(naive_step, max(3, args.steps // 4), 2)
     tf_naive = sum(2.0 * M * N * K for N, K, _ in naive_sets) / (ms_naive * 1e-3)
+    # the platform's own bf16 GEMM (hipBLASLt through torch.mm) on unquantized bf16 weights of the
+    # same shapes, no dequantization: the rate the vendor library reaches on this box and shape
+    dense_sets = []
+    for i, (N, K, _fn) in enumerate(sets[:2]):
+        if args.quant == "int4":
+            L = wl.rtn_int4_linear(N, K, 5000 + i, dev)
+            wt = ops.dequant_w4(L.q, L.s, L.z, K, 128, torch.bfloat16)
+        else:
+            q, s_ = wl.int8_linear(N, K, 5000 + i, dev)
+            wt = ops.dequant_w8(q, s_, torch.bfloat16).to(torch.bfloat16)
+        dense_sets.append((N, K, wt))
+
+    def dense_step():
+        for N, K, wt in dense_sets:
+            torch.mm(xs[K], wt.t(), out=ys[N])
+
+    ms_dense = _time_steps(dense_step, max(3, args.steps // 4), 2)
+    tf_dense = sum(2.0 * M * N * K for N, K, _ in dense_sets) / (ms_dense * 1e-3)
+    del dense_sets
     bits = 4 if args.quant == "int4" else 8
     gemm = (f"gemm_rb_kernel<{bits}> + rb_reduce_kernel (register-B GEMM" if M > 512
             else f"gemm_wq_kernel<{bits}> (LDS-dequant GEMM")
@@ -415,6 +434,9 @@ def bench_c4(args, dev):
            "naive": {"value": round(tf_naive / 1e12, 3), "unit": "TFLOP/s",
                      "path": "imq dequant to bf16 + F.linear (hipBLASLt), both shapes, eager",
                      "fused_speedup": round(tf / tf_naive, 3)},
+           "bf16_gemm": {"value": round(tf_dense / 1e12, 3), "unit": "TFLOP/s",
+                         "path": "torch.mm (hipBLASLt) on unquantized bf16 weights, both shapes, eager",
+                         "fused_ratio": round(tf / tf_dense, 3)},
            "module_path": _c4_module_path(args.quant, shapes, dev)}
     cpu = None
     if not args.no_cpu:
