@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define IMQ_ABI_VERSION 5
+#define IMQ_ABI_VERSION 6
 
 #define IMQ_DT_BF16 0
 #define IMQ_DT_FP16 1
@@ -231,6 +231,40 @@ int imq_gptq_int2_solve(float* W, int64_t ldw, int64_t out, int64_t in_f, const 
                         int64_t group_size, int grid, double maxshrink, int64_t blocksize, uint8_t* qweight,
                         int64_t ldq, float* scale, float* zero, int64_t ldsz, float* dq, int64_t lddq,
                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- launch plans (no counterpart in the reference) -----------------------------------------
+ * For test harnesses and tooling: the launch plan the dispatcher computes for a shape, from the
+ * same host functions its launchers call, without a device (the device's LDS bytes per
+ * workgroup and CU count are arguments). The CPU bounds model of the kernels' address ranges
+ * checks its restated plans against these.
+ *   in[10] = {M, K_pad (K for int8), group_size (0 for int8), N, q_row_stride (bytes),
+ *             x_row_stride (elements), s_stride_n (elements), s_dtype, max_lds_bytes, cus};
+ *             group strides are 1, the zero point's strides and dtype are the scale's.
+ *   out[5] = {taken (1 when that kernel takes the call, else 0 and the rest 0), p1, p2, p3,
+ *             LDS bytes per workgroup}:
+ *     IMQ_PLAN_W4_LINE    int4 line kernel: p1 line-steps per wave, p2 waves
+ *     IMQ_PLAN_W4_KSPLIT  int4 K-split kernel: p1 splits, p2 row tiles per workgroup,
+ *                         p3 line-steps per split
+ *     IMQ_PLAN_W4_WSPLIT  int4 wave-split kernel: p1 line-steps per wave, p2 waves
+ *     IMQ_PLAN_W4_SKINNY  int4 skinny kernel: p1 K steps per wave per round, p2 waves
+ *                         (taken whenever K_pad is a whole number of 128-code steps)
+ *     IMQ_PLAN_W2_LINE    int2 line kernel: p1 line-steps per wave, p2 waves
+ *     IMQ_PLAN_W2_KSPLIT  int2 K-split kernel: p1 splits, p2 row tiles per workgroup
+ *     IMQ_PLAN_W8_LINE    int8 line kernel: p1 line-steps per wave, p2 waves
+ *     IMQ_PLAN_GEMM       LDS-dequant GEMM: p1 tile rows, p2 tile columns, p3 K splits
+ *     IMQ_PLAN_GEMM_RB    register-B GEMM (int4 with group_size, int8 when it is 0):
+ *                         p1 32-row blocks per wave, p2 K splits
+ * Returns IMQ_OK, or IMQ_ERR_INVALID for an unknown kind or a null pointer. */
+#define IMQ_PLAN_W4_LINE 1
+#define IMQ_PLAN_W4_KSPLIT 2
+#define IMQ_PLAN_W4_WSPLIT 3
+#define IMQ_PLAN_W4_SKINNY 4
+#define IMQ_PLAN_W2_LINE 5
+#define IMQ_PLAN_W2_KSPLIT 6
+#define IMQ_PLAN_W8_LINE 7
+#define IMQ_PLAN_GEMM 8
+#define IMQ_PLAN_GEMM_RB 9
+int imq_launch_plan(int kind, const int64_t* in, int64_t* out);
 
 #ifdef __cplusplus
 }

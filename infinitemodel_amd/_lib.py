@@ -75,7 +75,11 @@ SIGNATURES = {
     "imq_gptq_int2_solve": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_int, ctypes.c_double,
                                      _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
                                      _c_vp]),
+    "imq_launch_plan": (_c_int, [_c_int, _c_vp, _c_vp]),
 }
+
+IMQ_PLAN_W4_LINE, IMQ_PLAN_W4_KSPLIT, IMQ_PLAN_W4_WSPLIT, IMQ_PLAN_W4_SKINNY = 1, 2, 3, 4
+IMQ_PLAN_W2_LINE, IMQ_PLAN_W2_KSPLIT, IMQ_PLAN_W8_LINE, IMQ_PLAN_GEMM, IMQ_PLAN_GEMM_RB = 5, 6, 7, 8, 9
 
 
 class ImqUnavailable(RuntimeError):
@@ -134,3 +138,13 @@ def dtype_code(dt) -> int:
     if dt == torch.float32:
         return IMQ_DT_FP32
     raise TypeError(f"unsupported dtype {dt} (bf16/fp16/fp32 only)")
+
+
+def launch_plan(kind: int, M: int, K: int, G: int, N: int, sqn: int = 0, sxm: int = 0, ssn: int = 0,
+                sdt: int = IMQ_DT_BF16, max_lds: int = 160 * 1024, cus: int = 256):
+    """The dispatcher's launch plan for a shape (imq_launch_plan; host code only, no device):
+    None when that kernel does not take the call, else (p1, p2, p3, lds_bytes)."""
+    inp = (ctypes.c_int64 * 10)(M, K, G, N, sqn, sxm, ssn, sdt, max_lds, cus)
+    out = (ctypes.c_int64 * 5)()
+    call("imq_launch_plan", kind, ctypes.cast(inp, ctypes.c_void_p), ctypes.cast(out, ctypes.c_void_p))
+    return tuple(out[1:]) if out[0] else None

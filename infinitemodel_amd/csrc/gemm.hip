@@ -654,6 +654,18 @@ int gemm_bits(const GemmArgs& a, int sdt, int zdt, void* ws, int64_t wsb, hipStr
 
 // Workspace bytes a split-K launch of this shape may use (0: no launch splits K): the larger of
 // the register-B GEMM's plan (int4 / int8) and the LDS-dequant GEMM's (int2, other layouts).
+// The LDS-dequant GEMM's tile and split plan for an M x N x K call on a device of `cus` CUs,
+// without a device: out = {1, tile rows, tile columns, K splits}.
+void gemm_plan_query(int64_t M, int64_t N, int64_t K, int cus, int64_t* out) {
+  int s = 1;
+  if (use_big(M)) split_bytes<CfgBig>(M, N, K, cus, &s);
+  else split_bytes<CfgSmall>(M, N, K, cus, &s);
+  out[0] = 1;
+  out[1] = use_big(M) ? CfgBig::BM : CfgSmall::BM;
+  out[2] = use_big(M) ? CfgBig::BN : CfgSmall::BN;
+  out[3] = s;
+}
+
 int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 16 || N <= 0 || K % 64 != 0) return 0;
   const int cus = device_info().cus;

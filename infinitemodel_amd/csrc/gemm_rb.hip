@@ -124,6 +124,17 @@ bool rb_takes(int bits, int64_t M, int64_t N, int64_t K, int64_t G) {
   return M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff;
 }
 
+// The register-B GEMM's plan for an M x N x K call (int4 groups of G, or int8) on a device of
+// `cus` CUs, without a device: out = {takes the call, 32-row blocks per wave, K splits}.
+void rb_plan_query(int bits, int64_t M, int64_t N, int64_t K, int64_t G, int cus, int64_t* out) {
+  int ib = 0, s = 0;
+  const bool takes = rb_takes(bits, M, N, K, G);
+  if (takes) rb_plan(M, N, K, cus, &ib, &s);
+  out[0] = takes ? 1 : 0;
+  out[1] = ib;
+  out[2] = s;
+}
+
 int64_t rb_workspace_bytes(int bits, int64_t M, int64_t N, int64_t K, int cus) {
   if (!rb_takes(bits, M, N, K, 128)) return 0;
   int ib, s;

@@ -2083,22 +2083,30 @@ int skinny_grid(int NT, int W, size_t lds, const DevInfo& di) {
   return (int)(g < NT ? g : NT);
 }
 
-template <int SDT, int ZDT>
-int skinny_dispatch(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
-  SkinnyArgs a = a0;
-  const int KS = a.Kpad / kStep;
-  const int NT = (a.N + 15) / 16;
-  // S steps (S KB of packed weights) per wave per round, W waves per tile (<= 16). Measured on
-  // MI355X at Llama-8B shapes: many tiles (N >= 16K) prefer deep batches (S=8) in persistent
-  // workgroups; fewer tiles prefer splitting K over more waves (S=4), one tile per workgroup
-  // while x is small.
-  // (S=8 with more than 8 waves and fp16/fp32 scales would exceed the 16-wave register budget)
-  const bool wide = NT >= 1024 && KS >= 16 && (SDT == IMQ_DT_BF16 || (KS + 7) / 8 <= 8);
+// S steps (S KB of packed weights) per wave per round, W waves per tile (<= 16). Measured on
+// MI355X at Llama-8B shapes: many tiles (N >= 16K) prefer deep batches (S=8) in persistent
+// workgroups; fewer tiles prefer splitting K over more waves (S=4), one tile per workgroup while
+// x is small. (S=8 with more than 8 waves and fp16/fp32 scales would exceed the 16-wave register
+// budget.) Returns whether the deep form was chosen.
+bool skinny_shape(int KS, int NT, bool bf16_scales, int* So, int* Wo) {
+  const bool wide = NT >= 1024 && KS >= 16 && (bf16_scales || (KS + 7) / 8 <= 8);
   int S, W;
   if (wide) { S = 8; W = (KS + 7) / 8; }
   else { S = 4; W = (KS + 3) / 4; }
   if (W > 16) W = 16;
   if (W < 1) W = 1;
+  *So = S;
+  *Wo = W;
+  return wide;
+}
+
+template <int SDT, int ZDT>
+int skinny_dispatch(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
+  SkinnyArgs a = a0;
+  const int KS = a.Kpad / kStep;
+  const int NT = (a.N + 15) / 16;
+  int S, W;
+  const bool wide = skinny_shape(KS, NT, SDT == IMQ_DT_BF16, &S, &W);
   const size_t resident = (size_t)a.M * (KS * kStep + kXPad) * 2 + (size_t)KS * 64 + (size_t)2 * W * 256 * 4;
   if (resident <= (size_t)di.max_lds) {
     a.chunk_steps = KS;
@@ -2698,5 +2706,55 @@ int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t
     case IMQ_DT_FP32: return w8_dispatch<IMQ_DT_FP32>(a, di, st);
   }
   return IMQ_ERR_INVALID;
+}
+
+// The decode launchers' plans for a shape, without a device: the same plan functions the
+// launchers call, with the device's LDS bytes and CU count as arguments. in = {M, K_pad, G, N,
+// q_row_stride, x_row_stride, s_stride_n, s_dtype, max_lds, cus} (unit group strides, zero
+// strides and dtype equal to the scale's); out = {taken, p1, p2, p3, lds}.
+int decode_plan_query(int kind, const int64_t* in, int64_t* out) {
+  const int64_t M = in[0], Kpad = in[1], G = in[2], N = in[3], sqn = in[4], sxm = in[5], ssn = in[6];
+  const int sdt = (int)in[7], max_lds = (int)in[8], cus = (int)in[9];
+  int p1 = 0, p2 = 0, p3 = 0;
+  size_t lds = 0;
+  bool ok = false;
+  switch (kind) {
+    case IMQ_PLAN_W4_LINE:
+      ok = line_plan(M, Kpad, G, N, sqn, sxm, ssn, 1, ssn, 1, sdt, sdt, max_lds, &p1, &p2, &lds);
+      break;
+    case IMQ_PLAN_W4_KSPLIT:
+      ok = ksplit_plan(M, Kpad, G, N, sqn, sxm, ssn, 1, ssn, 1, sdt, sdt, max_lds, cus, &p1, &p2, &p3, &lds);
+      break;
+    case IMQ_PLAN_W4_WSPLIT:
+      p1 = wsplit_plan(M, Kpad, G, N, sqn, sxm, ssn, 1, ssn, 1, sdt, sdt, max_lds, cus);
+      ok = p1 != 0;
+      if (ok) {
+        p2 = kWsNW;
+        lds = (size_t)wsplit_lds(p1, kWsNW);
+      }
+      break;
+    case IMQ_PLAN_W4_SKINNY:
+      if (Kpad <= 0 || Kpad % kStep != 0 || N < 1) break;
+      skinny_shape((int)(Kpad / kStep), (int)((N + 15) / 16), sdt == IMQ_DT_BF16, &p1, &p2);
+      ok = true;
+      break;
+    case IMQ_PLAN_W2_LINE:
+      ok = line2_plan(M, Kpad, G, N, sqn, sxm, ssn, 1, ssn, 1, sdt, sdt, max_lds, &p1, &p2, &lds);
+      break;
+    case IMQ_PLAN_W2_KSPLIT:
+      ok = ksplit2_plan(M, Kpad, G, N, sqn, sxm, ssn, 1, ssn, 1, sdt, sdt, max_lds, cus, &p1, &p2, &lds);
+      break;
+    case IMQ_PLAN_W8_LINE:
+      ok = line8_plan(M, Kpad, N, sqn, sxm, max_lds, &p1, &p2, &lds);
+      break;
+    default:
+      return IMQ_ERR_INVALID;
+  }
+  out[0] = ok ? 1 : 0;
+  out[1] = ok ? p1 : 0;
+  out[2] = ok ? p2 : 0;
+  out[3] = ok ? p3 : 0;
+  out[4] = ok ? (int64_t)lds : 0;
+  return IMQ_OK;
 }
 }  // namespace imq

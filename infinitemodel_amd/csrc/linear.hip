@@ -24,6 +24,9 @@ int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, cons
             const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
             int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
 int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int decode_plan_query(int kind, const int64_t* in, int64_t* out);
+void gemm_plan_query(int64_t M, int64_t N, int64_t K, int cus, int64_t* out);
+void rb_plan_query(int bits, int64_t M, int64_t N, int64_t K, int64_t G, int cus, int64_t* out);
 template <int BITS>
 int generic_gemv(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
                  const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn,
@@ -55,6 +58,25 @@ extern "C" int64_t imq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K_pa
   const int64_t g = imq::gemm_workspace_bytes(M, N, K_pad);
   const int64_t d = imq::ksplit_workspace_bytes(M, N, K_pad);
   return g > d ? g : d;
+}
+
+extern "C" int imq_launch_plan(int kind, const int64_t* in, int64_t* out) {
+  if (!in || !out) return IMQ_ERR_INVALID;
+  for (int i = 0; i < 5; ++i) out[i] = 0;
+  const int64_t M = in[0], K = in[1], G = in[2], N = in[3];
+  const int cus = (int)in[9];
+  if (kind == IMQ_PLAN_GEMM) {
+    if (M <= 16 || N <= 0 || K <= 0 || K % 64 != 0 || cus <= 0) return IMQ_OK;
+    imq::gemm_plan_query(M, N, K, cus, out);
+    return IMQ_OK;
+  }
+  if (kind == IMQ_PLAN_GEMM_RB) {
+    if (cus <= 0) return IMQ_OK;
+    imq::rb_plan_query(G == 0 ? 8 : 4, M, N, K, G == 0 ? 128 : G, cus, out);
+    return IMQ_OK;
+  }
+  if (in[7] != IMQ_DT_BF16 && in[7] != IMQ_DT_FP16 && in[7] != IMQ_DT_FP32) return IMQ_ERR_INVALID;
+  return imq::decode_plan_query(kind, in, out);
 }
 
 extern "C" const char* imq_strerror(int status) {

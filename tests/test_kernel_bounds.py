@@ -5,6 +5,10 @@ the kernel's per-lane address arithmetic (load_round, the strip loads and the x 
 checks that every byte a launch can touch lies inside its buffer, for a matrix of shapes,
 scale dtypes, the de-alias padded row view and the exact-fit (no slack) allocation. It guards
 against out-of-bounds reads that a generous allocator would hide on the GPU.
+
+The restated launch plans are checked against the compiled dispatcher's own (imq_launch_plan,
+host code of libimq.so that needs no device) at the end of the file, so the model cannot drift
+from the kernels' real launch shapes unnoticed.
 """
 import math
 
@@ -562,7 +566,13 @@ def test_ksplit_plan_declines():
 WS_NW = 8
 
 
-def wsplit_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, cus=256):
+def wsplit_lds(R, NW=WS_NW):
+    """wsplit_lds in csrc/gemv.hip: per-wave activation slices and group sums, the double-buffered
+    partials, 8 tiles of buffered bf16 results."""
+    return NW * (16 * (R * LINE + 8) * 2 + 2 * R * 16 * 4) + 2 * NW * 256 * 4 + 8 * 256 * 2
+
+
+def wsplit_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, cus=256, max_lds=160 * 1024):
     """wsplit_plan in csrc/gemv.hip: R (line-steps per wave) or None when the kernel declines."""
     if not (4 < M <= 16) or G != 128 or Kpad not in (WS_NW * LINE, 2 * WS_NW * LINE):
         return None
@@ -570,9 +580,10 @@ def wsplit_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, cus=256):
         return None
     if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31:
         return None
-    if -(-N // 16) < 4 * cus:
+    R = Kpad // (WS_NW * LINE)
+    if wsplit_lds(R) > max_lds or -(-N // 16) < 4 * cus:
         return None
-    return Kpad // (WS_NW * LINE)
+    return R
 
 
 def wsplit_ranges(M, Kpad, N, sqn, sxm, ssn, vb, cus=256, clamp=True):
@@ -1256,3 +1267,89 @@ def test_dec_model_catches_expert_stride_times_row_stride():
     _, s_hi = dec_ranges(True, E, H, Kpad, vb, sqe, sqn, sse, ssn, [(E - 1, E - 1)], [H - 8],
                          scale_index=lambda ex, row: (ex * sse + row) * ssn)
     assert s_hi > E * sse * vb
+
+
+# ---- the restated plans against the compiled dispatcher's (imq_launch_plan) ---------------------
+# Every plan above restates a host function of the library; imq_launch_plan runs those functions
+# (host code, no device), so a drift between the model and the compiled dispatch fails here.
+
+def _lib_plan(kind, M, K, G, N, sqn, sxm, ssn, vb, max_lds, cus):
+    import os
+    from infinitemodel_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} is not built")
+    sdt = _lib.IMQ_DT_FP32 if vb == 4 else _lib.IMQ_DT_BF16
+    return _lib.launch_plan(kind, M, K, G, N, sqn, sxm, ssn, sdt, max_lds, cus)
+
+
+TIE_SHAPES = [(4096, 4096), (6144, 4096), (28672, 4096), (4096, 14336), (28672, 8192), (8192, 28672),
+              (16400, 2048), (16392, 4096), (37, 512), (100, 1536), (20, 1024), (64, 16384), (17, 256),
+              (151936, 3584), (2880, 2944), (80, 2560)]
+TIE_DEVICES = [(160 * 1024, 256), (64 * 1024, 256), (160 * 1024, 80), (160 * 1024, 32)]
+
+
+@pytest.mark.parametrize("max_lds,cus", TIE_DEVICES)
+@pytest.mark.parametrize("vb", [2, 4])
+def test_decode_plans_match_compiled_dispatch(max_lds, cus, vb):
+    from infinitemodel_amd import _lib
+    checked = 0
+    for N, K in TIE_SHAPES:
+        for M in (1, 2, 3, 4, 5, 8, 12, 16):
+            for pad in (0, 64):
+                sxm = K + pad
+                # int4 g128
+                Kp = -(-K // 128) * 128
+                sqn, ssn = Kp // 2 + pad, -(-Kp // 128) + pad // 2
+                args = (M, Kp, 128, N, sqn, sxm + (Kp - K), ssn, vb, max_lds, cus)
+                want = line_plan(M, Kp, 128, N, sqn, sxm + (Kp - K), ssn, vb, max_lds)
+                got = _lib_plan(_lib.IMQ_PLAN_W4_LINE, *args)
+                assert (got and (got[0], got[1], got[3])) == want, ("w4 line", N, K, M, pad)
+                want = ksplit_plan(M, Kp, 128, N, sqn, sxm + (Kp - K), ssn, vb, max_lds, cus)
+                got = _lib_plan(_lib.IMQ_PLAN_W4_KSPLIT, *args)
+                assert (got and (got[0], got[1], got[3], got[2])) == want, ("w4 ksplit", N, K, M, pad)
+                want = wsplit_plan(M, Kp, 128, N, sqn, sxm + (Kp - K), ssn, vb, cus, max_lds)
+                got = _lib_plan(_lib.IMQ_PLAN_W4_WSPLIT, *args)
+                assert (got and got[0]) == want, ("w4 wsplit", N, K, M, pad)
+                _, S, W = _dispatch(Kp, N, vb == 2)
+                got = _lib_plan(_lib.IMQ_PLAN_W4_SKINNY, *args)
+                assert got[:2] == (S, W), ("w4 skinny", N, K, M)
+                # int2 g64
+                K2 = -(-K // 64) * 64
+                sqn2, ssn2 = K2 // 4 + pad, K2 // 64 + pad // 2
+                args2 = (M, K2, 64, N, sqn2, K2 + pad, ssn2, vb, max_lds, cus)
+                want = line2_plan(M, K2, 64, N, sqn2, K2 + pad, ssn2, vb, max_lds)
+                got = _lib_plan(_lib.IMQ_PLAN_W2_LINE, *args2)
+                assert (got and (got[0], got[1], got[3])) == want, ("w2 line", N, K, M, pad)
+                want = ksplit2_plan(M, K2, 64, N, sqn2, K2 + pad, ssn2, vb, max_lds, cus)
+                got = _lib_plan(_lib.IMQ_PLAN_W2_KSPLIT, *args2)
+                assert (got and (got[0], got[1], got[3])) == want, ("w2 ksplit", N, K, M, pad)
+                # int8 per row (K as given, no padding)
+                want = line8_plan(M, K, N, K + pad, K + pad, max_lds)
+                got = _lib_plan(_lib.IMQ_PLAN_W8_LINE, M, K, 0, N, K + pad, K + pad, 0, vb, max_lds, cus)
+                assert (got and (got[0], got[1], got[3])) == want, ("w8 line", N, K, M, pad)
+                checked += 1
+    assert checked == len(TIE_SHAPES) * 8 * 2
+
+
+@pytest.mark.parametrize("cus", [256, 80, 32])
+def test_gemm_plans_match_compiled_dispatch(cus):
+    from infinitemodel_amd import _lib
+    for N, K in TIE_SHAPES:
+        K64 = -(-K // 64) * 64
+        for M in (17, 64, 128, 129, 512, 513, 2048, 4096):
+            BM, _threads = gemm_cfg(M, N)
+            T = -(-M // BM) * -(-N // 128)
+            s = split_plan(T, K64 // 64, cus)
+            got = _lib_plan(_lib.IMQ_PLAN_GEMM, M, K64, 128, N, 0, 0, 0, 2, 160 * 1024, cus)
+            assert got[:3] == (BM, 128, s), (N, K, M)
+
+
+def test_register_b_plan_at_the_prefill_shapes():
+    """The register-B GEMM's plan at the C4 prefill shapes on 256 CUs, as documented: 256-row
+    tiles (8 blocks per wave), one K split for 4096->14336, two for 14336->4096 (int4 and int8);
+    it declines 512 rows and below."""
+    from infinitemodel_amd import _lib
+    for G in (128, 0):
+        assert _lib_plan(_lib.IMQ_PLAN_GEMM_RB, 2048, 4096, G, 14336, 0, 0, 0, 2, 0, 256)[:2] == (8, 1)
+        assert _lib_plan(_lib.IMQ_PLAN_GEMM_RB, 2048, 14336, G, 4096, 0, 0, 0, 2, 0, 256)[:2] == (8, 2)
+        assert _lib_plan(_lib.IMQ_PLAN_GEMM_RB, 512, 4096, G, 14336, 0, 0, 0, 2, 0, 256) is None
