@@ -438,6 +438,9 @@ __global__ __launch_bounds__(64 * W) void w4_skinny_chunked_kernel(SkinnyArgs a)
 // wave partials meet in LDS once at the end (fixed order, deterministic).
 // ---------------------------------------------------------------------------------------------
 constexpr int kLine = 256;
+#ifndef IMQ_LINE_PAIRED
+#define IMQ_LINE_PAIRED 1
+#endif
 
 // lane c of each 16-lane row receives the value of lane c ^ 8 (DPP row_ror:8)
 IMQ_DEV float row_swap8(float v) {
@@ -550,7 +553,11 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
   const uint32_t magic = magic_bf16_128x2();
-  const uint16_t* xa = xw + (c < M ? c : M - 1) * xrow + 32 * ar;
+  // PAIRED (M <= 2): A lane row m < M reads activation row m in group 2l, M <= m < 2M row m - M
+  // in group 2l+1 (128 codes on), other rows repeat row 0 of group 2l (their D rows are unused)
+  constexpr bool PAIRED = MC <= 2 && IMQ_LINE_PAIRED;
+  const uint16_t* xa = PAIRED ? xw + (c < 2 * M ? c % M : 0) * xrow + 32 * ar + (c >= M && c < 2 * M ? 128 : 0)
+                              : xw + (c < M ? c : M - 1) * xrow + 32 * ar;
   const uint32_t* sc_c = szl + c * DPR;
   const uint32_t* sc_x = szl + (c ^ 8) * DPR;
   const uint32_t* zr_c = szl + 16 * DPR + c * DPR;
@@ -569,7 +576,7 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       A0[k] = *(const bf16x8_t*)(xa + i * kLine + 8 * k);
-      A1[k] = *(const bf16x8_t*)(xa + i * kLine + 128 + 8 * k);
+      if constexpr (!PAIRED) A1[k] = *(const bf16x8_t*)(xa + i * kLine + 128 + 8 * k);
     }
     // read unconditionally (the staged strip covers every i), then select: a conditional read
     // becomes a branch with an LDS round trip inside each line-step
@@ -579,24 +586,45 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
     const float cz0 = -(128.f + val(zr_c, 2 * i)) * s0;
     const float cz1 = -(128.f + val(zr_x, 2 * i + 1)) * s1;
     const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
-    u32x4_t gA, gB;
+    if constexpr (PAIRED) {
+      // A rows [0, M) hold group 2l, rows [M, 2M) group 2l+1, so each full-line load feeds its
+      // MFMAs as loaded: column c < 8 of load L0 (row c, group 2l) meets D rows [0, M), column
+      // c >= 8 (row c ^ 8, group 2l+1) D rows [M, 2M); L1 the other way round
+      f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      gA[d] = lo8 ? w0[d] : w1[d];
-      gB[d] = lo8 ? w1[d] : w0[d];
-    }
-    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < 4; ++k) {
+        a0 = mfma16x16x32(A0[k], unpack_nib8_bf16(w0[k], magic), a0);
+        a1 = mfma16x16x32(A0[k], unpack_nib8_bf16(w1[k], magic), a1);
+      }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      acc0 = mfma16x16x32(A0[k], unpack_nib8_bf16(gA[k], magic), acc0);
-      acc1 = mfma16x16x32(A1[k], unpack_nib8_bf16(gB[k], magic), acc1);
-    }
+      for (int r = 0; r < RC; ++r) {
+        const float accA = lo8 ? a0[r] : a1[r];            // row c, group 2l
+        const float accB = lo8 ? a1[MC + r] : a0[MC + r];  // row c ^ 8, group 2l+1
+        y0[r] = fmaf(cz0, xs0[r], y0[r]);
+        y1[r] = fmaf(cz1, xs1[r], y1[r]);
+        y0[r] = fmaf(s0, accA, y0[r]);
+        y1[r] = fmaf(s1, accB, y1[r]);
+      }
+    } else {
+      u32x4_t gA, gB;
 #pragma unroll
-    for (int r = 0; r < RC; ++r) {
-      y0[r] = fmaf(cz0, xs0[r], y0[r]);
-      y1[r] = fmaf(cz1, xs1[r], y1[r]);
-      y0[r] = fmaf(s0, acc0[r], y0[r]);
-      y1[r] = fmaf(s1, acc1[r], y1[r]);
+      for (int d = 0; d < 4; ++d) {
+        gA[d] = lo8 ? w0[d] : w1[d];
+        gB[d] = lo8 ? w1[d] : w0[d];
+      }
+      f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc0 = mfma16x16x32(A0[k], unpack_nib8_bf16(gA[k], magic), acc0);
+        acc1 = mfma16x16x32(A1[k], unpack_nib8_bf16(gB[k], magic), acc1);
+      }
+#pragma unroll
+      for (int r = 0; r < RC; ++r) {
+        y0[r] = fmaf(cz0, xs0[r], y0[r]);
+        y1[r] = fmaf(cz1, xs1[r], y1[r]);
+        y0[r] = fmaf(s0, acc0[r], y0[r]);
+        y1[r] = fmaf(s1, acc1[r], y1[r]);
+      }
     }
   }
   // D row m = 4*ar + r; rows m < M <= 4 live in lanes ar == 0
