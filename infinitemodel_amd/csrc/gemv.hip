@@ -1930,7 +1930,13 @@ __global__ __launch_bounds__(64 * MAXW) void w8_line_kernel(SkinnyArgs a) {
   // LDS is written and read by this wave only; its LDS operations execute in order
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-  const uint16_t* xa = xw + (c < M ? c : M - 1) * xrow + 16 * ar;
+  // PAIRED (M == 2): A lane row m < M reads activation row m in the line-step's first half,
+  // M <= m < 2M row m - M in its second half (64 codes on), other rows repeat row 0 (their D rows
+  // are unused). Measured on the int8 lm_head 3584 -> 152064: M = 2 4811-4831 -> 5138-5508 GB/s;
+  // at M = 1 it measured 2% slower, so M = 1 keeps the per-lane selects.
+  constexpr bool PAIRED = MC == 2 && IMQ_LINE_PAIRED;
+  const uint16_t* xa = PAIRED ? xw + (c < 2 * M ? c % M : 0) * xrow + 16 * ar + (c >= M && c < 2 * M ? 64 : 0)
+                              : xw + (c < M ? c : M - 1) * xrow + 16 * ar;
   float y0[4] = {0.f, 0.f, 0.f, 0.f}, y1[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
@@ -1940,24 +1946,41 @@ __global__ __launch_bounds__(64 * MAXW) void w8_line_kernel(SkinnyArgs a) {
     const f32x4_t xs1 = *(const f32x4_t*)(xs + (2 * i + 1) * 16 + 4 * ar);
     const bf16x8_t a00 = *(const bf16x8_t*)(xa + i * kLine8);
     const bf16x8_t a01 = *(const bf16x8_t*)(xa + i * kLine8 + 8);
-    const bf16x8_t a10 = *(const bf16x8_t*)(xa + i * kLine8 + 64);
-    const bf16x8_t a11 = *(const bf16x8_t*)(xa + i * kLine8 + 72);
     const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
-    u32x4_t gA, gB;
+    if constexpr (PAIRED) {
+      // each load feeds its MFMAs as loaded: lanes c < 8 of L0 (row c, first half) meet D rows
+      // [0, M), lanes c >= 8 (row c ^ 8, second half) D rows [M, 2M); L1 the other way round
+      f32x4_t p0 = {0.f, 0.f, 0.f, 0.f}, p1 = {0.f, 0.f, 0.f, 0.f};
+      p0 = mfma16x16x32(a00, biased_i8x8_bf16(w0[0], w0[1]), p0);
+      p1 = mfma16x16x32(a00, biased_i8x8_bf16(w1[0], w1[1]), p1);
+      p0 = mfma16x16x32(a01, biased_i8x8_bf16(w0[2], w0[3]), p0);
+      p1 = mfma16x16x32(a01, biased_i8x8_bf16(w1[2], w1[3]), p1);
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      gA[d] = lo8 ? w0[d] : w1[d];                   // own row c, first half
-      gB[d] = lo8 ? w1[d] : w0[d];                   // row c ^ 8, second half
-    }
-    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    acc0 = mfma16x16x32(a00, biased_i8x8_bf16(gA[0], gA[1]), acc0);
-    acc1 = mfma16x16x32(a10, biased_i8x8_bf16(gB[0], gB[1]), acc1);
-    acc0 = mfma16x16x32(a01, biased_i8x8_bf16(gA[2], gA[3]), acc0);
-    acc1 = mfma16x16x32(a11, biased_i8x8_bf16(gB[2], gB[3]), acc1);
+      for (int r = 0; r < RC; ++r) {
+        const float acc0 = lo8 ? p0[r] : p1[r];             // own row c, first half
+        const float acc1 = lo8 ? p1[MC + r] : p0[MC + r];   // row c ^ 8, second half
+        y0[r] = fmaf(v, fmaf(-128.f, xs0[r], acc0), y0[r]);
+        y1[r] = fmaf(v, fmaf(-128.f, xs1[r], acc1), y1[r]);
+      }
+    } else {
+      const bf16x8_t a10 = *(const bf16x8_t*)(xa + i * kLine8 + 64);
+      const bf16x8_t a11 = *(const bf16x8_t*)(xa + i * kLine8 + 72);
+      u32x4_t gA, gB;
 #pragma unroll
-    for (int r = 0; r < RC; ++r) {
-      y0[r] = fmaf(v, fmaf(-128.f, xs0[r], acc0[r]), y0[r]);
-      y1[r] = fmaf(v, fmaf(-128.f, xs1[r], acc1[r]), y1[r]);
+      for (int d = 0; d < 4; ++d) {
+        gA[d] = lo8 ? w0[d] : w1[d];                   // own row c, first half
+        gB[d] = lo8 ? w1[d] : w0[d];                   // row c ^ 8, second half
+      }
+      f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+      acc0 = mfma16x16x32(a00, biased_i8x8_bf16(gA[0], gA[1]), acc0);
+      acc1 = mfma16x16x32(a10, biased_i8x8_bf16(gB[0], gB[1]), acc1);
+      acc0 = mfma16x16x32(a01, biased_i8x8_bf16(gA[2], gA[3]), acc0);
+      acc1 = mfma16x16x32(a11, biased_i8x8_bf16(gB[2], gB[3]), acc1);
+#pragma unroll
+      for (int r = 0; r < RC; ++r) {
+        y0[r] = fmaf(v, fmaf(-128.f, xs0[r], acc0[r]), y0[r]);
+        y1[r] = fmaf(v, fmaf(-128.f, xs1[r], acc1[r]), y1[r]);
+      }
     }
   }
   // D row m = 4*ar + r; rows m < M <= 4 live in lanes ar == 0
