@@ -185,13 +185,9 @@ __global__ __launch_bounds__(64 * MAXW) void w4_skinny_kernel(SkinnyArgs a) {
     const int m = idx / nblk;
     const int b = idx - m * nblk;
     *(u32x4_t*)(xl + m * xls + 8 * b) = permute_x8(v);
-    float sum = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
     // the 16 blocks of one step are 16 consecutive idx (nblk is a multiple of 16, and idx
     // groups of 16 lie entirely inside or outside [0, xtotal))
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    const float sum = row_sum16(bf16x8_sum(v));
     if ((b & 15) == 0) xs[(b >> 4) * 16 + m] = sum;
   };
 #pragma unroll
@@ -533,12 +529,9 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
     const int idx = lane + 64 * u;
     const bool ok = idx < xtot;
     const int m = (ok ? idx : 0) / XB, b = (ok ? idx : 0) - m * XB;
-    float sum = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
+    float sum = bf16x8_sum(xv[u]);
     // the 16 blocks of one group are 16 consecutive idx (XB is a multiple of 16)
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    sum = row_sum16(sum);
     if (ok) {
       *(u32x4_t*)(xw + m * xrow + 8 * b) = permute_x8(xv[u]);
       if ((b & 15) == 0) xs[(b >> 4) * 16 + m] = sum;
@@ -745,12 +738,9 @@ __global__ __launch_bounds__(64 * NW) void w4_ksplit_kernel(SkinnyArgs a) {
     const int idx = threadIdx.x + NT * u;
     const bool ok = idx < xtot;
     const int m = (ok ? idx : 0) / XB, b = (ok ? idx : 0) - m * XB;
-    float sum = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
+    float sum = bf16x8_sum(xv[u]);
     // the 16 blocks of one group are 16 consecutive idx (XB and NT are multiples of 16)
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    sum = row_sum16(sum);
     if (ok) {
       *(u32x4_t*)(xw + m * xrow + 8 * b) = permute_x8(xv[u]);
       if ((b & 15) == 0) xs[(b >> 4) * 16 + m] = sum;
@@ -951,10 +941,10 @@ __global__ __launch_bounds__(64 * NW) void w4_wsplit_kernel(SkinnyArgs a) {
     if constexpr (SDT == IMQ_DT_FP32) {
       s0 = round_bf16_hw(__uint_as_float(tl.sw[2 * i]));
       z0 = round_bf16_hw(__uint_as_float(tl.zw[2 * i]));
-      s1 = round_bf16_hw(__uint_as_float((uint32_t)__shfl_xor((int)tl.sw[2 * i + 1], 8)));
-      z1 = round_bf16_hw(__uint_as_float((uint32_t)__shfl_xor((int)tl.zw[2 * i + 1], 8)));
+      s1 = round_bf16_hw(__uint_as_float(dpp_row_ror<8>(tl.sw[2 * i + 1])));
+      z1 = round_bf16_hw(__uint_as_float(dpp_row_ror<8>(tl.zw[2 * i + 1])));
     } else {
-      const uint32_t sx = (uint32_t)__shfl_xor((int)tl.sw[i], 8), zx = (uint32_t)__shfl_xor((int)tl.zw[i], 8);
+      const uint32_t sx = dpp_row_ror<8>(tl.sw[i]), zx = dpp_row_ror<8>(tl.zw[i]);
       s0 = raw_to_bf16_f32<SDT>(tl.sw[i] & 0xffffu);
       z0 = raw_to_bf16_f32<SDT>(tl.zw[i] & 0xffffu);
       s1 = raw_to_bf16_f32<SDT>(sx >> 16);
@@ -975,11 +965,8 @@ __global__ __launch_bounds__(64 * NW) void w4_wsplit_kernel(SkinnyArgs a) {
   for (int u = 0; u < XU; ++u) {
     const int idx = 64 * u + lane;
     const int m = idx / CPR, ch = idx - m * CPR;
-    float sum = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    float sum = bf16x8_sum(xv[u]);
+    sum = row_sum16(sum);
     if (m < M) {
       *(u32x4_t*)(xw + m * XROW + 8 * ch) = permute_x8(xv[u]);
       if ((ch & 15) == 0) xsum[(ch >> 4) * 16 + m] = sum;
@@ -1172,14 +1159,8 @@ __global__ __launch_bounds__(64 * MAXW) void w2_skinny_kernel(SkinnyArgs a) {
       const uint16_t* src = a.x + (int64_t)m * a.sxm + (int64_t)c0 * kStep2 + 16 * pr;
       const u32x4_t lo = *(const u32x4_t*)src;
       const u32x4_t hi = *(const u32x4_t*)(src + 8);
-      float sum = 0.f;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        sum += __uint_as_float(lo[d] << 16) + __uint_as_float(lo[d] & 0xffff0000u);
-        sum += __uint_as_float(hi[d] << 16) + __uint_as_float(hi[d] & 0xffff0000u);
-      }
-      sum += __shfl_xor(sum, 1, 4);
-      sum += __shfl_xor(sum, 2, 4);
+      float sum = bf16x8_sum(lo) + bf16x8_sum(hi);
+      sum = quad_sum4(sum);
       if (valid) {
         u32x4_t o0, o1;
         permute_x16(lo, hi, o0, o1);
@@ -1459,15 +1440,9 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
     const int idx = lane + 64 * u;
     const bool ok = idx < xtot;
     const int m = (ok ? idx : 0) / XP, p = (ok ? idx : 0) - m * XP;
-    float sum = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      sum += __uint_as_float(xlo[u][d] << 16) + __uint_as_float(xlo[u][d] & 0xffff0000u);
-      sum += __uint_as_float(xhi[u][d] << 16) + __uint_as_float(xhi[u][d] & 0xffff0000u);
-    }
+    float sum = bf16x8_sum(xlo[u]) + bf16x8_sum(xhi[u]);
     // the 4 pairs of one group are 4 consecutive idx (XP is a multiple of 4)
-    sum += __shfl_xor(sum, 1, 4);
-    sum += __shfl_xor(sum, 2, 4);
+    sum = quad_sum4(sum);
     if (ok) {
       u32x4_t o0, o1;
       permute_x16(xlo[u], xhi[u], o0, o1);
@@ -1630,15 +1605,9 @@ __global__ __launch_bounds__(64 * NW) void w2_ksplit_kernel(SkinnyArgs a) {
     const int idx = threadIdx.x + NT * u;
     const bool ok = idx < xtot;
     const int m = (ok ? idx : 0) / XP, p = (ok ? idx : 0) - m * XP;
-    float sum = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      sum += __uint_as_float(xlo[u][d] << 16) + __uint_as_float(xlo[u][d] & 0xffff0000u);
-      sum += __uint_as_float(xhi[u][d] << 16) + __uint_as_float(xhi[u][d] & 0xffff0000u);
-    }
+    float sum = bf16x8_sum(xlo[u]) + bf16x8_sum(xhi[u]);
     // the 4 pairs of one group are 4 consecutive idx (XP and NT are multiples of 4)
-    sum += __shfl_xor(sum, 1, 4);
-    sum += __shfl_xor(sum, 2, 4);
+    sum = quad_sum4(sum);
     if (ok) {
       u32x4_t o0, o1;
       permute_x16(xlo[u], xhi[u], o0, o1);
@@ -1754,12 +1723,8 @@ __global__ __launch_bounds__(64 * MAXW) void w8_skinny_kernel(SkinnyArgs a) {
       const int m = id / nblk;
       const int b = id - m * nblk;
       const u32x4_t v = *(const u32x4_t*)(a.x + (int64_t)m * a.sxm + (int64_t)c0 * kStep8 + 8 * b);
-      float sum = 0.f;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
-      sum += __shfl_xor(sum, 1, 8);
-      sum += __shfl_xor(sum, 2, 8);
-      sum += __shfl_xor(sum, 4, 8);
+      float sum = bf16x8_sum(v);
+      sum = half_row_sum8(sum);
       if (valid) {
         *(u32x4_t*)(xl + m * xls + 8 * b) = v;
         if ((b & 7) == 0) xs[(b >> 3) * 16 + m] = sum;
@@ -1916,12 +1881,9 @@ __global__ __launch_bounds__(64 * MAXW) void w8_line_kernel(SkinnyArgs a) {
     const int idx = lane + 64 * u;
     const bool ok = idx < xtot;
     const int m = (ok ? idx : 0) / XB, b = (ok ? idx : 0) - m * XB;
-    float sum = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) sum += __uint_as_float(xv[u][d] << 16) + __uint_as_float(xv[u][d] & 0xffff0000u);
+    float sum = bf16x8_sum(xv[u]);
     // the 8 blocks of one half line-step are 8 consecutive idx (XB is a multiple of 8)
-#pragma unroll
-    for (int off = 4; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 8);
+    sum = half_row_sum8(sum);
     if (ok) {
       *(u32x4_t*)(xw + m * xrow + 8 * b) = xv[u];
       if ((b & 7) == 0) xs[(b >> 3) * 16 + m] = sum;

@@ -160,6 +160,57 @@ IMQ_DEV u32x4_t permute_x8(u32x4_t v) {
   return p;
 }
 
+// Lane c of each 16-lane row receives lane (c - N) & 15 of the same row (DPP row_ror:N): a VALU
+// operand modifier instead of an LDS permute with its address arithmetic and round trip.
+template <int N>
+IMQ_DEV uint32_t dpp_row_ror(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + N, 0xf, 0xf, false);
+}
+template <int N>
+IMQ_DEV float dpp_row_ror(float v) { return __uint_as_float(dpp_row_ror<N>(__float_as_uint(v))); }
+
+// Sum over the 16 lanes of each row, returned to every lane. After the n-th step the values
+// repeat with period 16 >> n, so rotations by 8, 4, 2, 1 reach the same partner values as the
+// xor butterfly (`v += __shfl_xor(v, 8 / 4 / 2 / 1, 16)`) and give the same bits.
+IMQ_DEV float row_sum16(float v) {
+  v += dpp_row_ror<8>(v);
+  v += dpp_row_ror<4>(v);
+  v += dpp_row_ror<2>(v);
+  v += dpp_row_ror<1>(v);
+  return v;
+}
+
+// Sum over each group of 4 lanes (DPP quad_perm [1,0,3,2] then [2,3,0,1]): the xor-1 / xor-2
+// butterfly exactly.
+IMQ_DEV float quad_sum4(float v) {
+  v += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(v), 0xB1, 0xf, 0xf, false));
+  v += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(v), 0x4E, 0xf, 0xf, false));
+  return v;
+}
+
+// Sum over each group of 8 lanes: the quad sums, then the other quad's through row_half_mirror
+// (lane c of 8 reads lane 7 - c, which holds the other quad's sum).
+IMQ_DEV float half_row_sum8(float v) {
+  v = quad_sum4(v);
+  v += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(v), 0x141, 0xf, 0xf, false));
+  return v;
+}
+
+// Sum of the 8 bf16 values of a 16-byte block: four v_dot2c_f32_bf16 against (1, 1), one VALU
+// operation per two values (instead of two conversions and two adds).
+IMQ_DEV float bf16x8_sum(u32x4_t v) {
+  const bf16x2_t one = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+  float s = 0.f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    // the element goes through a scalar first: hipcc bit-casts a subscripted vector element
+    // `v[d]` from element 0 whatever d is
+    const uint32_t w = v[d];
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), one, s, false);
+  }
+  return s;
+}
+
 // 32x32x16 bf16: A lane l = row l%32, K 8*(l/32)..+8; B lane l = column l%32, same K; D lane l
 // holds column l%32, element r at row 8*(r/4) + 4*(l/32) + r%4. Twice the 16x16x32 rate.
 IMQ_DEV f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {

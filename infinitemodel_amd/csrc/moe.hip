@@ -736,12 +736,7 @@ IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint
 #pragma unroll
     for (int u = 0; u < XU; ++u) {
       const int bidx = lane + 64 * u;
-      float sum = 0.f;
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-        sum += __uint_as_float(xv[h][u][d] << 16) + __uint_as_float(xv[h][u][d] & 0xffff0000u);
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+      const float sum = row_sum16(bf16x8_sum(xv[h][u]));
       *(u32x4_t*)(xw + h * xrowl + 8 * bidx) = permute_x8(xv[h][u]);
       if ((bidx & 15) == 0) xs[h * 2 * S2 + (bidx >> 4)] = sum;
     }

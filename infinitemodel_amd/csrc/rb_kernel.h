@@ -788,11 +788,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
         for (int u = 0; u < 4; ++u) v[u] = *(const u32x4_t*)(Ht + row * HS + 32 * q + 8 * u);
         float sum = 0.f;
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int d = 0; d < 4; ++d) sum += __uint_as_float(v[u][d] << 16) + __uint_as_float(v[u][d] & 0xffff0000u);
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
+        for (int u = 0; u < 4; ++u) sum += bf16x8_sum(v[u]);
+        sum = quad_sum4(sum);
         if (row < cnt) {
           uint16_t* dst = a.y + (int64_t)(prow0 + row) * a.sym + tn * 128 + 32 * q;
 #pragma unroll
