@@ -191,7 +191,7 @@ def _w4_decode_kernel(M: int) -> str:
     """The kernels imq_linear_w4 runs for M decode rows at the C1 / C2 shapes (gemv.hip)."""
     if M <= 4:
         return f"w4_line_kernel (imq_linear_w4, M={M})"
-    return (f"w4_wsplit_kernel (gate_up) + w4_ksplit_kernel + splitk_rows_reduce_kernel (qkv, o, down) "
+    return (f"w4_wsplit_kernel (qkv, o, gate_up) + w4_ksplit_kernel + splitk_rows_reduce_kernel (down) "
             f"(imq_linear_w4, M={M})")
 
 

@@ -437,6 +437,9 @@ constexpr int kLine = 256;
 #ifndef IMQ_LINE_PAIRED
 #define IMQ_LINE_PAIRED 1
 #endif
+#ifndef IMQ_LINE_PAIRED4
+#define IMQ_LINE_PAIRED4 1
+#endif
 
 // lane c of each 16-lane row receives the value of lane c ^ 8 (DPP row_ror:8)
 IMQ_DEV float row_swap8(float v) {
@@ -549,8 +552,14 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
   // PAIRED (M <= 2): A lane row m < M reads activation row m in group 2l, M <= m < 2M row m - M
   // in group 2l+1 (128 codes on), other rows repeat row 0 of group 2l (their D rows are unused)
   constexpr bool PAIRED = MC <= 2 && IMQ_LINE_PAIRED;
+  // PAIRED4 (M 3..4): A rows 0-3 hold group 2l of activation rows 0-3, rows 4-7 group 2l+1 (rows
+  // past M repeat row M - 1, their D rows are dropped), so D rows 0-3 (lanes 0-15) accumulate
+  // group 2l and D rows 4-7 (lanes 16-31, hB) group 2l+1; A rows 8-15 are unused
+  constexpr bool PAIRED4 = MC == 4 && IMQ_LINE_PAIRED4;
+  const bool hB = ar == 1;
   const uint16_t* xa = PAIRED ? xw + (c < 2 * M ? c % M : 0) * xrow + 32 * ar + (c >= M && c < 2 * M ? 128 : 0)
-                              : xw + (c < M ? c : M - 1) * xrow + 32 * ar;
+                     : PAIRED4 ? xw + ((c & 3) < M ? (c & 3) : M - 1) * xrow + 32 * ar + ((c & 4) ? 128 : 0)
+                               : xw + (c < M ? c : M - 1) * xrow + 32 * ar;
   const uint32_t* sc_c = szl + c * DPR;
   const uint32_t* sc_x = szl + (c ^ 8) * DPR;
   const uint32_t* zr_c = szl + 16 * DPR + c * DPR;
@@ -563,13 +572,15 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
     const bool v = ls0 + i < KL;
-    const f32x4_t xs0 = *(const f32x4_t*)(xs + (2 * i) * 16 + 4 * ar);
-    const f32x4_t xs1 = *(const f32x4_t*)(xs + (2 * i + 1) * 16 + 4 * ar);
+    // PAIRED4 lanes read the sums of their own group's rows 0-3 (xs1 unused)
+    const f32x4_t xs0 = PAIRED4 ? *(const f32x4_t*)(xs + (2 * i + (hB ? 1 : 0)) * 16)
+                                : *(const f32x4_t*)(xs + (2 * i) * 16 + 4 * ar);
+    const f32x4_t xs1 = PAIRED4 ? xs0 : *(const f32x4_t*)(xs + (2 * i + 1) * 16 + 4 * ar);
     bf16x8_t A0[4], A1[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       A0[k] = *(const bf16x8_t*)(xa + i * kLine + 8 * k);
-      if constexpr (!PAIRED) A1[k] = *(const bf16x8_t*)(xa + i * kLine + 128 + 8 * k);
+      if constexpr (!PAIRED && !PAIRED4) A1[k] = *(const bf16x8_t*)(xa + i * kLine + 128 + 8 * k);
     }
     // read unconditionally (the staged strip covers every i), then select: a conditional read
     // becomes a branch with an LDS round trip inside each line-step
@@ -598,6 +609,22 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
         y0[r] = fmaf(s0, accA, y0[r]);
         y1[r] = fmaf(s1, accB, y1[r]);
       }
+    } else if constexpr (PAIRED4) {
+      // lanes 0-15: D rows 0-3 of column c < 8 of L0 / c >= 8 of L1 are group 2l of row c; lanes
+      // 16-31: D rows 4-7 of column c >= 8 of L0 / c < 8 of L1 are group 2l+1 of row c ^ 8
+      f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        a0 = mfma16x16x32(A0[k], unpack_nib8_bf16(w0[k], magic), a0);
+        a1 = mfma16x16x32(A0[k], unpack_nib8_bf16(w1[k], magic), a1);
+      }
+      const bool pick0 = lo8 != hB;
+      const float sl = hB ? s1 : s0, czl = hB ? cz1 : cz0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        y0[r] = fmaf(czl, xs0[r], y0[r]);
+        y0[r] = fmaf(sl, pick0 ? a0[r] : a1[r], y0[r]);
+      }
     } else {
       u32x4_t gA, gB;
 #pragma unroll
@@ -620,11 +647,16 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
       }
     }
   }
-  // D row m = 4*ar + r; rows m < M <= 4 live in lanes ar == 0
+  // D row m = 4*ar + r; rows m < M <= 4 live in lanes ar == 0 (PAIRED4: their group 2l+1 parts
+  // in lanes 16-31, brought over by a lane-xor-16 swizzle)
   float* rb = red + wave * (RC * 16);
 #pragma unroll
   for (int r = 0; r < RC; ++r) {
-    const float v = y0[r] + row_swap8(y1[r]);
+    float v;
+    if constexpr (PAIRED4)
+      v = y0[r] + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(row_swap8(y0[r])), 0x401F));
+    else
+      v = y0[r] + row_swap8(y1[r]);
     if (ar == 0) rb[r * 16 + c] = v;
   }
   lds_barrier();
@@ -2296,17 +2328,21 @@ int ksplit_w4(const SkinnyArgs& a0, int sdt, void* ws, int64_t wsb, const DevInf
 
 // Wave-split plan (4 < M <= 16, G == 128, K_pad == 8 R 256 with R 1 or 2, unit group strides,
 // same scale / zero dtype, 4-byte aligned scale / zero rows, the LDS of wsplit_lds within the
-// device's, at least 4 row tiles per CU; restated by the CPU bounds model in the tests): NW = 8
+// device's, at least one row tile per CU; restated by the CPU bounds model in the tests): NW = 8
 // waves, one workgroup per CU, the grid min(tiles, CUs). Returns R, or 0 when the kernel does not
-// take the call. Every workgroup reads all of x (M x K_pad bf16), which costs about as much as a
-// tile stream of the same bytes, and the first tile waits for it: the kernel pays off where a
-// workgroup streams many tiles (measured at M = 16: gate_up 4096 -> 28672, 7 tiles per CU, 20.8 us
-// against 24.0 us for K-split + reduction; qkv 4096 -> 6144 and o 4096 -> 4096, 1-2 tiles per
-// CU, 11.3 / 9.7 us against 10.3 / 8.2 us). PD = 2 tiles of prefetch measured best (3, 4: no gain
-// on gate_up, slower on short grids).
+// take the call. Every workgroup reads all of x (M x K_pad bf16) and the first tile waits for it,
+// so the kernel gains most where a workgroup streams many tiles (measured at M = 16: gate_up
+// 4096 -> 28672, 7 tiles per CU, 20.8 us against 24.0 us for K-split + reduction). With the
+// activation group sums as v_dot2 and DPP row sums the staging is short enough that 1-2 tiles per
+// CU also beat K-split + reduction (C2 M = 16 2458 -> 2487 GB/s, M = 8 2615 -> 2638 with qkv and
+// o on this kernel); below one tile per CU the K-split grid has more workgroups. PD = 2 tiles of
+// prefetch measured best (3, 4: no gain on gate_up, slower on short grids).
 constexpr int kWsNW = 8;
 #ifndef IMQ_WS_PD
 #define IMQ_WS_PD 2
+#endif
+#ifndef IMQ_WS_MIN_TILES
+#define IMQ_WS_MIN_TILES 1
 #endif
 int wsplit_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
                 int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int cus) {
@@ -2317,7 +2353,7 @@ int wsplit_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int6
   if ((ssn * vb) % 4 != 0 || (szn * vb) % 4 != 0) return 0;
   if (N * sqn >= (int64_t(1) << 46) || 16 * sqn >= (int64_t(1) << 31) || M * sxm * 2 >= (int64_t(1) << 31)) return 0;
   const int R = (int)(Kpad / (kWsNW * kLine));
-  if (wsplit_lds(R, kWsNW) > max_lds || (N + 15) / 16 < 4 * (int64_t)cus) return 0;
+  if (wsplit_lds(R, kWsNW) > max_lds || (N + 15) / 16 < IMQ_WS_MIN_TILES * (int64_t)cus) return 0;
   return R;
 }
 

@@ -368,6 +368,30 @@ def line_ranges(M, Kpad, N, sqn, sxm, ssn, vb, S2, W, sz_dword=None):
     return q_hi, s_hi, x_hi, y_hi
 
 
+def line_lds_reads(M, S2):
+    """Max exclusive element offsets of a wave's A-operand reads (bf16, in its staged x strip of M
+    rows) and group-sum reads (fp32, in its 2 * S2 * 16 sums) for the launched row class: M <= 2
+    pairs the two groups of a line-step in A rows [0, M) / [M, 2M); M 3..4 puts group 2l in A rows
+    0-3 and group 2l+1 in rows 4-7 (lanes 16-31 read their own group's sums); rows past M repeat an
+    existing row."""
+    xrow = S2 * LINE + 8
+    xa = xs = 0
+    for c in range(16):
+        for ar in range(4):
+            if M <= 2:
+                row = c % M if c < 2 * M else 0
+                off = 128 if M <= c < 2 * M else 0
+                sums = [(2 * i) * 16 + 4 * ar + 4 for i in range(S2)] + [(2 * i + 1) * 16 + 4 * ar + 4 for i in range(S2)]
+            else:
+                row = (c & 3) if (c & 3) < M else M - 1
+                off = 128 if c & 4 else 0
+                sums = [(2 * i + (1 if ar == 1 else 0)) * 16 + 4 for i in range(S2)]
+            for i in range(S2):
+                xa = max(xa, row * xrow + 32 * ar + i * LINE + off + 8 * 3 + 8)
+            xs = max(xs, *sums)
+    return xa, xs, M * xrow, 2 * S2 * 16
+
+
 LINE_SHAPES = [(4096, 4096), (6144, 4096), (28672, 4096), (4096, 14336), (37, 512), (100, 768), (17, 256),
                (48, 16384), (1000, 256)]
 
@@ -391,6 +415,8 @@ def test_line_reads_in_bounds(N, K, M, vb, pad):
     xrow = S2 * LINE + 8
     wave_lds = M * xrow * 2 + 2 * S2 * 16 * 4 + 2 * 16 * S2 * vb // 2 * 4
     assert W * wave_lds + W * rc * 16 * 4 <= lds
+    xa, xs, xa_lim, xs_lim = line_lds_reads(M, S2)
+    assert xa <= xa_lim and xs <= xs_lim
     assert q_hi <= (N - 1) * sqn + Kpad // 2          # exact fit: no padding after the last row
     assert s_hi <= N * ng * vb
     assert x_hi <= ((M - 1) * Kpad + Kpad) * 2
@@ -581,7 +607,7 @@ def wsplit_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, cus=256, max_lds=160 * 1024):
     if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31:
         return None
     R = Kpad // (WS_NW * LINE)
-    if wsplit_lds(R) > max_lds or -(-N // 16) < 4 * cus:
+    if wsplit_lds(R) > max_lds or -(-N // 16) < cus:
         return None
     return R
 
@@ -688,8 +714,9 @@ def test_wsplit_plan_declines():
     assert wsplit_plan(8, 14336, 128, 4096, 7168, 14336, 112, 2) is None  # K_pad not 2048 / 4096
     assert wsplit_plan(8, 4096, 64, 4096, 2048, 4096, 64, 2) is None      # G != 128
     assert wsplit_plan(8, 4096, 128, 4096, 2048, 4096, 33, 2) is None     # odd bf16 scale row stride
-    assert wsplit_plan(16, 4096, 128, 4096, 2048, 4096, 32, 2) is None    # 1 tile per CU: K-split
-    assert wsplit_plan(16, 4096, 128, 6144, 2048, 4096, 32, 2) is None    # qkv: 1.5 tiles per CU
+    assert wsplit_plan(16, 4096, 128, 2048, 2048, 4096, 32, 2) is None    # < 1 tile per CU: K-split
+    assert wsplit_plan(16, 4096, 128, 4096, 2048, 4096, 32, 2) == 2       # o: 1 tile per CU
+    assert wsplit_plan(16, 4096, 128, 6144, 2048, 4096, 32, 2) == 2       # qkv: 1.5 tiles per CU
     assert wsplit_plan(16, 4096, 128, 28672, 2048, 4096, 32, 2) == 2      # gate_up: 7 tiles per CU
     assert wsplit_plan(8, 2048, 128, 16384, 1024, 2048, 16, 2) == 1
 
