@@ -307,7 +307,7 @@ def line_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024):
     if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31 or 16 * ssn * vb >= 2 ** 31:
         return None
     KL = Kpad // LINE
-    S2 = 4 if M == 1 else 2
+    S2 = 2
     if -(-KL // S2) > 16:
         S2 = 4
     W = -(-KL // S2)
