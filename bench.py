@@ -20,9 +20,17 @@ linears, launched back to back on one stream and replayed as a HIP graph.
 Other configs print lines of the same shape: --config c1 (single 1x4096->4096 linear), c3 (int2
 g64 70B shapes), c4 (prefill, --quant int4|int8, --m 512|2048), c5 (OLMoE fused MoE, --m = T),
 gptoss (gpt-oss-20b fused experts, --m = T), head (int8 lm_head decode at the Qwen2.5-7B head,
-152064 x 3584, --m rows), ``ceiling`` (the C2 weights read by a read-only streaming kernel, one
-launch per linear and one persistent launch, beside the decode kernels) and ``copy`` (the plain
-device copy used to calibrate the PMC byte counters).
+152064 x 3584, --m rows, two distinct copies) and the hardware ceilings of libimq's probes:
+``ceiling`` (the C2 weights read by the read-only stream probe, one launch per linear and one
+persistent launch, beside the decode kernels), ``stream`` (4 GiB read-only and 1 GiB copies),
+``launch`` (a chain of empty kernels), ``mfma`` (the bf16 MFMA issue peak) and ``copy`` (torch's
+device copy, which calibrates the PMC byte counters).
+
+Profiles of a line: ``rocprofv3 --kernel-trace --output-format csv -d DIR -o NAME -- python bench.py
+...`` records every dispatch; ``python bench.py --trace-summary DIR/NAME_kernel_trace.csv --launches
+L --steps K`` summarizes the last L dispatches -- the timed steps, which are the last GPU work of a
+``--no-cpu`` run (L = K x launches_per_step) -- per kernel and per launch position, with the
+kernel time per step to set beside the line's ms_per_step.
 """
 from __future__ import annotations
 
@@ -44,12 +52,17 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "gptoss", "head", "copy", "ceiling"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "gptoss", "head", "copy", "ceiling", "stream",
+                                                    "launch", "mfma"])
     ap.add_argument("--m", type=int, default=None, help="rows: C2/C3/C4 M, C5 tokens T")
     ap.add_argument("--quant", default="int4", choices=["int4", "int8"], help="C4 weight format")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--trace-summary", default=None, metavar="CSV",
+                    help="summarize the last --launches dispatches of a rocprofv3 kernel-trace CSV (no GPU)")
+    ap.add_argument("--launches", type=int, default=None, help="timed dispatches (steps x launches per step)")
+    ap.add_argument("--period", type=int, default=None, help="launches per step, for per-position means")
     return ap.parse_args()
 
 
@@ -570,24 +583,32 @@ def bench_gptoss(args, dev):
 # int8 lm_head decode (head_quant=int8) at the Qwen2.5-7B head
 # ---------------------------------------------------------------------------------------------
 def bench_head(args, dev):
+    """Two distinct copies of the head (1.09 GB, past the 256 MB MALL) launched alternately, so no
+    launch finds its matrix cached from the one before."""
     import torch
     from infinitemodel_amd import ops, workloads as wl
     M = args.m or 1
     N, K = 152064, 3584
-    q, s = wl.int8_linear(N, K, 17, dev, dtype=torch.bfloat16)
+    heads = [wl.int8_linear(N, K, 17 + i, dev, dtype=torch.bfloat16) for i in range(2)]
     x = wl.activations(M, K, 18, dev)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    ms = _time_steps(_graph_or_eager(lambda: ops.linear_w8(x, q, s, out=y), not args.no_graph), args.steps,
-                     args.warmup)
+
+    def step():
+        for q, s in heads:
+            ops.linear_w8(x, q, s, out=y)
+
+    ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
     nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
-    roof = _hbm_roofline("imq_linear_w8 decode kernel", nbytes, ms * 1e3, _traffic(f"head_m{M}"))
-    cfg = {"workload": f"int8 lm_head 3584 -> 152064 (Qwen2.5-7B), M={M}", "M": M, "launches_per_step": 1,
-           "weights": "int8 per-row symmetric, bf16 scale", "distinct_bytes_per_step": nbytes}
+    roof = _hbm_roofline("imq_linear_w8 decode kernel", nbytes, ms * 1e3 / len(heads), _traffic(f"head_m{M}"))
+    cfg = {"workload": f"int8 lm_head 3584 -> 152064 (Qwen2.5-7B), M={M}, {len(heads)} distinct copies per step",
+           "M": M, "launches_per_step": len(heads),
+           "weights": "int8 per-row symmetric, bf16 scale", "distinct_bytes_per_step": nbytes * len(heads)}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path
         n = cpu_path.tune_cpu_threads()
         rows = 16384
+        q, s = heads[0]
         qc, sc_, xc = q[:rows].cpu(), s[:rows].cpu(), x.cpu()
         med, runs = _cpu_time(lambda: cpu_path.naive_linear_int8(xc, qc, sc_), args.cpu_seconds)
         cb = rows * K + rows * 2 + M * K * 2 + M * rows * 2
@@ -595,69 +616,211 @@ def bench_head(args, dev):
                "sample": f"the reference's CPU int8 forward (naive dequant + F.linear, worker_quant.py:"
                          f"411-417, 439-440) over the first {rows} head rows, median of {runs}",
                "cpu": _cpu_model()}
-    return _line(round(nbytes / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
+    return _line(round(nbytes * len(heads) / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
 
 
 # ---------------------------------------------------------------------------------------------
-# Read-only ceiling of the C2 decode pass (the measurement probes of libimq)
+# Hardware ceilings (the measurement probes of libimq, csrc/probe.hip)
 # ---------------------------------------------------------------------------------------------
-def bench_ceiling(args, dev):
-    """The C2 stack's weight bytes (codes + scale + zero of all 128 linears, 3.7 GB) read by a
-    read-only streaming kernel: (a) one launch per linear, the ceiling of any one-launch-per-linear
-    design; (b) one persistent launch over all of them, the ceiling with no launch boundaries;
-    (c) the decode kernels themselves on the same weights at M=1. value = (a)."""
-    import torch
-    from infinitemodel_amd import _lib, ops, workloads as wl
-    L = _lib.lib()
-    lins = wl.llama8b_stack(dev)
-    st = lambda: torch.cuda.current_stream(dev).cuda_stream   # noqa: E731
-    sink = torch.empty(int(L.imq_probe_sink_bytes()) // 4 + 1, dtype=torch.int32, device=dev)
-    per_linear = []
-    allp, alln = [], []
-    for lin in lins:
-        bufs = [lin.q, lin.s, lin.z]
+PROBE_SWEEP = [(u, w, nt) for u in (2, 4, 8, 16) for w in (1, 2, 4, 8) for nt in (0, 1)]
+
+
+class _Probe:
+    """Read-only stream launches (imq_probe_stream) over fixed buffer lists."""
+
+    def __init__(self, dev):
+        import torch
+        from infinitemodel_amd import _lib
+        self.L = _lib.lib()
+        self.call = _lib.call
+        self.dev = dev
+        self.sink = torch.empty(int(self.L.imq_probe_sink_bytes()) // 4 + 1, dtype=torch.int32, device=dev)
+
+    def buffers(self, bufs):
+        """(ptrs, n16s, total) device tables for a list of contiguous 16-byte-aligned tensors."""
+        import torch
         for b in bufs:
-            assert b.is_contiguous() and (b.numel() * b.element_size()) % 16 == 0 and b.data_ptr() % 16 == 0
-        ptrs = torch.tensor([b.data_ptr() for b in bufs], dtype=torch.int64, device=dev)
-        n16 = torch.tensor([b.numel() * b.element_size() // 16 for b in bufs], dtype=torch.int64, device=dev)
-        per_linear.append((ptrs, n16, int(n16.max())))
-        allp += [b.data_ptr() for b in bufs]
-        alln += [b.numel() * b.element_size() // 16 for b in bufs]
-    all_ptrs = torch.tensor(allp, dtype=torch.int64, device=dev)
-    all_n16 = torch.tensor(alln, dtype=torch.int64, device=dev)
-    weight_bytes = 16 * sum(alln)
+            nb = b.numel() * b.element_size()
+            assert b.is_contiguous() and nb % 16 == 0 and b.data_ptr() % 16 == 0 and nb >= 16
+        ptrs = torch.tensor([b.data_ptr() for b in bufs], dtype=torch.int64, device=self.dev)
+        n16 = [b.numel() * b.element_size() // 16 for b in bufs]
+        return ptrs, torch.tensor(n16, dtype=torch.int64, device=self.dev), sum(n16), len(bufs)
 
-    def per_launch():
-        for ptrs, n16, mx in per_linear:
-            _lib.call("imq_probe_read_seq", ptrs.data_ptr(), n16.data_ptr(), 3, mx, sink.data_ptr(),
-                      sink.numel() * 4, st())
+    def read(self, tab, cfg):
+        import torch
+        ptrs, n16, total, nbuf = tab
+        u, w, nt = cfg
+        self.call("imq_probe_stream", ptrs.data_ptr(), n16.data_ptr(), nbuf, total, u, w, nt,
+                  self.sink.data_ptr(), self.sink.numel() * 4, torch.cuda.current_stream(self.dev).cuda_stream)
 
-    def persistent():
-        _lib.call("imq_probe_read_seq", all_ptrs.data_ptr(), all_n16.data_ptr(), len(alln), max(alln),
-                  sink.data_ptr(), sink.numel() * 4, st())
 
+def _cfg_name(cfg) -> str:
+    return f"U{cfg[0]}_wg{cfg[1]}{'_nt' if cfg[2] else ''}"
+
+
+def bench_ceiling(args, dev):
+    """The C2 stack's weights (codes + scale + zero of all 128 linears, 3.7 GB) read by the
+    read-only stream probe, every probe configuration of PROBE_SWEEP (loads per lane, workgroups
+    per CU, non-temporal loads):
+      per kind (qkv / o / gate_up / down): 32 launches of that kind's 32 distinct linears as one
+        graph, the fastest configuration per kind -- the per-launch ceiling of that linear -- beside
+        the decode kernels (imq_linear_w4 at M=1) on the same 32 linears;
+      the whole pass: 128 launches in layer order with each kind's fastest configuration (value),
+        the decode kernels over the same pass, and one persistent launch over all 384 buffers
+        (the same bytes with no launch boundary, fastest configuration)."""
+    import torch
+    from infinitemodel_amd import ops, workloads as wl
+    pr = _Probe(dev)
+    lins = wl.llama8b_stack(dev)
+    kinds = [n for n, _, _ in wl.LLAMA8B_PROJ]
+    tabs = [pr.buffers([L.q, L.s, L.z]) for L in lins]
+    kind_of = [L.name.split(".")[1] for L in lins]
+    wbytes = [16 * t[2] for t in tabs]
     x_in = wl.activations(1, 4096, 1, dev)
     x_dn = wl.activations(1, 14336, 2, dev)
     ys = {n: torch.empty((1, N), dtype=torch.bfloat16, device=dev) for n, _, N in wl.LLAMA8B_PROJ}
-
-    def decode():
-        for lin in lins:
-            kind = lin.name.split(".")[1]
-            ops.linear_w4(x_dn if kind == "down" else x_in, lin.q, lin.G, (lin.s, lin.z), out=ys[kind])
-
     g = not args.no_graph
-    ms_a = _time_steps(_graph_or_eager(per_launch, g), args.steps, args.warmup)
-    ms_b = _time_steps(_graph_or_eager(persistent, g), args.steps, args.warmup)
-    ms_c = _time_steps(_graph_or_eager(decode, g), args.steps, args.warmup)
-    gbs = lambda ms: round(weight_bytes / (ms * 1e-3) / 1e9, 2)   # noqa: E731
-    roof = _hbm_roofline("probe_read_seq_kernel (one launch per linear)", weight_bytes / len(lins),
-                         ms_a * 1e3 / len(lins), None)
+    st, wu = max(5, args.steps // 2), 2
+
+    def t_us(fn, n):
+        return _time_steps(_graph_or_eager(fn, g), st, wu) * 1e3 / n
+
+    per_kind = {}
+    best = {}
+    for k in kinds:
+        ids = [i for i, kk in enumerate(kind_of) if kk == k]
+        sweep = {}
+        for cfg in PROBE_SWEEP:
+            sweep[_cfg_name(cfg)] = round(t_us(lambda ids=ids, cfg=cfg: [pr.read(tabs[i], cfg) for i in ids],
+                                               len(ids)), 3)
+        bname = min(sweep, key=sweep.get)
+        best[k] = next(c for c in PROBE_SWEEP if _cfg_name(c) == bname)
+        x = x_dn if k == "down" else x_in
+
+        def dec(ids=ids, x=x, k=k):
+            for i in ids:
+                L = lins[i]
+                ops.linear_w4(x, L.q, L.G, (L.s, L.z), out=ys[k])
+
+        d_us = t_us(dec, len(ids))
+        b = wbytes[ids[0]]
+        per_kind[k] = {"weight_bytes": b, "probe_best": bname, "probe_us": sweep[bname],
+                       "probe_gbs": round(b / (sweep[bname] * 1e-6) / 1e9, 1),
+                       "decode_us": round(d_us, 3), "decode_over_probe": round(d_us / sweep[bname], 3),
+                       "sweep_us": sweep}
+
+    def pass_probe():
+        for i in range(len(lins)):
+            pr.read(tabs[i], best[kind_of[i]])
+
+    def pass_decode():
+        for L, k in zip(lins, kind_of):
+            ops.linear_w4(x_dn if k == "down" else x_in, L.q, L.G, (L.s, L.z), out=ys[k])
+
+    ms_a = _time_steps(_graph_or_eager(pass_probe, g), args.steps, args.warmup)
+    ms_c = _time_steps(_graph_or_eager(pass_decode, g), args.steps, args.warmup)
+    all_tab = pr.buffers([b for L in lins for b in (L.q, L.s, L.z)])
+    pers = {}
+    for cfg in PROBE_SWEEP:
+        pers[_cfg_name(cfg)] = round(_time_steps(_graph_or_eager(lambda cfg=cfg: pr.read(all_tab, cfg), g), st, wu), 5)
+    pbest = min(pers, key=pers.get)
+    total = sum(wbytes)
+    gbs = lambda ms: round(total / (ms * 1e-3) / 1e9, 2)   # noqa: E731
+    roof = _hbm_roofline("probe_stream_kernel (one launch per linear, fastest configuration per kind)",
+                         total / len(lins), ms_a * 1e3 / len(lins), None)
     cfg = {"workload": "C2 llama-3-8b int4 weights (128 linears, codes + scale + zero), read-only ceilings",
-           "weight_bytes_per_step": weight_bytes, "distinct_bytes_per_step": weight_bytes,
-           "per_linear_launch_gbs": gbs(ms_a), "persistent_launch_gbs": gbs(ms_b),
-           "decode_kernels_gbs": gbs(ms_c), "persistent_ms": round(ms_b, 5), "decode_ms": round(ms_c, 5),
-           "note": "GB/s over the weight bytes only (the decode line adds x and y, 0.1%)"}
+           "weight_bytes_per_step": total, "distinct_bytes_per_step": total,
+           "per_launch_pass_gbs": gbs(ms_a), "decode_pass_gbs": gbs(ms_c), "decode_ms": round(ms_c, 5),
+           "persistent_best": pbest, "persistent_ms": pers[pbest], "persistent_gbs": gbs(pers[pbest]),
+           "persistent_sweep_ms": pers, "per_kind": per_kind,
+           "note": "GB/s over the weight bytes only (the decode line adds x and y, 0.1%); per-kind figures "
+                   "are 32 launches of one kind as one graph"}
     return _line(gbs(ms_a), "GB/s", ms_a, args, cfg, roof, None, data="synthetic: the C2 stack's RTN-packed weights")
+
+
+def bench_stream(args, dev):
+    """HBM stream ceilings on buffers far past the 256 MB MALL: the read-only probe over one 4 GiB
+    buffer (every PROBE_SWEEP configuration, one launch per step), the probe's copy kernel and
+    torch's copy over 1 GiB -> 1 GiB. value = the fastest read-only configuration."""
+    import torch
+    pr = _Probe(dev)
+    big = torch.empty(4 << 30, dtype=torch.uint8, device=dev).fill_(3)
+    tab = pr.buffers([big])
+    st, wu = max(5, args.steps // 2), 2
+    reads = {}
+    for cfg in PROBE_SWEEP:
+        ms = _time_steps(lambda cfg=cfg: pr.read(tab, cfg), st, wu)
+        reads[_cfg_name(cfg)] = round(big.numel() / (ms * 1e-3) / 1e9, 1)
+    del big, tab
+    torch.cuda.empty_cache()
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    copies = {}
+    for u in (2, 4, 8):
+        for w in (2, 4, 8):
+            ms = _time_steps(lambda u=u, w=w: pr.call("imq_probe_copy", b.data_ptr(), a.data_ptr(), n, u, w,
+                                                      torch.cuda.current_stream(dev).cuda_stream), st, wu)
+            copies[f"U{u}_wg{w}"] = round(2 * n / (ms * 1e-3) / 1e9, 1)
+    ok = bool(torch.equal(a[:: 1 << 20], b[:: 1 << 20]))
+    ms_t = _time_steps(lambda: b.copy_(a), st, wu)
+    rbest = max(reads, key=reads.get)
+    cbest = max(copies, key=copies.get)
+    ms = big_ms = 4 * (1 << 30) / (reads[rbest] * 1e9) * 1e3
+    roof = _hbm_roofline(f"probe_stream_kernel {rbest} (4 GiB read-only)", 4 << 30, big_ms * 1e3, None)
+    cfg = {"workload": "HBM stream ceilings: 4 GiB read-only, 1 GiB -> 1 GiB copy", "read_best": rbest,
+           "read_sweep_gbs": reads, "copy_best": cbest, "copy_gbs": copies[cbest], "copy_sweep_gbs": copies,
+           "copy_checked": ok, "torch_copy_gbs": round(2 * n / (ms_t * 1e-3) / 1e9, 1),
+           "note": "copy GB/s count bytes read + bytes written"}
+    return _line(reads[rbest], "GB/s", ms, args, cfg, roof, None, data="synthetic: constant-filled buffers")
+
+
+def bench_launch(args, dev):
+    """Launch cost of a chain of dependent kernels on one stream: 128 empty kernels (one
+    workgroup per CU, and one workgroup), replayed as a HIP graph and launched eagerly.
+    value = µs per launch, graph, one workgroup per CU."""
+    import torch
+    from infinitemodel_amd import _lib
+    L = _lib.lib()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    st = lambda: torch.cuda.current_stream(dev).cuda_stream   # noqa: E731
+    out = {}
+    for grid in (cus, 1):
+        def chain(grid=grid):
+            for _ in range(128):
+                _lib.call("imq_probe_empty", grid, st())
+        out[f"graph_grid{grid}_us"] = round(_time_steps(_graph_or_eager(chain, True), args.steps, args.warmup)
+                                            * 1e3 / 128, 3)
+        out[f"eager_grid{grid}_us"] = round(_time_steps(chain, max(5, args.steps // 4), 2) * 1e3 / 128, 3)
+    v = out[f"graph_grid{cus}_us"]
+    cfg = {"workload": "128 dependent empty kernels per step on one stream", "cus": cus, **out}
+    return _line(v, "us/launch", v * 128 / 1e3, args, cfg, None, None, hib=False, dtype="none",
+                 data="synthetic: empty kernels")
+
+
+def bench_mfma(args, dev):
+    """MFMA issue peak: 4 independent accumulator chains per wave of v_mfma_f32_32x32x16_bf16
+    (and v_mfma_f32_16x16x32_bf16) on register operands, 1 / 2 / 4 workgroups of 4 waves per CU.
+    value = the fastest 32x32x16 figure (TFLOP/s)."""
+    import torch
+    pr = _Probe(dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    iters = 20000
+    res, mss = {}, {}
+    for kind, name, fl in ((0, "32x32x16", 32768), (1, "16x16x32", 16384)):
+        for w in (1, 2, 4):
+            ms = _time_steps(lambda kind=kind, w=w: pr.call("imq_probe_mfma", kind, iters, w, pr.sink.data_ptr(),
+                                                           pr.sink.numel() * 4,
+                                                           torch.cuda.current_stream(dev).cuda_stream),
+                             max(5, args.steps // 4), 2)
+            flops = cus * w * 4 * 4 * iters * fl
+            res[f"{name}_wg{w}"] = round(flops / (ms * 1e-3) / 1e12, 1)
+            mss[f"{name}_wg{w}"] = ms
+    best = max((k for k in res if k.startswith("32x32")), key=res.get)
+    roof = {"bound": "mfma", "achieved": res[best], "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s",
+            "frac": round(res[best] * 1e12 / BF16_PEAK, 4), "traffic": None, "kernel": f"probe_mfma_kernel {best}"}
+    cfg = {"workload": "bf16 MFMA issue peak on register operands", "iters": iters, "tflops": res}
+    return _line(res[best], "TFLOP/s", mss[best], args, cfg, roof, None, data="synthetic: register operands")
 
 
 # ---------------------------------------------------------------------------------------------
@@ -674,12 +837,53 @@ def bench_copy(args, dev):
                  {"workload": "device copy 1 GiB -> 1 GiB", "bytes_read": n, "bytes_written": n}, roof, None)
 
 
+def trace_summary(path: str, launches: int, steps: int, period=None) -> str:
+    """Markdown summary of the last ``launches`` dispatches of a rocprofv3 kernel-trace CSV: per
+    kernel the count, mean / min / max duration (µs) and total; with ``period`` (launches per step)
+    the mean per launch position; and the kernel time per step (total / steps)."""
+    import csv
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r.get("Kind", "KERNEL_DISPATCH") != "KERNEL_DISPATCH":
+                continue
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    if launches > len(rows):
+        raise SystemExit(f"{path} holds {len(rows)} dispatches, fewer than --launches {launches}")
+    sel = rows[-launches:]
+    by = {}
+    for b, e, n in sel:
+        by.setdefault(n, []).append((e - b) / 1e3)
+    total = sum(sum(v) for v in by.values())
+    out = [f"last {launches} of {len(rows)} dispatches ({steps} timed steps), "
+           f"window {(sel[-1][1] - sel[0][0]) / 1e3:.1f} µs, kernel time {total:.1f} µs, "
+           f"**kernel time per step {total / steps:.2f} µs**", "",
+           "| kernel | count | mean µs | min µs | max µs | total µs |", "|---|---|---|---|---|---|"]
+    for n, v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        short = n if len(n) <= 110 else n[:107] + "..."
+        out.append(f"| `{short}` | {len(v)} | {sum(v) / len(v):.3f} | {min(v):.3f} | {max(v):.3f} | {sum(v):.1f} |")
+    if period:
+        out += ["", f"mean µs per launch position (period {period}):", "",
+                "| position | kernel | mean µs |", "|---|---|---|"]
+        for p in range(period):
+            v = [(e - b) / 1e3 for i, (b, e, n) in enumerate(sel) if i % period == p]
+            out.append(f"| {p} | `{sel[p][2][:60]}` | {sum(v) / len(v):.3f} |")
+    return "\n".join(out)
+
+
 BENCH = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "gptoss": bench_gptoss,
-         "head": bench_head, "copy": bench_copy, "ceiling": bench_ceiling}
+         "head": bench_head, "copy": bench_copy, "ceiling": bench_ceiling, "stream": bench_stream,
+         "launch": bench_launch, "mfma": bench_mfma}
 
 
 def main():
     args = _parse()
+    if args.trace_summary:
+        if not args.launches:
+            raise SystemExit("--trace-summary needs --launches (steps x launches per step)")
+        print(trace_summary(args.trace_summary, args.launches, args.steps, args.period), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the quantized-linear hot path runs per GPU and this "
               "build's GPU boxes have one GPU; use --gpus 1",

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define IMQ_ABI_VERSION 6
+#define IMQ_ABI_VERSION 7
 
 #define IMQ_DT_BF16 0
 #define IMQ_DT_FP16 1
@@ -101,6 +101,17 @@ int imq_pack_w8(const void* W, int64_t w_row_stride, int w_dtype, int64_t N, int
  * Without it (or when too small) K is not split. */
 int64_t imq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K_pad);
 
+/* Workspace bytes imq_linear_w4 uses for exactly this call (the same arguments as imq_linear_w4,
+ * without the pointers) on the current device: 0 when the kernels it picks keep every partial
+ * inside the workgroup (the decode line and wave-split kernels), the fp32 partials of the K-split
+ * or split-K plan otherwise; -1 for invalid sizes. imq_linear_workspace_bytes above is the
+ * shape-only upper bound over the int4 / int2 / int8 families. No counterpart in the reference
+ * (its Triton ops allocate internally). */
+int64_t imq_linear_w4_workspace_bytes(int64_t M, int64_t K_pad, int64_t N, int64_t group_size,
+                                      int64_t q_row_stride, int64_t x_row_stride, int64_t s_stride_n,
+                                      int64_t s_stride_g, int s_dtype, int64_t z_stride_n,
+                                      int64_t z_stride_g, int z_dtype);
+
 int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad, const void* qweight,
                   int64_t q_row_stride, const void* scale, int64_t s_stride_n, int64_t s_stride_g,
                   int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
@@ -127,8 +138,8 @@ int imq_linear_w8(const void* x, int64_t x_row_stride, int64_t M, int64_t K, con
  * kernels and results as imq_linear_w4 without the workspace arguments. The K-split / split-K
  * partials go to a static scratch array of IMQ_NOALLOC_SCRATCH_BYTES bytes that each GPU the
  * library runs on holds from the first call on that GPU until the process ends; nothing is
- * allocated or freed per call. Shapes whose workspace need (imq_linear_workspace_bytes) exceeds
- * it return IMQ_ERR_SCRATCH before any launch. Every call on one GPU shares that GPU's array and
+ * allocated or freed per call. Calls whose own workspace need (imq_linear_w4_workspace_bytes)
+ * exceeds it return IMQ_ERR_SCRATCH before any launch. Every call on one GPU shares that GPU's array and
  * it keeps the last call's partials (they need no clearing: each call writes every partial it
  * reads), so calls that may overlap on one GPU (other streams, or unordered work) race: order
  * them on one stream. */
@@ -198,17 +209,27 @@ int imq_moe_experts_w4_ex(const void* hidden, int64_t h_row_stride, int64_t T, i
                           void* stream);
 
 /* ---- measurement probes ---------------------------------------------------------------------
- * No counterpart in the reference: read-only HBM streaming kernels that set the practical ceiling
- * the decode kernels are measured against (bench.py --config ceiling). Nothing is written.
- *   imq_probe_read: one launch reads `bytes` (a multiple of 16, 16-byte aligned) of `buf`.
- *   imq_probe_read_seq: one launch reads nbuf buffers in order; `ptrs` is a device array of nbuf
- *     uint64 addresses (16-byte aligned), `n16s` a device array of nbuf int64 sizes in 16-byte
- *     units, max_n16 the largest of them (sizes the grid).
+ * No counterpart in the reference: the hardware ceilings the hot-path kernels are measured
+ * against (bench.py --config ceiling | stream | launch | mfma).
+ *   imq_probe_stream: one read-only launch over nbuf buffers taken in order; `ptrs` is a device
+ *     array of nbuf uint64 addresses (16-byte aligned), `n16s` a device array of nbuf int64 sizes
+ *     in 16-byte words (buffers of 0 words are skipped), total_n16 their sum (sizes the grid).
+ *     loads_per_lane U in {1, 2, 4, 8, 16} (a workgroup of 256 lanes reads 256 U words per chunk,
+ *     the next chunk's loads issued before the current one's are consumed), at most wg_per_cu
+ *     (1..32) workgroups per CU, nontemporal != 0 for non-temporal loads. Nothing is written.
+ *   imq_probe_copy: dst[0:bytes) = src[0:bytes) (bytes a multiple of 16, both 16-byte aligned),
+ *     U in {2, 4, 8} loads then U non-temporal stores per lane.
+ *   imq_probe_empty: one empty kernel of `grid` workgroups of 64 lanes.
+ *   imq_probe_mfma: cus * wg_per_cu workgroups of 4 waves, each wave running 4 independent
+ *     accumulator chains of `iters` MFMAs: kind 0 = v_mfma_f32_32x32x16_bf16 (32768 flops each),
+ *     kind 1 = v_mfma_f32_16x16x32_bf16 (16384 flops each).
  *   `sink`: device memory of at least imq_probe_sink_bytes() bytes (never written in practice). */
 int64_t imq_probe_sink_bytes(void);
-int imq_probe_read(const void* buf, int64_t bytes, void* sink, int64_t sink_bytes, void* stream);
-int imq_probe_read_seq(const void* ptrs, const void* n16s, int nbuf, int64_t max_n16, void* sink,
-                       int64_t sink_bytes, void* stream);
+int imq_probe_stream(const void* ptrs, const void* n16s, int nbuf, int64_t total_n16, int loads_per_lane,
+                     int wg_per_cu, int nontemporal, void* sink, int64_t sink_bytes, void* stream);
+int imq_probe_copy(void* dst, const void* src, int64_t bytes, int loads_per_lane, int wg_per_cu, void* stream);
+int imq_probe_empty(int grid, void* stream);
+int imq_probe_mfma(int kind, int64_t iters, int wg_per_cu, void* sink, int64_t sink_bytes, void* stream);
 
 /* GPTQ int2 solver (the calibrated int2 packer's quantization, after its Cholesky stage).
  *   imq_gptq_int2_params: the group search alone -- replaces gptq_pack.py:78-100 (_find_params):

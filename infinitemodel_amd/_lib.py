@@ -43,6 +43,8 @@ SIGNATURES = {
                              _c_i64, _c_vp]),
     "imq_pack_w8": (_c_int, [_c_vp, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
     "imq_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "imq_linear_w4_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                               _c_int, _c_i64, _c_i64, _c_int]),
     "imq_linear_w4": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_int,
                                _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
                                _c_vp]),
@@ -68,8 +70,10 @@ SIGNATURES = {
                                        _c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int,
                                        _c_float, _c_float, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
     "imq_probe_sink_bytes": (_c_i64, []),
-    "imq_probe_read": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
-    "imq_probe_read_seq": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_vp, _c_i64, _c_vp]),
+    "imq_probe_stream": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
+    "imq_probe_copy": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
+    "imq_probe_empty": (_c_int, [_c_int, _c_vp]),
+    "imq_probe_mfma": (_c_int, [_c_int, _c_i64, _c_int, _c_vp, _c_i64, _c_vp]),
     "imq_gptq_int2_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "imq_gptq_int2_params": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, ctypes.c_double, _c_vp, _c_vp, _c_vp]),
     "imq_gptq_int2_solve": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_int, ctypes.c_double,

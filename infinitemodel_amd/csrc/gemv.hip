@@ -2388,6 +2388,27 @@ int wsplit_w4(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
   return IMQ_ERR_UNSUPPORTED;
 }
 
+// Workspace bytes the int4 decode dispatch (skinny_w4) uses for this call on the current device:
+// the K-split partials when the K-split kernel is the first fast kernel that takes the call, else
+// 0 (the line and wave-split kernels keep every partial in the workgroup). Pointer alignment is not
+// known here and taken as satisfied; an unaligned call falls back to kernels without a workspace,
+// so the figure stays an upper bound.
+int64_t w4_decode_workspace_bytes(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm,
+                                  int64_t ssn, int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt) {
+  if (M < 1 || M > 16 || G % kStep != 0 || Kpad % G != 0 || Kpad <= 0 || sdt != zdt) return 0;
+  if (((G / kStep) & (G / kStep - 1)) != 0 || (sqn & 15) || (sxm & 7) || N > (1 << 30) || Kpad > (1 << 28))
+    return 0;
+  const DevInfo di = device_info();
+  int S2, W;
+  size_t lds;
+  if (line_plan(M, Kpad, G, N, sqn, sxm, ssn, ssg, szn, szg, sdt, zdt, di.max_lds, &S2, &W, &lds)) return 0;
+  if (wsplit_plan(M, Kpad, G, N, sqn, sxm, ssn, ssg, szn, szg, sdt, zdt, di.max_lds, di.cus)) return 0;
+  int splits, nw, s2;
+  if (ksplit_plan(M, Kpad, G, N, sqn, sxm, ssn, ssg, szn, szg, sdt, zdt, di.max_lds, di.cus, &splits, &nw, &s2, &lds))
+    return (int64_t)splits * M * N * 4;
+  return 0;
+}
+
 // Fast path eligibility + launch. Returns IMQ_ERR_UNSUPPORTED when the caller must fall back.
 // ws / wsb: the caller's optional workspace (the K-split path of 4 < M <= 16 needs one).
 int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,

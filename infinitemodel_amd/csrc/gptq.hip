@@ -288,6 +288,8 @@ extern "C" int imq_gptq_int2_solve(float* W, int64_t ldw, int64_t out, int64_t i
   const int64_t ng = (in_f + G - 1) / G, in_pad = ng * G;
   if (ldw < in_f || ldh < in_f || ldq < in_pad / 4 || ldsz < ng || (dq && lddq < in_f)) return IMQ_ERR_INVALID;
   if (out > 0x7fffffff || in_pad > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  // the update kernel's grid.y is the 64-row tile count: refuse before anything is written
+  if ((out + 63) / 64 > 65535) return IMQ_ERR_UNSUPPORTED;
   const int64_t need = imq_gptq_int2_workspace_bytes(out, blocksize);
   if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15)) return IMQ_ERR_INVALID;
   GptqShrink sh;
@@ -304,7 +306,6 @@ extern "C" int imq_gptq_int2_solve(float* W, int64_t ldw, int64_t out, int64_t i
     if (i2 < in_f) {
       GptqUpdateArgs u{W, ldw, (int)out, (int)in_f, (int)i1, (int)(i2 - i1), (int)i2, Hinv, ldh, err};
       const int64_t gx = (in_f - i2 + 63) / 64, gy = (out + 63) / 64;
-      if (gy > 65535) return IMQ_ERR_UNSUPPORTED;
       gptq_update_kernel<<<dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, st>>>(u);
       IMQ_LAUNCH_CHECK();
     }

@@ -15,6 +15,8 @@ int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
               int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
 int64_t ksplit_workspace_bytes(int64_t M, int64_t N, int64_t Kpad);
+int64_t w4_decode_workspace_bytes(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm,
+                                  int64_t ssn, int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt);
 int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
               int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
@@ -58,6 +60,17 @@ extern "C" int64_t imq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K_pa
   const int64_t g = imq::gemm_workspace_bytes(M, N, K_pad);
   const int64_t d = imq::ksplit_workspace_bytes(M, N, K_pad);
   return g > d ? g : d;
+}
+
+extern "C" int64_t imq_linear_w4_workspace_bytes(int64_t M, int64_t K_pad, int64_t N, int64_t group_size,
+                                                 int64_t q_row_stride, int64_t x_row_stride, int64_t s_stride_n,
+                                                 int64_t s_stride_g, int s_dtype, int64_t z_stride_n,
+                                                 int64_t z_stride_g, int z_dtype) {
+  if (M < 0 || N < 0 || K_pad <= 0 || group_size <= 0 || K_pad % group_size) return -1;
+  if (M == 0 || N == 0) return 0;
+  if (M > 16) return imq::gemm_workspace_bytes(M, N, K_pad);
+  return imq::w4_decode_workspace_bytes(M, K_pad, group_size, N, q_row_stride, x_row_stride, s_stride_n, s_stride_g,
+                                        z_stride_n, z_stride_g, s_dtype, z_dtype);
 }
 
 extern "C" int imq_launch_plan(int kind, const int64_t* in, int64_t* out) {
@@ -169,8 +182,12 @@ extern "C" int imq_linear_w4_noalloc(const void* x, int64_t x_row_stride, int64_
   if (rc != IMQ_OK) return rc;
   if (M == 0 || N == 0) return IMQ_OK;
   // The partials of the K-split / split-K launches need no initialisation (every element a
-  // reduction reads is written first by the same call), so the array is never cleared.
-  if (imq_linear_workspace_bytes(M, N, K_pad) > IMQ_NOALLOC_SCRATCH_BYTES) return IMQ_ERR_SCRATCH;
+  // reduction reads is written first by the same call), so the array is never cleared. The need
+  // is this call's own (the dispatcher's plans for these strides on this device): shapes whose
+  // kernels keep their partials in the workgroup need none, whatever their size.
+  const int64_t need = imq_linear_w4_workspace_bytes(M, K_pad, N, group_size, q_row_stride, x_row_stride, s_stride_n,
+                                                     s_stride_g, s_dtype, z_stride_n, z_stride_g, z_dtype);
+  if (need > IMQ_NOALLOC_SCRATCH_BYTES) return IMQ_ERR_SCRATCH;
   void* ws = nullptr;
   rc = scratch_ptr(&ws);
   if (rc != IMQ_OK) return rc;

@@ -203,7 +203,16 @@ def _linear_g(fn: str, codes_per_byte: int, x, qweight, group_size: int, sz, out
         raise ValueError("out must be a bf16 [M, N] tensor with unit column stride")
     y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
-        ws, wsb = _workspace(dev, M, N, Kpad)
+        if fn == "imq_linear_w4":
+            # this call's own need (0 for the decode kernels that keep their partials in the
+            # workgroup), not the shape-only bound over all formats
+            need = int(_lib.lib().imq_linear_w4_workspace_bytes(
+                M, Kpad, N, group_size, qweight.stride(0), x.stride(0), scale.stride(0), scale.stride(1),
+                dtype_code(scale.dtype), zero.stride(0), zero.stride(1), dtype_code(zero.dtype)))
+            w = _scratch(dev, need)
+            ws, wsb = (0, 0) if w is None else (w.data_ptr(), w.numel())
+        else:
+            ws, wsb = _workspace(dev, M, N, Kpad)
         call(fn, _ptr(x), x.stride(0), M, Kpad, _ptr(qweight), qweight.stride(0), _ptr(scale), scale.stride(0),
              scale.stride(1), dtype_code(scale.dtype), _ptr(zero), zero.stride(0), zero.stride(1),
              dtype_code(zero.dtype), N, group_size, _ptr(y), y.stride(0), ws, wsb, _stream(dev))

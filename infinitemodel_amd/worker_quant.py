@@ -804,9 +804,13 @@ def _moe_fused_compute(experts_mod, hidden_states, top_k_index, top_k_weights):
     weighted combine into ``[T, H]``."""
     from . import ops
     gu, dn = experts_mod.gate_up_proj, experts_mod.down_proj
+    # no host-side id check: the router's top-k ids lie in [0, E) by construction, the reference's
+    # fused compute (worker_quant.py:2167-2191) checks none, and the kernels clamp any id outside
+    # [0, E) to expert 0, so the layer never waits on a device-to-host read
     out = ops.moe_experts_w4(hidden_states, top_k_index, top_k_weights,
                              (*gu._kernel_tensors(), int(gu.in_features)),
-                             (*dn._kernel_tensors(), int(dn.in_features)), int(gu.group_size))
+                             (*dn._kernel_tensors(), int(dn.in_features)), int(gu.group_size),
+                             check_ids=False)
     return out.to(hidden_states.dtype)
 
 
@@ -918,7 +922,7 @@ def _gptoss_fused_compute(experts_mod, hidden_states, router_indices, routing_we
                              act="gptoss", gu_bias=experts_mod.gate_up_proj_bias,
                              dn_bias=experts_mod.down_proj_bias,
                              alpha=float(getattr(experts_mod, "alpha", 1.702)),
-                             limit=float(getattr(experts_mod, "limit", 7.0)))
+                             limit=float(getattr(experts_mod, "limit", 7.0)), check_ids=False)
     return out.to(hidden_states.dtype)
 
 

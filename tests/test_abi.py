@@ -81,7 +81,7 @@ def test_exports_are_c_linkage():
 
 
 def test_abi_version_and_strerror(L):
-    assert L.imq_abi_version() == 6
+    assert L.imq_abi_version() == 7
     assert L.imq_strerror(0) == b"ok"
     for rc in (_lib.IMQ_ERR_INVALID, _lib.IMQ_ERR_UNSUPPORTED, _lib.IMQ_ERR_ALIGN, _lib.IMQ_ERR_SCRATCH):
         assert len(L.imq_strerror(rc)) > 5
@@ -108,6 +108,28 @@ def test_linear_workspace_bytes_host_rules(L):
     assert L.imq_linear_workspace_bytes(-1, 4096, 4096) < 0
 
 
+def _w4_need(L, M, K, N, G=128, sdt=0):
+    return L.imq_linear_w4_workspace_bytes(M, K, N, G, K // 2, K, K // G, 1, sdt, K // G, 1, sdt)
+
+
+def test_linear_w4_workspace_bytes_host_rules(L):
+    """The per-call query follows the dispatcher's plans: decode rows M <= 4 take the line kernel
+    (no partials); 4 < M <= 16 at K_pad 14336 take the K-split kernel ([splits][M][N] fp32,
+    1024-code splits); a skinny-only shape and invalid sizes. (Which K_pad 2048 / 4096 shapes the
+    wave-split kernel takes depends on the device's LDS, so the GPU tests cover them.)"""
+    assert _w4_need(L, 1, 4096, 4096) == 0
+    assert _w4_need(L, 4, 14336, 4096) == 0
+    assert _w4_need(L, 16, 14336, 4096) == 14 * 16 * 4096 * 4
+    assert _w4_need(L, 8, 14336, 4096) == 14 * 8 * 4096 * 4
+    assert _w4_need(L, 8, 384, 96) == 0          # K_pad % 256: skinny kernel
+    assert _w4_need(L, 0, 4096, 4096) == 0
+    assert _w4_need(L, -1, 4096, 4096) < 0
+    assert L.imq_linear_w4_workspace_bytes(1, 4000, 4096, 128, 2000, 4000, 32, 1, 0, 32, 1, 0) < 0
+    # never above the shape-only bound
+    for M, K, N in ((16, 14336, 4096), (5, 4096, 6144), (16, 4096, 28672), (512, 14336, 4096)):
+        assert 0 <= _w4_need(L, M, K, N) <= L.imq_linear_workspace_bytes(M, N, K)
+
+
 def test_invalid_arguments_are_rejected_on_the_host(L):
     """Null pointers and inconsistent shapes return IMQ_ERR_INVALID without a device call."""
     nul = None
@@ -131,15 +153,15 @@ def test_invalid_arguments_are_rejected_on_the_host(L):
 
 def test_noalloc_rejects_on_the_host(L):
     """imq_linear_w4_noalloc validates like imq_linear_w4 and refuses, before any device call,
-    shapes whose workspace need exceeds its static scratch (IMQ_ERR_SCRATCH)."""
+    calls whose own workspace need exceeds its static scratch (IMQ_ERR_SCRATCH)."""
     nul = None
     rc = L.imq_linear_w4_noalloc(nul, 4096, 1, 4096, nul, 2048, nul, 32, 1, 0, nul, 32, 1, 0, 4096, 128, nul,
                                  4096, nul)
     assert rc == _lib.IMQ_ERR_INVALID
     one = ctypes.c_void_p(16)   # never dereferenced: the size check fails first
-    M, N, K = 16, 1 << 20, 4096
-    need = L.imq_linear_workspace_bytes(M, N, K)
-    assert need > _lib.IMQ_NOALLOC_SCRATCH_BYTES
+    M, N, K = 16, 1 << 20, 14336     # K-split: 14 splits x 16 x 2^20 x 4 B of partials
+    need = _w4_need(L, M, K, N)
+    assert need == 14 * 16 * N * 4 > _lib.IMQ_NOALLOC_SCRATCH_BYTES
     rc = L.imq_linear_w4_noalloc(one, K, M, K, one, K // 2, one, K // 128, 1, 0, one, K // 128, 1, 0, N, 128, one,
                                  N, nul)
     assert rc == _lib.IMQ_ERR_SCRATCH

@@ -74,6 +74,38 @@ def test_quantlinear4_naive_path_when_disabled(dev, monkeypatch):
     assert torch.equal(m(x), F.linear(x, m._dequant(torch.bfloat16)))
 
 
+def test_quantlinear4_prefill_threshold_falls_through(dev):
+    """A bound module whose measured threshold is the 64-row bucket (worker_quant.py:817-853):
+    calls whose row bucket reaches 64 (33..64 rows and above) run the naive F.linear over the HIP
+    dequant, bit for bit; 32 rows and fewer keep the fused op, bit for bit its output."""
+    import torch
+    import torch.nn.functional as F
+    from infinitemodel_amd import ops
+    m, c = _q4(dev, 512, 1000, 7, bias=True)
+    m.prepare_fused()
+    assert m._fused is not None
+    m._naive_m_min = 64
+    w = m._dequant(torch.bfloat16)
+    qw, pair, op, in_pad = m._fused
+    assert op is ops.linear_w4
+    for rows in (1, 16, 32, 33, 64, 100):
+        x = C.to_torch(C.bf16_normal(C.rng(rows), (rows, 1000)), "bf16", dev)
+        y = m(x)
+        if rows <= 32:
+            xp = torch.nn.functional.pad(x, (0, in_pad - 1000))
+            ref = op(xp, qw, 128, pair) + m.bias
+        else:
+            ref = F.linear(x, w, m.bias)
+        assert torch.equal(y, ref), rows
+    # leading dims are rows: 2 x 20 = 40 rows -> bucket 64 -> naive
+    x = C.to_torch(C.bf16_normal(C.rng(9), (2, 20, 1000)), "bf16", dev)
+    assert torch.equal(m(x), F.linear(x, w, m.bias))
+    # and the fused rows still match the oracle
+    x = C.bf16_normal(C.rng(10), (32, 1000))
+    ref = oq.linear_ref(x, c["Wd"]) + C.t2np(m.bias)
+    assert oq.max_rel(C.t2np(m(C.to_torch(x, "bf16", dev))), ref) <= MAX_REL
+
+
 def test_quantlinear2_module(dev):
     import torch
     from infinitemodel_amd import ops
@@ -154,4 +186,18 @@ def test_fused_moe_forward_on_olmoe_experts(dev):
         y = ex(C.to_torch(x, "bf16", dev), torch.from_numpy(idx).to(dev), C.to_torch(w, "bf16", dev))
         assert ex._fused_moe_ok is True
         exact = om.moe_exact(x, idx, w, Dgu, Ddn)
+        assert oq.max_rel(C.t2np(y), exact) <= MAX_REL, T
+    # the installed forward never waits on the device (no id check read back per layer), also at
+    # the grouped-GEMM token counts
+    for T in (1, 16, 300):
+        idx, w = om.route_topk(r.standard_normal((T, E)).astype(np.float32), k)
+        xt = C.to_torch(C.bf16_normal(r, (T, H)), "bf16", dev)
+        it, wt = torch.from_numpy(idx).to(dev), C.to_torch(w, "bf16", dev)
+        torch.cuda.synchronize()
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            y = ex(xt, it, wt)
+        finally:
+            torch.cuda.set_sync_debug_mode("default")
+        exact = om.moe_exact(C.t2np(xt), idx, w, Dgu, Ddn)
         assert oq.max_rel(C.t2np(y), exact) <= MAX_REL, T

@@ -34,7 +34,9 @@ def _run_pair(dev, M, N, K, seed):
     L = _lib.lib()
     x, q, s, z = _case(dev, M, N, K, seed)
     st = torch.cuda.current_stream(dev).cuda_stream
-    need = int(L.imq_linear_workspace_bytes(M, N, K))
+    need = int(L.imq_linear_w4_workspace_bytes(M, K, N, 128, q.stride(0), x.stride(0), s.stride(0), s.stride(1),
+                                                _lib.IMQ_DT_BF16, z.stride(0), z.stride(1), _lib.IMQ_DT_BF16))
+    assert need <= L.imq_linear_workspace_bytes(M, N, K)
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
     y_ref = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     y_na = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
@@ -51,8 +53,8 @@ def _run_pair(dev, M, N, K, seed):
 @pytest.mark.parametrize("first,second", [
     # prefill split-K: C4 14336 -> 4096 at M=512 (32 MiB of partials), then a smaller split-K shape
     ((512, 4096, 14336), (64, 4096, 4096)),
-    # decode K-split: C2 gate_up at M=16 (7.3 MB of partials), then down at M=8
-    ((16, 28672, 4096), (8, 4096, 14336)),
+    # decode K-split: C2 down at M=16 (3.7 MB of partials), then down at M=8
+    ((16, 4096, 14336), (8, 4096, 14336)),
 ])
 def test_noalloc_matches_workspace_entry(dev, first, second):
     n1 = _run_pair(dev, *first, seed=11)
@@ -61,9 +63,13 @@ def test_noalloc_matches_workspace_entry(dev, first, second):
 
 
 def test_noalloc_decode_rows_without_partials(dev):
-    """M <= 4 takes the line kernel (no partials): still identical, twice in a row."""
+    """M <= 4 takes the line kernel and C2 gate_up at M = 16 the wave-split kernel (no partials
+    either): still identical, twice in a row, and the allocation-free entry takes wave-split shapes
+    of any width (no scratch needed)."""
     assert _run_pair(dev, 4, 6144, 4096, seed=13) == 0
     assert _run_pair(dev, 1, 4096, 4096, seed=14) == 0
+    assert _run_pair(dev, 16, 28672, 4096, seed=16) == 0
+    assert _run_pair(dev, 16, 1 << 19, 4096, seed=17) == 0
 
 
 def test_noalloc_rejects_oversize_on_gpu(dev):
@@ -71,9 +77,11 @@ def test_noalloc_rejects_oversize_on_gpu(dev):
     nothing (the output keeps its contents)."""
     import torch
     L = _lib.lib()
-    M, N, K = 16, 1 << 19, 4096      # 4 splits x 16 x 524288 x 4 B = 128 MiB of partials
-    assert L.imq_linear_workspace_bytes(M, N, K) > _lib.IMQ_NOALLOC_SCRATCH_BYTES
+    M, N, K = 16, 1 << 19, 14336     # K-split: 14 splits x 16 x 524288 x 4 B = 448 MiB of partials
     x, q, s, z = _case(dev, M, N, K, seed=15)
+    need = L.imq_linear_w4_workspace_bytes(M, K, N, 128, q.stride(0), x.stride(0), s.stride(0), s.stride(1),
+                                           _lib.IMQ_DT_BF16, z.stride(0), z.stride(1), _lib.IMQ_DT_BF16)
+    assert need == 14 * M * N * 4 > _lib.IMQ_NOALLOC_SCRATCH_BYTES
     y = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
     rc = L.imq_linear_w4_noalloc(*_args(x, q, s, z, y), torch.cuda.current_stream(dev).cuda_stream)
     assert rc == _lib.IMQ_ERR_SCRATCH
