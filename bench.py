@@ -242,10 +242,34 @@ def cpu_c2(args, M: int, layers: int = 8):
             cpu_path.tinygemm_linear(x_dn if name == "down" else x_in, mat2, 128, sz)
 
     med, runs = _cpu_time(one_pass, args.cpu_seconds)
+    del packs
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
             "sample": f"C2 shapes, {layers} layers x 4 linears (0.93 GB of int4 weights, beyond host cache), "
                       f"M={M}, torch tinygemm _weight_int4pack_mm_for_cpu, median of {runs} passes",
-            "ms_per_layer": round(med * 1e3 / layers, 3), "cpu": _cpu_model()}
+            "ms_per_layer": round(med * 1e3 / layers, 3), "cpu": _cpu_model(),
+            "naive": _cpu_naive_int4(args, [(N, K) for _, K, N in wl.LLAMA8B_PROJ] * 2, M,
+                                     "C2 shapes, 2 layers x 4 linears (232 MB of int4 weights)")}
+
+
+def _cpu_naive_int4(args, shapes, M: int, what: str) -> dict:
+    """The reference's naive CPU int4 forward (worker_quant.py:847-853: the bf16 dequant and a bf16
+    F.linear below 16 rows, the fp32 dequant and an fp32 GEMM from 16 rows) over ``shapes``
+    (N, K), timed beside tinygemm on the same host cores."""
+    import torch
+    from oracle import cpu_path
+    n = cpu_path.tune_cpu_threads()
+    packs = [(K, _cpu_int4_random(N, K, 7000 + i)) for i, (N, K) in enumerate(shapes)]
+    xs = {K: torch.randn(M, K).to(torch.bfloat16) for _, K in shapes}
+
+    def one():
+        for K, (q, s, z) in packs:
+            cpu_path.naive_linear(xs[K], q, s, z, K, 128, bits=4)
+
+    med, runs = _cpu_time(one, max(2.0, args.cpu_seconds / 2), min_runs=2)
+    nbytes = sum(N * K // 2 + N * (K // 128) * 4 + M * K * 2 + M * N * 2 for N, K in shapes)
+    rule = "bf16 dequant + bf16 F.linear" if M < 16 else "fp32 dequant + fp32 GEMM"
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": n,
+            "sample": f"{what}, M={M}, naive rule ({rule}), median of {runs} passes"}
 
 
 # ---------------------------------------------------------------------------------------------
@@ -283,7 +307,8 @@ def bench_c1(args, dev):
         med, runs = _cpu_time(one, args.cpu_seconds)
         cpu = {"value": round(b * len(packs) / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
                "sample": f"C1 shape, 48 distinct weights (0.43 GB), torch tinygemm, median of {runs} passes",
-               "cpu": _cpu_model()}
+               "cpu": _cpu_model(),
+               "naive": _cpu_naive_int4(args, [(4096, 4096)] * 8, M, "C1 shape, 8 distinct weights (71 MB)")}
     return _line(round(b * len(lins) / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
 
 

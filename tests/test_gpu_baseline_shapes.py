@@ -134,6 +134,35 @@ def test_c4_prefill_int4_m2048(dev, N, K):
         _assert_close(_run_w4(dev, c, x), oq.linear_ref(x, Wb), (N, K, M, out))
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_register_b_ragged_split_k(dev, bits):
+    """The register-B GEMM with ragged rows and columns AND K splits: M = 600, N = 1000, K = 14336
+    runs 128-row tiles with four K splits on 256 CUs (the plan the CPU bounds model restates), so
+    partial stores of ragged tiles and the reduction's column tails are exercised; then twice in a
+    row, bit-identical."""
+    import torch
+    from infinitemodel_amd import ops
+    M, N, K = 600, 1000, 14336
+    x = _x(M, K, seed=91)
+    if bits == 4:
+        c = C.int4_case.__wrapped__(N, K, 128, seed=92)
+        Wb = oq.round_to(oq.dequant_exact(oq.unpack_int4(c["q"]), c["s"], c["z"], 128, c["in_f"]).astype(np.float32),
+                         "bf16")
+        q, s_, z = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev), C.to_torch(c["z"], "bf16", dev)
+        run = lambda: ops.linear_w4(C.to_torch(x, "bf16", dev), q, 128, (s_, z))   # noqa: E731
+        ref = oq.linear_ref(x, Wb)
+    else:
+        c = C.int8_case.__wrapped__(N, K, seed=93, dt="bf16")
+        q, s_ = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev)
+        run = lambda: ops.linear_w8(C.to_torch(x, "bf16", dev), q, s_)   # noqa: E731
+        ref = oq.int8_gemm_ref(x, c["q"], c["s"])
+    y1 = run()
+    y2 = run()
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    _assert_close(C.t2np(y1), ref, (bits, M, N, K))
+
+
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
 def test_c4_prefill_int8_fp16_scale_m2048(dev, N, K):
     """int8 per-row symmetric with fp16 scales (the C4 int8 weights) at M = 2048."""

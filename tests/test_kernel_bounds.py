@@ -1380,3 +1380,166 @@ def test_register_b_plan_at_the_prefill_shapes():
         assert _lib_plan(_lib.IMQ_PLAN_GEMM_RB, 2048, 4096, G, 14336, 0, 0, 0, 2, 0, 256)[:2] == (8, 1)
         assert _lib_plan(_lib.IMQ_PLAN_GEMM_RB, 2048, 14336, G, 4096, 0, 0, 0, 2, 0, 256)[:2] == (8, 2)
         assert _lib_plan(_lib.IMQ_PLAN_GEMM_RB, 512, 4096, G, 14336, 0, 0, 0, 2, 0, 256) is None
+
+
+# ---- register-B prefill GEMM, dense form (csrc/rb_kernel.h gemm_rb_kernel MOE 0, gemm_rb.hip) ---
+# NW = 4 waves of 64 columns (BN 256), BM = 32 IB rows, K steps of 64. The model restates
+# rb_plan, the launcher's split-K shape (kps = ceil(KT / s), KT_split = min(KT - kt0, kps)), the
+# XCD-aware grouped tile mapping, the activation plan (row clamp to M - 1, 8 chunks of 16 bytes
+# per row), the weight plan (column clamp to N - 1, 16 bytes per half-wave per step for int4, 32
+# for int8), the group index of the scale / zero loads, the swizzled LDS stores and the masked
+# partial / output stores, and checks every access against its buffer -- plus that the workgroups
+# cover every (row tile, column tile, split) once and every output element once per split.
+RB_BK, RB_NW = 64, 4
+
+
+def rb_plan(M, N, K, cus=256):
+    """rb_plan in csrc/gemm_rb.hip: (32-row blocks per wave, K splits)."""
+    T8 = -(-M // 256) * -(-N // 256)
+    T4 = -(-M // 128) * -(-N // 256)
+    ib = 8 if (M > 128 and 2 * T8 >= cus) else 4
+    T = T8 if ib == 8 else T4
+    KT = K // RB_BK
+    s = 1
+    while s < 4 and 2 * T * s <= cus and KT // (2 * s) >= 16:
+        s *= 2
+    return ib, s
+
+
+def rb_tile(b, tiles_m, tiles_n, BM, BN):
+    """The dense form's tile mapping of workgroup b: (split, m0, n0)."""
+    T = tiles_m * tiles_n
+    split, L = divmod(b, T)
+    if T % 8 == 0:
+        L = (L & 7) * (T >> 3) + (L >> 3)
+    per_group = 8 * tiles_n
+    grp = L // per_group
+    first_m = grp * 8
+    gm = min(tiles_m - first_m, 8)
+    in_grp = L - grp * per_group
+    return split, (first_m + in_grp % gm) * BM, (in_grp // gm) * BN
+
+
+def rb_swz(row, ch):
+    return (row * 8 + (ch ^ ((row >> 1) & 7))) * 8
+
+
+def rb_store_rows(ib):
+    """Row offsets (within the tile) of the MFMA output elements a lane stores: 32 i + 8 (r >> 2) +
+    4 h + (r & 3) over i < IB, r < 16, h < 2 (the 32x32 MFMA's D layout)."""
+    return sorted(32 * i + 8 * (r >> 2) + 4 * h + (r & 3) for i in range(ib) for r in range(16) for h in range(2))
+
+
+def rb_ranges(M, N, K, bits, G, sxm, sqn, ssn, ssg, sym, cus=256, row_clamp=True):
+    """Every global element / byte range the dense register-B GEMM reads or writes, and the LDS
+    range of its activation stores, as (lo, hi) pairs per buffer; with the coverage checks."""
+    import numpy as np
+    ib, s = rb_plan(M, N, K, cus)
+    BM, BN, NTHR = 32 * ib, 64 * RB_NW, 64 * RB_NW
+    tiles_m, tiles_n = -(-M // BM), -(-N // BN)
+    KT = K // RB_BK
+    kps = -(-KT // s)
+    XC = BM * 8 // NTHR
+    QV = 2 if bits == 8 else 1
+    gsh = 0 if bits == 8 else int(math.log2(G))
+    step = RB_BK * bits // 8
+    # a lane's stored rows are each tile row once, and the activation plan's ids cover BM rows x 8 chunks
+    assert rb_store_rows(ib) == list(range(BM))
+    ids = np.arange(XC * NTHR)
+    rows, chs = ids >> 3, ids & 7
+    assert rows.max() == BM - 1
+    swz = (rows * 8 + (chs ^ ((rows >> 1) & 7))) * 8
+    assert len(set(swz.tolist())) == BM * 8           # the swizzle is a permutation of the chunks
+    r = {"lds": [int(swz.min()), int(swz.max()) + 8]}
+    cols = np.arange(BN)                               # n0 + 64 w + 32 j + c over w, j, c
+    lo = {k: math.inf for k in ("x", "q", "s", "part", "y")}
+    hi = {k: -math.inf for k in lo}
+    cover = np.zeros((s, M, N), dtype=np.int8)
+    seen = set()
+    for b in range(tiles_m * tiles_n * s):
+        split, m0, n0 = rb_tile(b, tiles_m, tiles_n, BM, BN)
+        assert (split, m0, n0) not in seen
+        seen.add((split, m0, n0))
+        kt0 = split * kps
+        kts = min(KT - kt0, kps)
+        assert kts >= 1, (M, N, K, b)
+        kt_lo, kt_hi = kt0, kt0 + kts - 1            # load_a / load_b clamp ktl to KT_split - 1
+        rr = np.where((m0 + rows < M) | (not row_clamp), rows, M - 1 - m0)
+        xb = (m0 + rr) * sxm + chs * 8
+        lo["x"] = min(lo["x"], int(xb.min()) + kt_lo * RB_BK)
+        hi["x"] = max(hi["x"], int(xb.max()) + kt_hi * RB_BK + 8)
+        n = np.minimum(n0 + cols, N - 1)
+        for h in range(2):
+            qb = n * sqn + (32 if bits == 8 else 16) * h
+            lo["q"] = min(lo["q"], int(qb.min()) + kt_lo * step)
+            hi["q"] = max(hi["q"], int(qb.max()) + kt_hi * step + 16 * QV)
+            if bits != 8:
+                g_lo, g_hi = (kt_lo * RB_BK + 32 * h) >> gsh, (kt_hi * RB_BK + 32 * h) >> gsh
+                lo["s"] = min(lo["s"], int(n.min()) * ssn + g_lo * ssg)
+                hi["s"] = max(hi["s"], int(n.max()) * ssn + g_hi * ssg + 1)
+            else:
+                lo["s"] = min(lo["s"], int(n.min()) * ssn)
+                hi["s"] = max(hi["s"], int(n.max()) * ssn + 1)
+        m_hi, n_hi = min(m0 + BM, M), min(n0 + BN, N)  # stores are masked to m < M, n < N
+        cover[split, m0:m_hi, n0:n_hi] += 1
+        if s > 1:
+            lo["part"] = min(lo["part"], split * M * N + m0 * N + n0)
+            hi["part"] = max(hi["part"], split * M * N + (m_hi - 1) * N + n_hi)
+        else:
+            lo["y"] = min(lo["y"], m0 * sym + n0)
+            hi["y"] = max(hi["y"], (m_hi - 1) * sym + n_hi)
+    assert len(seen) == tiles_m * tiles_n * s
+    assert (cover == 1).all(), "every output element once per split"
+    for k in lo:
+        r[k] = [lo[k], hi[k]]
+    return r, (ib, s, BM)
+
+
+RB_CASES = [(600, 1000, 14336, 4, 128), (600, 1000, 14336, 8, 0), (2100, 4000, 256, 4, 128),
+            (513, 96, 512, 4, 64), (1000, 1000, 4096, 4, 32), (2048, 4096, 14336, 8, 0),
+            (777, 300, 2048, 8, 0), (1030, 2600, 6144, 4, 128)]
+
+
+@pytest.mark.parametrize("M,N,K,bits,G", RB_CASES)
+@pytest.mark.parametrize("pad", [0, 64])
+def test_register_b_in_bounds_and_covering(M, N, K, bits, G, pad):
+    row_bytes = K * bits // 8
+    sqn = row_bytes + pad
+    ng = K // G if G else 1
+    ssn = ng + (8 if pad else 0)
+    sxm = K + (8 if pad else 0)
+    rg, (ib, s, BM) = rb_ranges(M, N, K, bits, G, sxm, sqn, ssn, 1, N)
+    assert rg["x"][0] >= 0 and rg["x"][1] <= (M - 1) * sxm + K
+    assert rg["q"][0] >= 0 and rg["q"][1] <= (N - 1) * sqn + row_bytes
+    assert rg["s"][0] >= 0 and rg["s"][1] <= (N - 1) * ssn + ng
+    assert rg["lds"][0] >= 0 and rg["lds"][1] <= BM * RB_BK
+    if s > 1:
+        assert rg["part"][0] >= 0 and rg["part"][1] <= s * M * N
+    else:
+        assert rg["y"][0] >= 0 and rg["y"][1] <= (M - 1) * N + N
+
+
+def test_register_b_ragged_split_case_is_split():
+    """The GPU parity case M=600, N=1000, K=14336 runs 128-row tiles with four K splits on 256 CUs
+    (partial stores of ragged tiles and the reduction's tails), as the restated and compiled plans
+    both say."""
+    from infinitemodel_amd import _lib
+    assert rb_plan(600, 1000, 14336) == (4, 4)
+    for G in (128, 0):
+        assert _lib_plan(_lib.IMQ_PLAN_GEMM_RB, 600, 14336, G, 1000, 0, 0, 0, 2, 0, 256)[:2] == (4, 4)
+
+
+@pytest.mark.parametrize("cus", [256, 80, 32])
+def test_register_b_plans_match_compiled_dispatch(cus):
+    from infinitemodel_amd import _lib
+    for M, N, K, bits, G in RB_CASES + [(4096, 14336, 4096, 4, 128), (8192, 4096, 14336, 4, 128)]:
+        got = _lib_plan(_lib.IMQ_PLAN_GEMM_RB, M, K, G if bits == 4 else 0, N, 0, 0, 0, 2, 0, cus)
+        assert got is not None and got[:2] == rb_plan(M, N, K, cus), (M, N, K, cus)
+
+
+def test_register_b_model_catches_missing_row_clamp():
+    """Negative control: without the activation row clamp, the ragged last row tile would read
+    past x."""
+    M, N, K = 600, 1000, 14336
+    rg, _ = rb_ranges(M, N, K, 4, 128, K, K // 2, K // 128, 1, N, row_clamp=False)
+    assert rg["x"][1] > (M - 1) * K + K
