@@ -27,9 +27,9 @@ persistent launch, beside the decode kernels), ``stream`` (4 GiB read-only and 1
 device copy, which calibrates the PMC byte counters).
 
 Profiles of a line: ``rocprofv3 --kernel-trace --output-format csv -d DIR -o NAME -- python bench.py
-...`` records every dispatch; ``python bench.py --trace-summary DIR/NAME_kernel_trace.csv --launches
-L --steps K`` summarizes the last L dispatches -- the timed steps, which are the last GPU work of a
-``--no-cpu`` run (L = K x launches_per_step) -- per kernel and per launch position, with the
+...`` records every dispatch; ``python bench.py --trace-summary DIR/NAME_kernel_trace.csv --steps K``
+summarizes the timed steps -- the dispatches between the two marker kernels (one empty workgroup,
+outside the timing events) that bracket them -- per kernel and per launch position, with the
 kernel time per step to set beside the line's ms_per_step.
 """
 from __future__ import annotations
@@ -60,8 +60,8 @@ def _parse():
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
-                    help="summarize the last --launches dispatches of a rocprofv3 kernel-trace CSV (no GPU)")
-    ap.add_argument("--launches", type=int, default=None, help="timed dispatches (steps x launches per step)")
+                    help="summarize the timed steps of a rocprofv3 kernel-trace CSV of a bench run (no GPU)")
+    ap.add_argument("--region", type=int, default=-1, help="which timed region of the traced run (-1: the last)")
     ap.add_argument("--period", type=int, default=None, help="launches per step, for per-position means")
     return ap.parse_args()
 
@@ -88,19 +88,34 @@ def _graph_or_eager(fn, use_graph: bool):
     return g.replay
 
 
+MARK_KERNEL = "probe_empty_kernel"
+
+
+def _mark():
+    """One empty one-workgroup kernel (imq_probe_empty) on the current stream: it delimits the
+    timed steps in a rocprofv3 kernel trace (outside the timing events)."""
+    import torch
+    from infinitemodel_amd import _lib
+    _lib.call("imq_probe_empty", 1, torch.cuda.current_stream().cuda_stream)
+
+
 def _time_steps(step, steps: int, warmup: int) -> float:
     """ms per step: warmup, then EXACTLY ``steps`` steps bracketed by a device synchronize and
-    HIP events on the current stream (the stream the graph replays on)."""
+    HIP events on the current stream (the stream the graph replays on). A marker kernel is
+    launched just before the first event and just after the second, so a kernel trace of the run
+    shows exactly which dispatches the line's time covers (``--trace-summary``)."""
     import torch
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    _mark()
     t0.record()
     for _ in range(steps):
         step()
     t1.record()
+    _mark()
     torch.cuda.synchronize()
     return t0.elapsed_time(t1) / steps
 
@@ -862,10 +877,12 @@ def bench_copy(args, dev):
                  {"workload": "device copy 1 GiB -> 1 GiB", "bytes_read": n, "bytes_written": n}, roof, None)
 
 
-def trace_summary(path: str, launches: int, steps: int, period=None) -> str:
-    """Markdown summary of the last ``launches`` dispatches of a rocprofv3 kernel-trace CSV: per
-    kernel the count, mean / min / max duration (µs) and total; with ``period`` (launches per step)
-    the mean per launch position; and the kernel time per step (total / steps)."""
+def trace_summary(path: str, steps: int, region: int = -1, period=None) -> str:
+    """Markdown summary of the timed steps in a rocprofv3 kernel-trace CSV: the dispatches between
+    the two marker kernels ``_time_steps`` launches around them (``region``: which timed region of
+    the run, -1 = the last), per kernel the count, mean / min / max duration (µs) and total; with
+    ``period`` (launches per step) the mean per launch position; and the kernel time per step
+    (total / steps), to set beside the line's ms_per_step."""
     import csv
     rows = []
     with open(path, newline="") as f:
@@ -874,14 +891,19 @@ def trace_summary(path: str, launches: int, steps: int, period=None) -> str:
                 continue
             rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
     rows.sort()
-    if launches > len(rows):
-        raise SystemExit(f"{path} holds {len(rows)} dispatches, fewer than --launches {launches}")
-    sel = rows[-launches:]
+    marks = [i for i, (_, _, n) in enumerate(rows) if MARK_KERNEL in n]
+    if len(marks) < 2 or len(marks) % 2:
+        raise SystemExit(f"{path}: {len(marks)} marker dispatches ({MARK_KERNEL}), expected pairs")
+    pairs = list(zip(marks[0::2], marks[1::2]))
+    a, b = pairs[region]
+    sel = rows[a + 1:b]
+    if not sel or len(sel) % steps:
+        raise SystemExit(f"{path}: {len(sel)} dispatches in the timed region, not a multiple of {steps} steps")
     by = {}
-    for b, e, n in sel:
-        by.setdefault(n, []).append((e - b) / 1e3)
+    for t0, t1, n in sel:
+        by.setdefault(n, []).append((t1 - t0) / 1e3)
     total = sum(sum(v) for v in by.values())
-    out = [f"last {launches} of {len(rows)} dispatches ({steps} timed steps), "
+    out = [f"timed region {region} of {len(pairs)}: {len(sel)} dispatches = {steps} steps x {len(sel) // steps}, "
            f"window {(sel[-1][1] - sel[0][0]) / 1e3:.1f} µs, kernel time {total:.1f} µs, "
            f"**kernel time per step {total / steps:.2f} µs**", "",
            "| kernel | count | mean µs | min µs | max µs | total µs |", "|---|---|---|---|---|---|"]
@@ -892,8 +914,8 @@ def trace_summary(path: str, launches: int, steps: int, period=None) -> str:
         out += ["", f"mean µs per launch position (period {period}):", "",
                 "| position | kernel | mean µs |", "|---|---|---|"]
         for p in range(period):
-            v = [(e - b) / 1e3 for i, (b, e, n) in enumerate(sel) if i % period == p]
-            out.append(f"| {p} | `{sel[p][2][:60]}` | {sum(v) / len(v):.3f} |")
+            v = [(t1 - t0) / 1e3 for i, (t0, t1, n) in enumerate(sel) if i % period == p]
+            out.append(f"| {p} | `{sel[p][2][:70]}` | {sum(v) / len(v):.3f} |")
     return "\n".join(out)
 
 
@@ -905,9 +927,7 @@ BENCH = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": b
 def main():
     args = _parse()
     if args.trace_summary:
-        if not args.launches:
-            raise SystemExit("--trace-summary needs --launches (steps x launches per step)")
-        print(trace_summary(args.trace_summary, args.launches, args.steps, args.period), flush=True)
+        print(trace_summary(args.trace_summary, args.steps, args.region, args.period), flush=True)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the quantized-linear hot path runs per GPU and this "

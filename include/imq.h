@@ -33,6 +33,8 @@ extern "C" {
 #define IMQ_DT_BF16 0
 #define IMQ_DT_FP16 1
 #define IMQ_DT_FP32 2
+#define IMQ_DT_I32 3 /* integer ids (imq_moe_experts_w4_ex idx_dtype) */
+#define IMQ_DT_I64 4
 
 /* MoE expert activations (imq_moe_experts_w4_ex) */
 #define IMQ_ACT_SILU_GLU 0 /* gate_up rows [gate (I) | up (I)]: h = silu(gate) * up */
@@ -195,9 +197,11 @@ int imq_moe_experts_w4(const void* hidden, int64_t h_row_stride, int64_t T, int6
  *     up = y[2i+1] + b (clamped to [-limit, limit]), h = (up + 1) * gate * sigmoid(alpha * gate).
  *   out[t] = sum_j w[t,j] * (down_e(h) + dn_bias[e]), e = topk_idx[t,j]. Same workspace as
  *   imq_moe_experts_w4. gpt-oss experts are transpose-packed: gate_up [E, 2I, H_pad/2] with the
- *   interleaved rows, down [E, H, I_pad/2]. */
+ *   interleaved rows, down [E, H, I_pad/2].
+ *   topk_idx [T, k] contiguous of idx_dtype IMQ_DT_I32 or IMQ_DT_I64 (the int64 ids torch's top-k
+ *   returns are read as they are, as the reference's MoE op reads them: no conversion launch). */
 int imq_moe_experts_w4_ex(const void* hidden, int64_t h_row_stride, int64_t T, int64_t H, int64_t top_k,
-                          const int32_t* topk_idx, const void* topk_w, int64_t E,
+                          const void* topk_idx, int idx_dtype, const void* topk_w, int64_t E,
                           const void* gu_q, int64_t gu_q_stride_e, int64_t gu_q_row_stride, int64_t gu_K_pad,
                           const void* gu_s, const void* gu_z, int64_t gu_sz_stride_e, int64_t gu_sz_stride_n,
                           int64_t I, const void* dn_q, int64_t dn_q_stride_e, int64_t dn_q_row_stride,

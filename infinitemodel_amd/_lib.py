@@ -18,7 +18,7 @@ import threading
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("IMQ_LIB_PATH") or os.path.join(HERE, "_lib", "libimq.so")
 
-IMQ_DT_BF16, IMQ_DT_FP16, IMQ_DT_FP32 = 0, 1, 2
+IMQ_DT_BF16, IMQ_DT_FP16, IMQ_DT_FP32, IMQ_DT_I32, IMQ_DT_I64 = 0, 1, 2, 3, 4
 IMQ_OK, IMQ_ERR_INVALID, IMQ_ERR_UNSUPPORTED, IMQ_ERR_ALIGN, IMQ_ERR_SCRATCH = 0, -1, -2, -3, -4
 IMQ_NOALLOC_SCRATCH_BYTES = 64 << 20
 
@@ -64,7 +64,7 @@ SIGNATURES = {
                                     _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                                     _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64,
                                     _c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
-    "imq_moe_experts_w4_ex": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64,
+    "imq_moe_experts_w4_ex": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_i64,
                                        _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                                        _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64,
                                        _c_int, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int,

@@ -45,6 +45,16 @@ namespace {
 constexpr int64_t kAlign = 256;
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
+// The routed experts' ids as the caller holds them: int32, or int64 as torch's top-k returns
+// them (the reference's MoE op reads those directly), so no conversion launch precedes a layer.
+struct Ids {
+  const void* p;
+  int is64;
+  IMQ_HOST_DEV int at(int64_t i) const {
+    return is64 ? (int)((const int64_t*)p)[i] : ((const int32_t*)p)[i];
+  }
+};
+
 // One wave per (row b, output channel n). Lane l handles 8-code words l, l+64, ...
 // Output fp32 (OUT_F32) or bf16. x row for b is x + (b / xdiv) * sxm; its columns >= xk (a
 // multiple of 8) are never read but taken as zero, as the reference's zero-padded activation
@@ -52,14 +62,14 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 template <int SDT, bool OUT_F32>
 __global__ __launch_bounds__(256) void moe_rows_kernel(
     const uint16_t* __restrict__ x, int64_t sxm, int64_t xdiv, int64_t xk, int64_t B, int64_t Kpad,
-    const int32_t* __restrict__ eid, int64_t E, const uint8_t* __restrict__ q, int64_t sqe, int64_t sqn,
+    Ids eid, int64_t E, const uint8_t* __restrict__ q, int64_t sqe, int64_t sqn,
     const void* __restrict__ sc, int64_t sse, int64_t ssn, int64_t ssg, const void* __restrict__ zr,
     int64_t sze, int64_t szn, int64_t szg, int64_t N, int64_t G, void* __restrict__ y, int64_t sym) {
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t b = blockIdx.y;
   if (n >= N || b >= B) return;
-  int64_t e = eid[b];
+  int64_t e = eid.at(b);
   if (e < 0 || e >= E) e = 0;   // out-of-range ids are rejected on the host; keep loads in bounds
   const uint8_t* qr = q + e * sqe + n * sqn;
   const uint16_t* xr = x + (b / xdiv) * sxm;
@@ -110,7 +120,7 @@ IMQ_DEV float gptoss_glu(float g, float u, float alpha, float limit) {
 // routed expert eid[b] (stride sbe, dtype bdt) is added to gu first when given.
 template <int ACT>
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ gu, int64_t B, int64_t I, int64_t hk,
-                                                     int64_t hs, const int32_t* __restrict__ eid, int64_t E,
+                                                     int64_t hs, Ids eid, int64_t E,
                                                      const void* __restrict__ bias, int64_t sbe, int bdt,
                                                      float alpha, float limit, uint16_t* __restrict__ h) {
   const int64_t total = B * hk;
@@ -124,7 +134,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
       float g = gu[b * 2 * I + ig];
       float u = gu[b * 2 * I + iu];
       if (bias) {
-        int64_t e = eid[b];
+        int64_t e = eid.at(b);
         e = (e >= 0 && e < E) ? e : 0;
         g += load_bias(bias, bdt, e * sbe + ig);
         u += load_bias(bias, bdt, e * sbe + iu);
@@ -138,7 +148,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 
 // out[t][n] = bf16(sum_j w[t][j] * (z[t*k + j][n] + bias[e(t, j)][n])), j in slot order (fixed).
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ z, const uint16_t* __restrict__ w,
-                                                      int64_t T, int64_t k, int64_t H, const int32_t* __restrict__ eid,
+                                                      int64_t T, int64_t k, int64_t H, Ids eid,
                                                       int64_t E, const void* __restrict__ bias, int64_t sbe, int bdt,
                                                       uint16_t* __restrict__ out, int64_t so) {
   const int64_t total = T * H;
@@ -150,7 +160,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     for (int64_t j = 0; j < k; ++j) {
       float v = z[(tok * k + j) * H + n];
       if (bias) {
-        int64_t e = eid[tok * k + j];
+        int64_t e = eid.at(tok * k + j);
         e = (e >= 0 && e < E) ? e : 0;
         v += load_bias(bias, bdt, e * sbe + n);
       }
@@ -184,7 +194,7 @@ constexpr int kMoeLine = 256;
 // Workgroups past the first (rs != nullptr): rs[t][g] = the fp32 sum of row t of x over columns
 // [128 g, 128 g + 128), g < ng -- one wave per (row, group), a fixed-order wave reduction; they
 // run beside the sort in the same launch.
-__global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restrict__ idx, int B, int E,
+__global__ __launch_bounds__(1024) void moe_sort_kernel(Ids idx, int B, int E,
                                                         int32_t* __restrict__ off, int32_t* __restrict__ perm,
                                                         int32_t* __restrict__ hit, int32_t* __restrict__ mtl,
                                                         int bm, const uint16_t* __restrict__ x = nullptr,
@@ -209,7 +219,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
   __syncthreads();
   int ec[4];                           // the first 4 of this thread's ids stay in registers
   for (int b = tid, i = 0; b < B; b += nt, ++i) {
-    int e = idx[b];
+    int e = idx.at(b);
     e = (e >= 0 && e < E) ? e : 0;   // ids outside [0, E) are clamped, so every access stays in bounds
     if (i < 4) ec[i] = e;
     atomicAdd(&cnt[e], 1);
@@ -257,7 +267,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
   }
   __syncthreads();
   for (int b = tid, i = 0; b < B; b += nt, ++i) {
-    int e = i < 4 ? ec[i] : idx[b];
+    int e = i < 4 ? ec[i] : idx.at(b);
     e = (e >= 0 && e < E) ? e : 0;
     perm[atomicAdd(&cnt[e], 1)] = b;
   }
@@ -287,7 +297,7 @@ struct MoeLineArgs {
   float alpha, limit;    // MODE 2 activation
   int xk;                // valid x columns (a multiple of 8): columns past them read as zero
   // direct decode form (no sort): an item is (routed row b, row block), expert idx[b], one row
-  const int32_t* idx;
+  Ids idx;
   int nrows;             // routed rows B
   int direct;
 };
@@ -321,7 +331,7 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   if (a.direct) {
     beg = item / a.NB;
     end = beg + 1;
-    e = a.idx[beg];
+    e = a.idx.at(beg);
     e = (e >= 0 && e < a.E) ? e : 0;   // ids outside [0, E) are clamped, as in the sort
   } else {
     e = a.hit[item / a.NB];
@@ -634,7 +644,7 @@ struct MoeDecArgs {
   int xk;                  // valid x columns (a multiple of 8): columns past them read as zero
   int Kpad;                // kernel K (a multiple of 256)
   int k;                   // top_k
-  const int32_t* idx;      // [B] expert of each routed row
+  Ids idx;                 // [B] expert of each routed row
   const uint16_t* topk_w;  // [B] routing weights, bf16 (dn)
   int E;
   const uint8_t* q;
@@ -808,7 +818,7 @@ __global__ __launch_bounds__(1024) void moe_gu_line_kernel(MoeDecArgs a) {
   const int W = blockDim.x >> 6;
   const int wbytes = dec_wave_lds(S2, VB, false);
   const int b = blockIdx.x / a.NR, u = blockIdx.x - b * a.NR;
-  int e = a.idx[b];
+  int e = a.idx.at(b);
   e = (e >= 0 && e < a.E) ? e : 0;   // ids outside [0, E) are clamped, as in the sort
   const int tile = ACT == 0 ? wave / a.Wk : 0;
   const int wk = wave - tile * a.Wk;
@@ -862,7 +872,7 @@ __global__ __launch_bounds__(1024) void moe_dn_line_kernel(MoeDecArgs a) {
   const int j = PAIR ? 2 * grp : grp;
   const bool has2 = PAIR && j + 1 < a.k;                           // odd k: the last pair is one slot
   const int b = t * a.k + j, b2 = has2 ? b + 1 : b;
-  int e = a.idx[b], e2 = a.idx[b2];
+  int e = a.idx.at(b), e2 = a.idx.at(b2);
   e = (e >= 0 && e < a.E) ? e : 0;
   e2 = (e2 >= 0 && e2 < a.E) ? e2 : 0;
   float v = dec_tile_partial<S2, SDT, XCL, PAIR>(a, e, ROWS * rt, a.x + (int64_t)b * a.sxm, wk * S2,
@@ -1042,7 +1052,7 @@ int moe_line_sdt(const MoeLineArgs& a, int rows, int64_t maxhit, int sdt, hipStr
 }
 
 template <bool OUT_F32>
-int launch_rows(const uint16_t* x, int64_t sxm, int64_t xdiv, int64_t xk, int64_t B, int64_t Kpad, const int32_t* eid,
+int launch_rows(const uint16_t* x, int64_t sxm, int64_t xdiv, int64_t xk, int64_t B, int64_t Kpad, Ids eid,
                 int64_t E, const uint8_t* q, int64_t sqe, int64_t sqn, const void* sc, int64_t sse, int64_t ssn,
                 int64_t ssg, const void* zr, int64_t sze, int64_t szn, int64_t szg, int sdt, int64_t N, int64_t G,
                 void* y, int64_t sym, hipStream_t st) {
@@ -1082,7 +1092,7 @@ extern "C" int imq_moe_rows_w4(const void* x, int64_t x_row_stride, int64_t B, i
   if (q_row_stride < K_pad / 2 || x_row_stride < K_pad || y_row_stride < N) return IMQ_ERR_INVALID;
   if (!aligned(qweight, 4) || (q_row_stride % 4) || (q_stride_e % 4) || !aligned(x, 16) || (x_row_stride % 8))
     return IMQ_ERR_ALIGN;
-  return launch_rows<false>((const uint16_t*)x, x_row_stride, 1, K_pad, B, K_pad, eid, E, (const uint8_t*)qweight,
+  return launch_rows<false>((const uint16_t*)x, x_row_stride, 1, K_pad, B, K_pad, Ids{eid, 0}, E, (const uint8_t*)qweight,
                             q_stride_e, q_row_stride, scale, s_stride_e, s_stride_n, s_stride_g, zero,
                             z_stride_e, z_stride_n, z_stride_g, sz_dtype, N, group_size, y, y_row_stride,
                             (hipStream_t)stream);
@@ -1126,7 +1136,7 @@ namespace {
 struct MoeCall {
   const uint16_t* hidden;
   int64_t hs, T, H, k;
-  const int32_t* idx;
+  Ids idx;
   const uint16_t* topk_w;
   int64_t E;
   const uint8_t* gq;
@@ -1381,8 +1391,8 @@ int moe_per_row(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
 }  // namespace
 
 extern "C" int imq_moe_experts_w4_ex(
-    const void* hidden, int64_t h_row_stride, int64_t T, int64_t H, int64_t top_k, const int32_t* topk_idx,
-    const void* topk_w, int64_t E, const void* gu_q, int64_t gu_q_stride_e, int64_t gu_q_row_stride, int64_t gu_K_pad,
+    const void* hidden, int64_t h_row_stride, int64_t T, int64_t H, int64_t top_k, const void* topk_idx,
+    int idx_dtype, const void* topk_w, int64_t E, const void* gu_q, int64_t gu_q_stride_e, int64_t gu_q_row_stride, int64_t gu_K_pad,
     const void* gu_s, const void* gu_z, int64_t gu_sz_stride_e, int64_t gu_sz_stride_n, int64_t I, const void* dn_q,
     int64_t dn_q_stride_e, int64_t dn_q_row_stride, int64_t dn_K_pad, const void* dn_s, const void* dn_z,
     int64_t dn_sz_stride_e, int64_t dn_sz_stride_n, int sz_dtype, int64_t group_size, const void* gu_bias,
@@ -1391,6 +1401,7 @@ extern "C" int imq_moe_experts_w4_ex(
   if (!hidden || !topk_idx || !topk_w || !gu_q || !gu_s || !gu_z || !dn_q || !dn_s || !dn_z || !out)
     return IMQ_ERR_INVALID;
   if (T < 0 || H <= 0 || top_k <= 0 || E <= 0 || I <= 0 || group_size <= 0 || group_size % 8) return IMQ_ERR_INVALID;
+  if (idx_dtype != IMQ_DT_I32 && idx_dtype != IMQ_DT_I64) return IMQ_ERR_INVALID;
   if (sz_dtype != IMQ_DT_BF16 && sz_dtype != IMQ_DT_FP16 && sz_dtype != IMQ_DT_FP32) return IMQ_ERR_INVALID;
   if (act != IMQ_ACT_SILU_GLU && act != IMQ_ACT_GPTOSS) return IMQ_ERR_INVALID;
   if ((gu_bias || dn_bias) && bias_dtype != IMQ_DT_BF16 && bias_dtype != IMQ_DT_FP16 && bias_dtype != IMQ_DT_FP32)
@@ -1412,7 +1423,8 @@ extern "C" int imq_moe_experts_w4_ex(
       (gu_q_stride_e % 4) || (dn_q_stride_e % 4) || !aligned(hidden, 16) || (h_row_stride % 8) ||
       !aligned(workspace, 256))
     return IMQ_ERR_ALIGN;
-  const MoeCall c{(const uint16_t*)hidden, h_row_stride, T, H, top_k, topk_idx, (const uint16_t*)topk_w, E,
+  const MoeCall c{(const uint16_t*)hidden, h_row_stride, T, H, top_k, Ids{topk_idx, idx_dtype == IMQ_DT_I64},
+                  (const uint16_t*)topk_w, E,
                   (const uint8_t*)gu_q, gu_q_stride_e, gu_q_row_stride, gu_K_pad, gu_s, gu_z, gu_sz_stride_e,
                   gu_sz_stride_n, I, (const uint8_t*)dn_q, dn_q_stride_e, dn_q_row_stride, dn_K_pad, dn_s, dn_z,
                   dn_sz_stride_e, dn_sz_stride_n, sz_dtype, G, gu_bias, gu_bias_stride_e, dn_bias, dn_bias_stride_e,
@@ -1436,7 +1448,7 @@ extern "C" int imq_moe_experts_w4(const void* hidden, int64_t h_row_stride, int6
   if (group_size <= 0) return IMQ_ERR_INVALID;
   const int64_t H_pad = imq_cdiv(H, group_size) * group_size;
   const int64_t I_pad = imq_cdiv(I, group_size) * group_size;
-  return imq_moe_experts_w4_ex(hidden, h_row_stride, T, H, top_k, topk_idx, topk_w, E, gu_q, gu_q_stride_e,
+  return imq_moe_experts_w4_ex(hidden, h_row_stride, T, H, top_k, topk_idx, IMQ_DT_I32, topk_w, E, gu_q, gu_q_stride_e,
                                gu_q_row_stride, H_pad, gu_s, gu_z, gu_sz_stride_e, gu_sz_stride_n, I, dn_q,
                                dn_q_stride_e, dn_q_row_stride, I_pad, dn_s, dn_z, dn_sz_stride_e, dn_sz_stride_n,
                                sz_dtype, group_size, nullptr, 0, nullptr, 0, IMQ_DT_BF16, IMQ_ACT_SILU_GLU, 0.f, 0.f,

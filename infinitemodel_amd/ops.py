@@ -344,7 +344,9 @@ def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=
         # rows of exactly H columns (H % 8 == 0) are read as zero past H by the kernels; past 16
         # tokens every row is re-read by many passes and one zero-padded copy is cheaper
         x = torch.nn.functional.pad(x[:, :H], (0, gK - H)).contiguous()
-    idx = topk_idx.to(torch.int32).contiguous()
+    # int64 ids (torch's top-k) and int32 ids are read by the kernels as they are
+    idx = topk_idx if topk_idx.dtype in (torch.int64, torch.int32) else topk_idx.to(torch.int64)
+    idx = idx.contiguous()
     if check_ids:
         _check_expert_ids(idx, E)
     w = topk_w.to(torch.bfloat16).contiguous()
@@ -353,7 +355,8 @@ def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=
         workspace = _scratch(dev, max(need, 1))
     out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
-        call("imq_moe_experts_w4_ex", _ptr(x), x.stride(0), T, H, k, _ptr(idx), _ptr(w), E,
+        call("imq_moe_experts_w4_ex", _ptr(x), x.stride(0), T, H, k, _ptr(idx),
+             _lib.IMQ_DT_I64 if idx.dtype == torch.int64 else _lib.IMQ_DT_I32, _ptr(w), E,
              _ptr(gq), gq.stride(0), gq.stride(1), gK, _ptr(gs), _ptr(gz), gs.stride(0), gs.stride(1), I,
              _ptr(dq), dq.stride(0), dq.stride(1), dK, _ptr(ds), _ptr(dz), ds.stride(0), ds.stride(1),
              dtype_code(sdt), group_size,

@@ -102,6 +102,30 @@ def test_moe_olmoe_shape_prefill(dev, T):
     _run(dev, E=64, H=2048, I=1024, k=8, T=T, seed=3000)
 
 
+@pytest.mark.parametrize("T", [1, 16, 300])
+def test_moe_int32_and_int64_ids_identical(dev, T):
+    """The kernels read the routing ids as int64 (torch's top-k output, as the reference's fused
+    op reads them) or int32: the same routing gives bit-identical outputs on every dispatch path
+    (T = 1 direct decode, T = 16 token-sorted line kernels, T = 300 the register-B grouped GEMM),
+    and the int64 call launches no conversion kernel of its own."""
+    import torch
+    from infinitemodel_amd import ops
+    E, H, I, k, G = 64, 2048, 1024, 8, 128
+    gu, dn, _, _ = _layer(E, H, I, G, 3000)
+    t = lambda a: C.to_torch(a, "bf16", dev)  # noqa: E731
+    r = C.rng(77 + T)
+    idx, w = om.route_topk(r.standard_normal((T, E)).astype(np.float32), k)
+    x, wt = t(C.bf16_normal(r, (T, H))), t(w)
+    a = (C.u8(gu[0], dev), t(gu[1]), t(gu[2]), H)
+    b = (C.u8(dn[0], dev), t(dn[1]), t(dn[2]), I)
+    i64 = torch.from_numpy(idx).to(dev)
+    assert i64.dtype == torch.int64
+    y64 = ops.moe_experts_w4(x, i64, wt, a, b, G, check_ids=False)
+    y32 = ops.moe_experts_w4(x, i64.to(torch.int32), wt, a, b, G, check_ids=False)
+    torch.cuda.synchronize()
+    assert torch.equal(y64.view(torch.int16), y32.view(torch.int16)), T
+
+
 def test_moe_repeat_identical(dev):
     import torch
     from infinitemodel_amd import ops
