@@ -758,7 +758,9 @@ IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // wave-private LDS, in-order
 
   const uint32_t magic = magic_bf16_128x2();
-  const uint16_t* xa = xw + ((PAIR && c == 1) ? xrowl : 0) + 32 * ar;   // A row 1: the second activation
+  // A row 1: PAIR the second activation row; else the line-step's second group (128 codes on), so
+  // each full-line load feeds its MFMAs as loaded (the line kernel's M = 1 form)
+  const uint16_t* xa = xw + ((PAIR && c == 1) ? xrowl : 0) + ((!PAIR && c == 1) ? 128 : 0) + 32 * ar;
   // group sums of the activation each lane's column meets: y0 columns 0-7 / 8-15 are expert e / e2,
   // y1 (read across the row swap) the other way round
   const float* xs0p = xs + ((PAIR && !lo8) ? 2 * S2 : 0);
@@ -776,18 +778,36 @@ IMQ_DEV float dec_tile_partial(const MoeDecArgs& a, int e, int rbase, const uint
   for (int i = 0; i < S2; ++i) {
     const bool v = ls0 + i < KL;
     const float xs0 = xs0p[2 * i], xs1 = xs1p[2 * i + 1];
-    bf16x8_t A0[4], A1[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      A0[kk] = *(const bf16x8_t*)(xa + i * kDLine + 8 * kk);
-      A1[kk] = *(const bf16x8_t*)(xa + i * kDLine + 128 + 8 * kk);
-    }
     float s0 = val(sc_c, 2 * i), s1 = val(sc_x, 2 * i + 1);   // read, then select
     s0 = v ? s0 : 0.f;
     s1 = v ? s1 : 0.f;
     const float cz0 = -(128.f + val(zr_c, 2 * i)) * s0;
     const float cz1 = -(128.f + val(zr_x, 2 * i + 1)) * s1;
     const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
+    if constexpr (!PAIR) {
+      // column c < 8 of load L0 is row c's group 2l (D row 0), c >= 8 row c ^ 8's group 2l+1 (D
+      // row 1); load L1 the other way round
+      bf16x8_t A[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) A[kk] = *(const bf16x8_t*)(xa + i * kDLine + 8 * kk);
+      f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        a0 = mfma16x16x32(A[kk], unpack_nib8_bf16(w0[kk], magic), a0);
+        a1 = mfma16x16x32(A[kk], unpack_nib8_bf16(w1[kk], magic), a1);
+      }
+      y0 = fmaf(cz0, xs0, y0);
+      y1 = fmaf(cz1, xs1, y1);
+      y0 = fmaf(s0, lo8 ? a0[0] : a1[0], y0);   // row c, group 2l
+      y1 = fmaf(s1, lo8 ? a1[1] : a0[1], y1);   // row c ^ 8, group 2l+1
+      continue;
+    }
+    bf16x8_t A0[4], A1[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      A0[kk] = *(const bf16x8_t*)(xa + i * kDLine + 8 * kk);
+      A1[kk] = *(const bf16x8_t*)(xa + i * kDLine + 128 + 8 * kk);
+    }
     u32x4_t gA, gB;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -818,12 +838,12 @@ __global__ __launch_bounds__(1024) void moe_gu_line_kernel(MoeDecArgs a) {
   const int W = blockDim.x >> 6;
   const int wbytes = dec_wave_lds(S2, VB, false);
   const int b = blockIdx.x / a.NR, u = blockIdx.x - b * a.NR;
-  int e = a.idx.at(b);
-  e = (e >= 0 && e < a.E) ? e : 0;   // ids outside [0, E) are clamped, as in the sort
   const int tile = ACT == 0 ? wave / a.Wk : 0;
   const int wk = wave - tile * a.Wk;
   const int rbase = ACT == 0 ? (tile == 0 ? 16 * u : a.I + 16 * u) : 16 * u;
   const uint16_t* xrow = a.x + (int64_t)(b / a.k) * a.sxm;
+  int e = a.idx.at(b);
+  e = (e >= 0 && e < a.E) ? e : 0;   // ids outside [0, E) are clamped, as in the sort
   const float v = dec_tile_partial<S2, SDT, XCL, false>(a, e, rbase, xrow, wk * S2, a.Kpad / kDLine,
                                                         smem + (size_t)wave * wbytes, lane, e, xrow);
   float* red = (float*)(smem + (size_t)W * wbytes);  // [W][16]

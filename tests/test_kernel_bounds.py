@@ -1543,3 +1543,22 @@ def test_register_b_model_catches_missing_row_clamp():
     M, N, K = 600, 1000, 14336
     rg, _ = rb_ranges(M, N, K, 4, 128, K, K // 2, K // 128, 1, N, row_clamp=False)
     assert rg["x"][1] > (M - 1) * K + K
+
+
+def test_dec_a_operand_lds_reads_stay_in_the_staged_rows():
+    """MoE decode (dec_tile_partial): lane (c, ar) reads its A operands at xa + i * 256 + 8 kk
+    (16 bytes) with xa = row offset + 32 ar + (gate_up form, c == 1: 128, the line-step's second
+    group; slot-pair form, c == 1: the second staged row). Every read stays inside the staged
+    row(s) of S2 * 256 + 8 elements, for both forms and S2 2 / 4."""
+    for S2 in (2, 4):
+        xrowl = S2 * 256 + 8
+        for pair in (False, True):
+            nx = 2 if pair else 1
+            for c in range(16):
+                for ar in range(4):
+                    base = (xrowl if (pair and c == 1) else 0) + (128 if (not pair and c == 1) else 0) + 32 * ar
+                    row0 = xrowl if (pair and c == 1) else 0
+                    for i in range(S2):
+                        for kk in range(4):
+                            lo = base + i * 256 + 8 * kk
+                            assert row0 <= lo and lo + 8 <= row0 + S2 * 256 <= nx * xrowl, (S2, pair, c, ar, i, kk)
