@@ -16,6 +16,9 @@ linears, launched back to back on one stream and replayed as a HIP graph.
   cpu_baseline the reference's CPU int4 path (torch tinygemm, as worker_quant.py:732-759 binds
                it) on a bounded sample: 8 layers of the same shapes (0.93 GB, beyond host cache),
                median pass time on this host's cores
+  also         measured after the C2 line in the same run (--no-also skips them): C4 prefill's
+               fused step, int4 and int8 at M = 2048 and 512, TFLOP/s (the naive, bf16-GEMM and
+               CPU legs are --config c4's)
 
 Other configs print lines of the same shape: --config c1 (single 1x4096->4096 linear), c3 (int2
 g64 70B shapes), c4 (prefill, --quant int4|int8, --m 512|2048), c5 (OLMoE fused MoE, --m = T),
@@ -30,7 +33,8 @@ Profiles of a line: ``rocprofv3 --kernel-trace --output-format csv -d DIR -o NAM
 ...`` records every dispatch; ``python bench.py --trace-summary DIR/NAME_kernel_trace.csv --steps K``
 summarizes the timed steps -- the dispatches between the two marker kernels (one empty workgroup,
 outside the timing events) that bracket them -- per kernel and per launch position, with the
-kernel time per step to set beside the line's ms_per_step.
+kernel time per step to set beside the line's ms_per_step (profile the default line with
+--no-also, or pick its region with --region 0).
 """
 from __future__ import annotations
 
@@ -58,6 +62,8 @@ def _parse():
     ap.add_argument("--quant", default="int4", choices=["int4", "int8"], help="C4 weight format")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
+    ap.add_argument("--no-also", action="store_true",
+                    help="default run: skip the C4 prefill lines measured after the C2 line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="summarize the timed steps of a rocprofv3 kernel-trace CSV of a bench run (no GPU)")
@@ -411,30 +417,62 @@ def _c4_module_path(quant: str, shapes, dev) -> dict:
     return out
 
 
-def bench_c4(args, dev):
+C4_SHAPES = [(14336, 4096), (4096, 14336)]
+
+
+def _c4_fused(quant: str, M: int, dev, steps: int, warmup: int, use_graph: bool = True):
+    """The fused prefill step of C4: 6 copies of each shape (374 MB int4 / 705 MB int8, past the
+    MALL) through imq_linear_w4 / imq_linear_w8, timed as _time_steps does. Returns (ms per step,
+    TFLOP/s, the (N, K, fn) sets, the activations by K, the outputs by N)."""
     import torch
     from infinitemodel_amd import ops, workloads as wl
-    M = args.m or 2048
-    shapes = [(14336, 4096), (4096, 14336)]
     sets = []
-    for i in range(6):        # 6 copies of each shape: 374 MB (int4) / 705 MB (int8), past the MALL
-        for j, (N, K) in enumerate(shapes):
-            if args.quant == "int4":
+    for i in range(6):
+        for j, (N, K) in enumerate(C4_SHAPES):
+            if quant == "int4":
                 L = wl.rtn_int4_linear(N, K, 5000 + 2 * i + j, dev)
                 sets.append((N, K, lambda x, y, L=L: ops.linear_w4(x, L.q, 128, (L.s, L.z), out=y)))
             else:
                 q, s = wl.int8_linear(N, K, 5000 + 2 * i + j, dev)
                 sets.append((N, K, lambda x, y, q=q, s=s: ops.linear_w8(x, q, s, out=y)))
-    xs = {K: wl.activations(M, K, 9, dev) for _, K in shapes}
-    ys = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for N, _ in shapes}
+    xs = {K: wl.activations(M, K, 9, dev) for _, K in C4_SHAPES}
+    ys = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for N, _ in C4_SHAPES}
 
     def step():
         for N, K, fn in sets:
             fn(xs[K], ys[N])
 
-    ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
+    ms = _time_steps(_graph_or_eager(step, use_graph), steps, warmup)
     flops = sum(2.0 * M * N * K for N, K, _ in sets)
-    tf = flops / (ms * 1e-3)
+    return ms, flops / (ms * 1e-3), sets, xs, ys
+
+
+def also_c4(args, dev) -> list:
+    """C4's fused prefill lines (int4 / int8 at M = 2048 and 512), measured inside the default
+    run after its own line so that they run under the same clock; value in TFLOP/s of the fused
+    step alone (the naive, bf16-GEMM and CPU legs are bench.py --config c4's)."""
+    import torch
+    out = []
+    steps, warmup = min(args.steps, 20), min(args.warmup, 5)
+    for quant in ("int4", "int8"):
+        for M in (2048, 512):
+            ms, tf, sets, xs, ys = _c4_fused(quant, M, dev, steps, warmup, not args.no_graph)
+            out.append({"workload": f"C4 prefill {quant} 4096->14336 and 14336->4096, M={M}",
+                        "value": round(tf / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(ms, 5),
+                        "steps": steps, "warmup": warmup, "frac_of_peak": round(tf / BF16_PEAK, 4),
+                        "launches_per_step": len(sets)})
+            del sets, xs, ys
+            torch.cuda.empty_cache()
+    return out
+
+
+def bench_c4(args, dev):
+    import torch
+    from infinitemodel_amd import ops, workloads as wl
+    M = args.m or 2048
+    shapes = C4_SHAPES
+    ms, tf, sets, xs, ys = _c4_fused(args.quant, M, dev, args.steps, args.warmup, not args.no_graph)
+    flops = sum(2.0 * M * N * K for N, K, _ in sets)
     # the module's naive prefill path on the same weights: the bit-exact HIP dequant to bf16, then
     # the bf16 GEMM (hipBLASLt, as F.linear) -- what _bench_large_m_naive weighs the fused kernel
     # against
@@ -941,6 +979,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     line = BENCH[args.config](args, dev)
+    if args.config == "c2" and args.m in (None, 1) and not args.no_also:
+        line["also"] = also_c4(args, dev)
     print(json.dumps(line), flush=True)
 
 

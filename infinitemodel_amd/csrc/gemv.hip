@@ -2594,7 +2594,10 @@ int line_w2(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
 // same scale / zero dtype; restated by the CPU bounds model in the tests): S2 = 2 line-steps (1024
 // codes, the int4 K-split's split width) per split, NW = 8 row tiles when that still yields two
 // workgroups per CU, else 4.
-constexpr int kKs2S2 = 2;
+#ifndef IMQ_KS2_S2
+#define IMQ_KS2_S2 2
+#endif
+constexpr int kKs2S2 = IMQ_KS2_S2;
 bool ksplit2_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
                   int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int cus, int* splitso,
                   int* nwo, size_t* ldso) {
