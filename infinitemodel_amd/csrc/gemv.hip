@@ -1567,8 +1567,17 @@ IMQ_HOST_DEV inline int ksplit2_lds(int M, int S2, int NW) {
   return M * (S2 * kLine2 + 8) * 2 + S2 * 8 * 16 * 4 + NW * sz2_bytes(S2 * 8);
 }
 
+// At most 168 VGPRs (three waves per SIMD): three 4-wave workgroups share a CU, so one
+// workgroup's weight loads are in flight while another computes (the unbounded kernel takes 165-170
+// registers and fit one 8-wave or two 4-wave workgroups per CU; 128 spills).
+#ifndef IMQ_W2KS_WPE
+#define IMQ_W2KS_WPE 3
+#endif
+#ifndef IMQ_W2KS_PIPE
+#define IMQ_W2KS_PIPE 0
+#endif
 template <int S2, int MC, int SDT, int NW>
-__global__ __launch_bounds__(64 * NW) void w2_ksplit_kernel(SkinnyArgs a) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(IMQ_W2KS_WPE))) void w2_ksplit_kernel(SkinnyArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
   constexpr int GPL = 8;                              // groups per line-step
@@ -1656,6 +1665,76 @@ __global__ __launch_bounds__(64 * NW) void w2_ksplit_kernel(SkinnyArgs a) {
   const float* sz_c = szf + c * sz2_row(NGW);
   const float* sz_x = szf + (c ^ 8) * sz2_row(NGW);
   float y0[4] = {0.f, 0.f, 0.f, 0.f}, y1[4] = {0.f, 0.f, 0.f, 0.f};
+#if IMQ_W2KS_PIPE
+  // Software-pipelined over the S2 * 4 group pairs t: the MFMAs of pair t are issued, then the
+  // LDS operands of pair t + 1 are read, and only then is pair t - 1's scale applied to its
+  // sums (a scheduling barrier keeps that order) -- so two pairs of sums are live instead of all
+  // of them and the fma epilogue runs under the next MFMAs.
+  constexpr int TT = S2 * 4;
+  struct Ops {
+    f32x4_t xsA, xsB;
+    bf16x8_t a0, a1, b0, b1;
+    f32x2_t pA, pB;
+  };
+  auto load_ops = [&](int t, Ops& o) {
+    const int gA = GPL * (t >> 2) + (t & 3), gB = gA + 4;
+    o.xsA = *(const f32x4_t*)(xs + gA * 16 + 4 * ar);
+    o.xsB = *(const f32x4_t*)(xs + gB * 16 + 4 * ar);
+    o.a0 = *(const bf16x8_t*)(xa + 64 * gA);
+    o.a1 = *(const bf16x8_t*)(xa + 64 * gA + 8);
+    o.b0 = *(const bf16x8_t*)(xa + 64 * gB);
+    o.b1 = *(const bf16x8_t*)(xa + 64 * gB + 8);
+    o.pA = *(const f32x2_t*)(sz_c + 2 * gA);   // (s, -(128 + z) * s)
+    o.pB = *(const f32x2_t*)(sz_x + 2 * gB);
+  };
+  Ops op[2];
+  f32x4_t acA[2], acB[2];
+  uint32_t dA[4], dB[4];
+  float sAp = 0.f, sBp = 0.f;
+  load_ops(0, op[0]);
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int cur = t & 1, k = t & 3;
+    if (k == 0) {
+      const u32x4_t w0 = wb[2 * (t >> 2)], w1 = wb[2 * (t >> 2) + 1];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        dA[d] = lo8 ? w0[d] : w1[d];
+        dB[d] = lo8 ? w1[d] : w0[d];
+      }
+      transpose4_lanerows(dA);    // dA[k]: dword ar of group k of row c
+      transpose4_lanerows(dB);    // dB[k]: dword ar of group 4 + k of row c ^ 8
+    }
+    const f32x4_t z4 = {0.f, 0.f, 0.f, 0.f};
+    acA[cur] = mfma16x16x32(op[cur].a0, unpack_crumb8_bf16(dA[k], 0, magic), z4);
+    acB[cur] = mfma16x16x32(op[cur].b0, unpack_crumb8_bf16(dB[k], 0, magic), z4);
+    acA[cur] = mfma16x16x32(op[cur].a1, unpack_crumb8_bf16(dA[k], 1, magic), acA[cur]);
+    acB[cur] = mfma16x16x32(op[cur].b1, unpack_crumb8_bf16(dB[k], 1, magic), acB[cur]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      y0[r] = fmaf(op[cur].pA[1], op[cur].xsA[r], y0[r]);
+      y1[r] = fmaf(op[cur].pB[1], op[cur].xsB[r], y1[r]);
+    }
+    const float sAc = op[cur].pA[0], sBc = op[cur].pB[0];
+    if (t + 1 < TT) load_ops(t + 1, op[cur ^ 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t > 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        y0[r] = fmaf(sAp, acA[cur ^ 1][r], y0[r]);
+        y1[r] = fmaf(sBp, acB[cur ^ 1][r], y1[r]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    sAp = sAc;
+    sBp = sBc;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    y0[r] = fmaf(sAp, acA[(TT - 1) & 1][r], y0[r]);
+    y1[r] = fmaf(sBp, acB[(TT - 1) & 1][r], y1[r]);
+  }
+#else
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
     const u32x4_t w0 = wb[2 * i], w1 = wb[2 * i + 1];
@@ -1693,6 +1772,7 @@ __global__ __launch_bounds__(64 * NW) void w2_ksplit_kernel(SkinnyArgs a) {
       }
     }
   }
+#endif
   float* pbase = a.part + (size_t)split * M * a.N + row0 + c;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -2592,12 +2672,14 @@ int line_w2(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
 
 // int2 K-split plan (4 < M <= 16, G == 64, K_pad a multiple of 512, N % 4 == 0, unit group strides,
 // same scale / zero dtype; restated by the CPU bounds model in the tests): S2 = 2 line-steps (1024
-// codes, the int4 K-split's split width) per split, NW = 8 row tiles when that still yields two
-// workgroups per CU, else 4.
+// codes, the int4 K-split's split width) per split, NW = 4 row tiles per workgroup (three resident
+// per CU at the kernel's register bound; measured at C3: 8 tiles per workgroup, one resident,
+// M=8 1967 -> 2304 GB/s, M=16 1851 -> 2053).
 #ifndef IMQ_KS2_S2
 #define IMQ_KS2_S2 2
 #endif
 constexpr int kKs2S2 = IMQ_KS2_S2;
+constexpr int kKs2NW = 4;
 bool ksplit2_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int64_t sxm, int64_t ssn,
                   int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt, int max_lds, int cus, int* splitso,
                   int* nwo, size_t* ldso) {
@@ -2609,7 +2691,7 @@ bool ksplit2_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, in
   if (16 * sqn >= (int64_t(1) << 31) || M * sxm * 2 >= (int64_t(1) << 31)) return false;
   if (16 * ssn * vb >= (int64_t(1) << 31) || 16 * szn * vb >= (int64_t(1) << 31)) return false;
   const int64_t splits = (Kpad / kLine2 + kKs2S2 - 1) / kKs2S2;
-  const int nw = splits * ((N + 127) / 128) >= 2 * (int64_t)cus ? 8 : 4;
+  const int nw = kKs2NW;
   const int64_t rbs = (N + 16 * nw - 1) / (16 * nw);
   if (splits * rbs > 0x7fffffff) return false;
   const size_t lds = (size_t)ksplit2_lds((int)M, kKs2S2, nw);
@@ -2646,18 +2728,10 @@ int ksplit_w2(const SkinnyArgs& a0, int sdt, void* ws, int64_t wsb, const DevInf
   if (((uintptr_t)a0.y & 7) || (a0.sym & 3)) return IMQ_ERR_UNSUPPORTED;   // 8-byte y stores
   SkinnyArgs a = a0;
   a.part = (float*)ws;
-  if (nw == 8) {
-    switch (sdt) {
-      case IMQ_DT_BF16: return ksplit2_launch<IMQ_DT_BF16, 8>(a, splits, lds, st);
-      case IMQ_DT_FP16: return ksplit2_launch<IMQ_DT_FP16, 8>(a, splits, lds, st);
-      case IMQ_DT_FP32: return ksplit2_launch<IMQ_DT_FP32, 8>(a, splits, lds, st);
-    }
-  } else {
-    switch (sdt) {
-      case IMQ_DT_BF16: return ksplit2_launch<IMQ_DT_BF16, 4>(a, splits, lds, st);
-      case IMQ_DT_FP16: return ksplit2_launch<IMQ_DT_FP16, 4>(a, splits, lds, st);
-      case IMQ_DT_FP32: return ksplit2_launch<IMQ_DT_FP32, 4>(a, splits, lds, st);
-    }
+  switch (sdt) {
+    case IMQ_DT_BF16: return ksplit2_launch<IMQ_DT_BF16, kKs2NW>(a, splits, lds, st);
+    case IMQ_DT_FP16: return ksplit2_launch<IMQ_DT_FP16, kKs2NW>(a, splits, lds, st);
+    case IMQ_DT_FP32: return ksplit2_launch<IMQ_DT_FP32, kKs2NW>(a, splits, lds, st);
   }
   return IMQ_ERR_UNSUPPORTED;
 }

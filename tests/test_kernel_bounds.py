@@ -966,7 +966,7 @@ def ksplit2_plan(M, Kpad, G, N, sqn, sxm, ssn, vb, max_lds=160 * 1024, cus=256):
     if 16 * sqn >= 2 ** 31 or M * sxm * 2 >= 2 ** 31 or 16 * ssn * vb >= 2 ** 31:
         return None
     splits = -(-(Kpad // LINE2) // KS2_S2)
-    nw = 8 if splits * -(-N // 128) >= 2 * cus else 4
+    nw = 4
     lds = M * (KS2_S2 * LINE2 + 8) * 2 + KS2_S2 * 8 * 16 * 4 + nw * sz2_bytes(KS2_S2 * 8)
     if lds > max_lds:
         return None
