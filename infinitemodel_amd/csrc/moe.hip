@@ -26,7 +26,7 @@ int moe_gemm_w4(int mode, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t
                 const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off, const int32_t* perm, int k,
                 const void* bias, int64_t sbe, int bdt, float alpha, float limit, uint16_t* h, int64_t hs,
                 float* yr, hipStream_t st, bool check_only = false);
-int moe_rb(int mode, int ib, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t K, const uint8_t* q,
+int moe_rb(int mode, int ib, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t K, int64_t xk, const uint8_t* q,
            int64_t sqe, int64_t sqn, const void* sc, const void* zr, int64_t sse, int64_t ssn, int sdt, int64_t N,
            int64_t I, const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off,
            const int32_t* perm, int k, const void* bias, int64_t sbe, int bdt, float alpha, float limit,
@@ -192,14 +192,14 @@ constexpr int kMoeLine = 256;
 // per block: (expert | rows of the block << 16, first sorted row), bm sorted rows per block -- at
 // most ceil(B / bm) + (hit experts) blocks.
 // Workgroups past the first (rs != nullptr): rs[t][g] = the fp32 sum of row t of x over columns
-// [128 g, 128 g + 128), g < ng -- one wave per (row, group), a fixed-order wave reduction; they
-// run beside the sort in the same launch.
+// [128 g, 128 g + 128), g < ng, columns at or past xk (even) read as zero -- one wave per (row,
+// group), a fixed-order wave reduction; they run beside the sort in the same launch.
 __global__ __launch_bounds__(1024) void moe_sort_kernel(Ids idx, int B, int E,
                                                         int32_t* __restrict__ off, int32_t* __restrict__ perm,
                                                         int32_t* __restrict__ hit, int32_t* __restrict__ mtl,
                                                         int bm, const uint16_t* __restrict__ x = nullptr,
                                                         int64_t sxm = 0, int64_t T = 0, int ng = 0,
-                                                        float* __restrict__ rs = nullptr) {
+                                                        float* __restrict__ rs = nullptr, int xk = 0) {
   extern __shared__ int32_t cnt[];     // [E]: counts, then scatter cursors
   const int tid = threadIdx.x, nt = blockDim.x;
   if (blockIdx.x > 0) {
@@ -208,7 +208,10 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(Ids idx, int B, int E,
     if (rs == nullptr || wid >= T * ng) return;
     const int64_t t = wid / ng;
     const int g = (int)(wid - t * ng);
-    const uint32_t v = *(const uint32_t*)(x + t * sxm + 128 * g + 2 * lane);
+    const int col = 128 * g + 2 * lane;            // columns at or past xk count as zero
+    const bool in = col < xk;
+    uint32_t v = *(const uint32_t*)(x + t * sxm + (in ? col : xk - 2));
+    v = in ? v : 0u;
     float sum = __uint_as_float(v << 16) + __uint_as_float(v & 0xffff0000u);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
@@ -1200,6 +1203,7 @@ struct MoeCall {
 #define IMQ_MOE_GEMM_WORK 81920
 #endif
 constexpr int64_t kMoeRbWork = IMQ_MOE_RB_WORK;
+constexpr int64_t kRbKStep = 64;   // the register-B kernel's K step (RB_BK)
 constexpr int64_t kMoeGemmWork = IMQ_MOE_GEMM_WORK;
 int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream_t st) {
   const int64_t B = c.T * c.k;
@@ -1221,9 +1225,12 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream
   float* rsx = (float*)(ws + L.rsx);
   float* rsh = (float*)(ws + L.rsh);
   const int ngx = (int)imq_cdiv(c.H, 128), ngh = (int)imq_cdiv(c.I, 128);
+  // the register-B form skips down's K steps past I when I is a multiple of the 64-column K
+  // step; otherwise h's columns past I are zeroed after gate_up
+  const int64_t dxk = c.I % kRbKStep == 0 ? c.I : c.dK;
   auto gate_up = [&](bool check) {
     if (rb)
-      return moe_rb(gmode, ib, c.hidden, c.hs, c.T, c.gK, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
+      return moe_rb(gmode, ib, c.hidden, c.hs, c.T, c.gK, c.xk, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
                     2 * c.I, c.I, mtl + 2, mtl, max_mt, off, perm, (int)c.k, c.gb, c.gbe, c.bdt, c.alpha, c.limit, h,
                     L.hw, nullptr, false, rsx, ngx, ngx, rsh, ngh, st, check);
     return moe_gemm_w4(gmode, c.hidden, c.hs, c.T, c.gK, c.gq, c.gqe, c.gqn, c.gs, c.gz, c.gse, c.gsn, c.sdt,
@@ -1232,7 +1239,7 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream
   };
   auto down = [&](bool check) {
     if (rb)
-      return moe_rb(3, ib, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2,
+      return moe_rb(3, ib, h, L.hw, B, c.dK, dxk, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2,
                     mtl, max_mt, off, perm, (int)c.k, c.db, c.dbe, c.bdt, 0.f, 0.f, nullptr, 0, yr, true, rsh, ngh,
                     ngh, nullptr, 0, st, check);
     return moe_gemm_w4(3, h, L.hw, B, c.dK, c.dq, c.dqe, c.dqn, c.ds, c.dz, c.dse, c.dsn, c.sdt, c.H, 0, mtl + 2, mtl,
@@ -1242,6 +1249,7 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream
   if (gate_up(true) != IMQ_OK || down(true) != IMQ_OK) {
     // the LDS-dequant GEMM only above its own crossover, while the line kernels take the shape
     if (line_ok && B * c.gK < kMoeGemmWork * c.E) return IMQ_ERR_UNSUPPORTED;
+    if (c.xk != c.gK) return IMQ_ERR_UNSUPPORTED;   // the LDS-dequant GEMM reads K columns per row
     rb = false;
     bm = moe_gemm_bm();
     max_mt = imq_cdiv(B, bm) + hits;
@@ -1257,11 +1265,11 @@ int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream
   const int64_t rs_blocks = sums ? imq_cdiv(c.T * ngx, 16) : 0;
   if (rs_blocks > 0x7ffffffe) return IMQ_ERR_UNSUPPORTED;
   moe_sort_kernel<<<dim3((unsigned)(1 + rs_blocks)), dim3(1024), (size_t)c.E * 4, st>>>(
-      c.idx, (int)B, (int)c.E, off, perm, hit, mtl, bm, c.hidden, c.hs, c.T, ngx, sums ? rsx : nullptr);
+      c.idx, (int)B, (int)c.E, off, perm, hit, mtl, bm, c.hidden, c.hs, c.T, ngx, sums ? rsx : nullptr, (int)c.xk);
   IMQ_LAUNCH_CHECK();
   rc = gate_up(false);
   if (rc != IMQ_OK) return rc;
-  if (c.dK > c.I) {   // h's columns past I are read by down's K steps: zero them
+  if (c.dK > c.I && (!rb || dxk > c.I)) {   // h's columns past I that down's K steps read: zero them
     const int64_t total = B * (c.dK - c.I);
     const int64_t blocks = imq_cdiv(total, 256) < 4096 ? imq_cdiv(total, 256) : 4096;
     moe_zero_pad_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(h, B, c.I, c.dK, L.hw);
@@ -1343,7 +1351,7 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
     }
   }
   const bool gemm_shape = c.act == IMQ_ACT_GPTOSS || c.I % (moe_gemm_bn() / 2) == 0;
-  if (!direct && (!line_ok || B * c.gK >= kMoeRbWork * c.E) && c.xk == c.gK && gemm_shape) {
+  if (!direct && (!line_ok || B * c.gK >= kMoeRbWork * c.E) && gemm_shape) {
     const int rc = moe_gemm(c, ws, L, line_ok, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }

@@ -71,10 +71,12 @@ bool moe_rb_folded() { return IMQ_MOE_RB_FOLD != 0; }
 // measured on MI355X, 128-row blocks never paid: the folded form's registers then allow one wave
 // per SIMD and the dequantizing one dequantizes twice the MFMA work per weight load). mode 1: gate_up SiLU-GLU (N = 2I, I a multiple of 128); 2: gpt-oss gate_up
 // (N = 2I, interleaved rows); 3: down (N = H). x rows: hidden (modes 1, 2: row perm[p] / k) or h
-// (mode 3: row p), stride sxm, K columns; down writes yr as fp32 rows, or bf16 ones with yr_bf16
+// (mode 3: row p), stride sxm, K columns of which the first xk (a multiple of the 64-column K
+// step; 0: all) are read -- the K steps past them hold zero activations and are skipped; down
+// writes yr as fp32 rows, or bf16 ones with yr_bf16
 // (N % 64 == 0). check_only: validate the shape and layout, launch
 // nothing. IMQ_ERR_UNSUPPORTED for what the kernel does not cover.
-int moe_rb(int mode, int ib, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t K, const uint8_t* q,
+int moe_rb(int mode, int ib, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t K, int64_t xk, const uint8_t* q,
            int64_t sqe, int64_t sqn, const void* sc, const void* zr, int64_t sse, int64_t ssn, int sdt, int64_t N,
            int64_t I, const int32_t* mtl, const int32_t* nmt, int64_t max_mt, const int32_t* off,
            const int32_t* perm, int k, const void* bias, int64_t sbe, int bdt, float alpha, float limit,
@@ -85,12 +87,15 @@ int moe_rb(int mode, int ib, const uint16_t* x, int64_t sxm, int64_t xrows, int6
   if (mode == 1 && (I % 128 || N != 2 * I)) return IMQ_ERR_UNSUPPORTED;
   if (mode == 2 && (N % 2 || N != 2 * I)) return IMQ_ERR_UNSUPPORTED;
   if (((uintptr_t)x & 15) || (sxm & 7) || ((uintptr_t)q & 15) || (sqn & 15) || (sqe & 15)) return IMQ_ERR_UNSUPPORTED;
-  if (sxm < K || sqn < K / 2 || xrows <= 0 || (xrows + 1) * sxm > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  if (xk <= 0) xk = K;
+  if (xk % RB_BK || xk > K) return IMQ_ERR_UNSUPPORTED;
+  if (sxm < xk || sqn < K / 2 || xrows <= 0 || (xrows + 1) * sxm > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   if (mode != 3 && (hs % 8 || ((uintptr_t)h & 15))) return IMQ_ERR_UNSUPPORTED;   // 16-byte h row segments
   if (mode == 3 && yr_bf16 && (N % 64 || ((uintptr_t)yr & 15))) return IMQ_ERR_UNSUPPORTED;   // 16-byte y segments
   if (check_only) return IMQ_OK;
   if (moe_rb_folded() && (!rs || rs_stride < rs_groups || rs_groups < 0)) return IMQ_ERR_INVALID;
   RbArgs a{x, sxm, 0, (int)K, q, sqn, sc, ssn, 1, zr, ssn, 1, (int)N, 7, h, hs, 1, 0, 1, (int)(K / RB_BK), nullptr};
+  a.xk = (int)xk;
   a.rs = rs;
   a.rs_stride = rs_stride;
   a.rs_groups = rs_groups;

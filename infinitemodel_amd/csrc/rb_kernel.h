@@ -89,6 +89,9 @@ struct RbArgs {
   int rs_stride = 0, rs_groups = 0;
   float* hrs = nullptr;
   int hrs_stride = 0;
+  // MoE forms: valid x columns (a multiple of the K step, <= K; 0 means K): the K steps past them
+  // are skipped -- their activations are zero -- so rows need not be zero-padded to K
+  int xk = 0;
 };
 
 IMQ_DEV float rb_bias(const void* p, int dt, int64_t i) {
@@ -365,7 +368,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   u32x4_t qr[PD][2][QV];
   uint32_t sr[PD][2], zr[PD][2];
   const int kt0 = split * a.kps;
-  const int KT = (a.K / BK - kt0) < a.kps ? (a.K / BK - kt0) : a.kps;
+  const int KS = ((MOE != 0 && a.xk > 0) ? a.xk : a.K) / BK;   // K steps with nonzero activations
+  const int KT = (KS - kt0) < a.kps ? (KS - kt0) : a.kps;
 
   auto load_a = [&](auto setc, int ktl) {
     constexpr int set = decltype(setc)::value;

@@ -340,9 +340,11 @@ def moe_experts_w4(hidden, topk_idx, topk_w, gu, dn, group_size: int, workspace=
     gb, db = biases
     gK, dK = gq.shape[2] * 2, dq.shape[2] * 2
     x = _rows2d(hidden)
-    if x.shape[1] != gK and (x.shape[1] != H or H % 8 or T > 16):
-        # rows of exactly H columns (H % 8 == 0) are read as zero past H by the kernels; past 16
-        # tokens every row is re-read by many passes and one zero-padded copy is cheaper
+    if x.shape[1] != gK and (x.shape[1] != H or H % 8 or (T > 16 and (H % 64 or gK > 40 * 128))):
+        # rows of exactly H columns (H % 8 == 0) are read as zero past H by the decode and line
+        # kernels; past 16 tokens the register-B GEMM skips the K steps past H when H is a
+        # multiple of its 64-column step (and K within its 40 groups): other rows get one
+        # zero-padded copy, cheaper than every pass reading them clamped
         x = torch.nn.functional.pad(x[:, :H], (0, gK - H)).contiguous()
     # int64 ids (torch's top-k) and int32 ids are read by the kernels as they are
     idx = topk_idx if topk_idx.dtype in (torch.int64, torch.int32) else topk_idx.to(torch.int64)
