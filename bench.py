@@ -513,8 +513,8 @@ def bench_c4(args, dev):
     tf_dense = sum(2.0 * M * N * K for N, K, _ in dense_sets) / (ms_dense * 1e-3)
     del dense_sets
     bits = 4 if args.quant == "int4" else 8
-    gemm = (f"gemm_rb_kernel<{bits}> + rb_reduce_kernel (register-B GEMM" if M > 512
-            else f"gemm_wq_kernel<{bits}> (LDS-dequant GEMM")
+    gemm = (f"gemm_rb_kernel<{bits}> + splitk_sum_kernel (register-B GEMM" if M > 512
+            else f"gemm_wq_kernel<{bits}> + splitk_sum_kernel (LDS-dequant GEMM")
     roof = {"bound": "mfma", "achieved": round(tf / 1e12, 2), "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s",
             "frac": round(tf / BF16_PEAK, 4), "traffic": _traffic(f"c4_{args.quant}_m{M}"),
             "kernel": f"{gemm}, imq_linear_{'w4' if bits == 4 else 'w8'} prefill)",

@@ -21,6 +21,7 @@
 //     dealt round-robin over the 8 XCDs), and logical tiles run in groups of 8 tile-rows so the
 //     activation rows and weight columns a group shares stay in that XCD's L2.
 #include "imq_common.h"
+#include "splitk_sum.h"
 
 #include <type_traits>
 
@@ -485,7 +486,7 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
     return;
   }
 
-  // ---- split-K: each split stores its fp32 partial tile into [split][M][N]; splitk_reduce_kernel
+  // ---- split-K: each split stores its fp32 partial tile into [split][M][N]; splitk_sum_kernel
   // sums the splits in order (deterministic) and writes y. A second launch instead of arrival
   // counters: the device-scope fences a last-arriving reduction needs would write back and
   // invalidate the XCD's whole L2 once per workgroup, evicting the shared activation tiles.
@@ -520,33 +521,6 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
         const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m < a.M) a.y[(int64_t)m * a.sym + n] = (uint16_t)cvt_pk_bf16(acc[i][j][r] * sc8, 0.f);
       }
-    }
-  }
-}
-
-// y[m, n] = bf16(sum_s part[s][m][n] * scale[n]) over the splits in order; 4 columns per thread.
-template <int BITS, int SDT>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
-                                                            const void* __restrict__ sc, int64_t ssn,
-                                                            uint16_t* __restrict__ y, int64_t sym) {
-  const int64_t n4 = (N + 3) / 4;
-  const int64_t total = (int64_t)M * n4;
-  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
-    const int m = (int)(t / n4);
-    const int n = 4 * (int)(t - (int64_t)m * n4);
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < splits; ++sp) {
-      const float* src = part + ((size_t)sp * M + m) * N + n;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (n + q < N) v[q] += src[q];
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (n + q >= N) break;
-      float o = v[q];
-      if constexpr (BITS == 8) o *= load_as_f32<SDT>(sc, (int64_t)(n + q) * ssn);
-      y[(int64_t)m * sym + n + q] = (uint16_t)cvt_pk_bf16(o, 0.f);
     }
   }
 }
@@ -596,13 +570,7 @@ int launch_cfg(const GemmArgs& a0, void* ws, int64_t ws_bytes, hipStream_t st) {
   }
   kern<<<dim3((unsigned)(T * s)), dim3(C::NTHR), C::LDS, st>>>(a);
   IMQ_LAUNCH_CHECK();
-  if (s > 1) {
-    const int64_t total = (int64_t)a.M * ((a.N + 3) / 4);
-    const int64_t blocks = imq_cdiv(total, 256) < 8192 ? imq_cdiv(total, 256) : 8192;
-    splitk_reduce_kernel<BITS, SDT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a.part, s, a.M, a.N, a.sc, a.ssn,
-                                                                                 a.y, a.sym);
-    IMQ_LAUNCH_CHECK();
-  }
+  if (s > 1) return splitk_sum<BITS, SDT>(a.part, s, a.M, a.N, a.sc, a.ssn, a.y, a.sym, st);
   return IMQ_OK;
 }
 

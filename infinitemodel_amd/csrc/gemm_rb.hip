@@ -2,39 +2,13 @@
 // ("register-B" form): the dense launchers (tile plan, split-K partials and their reduction).
 // The kernel and its structure are described in rb_kernel.h.
 #include "rb_kernel.h"
+#include "splitk_sum.h"
 
 namespace imq {
 
 int64_t rb_workspace_bytes(int bits, int64_t M, int64_t N, int64_t K, int cus);
 
 namespace {
-
-// y[m, n] = bf16(sum_s part[s][m][n] * scale[n]) over the splits in order; 4 columns per thread.
-template <int BITS, int SDT>
-__global__ __launch_bounds__(256) void rb_reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
-                                                        const void* __restrict__ sc, int64_t ssn,
-                                                        uint16_t* __restrict__ y, int64_t sym) {
-  const int64_t n4 = (N + 3) / 4;
-  const int64_t total = (int64_t)M * n4;
-  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
-    const int m = (int)(t / n4);
-    const int n = 4 * (int)(t - (int64_t)m * n4);
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < splits; ++sp) {
-      const float* src = part + ((size_t)sp * M + m) * N + n;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (n + q < N) v[q] += src[q];
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (n + q >= N) break;
-      float o = v[q];
-      if constexpr (BITS == 8) o *= load_as_f32<SDT>(sc, (int64_t)(n + q) * ssn);
-      y[(int64_t)m * sym + n + q] = (uint16_t)cvt_pk_bf16(o, 0.f);
-    }
-  }
-}
 
 // Tile plan (measured on the C4 shapes): 256 rows per wave (IB 8) whenever those tiles cover at
 // least half of the CUs, else 128 rows (IB 4); then K is split in two or four while the grid still
@@ -80,13 +54,7 @@ int rb_launch(const RbArgs& a0, void* ws, int64_t wsb, hipStream_t st) {
   }
   kern<<<dim3((unsigned)(T * s)), dim3(64 * NW), lds, st>>>(a);
   IMQ_LAUNCH_CHECK();
-  if (s > 1) {
-    const int64_t total = (int64_t)a.M * ((a.N + 3) / 4);
-    const int64_t blocks = imq_cdiv(total, 256) < 8192 ? imq_cdiv(total, 256) : 8192;
-    rb_reduce_kernel<BITS, SDT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a.part, s, a.M, a.N, a.sc, a.ssn, a.y,
-                                                                             a.sym);
-    IMQ_LAUNCH_CHECK();
-  }
+  if (s > 1) return splitk_sum<BITS, SDT>(a.part, s, a.M, a.N, a.sc, a.ssn, a.y, a.sym, st);
   return IMQ_OK;
 }
 
