@@ -1202,7 +1202,15 @@ struct MoeCall {
 #ifndef IMQ_MOE_GEMM_WORK
 #define IMQ_MOE_GEMM_WORK 81920
 #endif
+#ifndef IMQ_MOE_RB_WORK_WIDE
+#define IMQ_MOE_RB_WORK_WIDE 8192
+#endif
 constexpr int64_t kMoeRbWork = IMQ_MOE_RB_WORK;
+// gate_up K past 2048 (line kernel workgroups of more than 4 waves, one resident per CU at their
+// register count): the register-B forms take over at a quarter of the work (measured, gpt-oss-20b
+// K 3072: T=32 2237 -> 2393 GB/s, T=64 2105 -> 2420; OLMoE K 2048 keeps the line kernels to
+// T=64, 2829 against 2398)
+constexpr int64_t kMoeRbWorkWide = IMQ_MOE_RB_WORK_WIDE;
 constexpr int64_t kRbKStep = 64;   // the register-B kernel's K step (RB_BK)
 constexpr int64_t kMoeGemmWork = IMQ_MOE_GEMM_WORK;
 int moe_gemm(const MoeCall& c, char* ws, const MoeWs& L, bool line_ok, hipStream_t st) {
@@ -1307,8 +1315,8 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   const bool sz_words = aligned(c.gs, 4) && aligned(c.gz, 4) && aligned(c.ds, 4) && aligned(c.dz, 4) &&
                         (c.gsn * vb) % 4 == 0 && (c.dsn * vb) % 4 == 0 && (c.gse * vb) % 4 == 0 &&
                         (c.dse * vb) % 4 == 0;
-  int s2, w;
-  const bool line_ok = sz_words && moe_line_shape(c.gK, &s2, &w) && moe_line_shape(c.dK, &s2, &w);
+  int s2, w, gw = 0;
+  const bool line_ok = sz_words && moe_line_shape(c.gK, &s2, &gw) && moe_line_shape(c.dK, &s2, &w);
   int32_t* off = (int32_t*)(ws + L.off);
   int32_t* perm = (int32_t*)(ws + L.perm);
   int32_t* hit = (int32_t*)(ws + L.hit);
@@ -1351,7 +1359,8 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
     }
   }
   const bool gemm_shape = c.act == IMQ_ACT_GPTOSS || c.I % (moe_gemm_bn() / 2) == 0;
-  if (!direct && (!line_ok || B * c.gK >= kMoeRbWork * c.E) && gemm_shape) {
+  const int64_t rb_work = gw > 4 ? kMoeRbWorkWide : kMoeRbWork;
+  if (!direct && (!line_ok || B * c.gK >= rb_work * c.E) && gemm_shape) {
     const int rc = moe_gemm(c, ws, L, line_ok, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }
