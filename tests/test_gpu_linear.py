@@ -418,6 +418,34 @@ def test_linear_w2_ksplit_without_workspace_matches(dev):
         assert torch.equal(ops.linear_w2(x, q, 64, (s, z)), y1)
 
 
+@pytest.mark.parametrize("N,K", [(4096, 4096), (4120, 8192), (28672, 8192)])
+@pytest.mark.parametrize("M", [5, 8])
+@pytest.mark.parametrize("sdt", ["fp16", "bf16"])
+def test_linear_w2_ksplit_wide_shapes(dev, N, K, M, sdt):
+    """int2 rows 4 < M <= 8 on grids of at least one 16-row tile per CU (the K-split kernel's
+    4-tile workgroups, three resident per CU): K_pad 4096 / 8192, a ragged last row block (4120
+    rows), C3's 8192 -> 28672, fp16 and bf16 scale / zero words."""
+    c = dict(C.int2_random_case(N, K, 64, seed=2500 + N + M, dt=sdt))
+    _linear_check(dev, c, M, seed=M, bits=2)
+
+
+@pytest.mark.parametrize("K", [4096, 8192])
+def test_linear_w2_ksplit_wide_fp32_scales_and_dealias(dev, K):
+    """fp32 scale / zero words and the +64-byte de-alias row view on those grids; repeated calls
+    are bit-identical."""
+    import torch
+    from infinitemodel_amd import ops
+    c = dict(C.int2_random_case(4096, K, 64, seed=2600 + K, dt="fp32"))
+    for M in (6, 8):
+        _linear_check(dev, c, M, seed=M, bits=2, view_pad=64)
+    c16 = C.int2_random_case(4096, K, 64, seed=2601, dt="fp16")
+    q, s, z = C.u8(c16["q"], dev), C.to_torch(c16["s"], "fp16", dev), C.to_torch(c16["z"], "fp16", dev)
+    x = C.to_torch(C.bf16_normal(C.rng(7), (7, K)), "bf16", dev)
+    y = ops.linear_w2(x, q, 64, (s, z))
+    for _ in range(3):
+        assert torch.equal(ops.linear_w2(x, q, 64, (s, z)), y)
+
+
 def test_linear_w2_fp32_scales(dev):
     c = dict(C.int2_random_case(160, 4096, 64, seed=2004, dt="fp32"))
     for M in (1, 3):
