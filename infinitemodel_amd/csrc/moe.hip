@@ -840,11 +840,12 @@ __global__ __launch_bounds__(1024) void moe_gu_line_kernel(MoeDecArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
   const int wbytes = dec_wave_lds(S2, VB, false);
-  const int b = blockIdx.x / a.NR, u = blockIdx.x - b * a.NR;
-  const int tile = ACT == 0 ? wave / a.Wk : 0;
+  // grid (unit, slot, token): routed row b = token k + slot with k = gridDim.y, no division
+  const int b = blockIdx.z * gridDim.y + blockIdx.y, u = blockIdx.x;
+  const int tile = (ACT == 0 && wave >= a.Wk) ? 1 : 0;   // SiLU-GLU: gate waves, then up waves
   const int wk = wave - tile * a.Wk;
   const int rbase = ACT == 0 ? (tile == 0 ? 16 * u : a.I + 16 * u) : 16 * u;
-  const uint16_t* xrow = a.x + (int64_t)(b / a.k) * a.sxm;
+  const uint16_t* xrow = a.x + (int64_t)blockIdx.z * a.sxm;
   int e = a.idx.at(b);
   e = (e >= 0 && e < a.E) ? e : 0;   // ids outside [0, E) are clamped, as in the sort
   const float v = dec_tile_partial<S2, SDT, XCL, false>(a, e, rbase, xrow, wk * S2, a.Kpad / kDLine,
@@ -890,7 +891,7 @@ __global__ __launch_bounds__(1024) void moe_dn_line_kernel(MoeDecArgs a) {
   const int W = blockDim.x >> 6;
   constexpr int ROWS = PAIR ? 8 : 16;               // output rows per workgroup
   const int wbytes = dec_wave_lds(S2, VB, PAIR);
-  const int t = blockIdx.x / a.NR, rt = blockIdx.x - t * a.NR;
+  const int t = blockIdx.y, rt = blockIdx.x;                       // grid (row tile, token)
   const int grp = wave / a.Wk, wk = wave - grp * a.Wk;            // group: slot pair or slot
   const int j = PAIR ? 2 * grp : grp;
   const bool has2 = PAIR && j + 1 < a.k;                           // odd k: the last pair is one slot
@@ -918,12 +919,12 @@ __global__ __launch_bounds__(1024) void moe_dn_line_kernel(MoeDecArgs a) {
 }
 
 template <class KERN>
-int dec_launch(KERN kern, int grid, int W, size_t lds, hipStream_t st, const MoeDecArgs& a) {
+int dec_launch(KERN kern, dim3 grid, int W, size_t lds, hipStream_t st, const MoeDecArgs& a) {
   if (lds > 65536) {
     hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (err != hipSuccess) return (int)err;
   }
-  kern<<<dim3((unsigned)grid), dim3(64 * W), lds, st>>>(a);
+  kern<<<grid, dim3(64 * W), lds, st>>>(a);
   IMQ_LAUNCH_CHECK();
   return IMQ_OK;
 }
@@ -954,8 +955,10 @@ int dec_gu(const MoeDecArgs& a0, int act, int64_t B, int max_lds, hipStream_t st
   a.NR = act == IMQ_ACT_GPTOSS ? 2 * a.I / 16 : a.I / 16;
   const int W = groups * Wk;
   const size_t lds = (size_t)W * dec_wave_lds(S2, SDT == IMQ_DT_FP32 ? 4 : 2, false) + (size_t)W * 16 * 4;
-  if (lds > (size_t)max_lds || B * a.NR > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
-  const int grid = (int)(B * a.NR);
+  const int64_t T = B / a.k;
+  if (lds > (size_t)max_lds || a.NR > 0x7fffffff || a.k > 65535 || T > 65535 || T * a.k != B)
+    return IMQ_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)a.NR, (unsigned)a.k, (unsigned)T);
   const bool xcl = a.xk < a.Kpad;
 #define IMQ_GU(S, A, X) dec_launch(moe_gu_line_kernel<S, SDT, A, X>, grid, W, lds, st, a)
   if (act == IMQ_ACT_GPTOSS) {
@@ -988,8 +991,8 @@ int dec_dn(const MoeDecArgs& a0, int64_t T, int64_t H, int max_lds, hipStream_t 
   a.NR = (int)(pair ? H / 8 : H / 16);
   const int W = groups * Wk;
   const size_t lds = (size_t)W * dec_wave_lds(S2, SDT == IMQ_DT_FP32 ? 4 : 2, pair) + (size_t)W * 16 * 4;
-  if (lds > (size_t)max_lds || T * a.NR > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
-  const int grid = (int)(T * a.NR);
+  if (lds > (size_t)max_lds || T > 65535) return IMQ_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)a.NR, (unsigned)T);
   const bool xcl = a.xk < a.Kpad;
 #define IMQ_DN(S, X, P) dec_launch(moe_dn_line_kernel<S, SDT, X, P>, grid, W, lds, st, a)
   if (pair) {
