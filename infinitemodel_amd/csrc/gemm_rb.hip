@@ -117,10 +117,14 @@ int gemm_rb(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, cons
             int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
   if (((uintptr_t)x & 15) || (sxm & 7) || ((uintptr_t)q & 15) || (sqn & 15)) return IMQ_ERR_UNSUPPORTED;
   if (sxm < 0 || sqn < 0 || 256 * sxm > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  // the kernel's buffer offsets from a tile's first row (activations, weights, scale / zero)
+  if ((256 * sxm + K) * 2 > 0x7fffffff || 256 * sqn + K > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   int gsh = 0;
   if (bits == 4) {
     while ((1 << gsh) < G) ++gsh;
-    if (ssg < 0 || szg < 0) return IMQ_ERR_UNSUPPORTED;
+    if (ssg < 0 || szg < 0 || ssn < 0 || szn < 0) return IMQ_ERR_UNSUPPORTED;
+    const int64_t ng = K / G + 1;
+    if ((256 * ssn + ng * ssg) * 4 > 0x7fffffff || (256 * szn + ng * szg) * 4 > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   }
   RbArgs a{x, sxm, (int)M, (int)K, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, gsh, y, sym, 0, 0, 1, 0, nullptr};
   switch (sdt) {

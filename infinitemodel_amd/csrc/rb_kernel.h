@@ -50,6 +50,10 @@ constexpr int RB_BK = 64;
 #ifndef RB_FOLD_EARLY_UNPACK
 #define RB_FOLD_EARLY_UNPACK 1
 #endif
+// Dense form: 1 loads activations, weights and scale / zero through buffer resources (see the kernel)
+#ifndef IMQ_RB_BUF
+#define IMQ_RB_BUF 1
+#endif
 
 struct RbArgs {
   const uint16_t* x;
@@ -101,6 +105,20 @@ IMQ_DEV float rb_bias(const void* p, int dt, int64_t i) {
 }
 
 IMQ_DEV int rb_swz(int row, int c) { return (row * 8 + (c ^ ((row >> 1) & 7))) * 8; }
+
+// A raw buffer resource over `base` (offsets are kept below 2^31 by the launcher, so the range
+// check never clips) and its loads: the per-lane offset in a VGPR, the per-step one in an SGPR.
+IMQ_DEV __amdgpu_buffer_rsrc_t rb_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+IMQ_DEV u32x4_t rb_bload128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+template <int DT>
+IMQ_DEV uint32_t rb_bload_raw(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  if constexpr (DT == IMQ_DT_FP32) return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+  else return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
 
 // w & m computed in a register the compiler cannot see through, so the byte extractions below
 // stay single v_cvt_f32_ubyteN instructions instead of being re-folded into per-nibble bit-field
@@ -204,6 +222,12 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
 
   // ---- activation load plan (32-bit offsets from the tile's first row); the MoE forms gather
   // rows through perm, so the folded form runs it after its first weight loads are out ------
+  // Dense form (BUF): every load goes through a buffer resource whose base is uniform over the
+  // workgroup (the tile's first activation row, weight row, scale and zero row); a lane's offset
+  // into it is fixed for the whole K loop and the step's offset is a scalar operand, so a step's
+  // loads cost no vector address arithmetic (64-bit per-lane addresses were a fifth of the loop's
+  // VALU instructions). gemm_rb keeps every offset below 2^31.
+  constexpr bool BUF = MOE == 0 && IMQ_RB_BUF;
   const uint16_t* xtile = a.x + (int64_t)m0 * a.sxm;
   int xo[XC], xl[XC];
   auto plan_a = [&]() {
@@ -218,14 +242,17 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
         const int p = prow0 + (row < cnt ? row : cnt - 1);                // sorted position
         r = MOE == 3 ? p : a.perm[p] / a.k;           // down reads h in sorted order, gate_up gathers
       }
-      xo[j] = (int)(r * a.sxm) + ch * 8;
-      xl[j] = rb_swz(row, ch);
+      xo[j] = ((int)(r * a.sxm) + ch * 8) * (BUF ? 2 : 1);   // BUF: bytes
+      xl[j] = 2 * rb_swz(row, ch);                    // bytes
     }
   };
   // ---- weight load plan: columns n0 + 64 wave + 32 j + c (MOE 1: gate column tn 32 NW + 32 wave
   // + c for j = 0, the matching up column I + that for j = 1), K bytes [32 h, +32) codes per step --
   const uint8_t* qb[2];
   int64_t sb[2], zb[2];
+  uint32_t qvo[2], svo[2], zvo[2];                  // BUF: byte offsets from the tile's rows
+  constexpr int SES = SDT == IMQ_DT_FP32 ? 4 : 2, ZES = ZDT == IMQ_DT_FP32 ? 4 : 2;
+  const int gh = (32 * h) >> a.gsh;                 // the lane half's group within a step (groups < 64)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     int n = MOE == 1 ? (j ? a.I : 0) + tn * (32 * NW) + 32 * wave + c : n0 + 64 * wave + 32 * j + c;
@@ -233,7 +260,15 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
     qb[j] = a.q + (int64_t)e * a.sqe + (int64_t)n * a.sqn + (BITS == 8 ? 32 : 16) * h;
     sb[j] = (int64_t)e * a.sse + (int64_t)n * a.ssn;
     zb[j] = (int64_t)e * a.sse + (int64_t)n * a.szn;
+    qvo[j] = (uint32_t)((n - n0) * (int)a.sqn + (BITS == 8 ? 32 : 16) * h);
+    svo[j] = (uint32_t)(((n - n0) * (int)a.ssn + gh * (int)a.ssg) * SES);
+    zvo[j] = (uint32_t)(((n - n0) * (int)a.szn + gh * (int)a.szg) * ZES);
   }
+  // (built unconditionally; the forms that do not use them drop them)
+  const __amdgpu_buffer_rsrc_t xrs = rb_rsrc(xtile);
+  const __amdgpu_buffer_rsrc_t qrs = rb_rsrc(a.q + (int64_t)n0 * a.sqn);
+  const __amdgpu_buffer_rsrc_t srs = rb_rsrc((const char*)a.sc + (int64_t)n0 * a.ssn * SES);
+  const __amdgpu_buffer_rsrc_t zrs = rb_rsrc((const char*)a.zr + (int64_t)n0 * a.szn * ZES);
 
   // MoE forms: the tile's scale / zero pairs for all K groups are staged in LDS once, as
   // [group][tile column] dwords (bf16 scale | bf16 zero << 16, both rounded to bf16 as the
@@ -375,11 +410,27 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
     constexpr int set = decltype(setc)::value;
     const int kt = kt0 + (ktl < KT ? ktl : KT - 1);
 #pragma unroll
-    for (int j = 0; j < XC; ++j) xr[set][j] = *(const u32x4_t*)(xtile + kt * BK + xo[j]);
+    for (int j = 0; j < XC; ++j) {
+      if constexpr (BUF) xr[set][j] = rb_bload128(xrs, xo[j], kt * (BK * 2));
+      else xr[set][j] = *(const u32x4_t*)(xtile + kt * BK + xo[j]);
+    }
   };
   auto load_b = [&](auto setc, int ktl) {
     constexpr int set = decltype(setc)::value;
     const int kt = kt0 + (ktl < KT ? ktl : KT - 1);
+    if constexpr (BUF) {
+      const uint32_t gs = (uint32_t)((kt * BK) >> a.gsh);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int v = 0; v < QV; ++v) qr[set][j][v] = rb_bload128(qrs, qvo[j] + 16 * v, kt * (BK * BITS / 8));
+        if constexpr (BITS != 8) {
+          sr[set][j] = rb_bload_raw<SDT>(srs, svo[j], gs * (uint32_t)a.ssg * SES);
+          zr[set][j] = rb_bload_raw<ZDT>(zrs, zvo[j], gs * (uint32_t)a.szg * ZES);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -404,7 +455,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   auto store_a = [&](auto setc, uint16_t* A) {
     constexpr int set = decltype(setc)::value;
 #pragma unroll
-    for (int j = 0; j < XC; ++j) *(u32x4_t*)(A + xl[j]) = FOLD ? permute_x8(xr[set][j]) : xr[set][j];
+    for (int j = 0; j < XC; ++j) *(u32x4_t*)((char*)A + xl[j]) = FOLD ? permute_x8(xr[set][j]) : xr[set][j];
   };
 
   // acc: the running sums (FOLD: the current group's sums of x (128 + q)); tot: FOLD's total
@@ -423,14 +474,14 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   float sfold[2] = {0.f, 0.f};   // FOLD: scale of the group whose sums acc holds
   int aoff[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) aoff[s] = rb_swz(c, 4 * h + s);   // + 32 rows (2048 elements) per i
+  for (int s = 0; s < 4; ++s) aoff[s] = 2 * rb_swz(c, 4 * h + s);   // bytes; + 32 rows (4096 bytes) per i
 
   bf16x8_t af[2][IB];        // A fragments of slice s live in af[s & 1], B fragments in bq[s & 1]
   bf16x8_t bq[2][2];         // (4 slices: the parity pattern repeats every step)
   auto read_frags = [&](auto pc, const uint16_t* A, int s) {
     constexpr int p = decltype(pc)::value;
 #pragma unroll
-    for (int i = 0; i < IB; ++i) af[p][i] = *(const bf16x8_t*)(A + aoff[s] + i * 32 * BK);
+    for (int i = 0; i < IB; ++i) af[p][i] = *(const bf16x8_t*)((const char*)A + aoff[s] + i * 64 * BK);
   };
 
   // The scale / zero of a B register set as (s, -z s), both taken to bf16 first.
