@@ -309,8 +309,23 @@ IMQ_DEV float moe_row_swap8(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
 }
 
-// XCL: activation rows shorter than K (a.xk < a.Kpad), read with the clamp-and-zero of xk.
-template <int S2, int NTL, int SDT, int MODE, bool XCL>
+// Raw buffer resources and loads of the token-sorted line kernel (offsets below 2^31, checked
+// by the launcher); nt: the weight stream's non-temporal hint.
+IMQ_DEV __amdgpu_buffer_rsrc_t moe_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+IMQ_DEV u32x4_t moe_bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+IMQ_DEV u32x4_t moe_bload_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2));
+}
+
+// XCL: activation rows shorter than K (a.xk < a.Kpad), columns past xk read as zero. XCL 1
+// (xk % 32 == 0): a lane's 32 columns of one (line-step, half) lie all below xk or all past it,
+// and past it the lane reads its row's first 32 columns and zeroes them -- one address per 32
+// columns, the rest immediate offsets. XCL 2 (xk % 8 == 0): clamped and zeroed per 8 columns.
+template <int S2, int NTL, int SDT, int MODE, int XCL>
 __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int VB = (SDT == IMQ_DT_FP32) ? 4 : 2;
@@ -323,23 +338,33 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   const bool lo8 = c < 8;
   const int KL = a.Kpad / kMoeLine;
   const int ls0 = wave * S2;
+  // The sort's outputs are read through the scalar cache: the item's expert, its row range and
+  // the routed rows of its first pass are uniform over the workgroup, and scalar loads count on
+  // lgkmcnt, so no wait for them queues behind the weight stream on the in-order vmcnt.
+  using cint32 = const __attribute__((address_space(4))) int32_t;
+  cint32* const chit = (cint32*)a.hit;
+  cint32* const coff = (cint32*)a.off;
+  cint32* const cperm = (cint32*)a.perm;
   // (hit expert, row block) work items, or (routed row, row block) in the direct form
-  const int items = a.direct ? a.nrows * a.NB : a.hit[a.E] * a.NB;
+  const int items = a.direct ? a.nrows * a.NB : chit[a.E] * a.NB;
 
   uint32_t* szl = (uint32_t*)smem + wave * (2 * NTL * 16 * DPR);
   float* red = (float*)(smem + (size_t)W * (2 * NTL * 16 * DPR) * 4);   // [W][NTL][16][16]
+  float* bst = red + W * NTL * 256;                                     // [NTL * 16] row biases
+  int* prow = (int*)(bst + NTL * 16);                                   // [16] first pass's routed rows
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
-  const int blk = item - (item / a.NB) * a.NB;
+  const int ib = item / a.NB;
+  const int blk = item - ib * a.NB;
   int e, beg, end;
   if (a.direct) {
-    beg = item / a.NB;
+    beg = ib;
     end = beg + 1;
     e = a.idx.at(beg);
     e = (e >= 0 && e < a.E) ? e : 0;   // ids outside [0, E) are clamped, as in the sort
   } else {
-    e = a.hit[item / a.NB];
-    beg = a.off[e];
-    end = a.off[e + 1];
+    e = chit[ib];
+    beg = coff[e];
+    end = coff[e + 1];
   }
   auto perm_at = [&](int p) -> int { return a.direct ? p : a.perm[p]; };
 
@@ -350,6 +375,23 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   auto bias_at = [&](int row) -> float {
     return a.bias != nullptr ? load_bias(a.bias, a.bdt, (int64_t)e * a.sbe + row) : 0.f;
   };
+  // ---- the item's row biases (one per row of the block), issued first: the epilogue reads them
+  // from LDS instead of waiting on a load after the reduction ----
+  // (unconditional: a load under a branch ends in a full wait where the paths join; without a
+  // bias the weights' first word is read and ignored. The aligned dword holding a 2-byte element
+  // lies in the element's page.)
+  const bool has_bias = a.bias != nullptr;
+  uint32_t bw;        // the raw dword; converted where it is stored, after the activation loads
+  bool bhi;
+  {
+    const int br = rbase((threadIdx.x >> 4) & (NTL - 1)) + (threadIdx.x & 15);
+    const int bsz = a.bdt == IMQ_DT_FP32 ? 4 : 2;
+    const char* bb = has_bias ? (const char*)a.bias : (const char*)a.q;
+    const int64_t boff = has_bias ? ((int64_t)e * a.sbe + br) * bsz : 0;
+    const int mis = (int)(((uintptr_t)bb + (uintptr_t)boff) & 3);   // 0, or 2 for the upper half
+    bw = *(const uint32_t*)(bb + boff - mis);
+    bhi = mis != 0;
+  }
   // ---- scale / zero words of this wave's groups for the 4 tiles -> wave LDS ----
   constexpr int ZN = 2 * NTL * 16 * DPR;
   constexpr int ZU = (ZN + 63) / 64;
@@ -372,24 +414,85 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
     zv[u] = *(const uint32_t*)((arr ? zbase : sbase) + ro);
   }
   // ---- weights: per tile and line-step one full-line load for rows 0-7 and one for rows 8-15 ----
-  const uint8_t* qe = a.q + (int64_t)e * a.sqe;
+  // buffer loads from the expert's first row: a lane's offsets (row c & 7 or 8 + (c & 7), its 16
+  // bytes of the line) are fixed, the tile's rows and the line-step are scalar offsets
+  const __amdgpu_buffer_rsrc_t qrs = moe_rsrc(a.q + (int64_t)e * a.sqe);
+  const uint32_t qv0 = (uint32_t)((c & 7) * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64));
+  const uint32_t qv1 = (uint32_t)((8 + (c & 7)) * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0));
   u32x4_t wb[NTL][2 * S2];
 #pragma unroll
   for (int t = 0; t < NTL; ++t) {
-    const uint8_t* q0 = qe + (int64_t)(rbase(t) + (c & 7)) * a.sqn + 16 * ar + (lo8 ? 0 : 64);
-    const uint8_t* q1 = qe + (int64_t)(rbase(t) + 8 + (c & 7)) * a.sqn + 16 * ar + (lo8 ? 64 : 0);
 #pragma unroll
     for (int i = 0; i < S2; ++i) {
       int l = ls0 + i;
       l = l < KL ? l : KL - 1;
-      wb[t][2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
-      wb[t][2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+      const uint32_t so = (uint32_t)(rbase(t) * (int)a.sqn + 128 * l);
+      wb[t][2 * i] = moe_bload_nt(qrs, qv0, so);
+      wb[t][2 * i + 1] = moe_bload_nt(qrs, qv1, so);
     }
+  }
+  // ---- activations of the first pass, issued behind the weights so both arrive in one wait ----
+  // Routed rows of the first pass, sorted positions beg .. beg + 15, with one scalar load (perm's
+  // workspace slot holds 16 spare entries past its B); lane i < 16 of sp holds row i and a lane
+  // picks its row with a cross-lane read. Placed after the weight loads, so that its wait (and
+  // that for beg) does not hold them back.
+  int sp = beg + (lane & 15);
+  if (!a.direct) {
+    typedef int32_t v16i __attribute__((ext_vector_type(16), aligned(4)));
+    const v16i pv = *(const __attribute__((address_space(4))) v16i*)(cperm + beg);   // one s_load_dwordx16
+#pragma unroll
+    for (int i = 0; i < 16; ++i) asm("v_writelane_b32 %0, %1, %2" : "+v"(sp) : "s"(pv[i]), "n"(i));
+  }
+  auto pick16 = [&](int i) -> int { return __shfl(sp, i, 64); };
+  // the lane's activation row as a byte offset into x (the launcher keeps x below 2^31 bytes)
+  const __amdgpu_buffer_rsrc_t xrs = moe_rsrc(a.x);
+  auto xrow_of = [&](int p0, bool first) -> uint32_t {
+    const int nrow = (end - p0) < 16 ? end - p0 : 16;
+    const int cc = c < nrow ? c : nrow - 1;           // A row of this lane (rows >= nrow repeat the last)
+    if constexpr (MODE != 1) {
+      const int rid = first ? pick16(cc) : perm_at(p0 + cc);
+      return (uint32_t)((rid / a.k) * (int)a.sxm * 2);   // gate_up: gather hidden rows
+    } else {
+      return (uint32_t)((p0 + cc) * (int)a.sxm * 2);
+    }
+  };
+  auto xcol = [&](int i, int h, int kk) -> int {
+    int l = ls0 + i;
+    l = l < KL ? l : KL - 1;
+    return kMoeLine * l + 128 * h + 32 * ar + 8 * kk;
+  };
+  u32x4_t X[S2][2][4];
+  // zo: 0, opaque to the compiler, so that the column offsets are computed where the loads are
+  // issued (per item, per pass) rather than hoisted out of the loops and held in registers
+  auto load_x = [&](uint32_t xo, int zo) {
+#pragma unroll
+    for (int i = 0; i < S2; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int cb = xcol(i, h, 0) + zo;                   // the lane's 32 columns [cb, cb + 32)
+        if constexpr (XCL == 1) cb = xcol(i, h, 0) < a.xk ? cb : zo;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          int col = cb + 8 * kk;
+          if constexpr (XCL == 2) col = col < a.xk ? col : a.xk - 8;
+          X[i][h][kk] = moe_bload(xrs, xo + 2 * (uint32_t)col, 0);
+        }
+      }
+  };
+  {
+    int zo = 0;
+    asm volatile("" : "+v"(zo));
+    load_x(xrow_of(beg, true), zo);
   }
 #pragma unroll
   for (int u = 0; u < ZU; ++u) {
     const int d = lane + 64 * u;
     if (d < ZN) szl[d] = zv[u];
+  }
+  if (threadIdx.x < 16) prow[threadIdx.x] = sp;        // for the epilogue (read after its barrier)
+  if (has_bias && threadIdx.x < 16 * NTL) {
+    const uint32_t hb = bhi ? (bw >> 16) : (bw & 0xffffu);
+    bst[threadIdx.x] = a.bdt == IMQ_DT_FP32 ? __uint_as_float(bw) : a.bdt == IMQ_DT_FP16 ? f16_bits_to_f32(hb) : bf16_bits_to_f32(hb);
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // wave-private LDS, in-order
 
@@ -398,18 +501,16 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
     if constexpr (VB == 4) return round_bf16_hw(__uint_as_float(p[g]));
     else return raw_to_bf16_f32<SDT>((g & 1) ? (p[g >> 1] >> 16) : (p[g >> 1] & 0xffffu));
   };
-  float s0[NTL][S2], s1[NTL][S2], cz0[NTL][S2], cz1[NTL][S2];
-#pragma unroll
-  for (int t = 0; t < NTL; ++t)
-#pragma unroll
-    for (int i = 0; i < S2; ++i) {
-      const bool v = ls0 + i < KL;
-      const float r0 = val(t, 0, c, 2 * i), r1 = val(t, 0, c ^ 8, 2 * i + 1);   // read, then select
-      s0[t][i] = v ? r0 : 0.f;
-      s1[t][i] = v ? r1 : 0.f;
-      cz0[t][i] = -(128.f + val(t, 1, c, 2 * i)) * s0[t][i];
-      cz1[t][i] = -(128.f + val(t, 1, c ^ 8, 2 * i + 1)) * s1[t][i];
-    }
+  // scale and -(128 + z) * scale of tile t, line-step i: read from the staged words at use (held
+  // in registers for all tiles they would crowd out the activation loads)
+  auto szpair = [&](int t, int i, float& s0, float& s1, float& cz0, float& cz1) {
+    const bool v = ls0 + i < KL;
+    const float r0 = val(t, 0, c, 2 * i), r1 = val(t, 0, c ^ 8, 2 * i + 1);   // read, then select
+    s0 = v ? r0 : 0.f;
+    s1 = v ? r1 : 0.f;
+    cz0 = -(128.f + val(t, 1, c, 2 * i)) * s0;
+    cz1 = -(128.f + val(t, 1, c ^ 8, 2 * i + 1)) * s1;
+  };
 
   const uint32_t magic = magic_bf16_128x2();
   const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
@@ -423,10 +524,11 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
         for (int i = 0; i < 2 * S2; ++i) asm volatile("" : "+v"(wb[t][i]));
     }
     const int nrow = (end - p0) < 16 ? end - p0 : 16;
-    const int pr = p0 + (c < nrow ? c : nrow - 1);    // A row of this lane (rows >= nrow repeat the last)
-    const uint16_t* xr;
-    if constexpr (MODE != 1) xr = a.x + (int64_t)(perm_at(pr) / a.k) * a.sxm;   // gate_up: gather hidden rows
-    else xr = a.x + (int64_t)pr * a.sxm;
+    if (p0 != beg) {
+      int zo = 0;
+      asm volatile("" : "+v"(zo));
+      load_x(xrow_of(p0, false), zo);
+    }
     f32x4_t y0[NTL], y1[NTL];
 #pragma unroll
     for (int t = 0; t < NTL; ++t) {
@@ -435,21 +537,14 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < S2; ++i) {
-      int l = ls0 + i;
-      l = l < KL ? l : KL - 1;
       bf16x8_t A[2][4];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const int col = kMoeLine * l + 128 * h + 32 * ar + 8 * kk;
-          u32x4_t v;
-          if constexpr (XCL) {
-            const bool xin = col < a.xk;
-            v = *(const u32x4_t*)(xr + (xin ? col : a.xk - 8));
-            if (!xin) v = u32x4_t{0u, 0u, 0u, 0u};
-          } else {
-            v = *(const u32x4_t*)(xr + col);
+          u32x4_t v = X[i][h][kk];
+          if constexpr (XCL != 0) {
+            if (!(xcol(i, h, XCL == 1 ? 0 : kk) < a.xk)) v = u32x4_t{0u, 0u, 0u, 0u};
           }
           A[h][kk] = __builtin_bit_cast(bf16x8_t, permute_x8(v));
         }
@@ -477,12 +572,14 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
           acc0 = mfma16x16x32(A[0][kk], unpack_nib8_bf16(gA[kk], magic), acc0);
           acc1 = mfma16x16x32(A[1][kk], unpack_nib8_bf16(gB[kk], magic), acc1);
         }
+        float s0, s1, cz0, cz1;
+        szpair(t, i, s0, s1, cz0, cz1);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          y0[t][r] = fmaf(cz0[t][i], xs0[r], y0[t][r]);
-          y1[t][r] = fmaf(cz1[t][i], xs1[r], y1[t][r]);
-          y0[t][r] = fmaf(s0[t][i], acc0[r], y0[t][r]);
-          y1[t][r] = fmaf(s1[t][i], acc1[r], y1[t][r]);
+          y0[t][r] = fmaf(cz0, xs0[r], y0[t][r]);
+          y1[t][r] = fmaf(cz1, xs1[r], y1[t][r]);
+          y0[t][r] = fmaf(s0, acc0[r], y0[t][r]);
+          y1[t][r] = fmaf(s1, acc1[r], y1[t][r]);
         }
       }
     }
@@ -504,8 +601,10 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
               g += red[((w * NTL + t) * 16 + m) * 16 + n];
               u += red[((w * NTL + t + HALF) * 16 + m) * 16 + n];
             }
-            g += bias_at(16 * HALF * blk + j);
-            u += bias_at(a.I + 16 * HALF * blk + j);
+            if (has_bias) {
+              g += bst[j];
+              u += bst[16 * HALF + j];
+            }
             const float hv = g / (1.f + __expf(-g)) * u;
             ((uint16_t*)a.out)[(int64_t)(p0 + m) * a.som + 16 * HALF * blk + j] = (uint16_t)f32_to_bf16_bits(hv);
           }
@@ -517,8 +616,10 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
               g += red[((w * NTL + (rg >> 4)) * 16 + m) * 16 + (rg & 15)];
               u += red[((w * NTL + (ru >> 4)) * 16 + m) * 16 + (ru & 15)];
             }
-            g += bias_at(16 * NTL * blk + rg);
-            u += bias_at(16 * NTL * blk + ru);
+            if (has_bias) {
+              g += bst[rg];
+              u += bst[ru];
+            }
             const float hv = gptoss_glu(g, u, a.alpha, a.limit);
             ((uint16_t*)a.out)[(int64_t)(p0 + m) * a.som + 8 * NTL * blk + j] = (uint16_t)f32_to_bf16_bits(hv);
           }
@@ -526,8 +627,9 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
           const int t = j >> 4, n = j & 15;
           float v = 0.f;
           for (int w = 0; w < W; ++w) v += red[((w * NTL + t) * 16 + m) * 16 + n];
-          v += bias_at(16 * NTL * blk + j);
-          ((float*)a.out)[(int64_t)perm_at(p0 + m) * a.som + 16 * NTL * blk + j] = v;
+          if (has_bias) v += bst[j];
+          const int orow = p0 == beg ? prow[m] : perm_at(p0 + m);
+          ((float*)a.out)[(int64_t)orow * a.som + 16 * NTL * blk + j] = v;
         }
       }
     }
@@ -1004,10 +1106,10 @@ int dec_dn(const MoeDecArgs& a0, int64_t T, int64_t H, int max_lds, hipStream_t 
 #undef IMQ_DN
 }
 
-template <int S2, int NTL, int SDT, int MODE, bool XCL>
+template <int S2, int NTL, int SDT, int MODE, int XCL>
 int moe_line_launch(const MoeLineArgs& a, int W, int grid, hipStream_t st) {
   const size_t lds = (size_t)W * 2 * NTL * 16 * (S2 * ((SDT == IMQ_DT_FP32) ? 4 : 2) / 2) * 4 +
-                     (size_t)W * NTL * 256 * 4;
+                     (size_t)W * NTL * 256 * 4 + (size_t)NTL * 16 * 4 + 16 * 4;
   auto kern = moe_line_kernel<S2, NTL, SDT, MODE, XCL>;
   if (lds > 65536) {
     hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1040,12 +1142,20 @@ int moe_line_go(MoeLineArgs a, int rows, int64_t maxhit, int S2, int W, hipStrea
   // at most min(E, routed rows) experts are hit: no workgroups for items that cannot exist
   const int64_t items = (maxhit < a.E ? maxhit : (int64_t)a.E) * a.NB;
   if (items > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
-  if (a.xk < a.Kpad) {
-    if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, true>(a, W, (int)items, st);
-    return moe_line_launch<2, NTL, SDT, MODE, true>(a, W, (int)items, st);
+  // the kernel's 32-bit buffer offsets: into one expert's rows, and into the activation rows
+  // (hidden rows for gate_up, sorted h rows for down)
+  const int64_t xrows = MODE == 1 ? (int64_t)a.nrows : (int64_t)a.nrows / a.k;
+  if ((int64_t)rows * a.sqn > 0x7fffffff || (xrows * a.sxm + a.Kpad) * 2 > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
+  if (a.xk < a.Kpad && a.xk % 32 == 0) {
+    if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, 1>(a, W, (int)items, st);
+    return moe_line_launch<2, NTL, SDT, MODE, 1>(a, W, (int)items, st);
   }
-  if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, false>(a, W, (int)items, st);
-  return moe_line_launch<2, NTL, SDT, MODE, false>(a, W, (int)items, st);
+  if (a.xk < a.Kpad) {
+    if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, 2>(a, W, (int)items, st);
+    return moe_line_launch<2, NTL, SDT, MODE, 2>(a, W, (int)items, st);
+  }
+  if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, 0>(a, W, (int)items, st);
+  return moe_line_launch<2, NTL, SDT, MODE, 0>(a, W, (int)items, st);
 }
 
 template <int SDT, int MODE>
@@ -1125,7 +1235,7 @@ extern "C" int imq_moe_rows_w4(const void* x, int64_t x_row_stride, int64_t B, i
 }
 
 namespace {
-// Workspace layout: [gu fp32 B x 2I][h bf16 B x hw][z fp32 B x H][off int32 E+1][perm int32 B]
+// Workspace layout: [gu fp32 B x 2I][h bf16 B x hw][z fp32 B x H][off int32 E+1][perm int32 B+16]
 // [hit int32 E+1], each 256-byte aligned; hw = I_pad rounded up to a multiple of 256, the widest
 // down K_pad a kernel layout may use. The token-sorted path uses h, z, off, perm and hit; the
 // per-row path gu, h and z.
@@ -1143,7 +1253,7 @@ MoeWs moe_ws(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t 
   w.z = w.h + align_up(B * w.hw * 2, kAlign);
   w.off = w.z + align_up(B * H * 4, kAlign);
   w.perm = w.off + align_up((E + 1) * 4, kAlign);
-  w.hit = w.perm + align_up(B * 4, kAlign);
+  w.hit = w.perm + align_up((B + 16) * 4, kAlign);   // 16 spare entries: the line kernel's scalar reads
   // the register-B grouped GEMM's row group sums (groups of 128): hidden rows, then h rows
   w.rsx = w.hit + align_up((E + 1) * 4, kAlign);
   w.rsh = w.rsx + align_up(T * imq_cdiv(H, 128) * 4, kAlign);
