@@ -433,7 +433,7 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   }
   // ---- activations of the first pass, issued behind the weights so both arrive in one wait ----
   // Routed rows of the first pass, sorted positions beg .. beg + 15, with one scalar load (perm's
-  // workspace slot holds 16 spare entries past its B); lane i < 16 of sp holds row i and a lane
+  // workspace slot holds spare entries past its B); lane i < 16 of sp holds row i and a lane
   // picks its row with a cross-lane read. Placed after the weight loads, so that its wait (and
   // that for beg) does not hold them back.
   int sp = beg + (lane & 15);
@@ -1235,7 +1235,7 @@ extern "C" int imq_moe_rows_w4(const void* x, int64_t x_row_stride, int64_t B, i
 }
 
 namespace {
-// Workspace layout: [gu fp32 B x 2I][h bf16 B x hw][z fp32 B x H][off int32 E+1][perm int32 B+16]
+// Workspace layout: [gu fp32 B x 2I][h bf16 B x hw][z fp32 B x H][off int32 E+1][perm int32 B+64]
 // [hit int32 E+1], each 256-byte aligned; hw = I_pad rounded up to a multiple of 256, the widest
 // down K_pad a kernel layout may use. The token-sorted path uses h, z, off, perm and hit; the
 // per-row path gu, h and z.
@@ -1253,7 +1253,7 @@ MoeWs moe_ws(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t 
   w.z = w.h + align_up(B * w.hw * 2, kAlign);
   w.off = w.z + align_up(B * H * 4, kAlign);
   w.perm = w.off + align_up((E + 1) * 4, kAlign);
-  w.hit = w.perm + align_up((B + 16) * 4, kAlign);   // 16 spare entries: the line kernel's scalar reads
+  w.hit = w.perm + align_up((B + 64) * 4, kAlign);   // 64 spare entries: the kernels' scalar reads
   // the register-B grouped GEMM's row group sums (groups of 128): hidden rows, then h rows
   w.rsx = w.hit + align_up((E + 1) * 4, kAlign);
   w.rsh = w.rsx + align_up(T * imq_cdiv(H, 128) * 4, kAlign);

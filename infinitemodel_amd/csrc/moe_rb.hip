@@ -20,7 +20,8 @@ namespace {
 constexpr int kMoeRbMaxGroups = 40;
 template <int SDT, int IB, int MOE>
 constexpr size_t moe_rb_lds(int ng) {
-  return (size_t)3 * 32 * IB * RB_BK * 2 + (size_t)ng * 256 * 4 + (IMQ_MOE_RB_FOLD ? (size_t)ng * 32 * IB * 4 : 0);
+  return (size_t)3 * 32 * IB * RB_BK * 2 + (size_t)ng * 256 * 4 + (IMQ_MOE_RB_FOLD ? (size_t)ng * 32 * IB * 4 : 0) +
+         (size_t)32 * IB * 4;   // RID: the block's routed rows
 }
 template <int SDT, int IB, int MOE>
 int moe_rb_launch(const RbArgs& a, int64_t max_mt, hipStream_t st) {

@@ -230,6 +230,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   constexpr bool BUF = MOE == 0 && IMQ_RB_BUF;
   const uint16_t* xtile = a.x + (int64_t)m0 * a.sxm;
   int xo[XC], xl[XC];
+  // MoE forms: the block's routed rows RID[row] = perm[prow0 + row] (0 past cnt), staged in LDS by
+  // plan_a for the row-sum staging and down's scatter. A wave's lanes of chunk j cover 8
+  // consecutive rows, whose perm entries are one scalar load (the workspace keeps BM spare
+  // entries past perm's B): scalar loads count on lgkmcnt, so the gather's addresses do not wait
+  // behind the weight loads issued before them on the in-order vmcnt.
+  int* const RID = (int*)((char*)lds + (size_t)3 * A_EL * 2 + (size_t)(a.K >> a.gsh) * BN * 4 +
+                          (FOLD ? (size_t)(a.K >> a.gsh) * BM * 4 : 0));
   auto plan_a = [&]() {
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
@@ -239,8 +246,18 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
       if constexpr (MOE == 0) {
         r = m0 + row < a.M ? row : a.M - 1 - m0;
       } else {
-        const int p = prow0 + (row < cnt ? row : cnt - 1);                // sorted position
-        r = MOE == 3 ? p : a.perm[p] / a.k;           // down reads h in sorted order, gate_up gathers
+        typedef int32_t v8i __attribute__((ext_vector_type(8), aligned(4)));
+        // the wave's first row of chunk j (row = rb8 + lane / 8), uniform
+        const int rb8 = (64 * __builtin_amdgcn_readfirstlane(wave) + NTHR * j) >> 3;
+        const v8i pv = *(const __attribute__((address_space(4))) v8i*)(a.perm + prow0 + rb8);
+        int pr = pv[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) pr = (lane >> 3) == i ? pv[i] : pr;
+        const bool ok = row < cnt;
+        if (ch == 0) RID[row] = ok ? pr : 0;
+        // down reads h in sorted order (rows past cnt repeat the last), gate_up gathers hidden rows
+        // (rows past cnt read token 0; their results are never stored)
+        r = MOE == 3 ? prow0 + (ok ? row : cnt - 1) : (ok ? pr / a.k : 0);
       }
       xo[j] = ((int)(r * a.sxm) + ch * 8) * (BUF ? 2 : 1);   // BUF: bytes
       xl[j] = 2 * rb_swz(row, ch);                    // bytes
@@ -298,8 +315,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
             const int idx = base + u * NTHR + tid;
             const int id = idx < total ? idx : total - 1;
             const int row = id / ng, g = id - row * ng;   // consecutive threads: consecutive groups of a row
-            const int p = prow0 + (row < cnt ? row : cnt - 1);
-            const int rid = MOE == 3 ? p : a.perm[p] / a.k;
+            const int rid = MOE == 3 ? prow0 + (row < cnt ? row : cnt - 1) : RID[row] / a.k;
             v[u] = g < a.rs_groups ? a.rs[(int64_t)rid * a.rs_stride + g] : 0.f;
             at[u] = idx < total ? g * BM + row : -1;
           }
@@ -394,6 +410,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   };
   if constexpr (!EARLY) plan_a();
   if constexpr (MOE != 0 && !EARLY) {
+    lds_barrier();     // RID, read by the row-sum staging
     stage_moe();
     __syncthreads();   // the prologue's weight-set loads read pairs other threads staged
   }
@@ -692,6 +709,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     if (sz_vec) sz_store();
     else sz_scalar();
+    lds_barrier();     // RID, read by the row-sum staging
     stage_rs();
     __syncthreads();
     load_s(std::integral_constant<int, 0>{}, 0);
@@ -857,6 +875,12 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
       // segments to the routed rows (N % 64 == 0, so a segment lies wholly inside or past N)
       constexpr int YS = BN + 8;
       uint16_t* Yt = lds;              // every wave is past its last step and the correction
+      // this thread's routed rows, read before the row tile may overwrite RID
+      constexpr int NIT = BM * (BN / 8) / NTHR;
+      static_assert(BM * (BN / 8) % NTHR == 0, "whole row-tile passes");
+      int rr[NIT];
+#pragma unroll
+      for (int i = 0; i < NIT; ++i) rr[i] = RID[(tid + NTHR * i) / (BN / 8)];
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -871,11 +895,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
           }
       }
       __syncthreads();
-      for (int it = tid; it < BM * (BN / 8); it += NTHR) {
+#pragma unroll
+      for (int i = 0; i < NIT; ++i) {
+        const int it = tid + NTHR * i;
         const int row = it / (BN / 8), ch = it - row * (BN / 8);
         const int n = n0 + 8 * ch;
         if (row < cnt && n < a.N)
-          *(u32x4_t*)(a.yrb + (int64_t)a.perm[prow0 + row] * a.N + n) = *(const u32x4_t*)(Yt + row * YS + 8 * ch);
+          *(u32x4_t*)(a.yrb + (int64_t)rr[i] * a.N + n) = *(const u32x4_t*)(Yt + row * YS + 8 * ch);
       }
     } else {
 #pragma unroll
@@ -888,7 +914,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int m = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (m < cnt) a.yr[(int64_t)a.perm[prow0 + m] * a.N + n] = res(i, j)[r] + bn;
+            if (m < cnt) a.yr[(int64_t)RID[m] * a.N + n] = res(i, j)[r] + bn;
           }
       }
     }
