@@ -565,10 +565,10 @@ MOE_LAYERS = 16     # C5 T=1: 16 x 8 hit experts x 3.34 MB = 428 MB of distinct 
 
 def _moe_kernels(B: int, E: int, gK: int) -> str:
     """The kernels one imq_moe_experts_w4 call launches for B routed rows, E experts and gate_up
-    K_pad gK (the dispatch rule of moe.hip): direct decode when 4 B <= E; the register-B grouped
-    GEMM when B gK >= 32768 E (8192 E when gK > 2048: line kernel workgroups of more than 4
-    waves); the token-sorted line kernels between."""
-    if 4 * B <= E:
+    K_pad gK (the dispatch rule of moe.hip): direct decode when 4 B <= 5 E (7 E when gK > 2048:
+    line kernel workgroups of more than 4 waves); the register-B grouped GEMM when B gK >= 32768 E
+    (8192 E when gK > 2048); the token-sorted line kernels between."""
+    if 4 * B <= (7 if gK > 2048 else 5) * E:
         return "moe_gu_line_kernel + moe_dn_line_kernel (direct decode)"
     if B * gK >= (8192 if gK > 2048 else 32768) * E:
         return ("moe_sort_kernel (with the hidden rows' group sums) + gemm_rb_kernel MoE forms "

@@ -1436,9 +1436,11 @@ int moe_sorted(const MoeCall& c, char* ws, const MoeWs& L, hipStream_t st) {
   uint16_t* h = (uint16_t*)(ws + L.h);
   float* yr = (float*)(ws + L.z);
   // Decode: with few routed rows per expert there is little weight reuse to win by grouping, and
-  // the sort plus the off -> perm -> x dependent loads dominate; rows then run directly
-  // (routed order, one row per item, expert idx[b]).
-  const bool direct = B * 4 <= c.E;
+  // the sort and combine launches plus the item's dependent loads dominate; rows then run
+  // directly (routed order, one row per item, expert idx[b]) up to 1.25 routed rows per expert
+  // (1.75 where gate_up's K takes more than 4 waves and the token-sorted kernel runs one
+  // workgroup per CU): measured crossovers on MI355X at the OLMoE and gpt-oss-20b shapes.
+  const bool direct = B * 4 <= c.E * (gw > 4 ? 7 : 5);
   if (direct && line_ok && c.I % 16 == 0 && c.H % 16 == 0) {
     // two line-kernel launches: gate_up with the activation, down with the weighted combine
     MoeDecArgs gu{c.hidden, c.hs, (int)c.xk, (int)c.gK, (int)c.k, c.idx, c.topk_w, (int)c.E, c.gq, c.gqe, c.gqn,

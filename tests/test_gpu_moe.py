@@ -72,16 +72,18 @@ def test_moe_ragged_intermediate(dev):
     _run(dev, E=5, H=384, I=200, k=3, T=7, seed=3)
 
 
-@pytest.mark.parametrize("T", [1, 16])
+@pytest.mark.parametrize("T", [1, 10, 11, 16])
 def test_moe_olmoe_shape(dev, T):
-    """BASELINE C5: E=64, top-8, H=2048, I=1024."""
+    """BASELINE C5: E=64, top-8, H=2048, I=1024. T = 10 (80 routed rows, 1.25 per expert) is the
+    last decode-kernel call, T = 11 the first token-sorted one."""
     _run(dev, E=64, H=2048, I=1024, k=8, T=T, seed=3000)
 
 
-@pytest.mark.parametrize("T,k,E", [(1, 2, 8), (5, 2, 8), (64, 2, 4), (40, 3, 6)])
+@pytest.mark.parametrize("T,k,E", [(1, 2, 8), (9, 2, 8), (64, 2, 4), (40, 3, 6)])
 def test_moe_token_sorted_path(dev, T, k, E):
     """Shapes of the token-sorted grouped path (G 128, H and I_pad multiples of 256, I % 32 == 0):
-    one token, a few, and experts with more than 16 routed rows (several MFMA passes)."""
+    a few tokens, and experts with more than 16 routed rows (several MFMA passes); one token runs
+    the direct decode kernels."""
     _run(dev, E=E, H=512, I=256, k=k, T=T, seed=40 + T)
 
 
@@ -189,7 +191,7 @@ def _run_gptoss(dev, E, H, I, k, T, seed, bias_std=0.02, pad_to_256=False):
     return y, exact
 
 
-@pytest.mark.parametrize("T", [1, 5, 40])
+@pytest.mark.parametrize("T", [1, 9, 40])
 def test_gptoss_token_sorted(dev, T):
     """Token-sorted path (H, I multiples of 256): interleaved gate / up row pairs, biases."""
     _run_gptoss(dev, E=8, H=512, I=256, k=2, T=T, seed=70 + T)
@@ -292,11 +294,13 @@ def test_moe_unpadded_hidden_and_pad_codes(dev, kernel_layout):
     assert oq.max_rel(C.t2np(y_un), exact) <= MAX_REL
 
 
-@pytest.mark.parametrize("T", [1, 2])
-def test_gptoss_decode_gpt20b_widths(dev, T):
-    """Decode rows (4 B <= E) at gpt-oss-20b widths in the kernel layout (K 2880 padded to 3072):
-    the two-launch line path with unpadded hidden rows and h read as zero past I."""
-    _run_gptoss(dev, E=16, H=2880, I=2880, k=2, T=T, seed=95 + T, pad_to_256=True)
+@pytest.mark.parametrize("T,E,k", [(1, 16, 2), (2, 16, 2), (14, 32, 4), (15, 32, 4)])
+def test_gptoss_decode_gpt20b_widths(dev, T, E, k):
+    """Decode rows at gpt-oss-20b widths in the kernel layout (K 2880 padded to 3072): the
+    two-launch line path with unpadded hidden rows and h read as zero past I. At E = 32, top-4,
+    T = 14 (56 routed rows, 1.75 per expert) is the last decode-kernel call, T = 15 the first
+    token-sorted one."""
+    _run_gptoss(dev, E=E, H=2880, I=2880, k=k, T=T, seed=95 + T, pad_to_256=True)
 
 
 @pytest.mark.parametrize("sdt", ["bf16", "fp16", "fp32"])
