@@ -98,10 +98,19 @@ struct RbArgs {
   int xk = 0;
 };
 
-IMQ_DEV float rb_bias(const void* p, int dt, int64_t i) {
-  if (dt == IMQ_DT_FP32) return ((const float*)p)[i];
-  if (dt == IMQ_DT_FP16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
-  return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+// Bias element i as the raw aligned dword holding it (which lies in the element's page), read
+// without a branch so it can go out with the first loads (a null bias reads `fb`'s first word);
+// rb_bias_of converts it where it is used.
+IMQ_DEV uint32_t rb_bias_word(const void* p, int dt, int64_t i, const void* fb, bool& hi) {
+  const char* b = p != nullptr ? (const char*)p : (const char*)fb;
+  const int64_t off = p != nullptr ? i * (dt == IMQ_DT_FP32 ? 4 : 2) : 0;
+  const int mis = (int)(((uintptr_t)b + (uintptr_t)off) & 3);
+  hi = mis != 0;
+  return *(const uint32_t*)(b + off - mis);
+}
+IMQ_DEV float rb_bias_of(uint32_t w, bool hi, int dt) {
+  const uint32_t h = hi ? (w >> 16) : (w & 0xffffu);
+  return dt == IMQ_DT_FP32 ? __uint_as_float(w) : dt == IMQ_DT_FP16 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
 }
 
 IMQ_DEV int rb_swz(int row, int c) { return (row * 8 + (c ^ ((row >> 1) & 7))) * 8; }
@@ -218,6 +227,24 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
     cnt = ec >> 16;
     prow0 = a.mtl[2 * mt + 1];
     n0 = tn * BN;
+  }
+  // MoE forms: the epilogue's row biases of this lane (MOE 1: gate and up column; MOE 2: the gate
+  // / up pair of both column blocks; MOE 3: both column blocks), read before the K loop
+  constexpr int NBW = MOE == 2 ? 4 : 2;
+  uint32_t bw_w[NBW];
+  bool bw_h[NBW];
+  if constexpr (MOE != 0) {
+#pragma unroll
+    for (int q = 0; q < NBW; ++q) {
+      int row;
+      if constexpr (MOE == 1) {
+        row = (q ? a.I : 0) + tn * (32 * NW) + 32 * (tid >> 6) + (tid & 31);
+      } else {
+        const int n = n0 + 64 * (tid >> 6) + 32 * (MOE == 2 ? q >> 1 : q) + (tid & 31) + (MOE == 2 ? (q & 1) : 0);
+        row = n < a.N ? n : a.N - 1;
+      }
+      bw_w[q] = rb_bias_word(a.bias, a.bdt, (int64_t)e * a.sbe + row, a.q, bw_h[q]);
+    }
   }
 
   // ---- activation load plan (32-bit offsets from the tile's first row); the MoE forms gather
@@ -806,9 +833,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
 
   // ---- epilogue: D lane l holds column l % 32, element r at row 8 (r / 4) + 4 (l / 32) + r % 4 ---
   if constexpr (MOE != 0) {
-    auto bias_at = [&](int row) -> float {
-      return a.bias != nullptr ? rb_bias(a.bias, a.bdt, (int64_t)e * a.sbe + row) : 0.f;
-    };
+    const bool has_bias = a.bias != nullptr;
+    auto bias_q = [&](int q) -> float { return has_bias ? rb_bias_of(bw_w[q], bw_h[q], a.bdt) : 0.f; };
     if constexpr (MOE == 1 || MOE == 2) {
       // h through LDS as [BM][HS] bf16 (rows padded against bank conflicts): the tile's 128 h
       // columns then leave as 16-byte row segments, and their sum per row (the bf16 values down
@@ -819,7 +845,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
       if constexpr (MOE == 1) {
         const int hc = 32 * wave + c;                   // tile-local h column; I % 128 == 0
         const int g = tn * (32 * NW) + hc;
-        const float bg = bias_at(g), bu = bias_at(a.I + g);
+        const float bg = bias_q(0), bu = bias_q(1);   // rows g, I + g
 #pragma unroll
         for (int i = 0; i < IB; ++i)
 #pragma unroll
@@ -833,7 +859,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
         for (int j = 0; j < 2; ++j) {
           const int n = n0 + 64 * wave + 32 * j + c;    // even lanes: gate rows, odd: the up rows
           const int hc = (64 * wave + 32 * j + c) >> 1;
-          const float bg = n < a.N ? bias_at(n) : 0.f, bu = n + 1 < a.N ? bias_at(n + 1) : 0.f;
+          const float bg = n < a.N ? bias_q(2 * j) : 0.f, bu = n + 1 < a.N ? bias_q(2 * j + 1) : 0.f;
 #pragma unroll
           for (int i = 0; i < IB; ++i)
 #pragma unroll
@@ -885,7 +911,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int col = 64 * wave + 32 * j + c;
-        const float bn = n0 + col < a.N ? bias_at(n0 + col) : 0.f;
+        const float bn = n0 + col < a.N ? bias_q(j) : 0.f;
 #pragma unroll
         for (int i = 0; i < IB; ++i)
 #pragma unroll
@@ -908,7 +934,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
       for (int j = 0; j < 2; ++j) {
         const int n = n0 + 64 * wave + 32 * j + c;
         if (n >= a.N) continue;
-        const float bn = bias_at(n);
+        const float bn = bias_q(j);
 #pragma unroll
         for (int i = 0; i < IB; ++i)
 #pragma unroll
