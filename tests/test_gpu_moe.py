@@ -97,10 +97,10 @@ def test_moe_token_sorted_scale_dtypes(dev, sdt):
     _run(dev, E=4, H=512, I=256, k=2, T=20, seed=9, sdt=sdt)
 
 
-@pytest.mark.parametrize("T", [256, 384])
+@pytest.mark.parametrize("T", [64, 256, 384])
 def test_moe_olmoe_shape_prefill(dev, T):
-    """BASELINE C5 at T = 256 (every expert hit, ~32 rows each: the token-sorted line kernels) and
-    T = 384 (~48 rows: the grouped GEMM)."""
+    """BASELINE C5 at T = 64 (~8 rows per expert: the token-sorted line kernels), T = 256 (every
+    expert hit, ~32 rows each) and T = 384 (~48 rows): the register-B grouped GEMM."""
     _run(dev, E=64, H=2048, I=1024, k=8, T=T, seed=3000)
 
 
