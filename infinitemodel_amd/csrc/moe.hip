@@ -321,10 +321,10 @@ IMQ_DEV u32x4_t moe_bload_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t s
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2));
 }
 
-// XCL: activation rows shorter than K (a.xk < a.Kpad), columns past xk read as zero. XCL 1
-// (xk % 32 == 0): a lane's 32 columns of one (line-step, half) lie all below xk or all past it,
-// and past it the lane reads its row's first 32 columns and zeroes them -- one address per 32
-// columns, the rest immediate offsets. XCL 2 (xk % 8 == 0): clamped and zeroed per 8 columns.
+// XCL: activation rows shorter than K (a.xk < a.Kpad), columns past xk read as zero. xk is a
+// multiple of 32 (H % 64 == 0 and I % 32 == 0 on this path): a lane's 32 columns of one
+// (line-step, half) lie all below xk or all past it, and past it the lane reads its row's first
+// 32 columns and zeroes them -- one address per 32 columns, the rest immediate offsets.
 template <int S2, int NTL, int SDT, int MODE, int XCL>
 __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -470,13 +470,9 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         int cb = xcol(i, h, 0) + zo;                   // the lane's 32 columns [cb, cb + 32)
-        if constexpr (XCL == 1) cb = xcol(i, h, 0) < a.xk ? cb : zo;
+        if constexpr (XCL != 0) cb = xcol(i, h, 0) < a.xk ? cb : zo;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          int col = cb + 8 * kk;
-          if constexpr (XCL == 2) col = col < a.xk ? col : a.xk - 8;
-          X[i][h][kk] = moe_bload(xrs, xo + 2 * (uint32_t)col, 0);
-        }
+        for (int kk = 0; kk < 4; ++kk) X[i][h][kk] = moe_bload(xrs, xo + 2 * (uint32_t)(cb + 8 * kk), 0);
       }
   };
   {
@@ -544,7 +540,7 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
         for (int kk = 0; kk < 4; ++kk) {
           u32x4_t v = X[i][h][kk];
           if constexpr (XCL != 0) {
-            if (!(xcol(i, h, XCL == 1 ? 0 : kk) < a.xk)) v = u32x4_t{0u, 0u, 0u, 0u};
+            if (!(xcol(i, h, 0) < a.xk)) v = u32x4_t{0u, 0u, 0u, 0u};
           }
           A[h][kk] = __builtin_bit_cast(bf16x8_t, permute_x8(v));
         }
@@ -1146,13 +1142,10 @@ int moe_line_go(MoeLineArgs a, int rows, int64_t maxhit, int S2, int W, hipStrea
   // (hidden rows for gate_up, sorted h rows for down)
   const int64_t xrows = MODE == 1 ? (int64_t)a.nrows : (int64_t)a.nrows / a.k;
   if ((int64_t)rows * a.sqn > 0x7fffffff || (xrows * a.sxm + a.Kpad) * 2 > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
-  if (a.xk < a.Kpad && a.xk % 32 == 0) {
+  if (a.xk < a.Kpad) {
+    if (a.xk % 32) return IMQ_ERR_UNSUPPORTED;      // not produced by this path (H % 64, I % 32)
     if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, 1>(a, W, (int)items, st);
     return moe_line_launch<2, NTL, SDT, MODE, 1>(a, W, (int)items, st);
-  }
-  if (a.xk < a.Kpad) {
-    if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, 2>(a, W, (int)items, st);
-    return moe_line_launch<2, NTL, SDT, MODE, 2>(a, W, (int)items, st);
   }
   if (S2 == 1) return moe_line_launch<1, NTL, SDT, MODE, 0>(a, W, (int)items, st);
   return moe_line_launch<2, NTL, SDT, MODE, 0>(a, W, (int)items, st);
