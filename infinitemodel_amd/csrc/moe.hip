@@ -372,9 +372,6 @@ __global__ __launch_bounds__(512) void moe_line_kernel(MoeLineArgs a) {
     if constexpr (MODE == 0) return (t < HALF) ? 16 * HALF * blk + 16 * t : a.I + 16 * HALF * blk + 16 * (t - HALF);
     else return 16 * NTL * blk + 16 * t;
   };
-  auto bias_at = [&](int row) -> float {
-    return a.bias != nullptr ? load_bias(a.bias, a.bdt, (int64_t)e * a.sbe + row) : 0.f;
-  };
   // ---- the item's row biases (one per row of the block), issued first: the epilogue reads them
   // from LDS instead of waiting on a load after the reduction ----
   // (unconditional: a load under a branch ends in a full wait where the paths join; without a
