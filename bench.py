@@ -105,6 +105,20 @@ def _mark():
     _lib.call("imq_probe_empty", 1, torch.cuda.current_stream().cuda_stream)
 
 
+def _w4_module_layout(lins):
+    """Give each int4 linear the packed layout the drop-in module binds (QuantLinear4 on ROCm:
+    line-tiled where the shape fits it, worker_quant._bind_group_rocm) and return the op that reads
+    it. The row-layout array is replaced, so the weights' footprint is unchanged."""
+    from infinitemodel_amd import ops
+    from infinitemodel_amd import worker_quant as wq
+    if not all(wq._W4_LINE_TILED and L.G == 128 and L.N % 16 == 0 and L.q.shape[1] % 128 == 0 and L.q.is_contiguous()
+               and L.s.dtype == L.z.dtype for L in lins):
+        return ops.linear_w4, "row"
+    for L in lins:
+        L.q = ops.w4_line_tile(L.q)
+    return ops.linear_w4_tiled, "line-tiled"
+
+
 def _time_steps(step, steps: int, warmup: int) -> float:
     """ms per step: warmup, then EXACTLY ``steps`` steps bracketed by a device synchronize and
     HIP events on the current stream (the stream the graph replays on). A marker kernel is
@@ -194,6 +208,7 @@ def bench_c2(args, dev):
     from infinitemodel_amd import ops, workloads as wl
     M = args.m or 1
     lins = wl.llama8b_stack(dev)
+    op, layout = _w4_module_layout(lins)
     x_in = wl.activations(M, 4096, 1, dev)
     x_dn = wl.activations(M, 14336, 2, dev)
     ys = {n: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for n, _, N in wl.LLAMA8B_PROJ}
@@ -201,7 +216,7 @@ def bench_c2(args, dev):
     for L in lins:
         kind = L.name.split(".")[1]
         x = x_dn if kind == "down" else x_in
-        launches.append(lambda L=L, x=x, y=ys[kind]: ops.linear_w4(x, L.q, L.G, (L.s, L.z), out=y))
+        launches.append(lambda L=L, x=x, y=ys[kind]: op(x, L.q, L.G, (L.s, L.z), out=y))
 
     def step():
         for fn in launches:
@@ -210,23 +225,27 @@ def bench_c2(args, dev):
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
     total = sum(L.algorithmic_bytes(M) for L in lins)
     per_launch_us = ms * 1e3 / len(lins)
-    roof = _hbm_roofline(_w4_decode_kernel(M), total / len(lins), per_launch_us, _traffic(f"c2_m{M}"))
+    roof = _hbm_roofline(_w4_decode_kernel(M, layout), total / len(lins), per_launch_us, _traffic(f"c2_m{M}"))
     cfg = {"workload": f"C2 llama-3-8b int4 g128 decode stack, 32 layers x (qkv, o, gate_up, down), M={M}",
            "layers": 32, "M": M, "launches_per_step": len(lins), "graph": not args.no_graph,
            "bytes_per_step": total, "distinct_bytes_per_step": total,
-           "weights": "int4 g128 asymmetric, bf16 scale/zero"}
+           "weights": "int4 g128 asymmetric, bf16 scale/zero", "packed_layout": layout}
     del lins
     torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_c2(args, M)
     return _line(round(total / (ms * 1e-3) / 1e9, 2), "GB/s", ms, args, cfg, roof, cpu)
 
 
-def _w4_decode_kernel(M: int) -> str:
-    """The kernels imq_linear_w4 runs for M decode rows at the C1 / C2 shapes (gemv.hip)."""
+def _w4_decode_kernel(M: int, layout: str = "row") -> str:
+    """The kernels the int4 decode entry runs for M decode rows at the C1 / C2 shapes (gemv.hip)."""
+    entry = "imq_linear_w4_tiled" if layout == "line-tiled" else "imq_linear_w4"
     if M <= 4:
-        return f"w4_line_kernel (imq_linear_w4, M={M})"
+        return f"w4_line_kernel ({entry}, M={M})"
+    if layout == "line-tiled":
+        return (f"w4_wsplit_kernel (gate_up) + w4_ksplit_kernel + splitk_rows_reduce_kernel (qkv, o, down) "
+                f"({entry}, M={M})")
     return (f"w4_wsplit_kernel (qkv, o, gate_up) + w4_ksplit_kernel + splitk_rows_reduce_kernel (down) "
-            f"(imq_linear_w4, M={M})")
+            f"({entry}, M={M})")
 
 
 def _cpu_int4_random(N, K, seed, G=128):
@@ -301,19 +320,21 @@ def bench_c1(args, dev):
     from infinitemodel_amd import ops, workloads as wl
     M = args.m or 1
     lins = [wl.rtn_int4_linear(4096, 4096, i, dev, name=f"c1.{i}") for i in range(64)]
+    op, layout = _w4_module_layout(lins)
     x = wl.activations(M, 4096, 0, dev)
     y = torch.empty((M, 4096), dtype=torch.bfloat16, device=dev)
 
     def step():
         for L in lins:
-            ops.linear_w4(x, L.q, 128, (L.s, L.z), out=y)
+            op(x, L.q, 128, (L.s, L.z), out=y)
 
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
     b = lins[0].algorithmic_bytes(M)
     us = ms * 1e3 / len(lins)
-    roof = _hbm_roofline(_w4_decode_kernel(M), b, us, _traffic(f"c1_m{M}"))
+    roof = _hbm_roofline(_w4_decode_kernel(M, layout), b, us, _traffic(f"c1_m{M}"))
     cfg = {"workload": f"C1 single int4 g128 linear {M}x4096->4096, {len(lins)} distinct copies per step",
-           "M": M, "launches_per_step": len(lins), "distinct_bytes_per_step": b * len(lins)}
+           "M": M, "launches_per_step": len(lins), "distinct_bytes_per_step": b * len(lins),
+           "packed_layout": layout}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path
@@ -431,7 +452,8 @@ def _c4_fused(quant: str, M: int, dev, steps: int, warmup: int, use_graph: bool 
         for j, (N, K) in enumerate(C4_SHAPES):
             if quant == "int4":
                 L = wl.rtn_int4_linear(N, K, 5000 + 2 * i + j, dev)
-                sets.append((N, K, lambda x, y, L=L: ops.linear_w4(x, L.q, 128, (L.s, L.z), out=y)))
+                op, _ = _w4_module_layout([L])
+                sets.append((N, K, lambda x, y, L=L, op=op: op(x, L.q, 128, (L.s, L.z), out=y)))
             else:
                 q, s = wl.int8_linear(N, K, 5000 + 2 * i + j, dev)
                 sets.append((N, K, lambda x, y, q=q, s=s: ops.linear_w8(x, q, s, out=y)))
@@ -751,6 +773,7 @@ def bench_ceiling(args, dev):
     from infinitemodel_amd import ops, workloads as wl
     pr = _Probe(dev)
     lins = wl.llama8b_stack(dev)
+    op, layout = _w4_module_layout(lins)
     kinds = [n for n, _, _ in wl.LLAMA8B_PROJ]
     tabs = [pr.buffers([L.q, L.s, L.z]) for L in lins]
     kind_of = [L.name.split(".")[1] for L in lins]
@@ -779,7 +802,7 @@ def bench_ceiling(args, dev):
         def dec(ids=ids, x=x, k=k):
             for i in ids:
                 L = lins[i]
-                ops.linear_w4(x, L.q, L.G, (L.s, L.z), out=ys[k])
+                op(x, L.q, L.G, (L.s, L.z), out=ys[k])
 
         d_us = t_us(dec, len(ids))
         b = wbytes[ids[0]]
@@ -794,7 +817,7 @@ def bench_ceiling(args, dev):
 
     def pass_decode():
         for L, k in zip(lins, kind_of):
-            ops.linear_w4(x_dn if k == "down" else x_in, L.q, L.G, (L.s, L.z), out=ys[k])
+            op(x_dn if k == "down" else x_in, L.q, L.G, (L.s, L.z), out=ys[k])
 
     ms_a = _time_steps(_graph_or_eager(pass_probe, g), args.steps, args.warmup)
     ms_c = _time_steps(_graph_or_eager(pass_decode, g), args.steps, args.warmup)

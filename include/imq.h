@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define IMQ_ABI_VERSION 7
+#define IMQ_ABI_VERSION 8
 
 #define IMQ_DT_BF16 0
 #define IMQ_DT_FP16 1
@@ -119,6 +119,30 @@ int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
                   int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
                   int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
                   int64_t workspace_bytes, void* stream);
+
+/* ---- line-tiled int4 weights ---------------------------------------------------------------------
+ * No counterpart in the reference: a device layout of the same bytes as a row-layout qweight
+ * [N, K_pad/2] (N a multiple of 16, K_pad of 256), permuted in 16-byte pieces so that the decode
+ * kernels' full-line weight loads read 256 contiguous bytes per 16 lanes instead of 8 partial
+ * 128-byte lines. In 16-row tile t the 2 KiB block of line-step l (bytes [128 l, 128 l + 128) of
+ * every row of the tile) sits at byte 2048 (t K_pad / 256 + l); its 16-byte slot 64 h + s (h 0..1,
+ * s 0..63) holds piece 4 (((s >> 3) & 1) ^ h) + (s >> 4) of tile row 8 h + (s & 7).
+ * imq_w4_line_tile / imq_w4_line_untile convert between the layouts, out of place (the tiled array
+ * is dense: N * K_pad / 2 bytes). imq_linear_w4_tiled takes the arguments of imq_linear_w4 and
+ * gives the same results bit for bit, with qweight tiled (q_row_stride = K_pad / 2, group_size
+ * 128); the decode line / wave-split / K-split kernels and both prefill GEMMs read the layout, and
+ * a call none of them takes returns IMQ_ERR_UNSUPPORTED. It serves the same reference operator as
+ * imq_linear_w4 (_w4a16_triton_op, worker_quant.py:1079-1225) for modules whose weights were
+ * tiled once at load. */
+int imq_w4_line_tile(const void* q_rows, int64_t q_row_stride, int64_t N, int64_t K_pad, void* q_tiled,
+                     void* stream);
+int imq_w4_line_untile(const void* q_tiled, int64_t N, int64_t K_pad, void* q_rows, int64_t q_row_stride,
+                       void* stream);
+int imq_linear_w4_tiled(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad, const void* qweight,
+                        int64_t q_row_stride, const void* scale, int64_t s_stride_n, int64_t s_stride_g,
+                        int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
+                        int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
+                        int64_t workspace_bytes, void* stream);
 
 /* int2 twin: replaces _w2a16_triton_op() (worker_quant.py:1775-1918: `_ksk2`, `_k2`).
  * K_pad = 4 * qweight columns. */

@@ -31,7 +31,7 @@ bool rb_takes(int bits, int64_t M, int64_t N, int64_t K, int64_t G);
 int64_t rb_workspace_bytes(int bits, int64_t M, int64_t N, int64_t K, int cus);
 int gemm_rb(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
             const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg, int zdt,
-            int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
+            int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st, bool tiled);
 
 namespace {
 
@@ -188,8 +188,11 @@ IMQ_DEV u32x4_t weight_chunk(const WRegs<BITS, WC>& r, int c, float s, float nzs
 // matching up rows; h = silu(gate) * up written as bf16 in sorted order), MOE 2 gpt-oss gate_up
 // (consecutive interleaved rows, its clamped GLU), MOE 3 down (fp32 rows plus the row bias, in
 // routed order, for the combine).
-template <class C, int BITS, int SDT, int ZDT, int MOE = 0>
+// TL: the dense int4 form on weights in the line-tiled layout (a separate instantiation, so the
+// row-layout loop is unchanged).
+template <class C, int BITS, int SDT, int ZDT, int MOE = 0, bool TL = false>
 __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
+  static_assert(!TL || (MOE == 0 && BITS == 4), "line-tiled weights: the dense int4 form");
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, XC = C::XC, WC = C::WC;
   constexpr int BK = C::BK, CH = C::CH, KS = C::KS;
   constexpr int PD = 2;   // register sets of loaded-but-not-yet-stored steps
@@ -260,6 +263,18 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
   constexpr int BYTES_STEP = BK * BITS / 8;
   const uint8_t* wtile = MOE == 0 ? a.q + (int64_t)n0 * a.sqn : a.q + (int64_t)e * a.sqe;
   const int wo = (int)((gn - (MOE == 0 ? n0 : 0)) * a.sqn) + part * (WC * BITS / 8);
+  // line-tiled weights (dense int4, K steps of 64 codes = 32 bytes): the thread's bytes at
+  // 32 kt + o of tile-relative row rr sit at tile rr / 16, line-step kt / 4, half hr, slot
+  // (rr & 7) + 8 ((kt / 2 & 1) ^ hr) + 16 (2 (kt & 1) + o / 16), byte o & 15 of the piece: a
+  // thread offset for each value of (kt / 2) & 1 plus the step's uniform 2048 (kt / 4) + 512 (kt & 1)
+  int wta = 0, wtb = 0;
+  if constexpr (TL) {
+    static_assert(BK == 64 && WC * BITS / 8 <= 16, "a step's bytes of a row lie in two 16-byte pieces");
+    const int rr = gn - n0, hr = (rr >> 3) & 1, o = part * (WC * BITS / 8);
+    const int tb = (rr >> 4) * 16 * (int)a.sqn + 1024 * hr + 16 * (rr & 7) + 256 * (o >> 4) + (o & 15);
+    wta = tb + 128 * hr;
+    wtb = tb + 128 * (1 - hr);
+  }
   int bl[WC / 8];
 #pragma unroll
   for (int c = 0; c < WC / 8; ++c) bl[c] = swz<C>(wrow, (WC / 8) * part + c);
@@ -275,7 +290,10 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
     const int kt = kt0 + ktl;
 #pragma unroll
     for (int j = 0; j < XC; ++j) xr[set][j] = *(const u32x4_t*)(xtile + kt * BK + xo[j]);
-    load_w(wr[set], wtile + kt * BYTES_STEP + wo);
+    if constexpr (TL)
+      load_w(wr[set], wtile + (((kt >> 1) & 1) ? wtb : wta) + 2048 * (kt >> 2) + 512 * (kt & 1));
+    else
+      load_w(wr[set], wtile + kt * BYTES_STEP + wo);
     if constexpr (BITS != 8) {
       const int g = (kt * BK + WC * part) >> a.gsh;
       sraw[set] = load_raw_bits<SDT>(a.sc, sbase + g * ssg);
@@ -544,7 +562,7 @@ int64_t split_bytes(int64_t M, int64_t N, int64_t K, int cus, int* splits_out = 
   return (int64_t)s * M * N * 4;
 }
 
-template <class C, int BITS, int SDT, int ZDT>
+template <class C, int BITS, int SDT, int ZDT, bool TL = false>
 int launch_cfg(const GemmArgs& a0, void* ws, int64_t ws_bytes, hipStream_t st) {
   GemmArgs a = a0;
   a.tiles_m = (a.M + C::BM - 1) / C::BM;
@@ -559,7 +577,7 @@ int launch_cfg(const GemmArgs& a0, void* ws, int64_t ws_bytes, hipStream_t st) {
   a.kps = (KT + s - 1) / s;
   a.part = s > 1 ? (float*)ws : nullptr;
   if (T * s > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
-  auto kern = gemm_wq_kernel<C, BITS, SDT, ZDT>;
+  auto kern = gemm_wq_kernel<C, BITS, SDT, ZDT, 0, TL>;
   if (C::LDS > 65536) {
     static int attr_set = 0;   // benign race: every caller sets the same attribute value
     if (!__atomic_load_n(&attr_set, __ATOMIC_ACQUIRE)) {
@@ -588,10 +606,10 @@ using CfgSmall = Cfg<IMQ_GEMM_CFG_SMALL>;
 // do not fill the CUs.
 inline bool use_big(int64_t M) { return M > 128; }
 
-template <int BITS, int SDT, int ZDT>
+template <int BITS, int SDT, int ZDT, bool TL = false>
 int launch_gemm(const GemmArgs& a, void* ws, int64_t wsb, hipStream_t st) {
-  if (use_big(a.M)) return launch_cfg<CfgBig, BITS, SDT, ZDT>(a, ws, wsb, st);
-  return launch_cfg<CfgSmall, BITS, SDT, ZDT>(a, ws, wsb, st);
+  if (use_big(a.M)) return launch_cfg<CfgBig, BITS, SDT, ZDT, TL>(a, ws, wsb, st);
+  return launch_cfg<CfgSmall, BITS, SDT, ZDT, TL>(a, ws, wsb, st);
 }
 
 template <int BITS, int SDT>
@@ -716,9 +734,11 @@ int moe_gemm_w4(int mode, const uint16_t* x, int64_t sxm, int64_t xrows, int64_t
 // for shapes the tiled kernel does not cover (K not a multiple of 64, groups below 32 codes or
 // not a power of two, misaligned operands, offsets beyond 32 bits); the caller then uses the
 // generic kernel. Without a large enough workspace the launch does not split K.
-int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
-            const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-            int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
+namespace {
+int gemm_wq_any(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
+                const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
+                int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st,
+                bool tiled) {
   if (M <= 0 || N <= 0) return IMQ_OK;
   if (K % 64 != 0 || M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   int gsh = 0;
@@ -734,17 +754,46 @@ int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, cons
   const int wbytes = bits == 2 ? 8 : 16;
   if (((uintptr_t)q % wbytes) || (sqn % wbytes)) return IMQ_ERR_UNSUPPORTED;
   if (rb_takes(bits, M, N, K, G)) {
-    const int rc = gemm_rb(bits, x, sxm, M, K, q, sqn, sc, ssn, ssg, sdt, zr, szn, szg, zdt, N, G, y, sym, ws, wsb, st);
+    const int rc = gemm_rb(bits, x, sxm, M, K, q, sqn, sc, ssn, ssg, sdt, zr, szn, szg, zdt, N, G, y, sym, ws, wsb, st,
+                           tiled);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }
   GemmArgs a{x, sxm, (int)M, (int)K, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, gsh, y, sym, 0, 0, 1, 0,
              nullptr};
+  if (tiled) {   // line-tiled int4 weights: scale and zero of one dtype
+    if (bits != 4 || sdt != zdt) return IMQ_ERR_UNSUPPORTED;
+    switch (sdt) {
+      case IMQ_DT_BF16: return launch_gemm<4, IMQ_DT_BF16, IMQ_DT_BF16, true>(a, ws, wsb, st);
+      case IMQ_DT_FP16: return launch_gemm<4, IMQ_DT_FP16, IMQ_DT_FP16, true>(a, ws, wsb, st);
+      case IMQ_DT_FP32: return launch_gemm<4, IMQ_DT_FP32, IMQ_DT_FP32, true>(a, ws, wsb, st);
+    }
+    return IMQ_ERR_INVALID;
+  }
   switch (bits) {
     case 4: return gemm_bits<4>(a, sdt, zdt, ws, wsb, st);
     case 2: return gemm_bits<2>(a, sdt, zdt, ws, wsb, st);
     case 8: return gemm_bits<8>(a, sdt, zdt, ws, wsb, st);
   }
   return IMQ_ERR_INVALID;
+}
+}  // namespace
+
+int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
+            const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
+            int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
+  return gemm_wq_any(bits, x, sxm, M, K, q, sqn, sc, ssn, ssg, sdt, zr, szn, szg, zdt, N, G, y, sym, ws, wsb, st,
+                     false);
+}
+
+// int4 groups of 128 in the line-tiled layout (rows of K / 2 bytes, N a multiple of 16, K a
+// multiple of 256): the same kernels and results as gemm_wq on the row layout; shapes they
+// decline return IMQ_ERR_UNSUPPORTED (no row-layout fallback may read these bytes).
+int gemm_wq_tiled(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, const void* sc,
+                  int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg, int zdt, int64_t N,
+                  uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
+  if (N % 16 != 0 || K % 256 != 0) return IMQ_ERR_UNSUPPORTED;
+  return gemm_wq_any(4, x, sxm, M, K, q, K / 2, sc, ssn, ssg, sdt, zr, szn, szg, zdt, N, 128, y, sym, ws, wsb, st,
+                     true);
 }
 
 }  // namespace imq

@@ -26,7 +26,7 @@ inline void rb_plan(int64_t M, int64_t N, int64_t K, int cus, int* ib, int* spli
   *splits = s;
 }
 
-template <int BITS, int SDT, int ZDT, int IB>
+template <int BITS, int SDT, int ZDT, int IB, bool TL>
 int rb_launch(const RbArgs& a0, void* ws, int64_t wsb, hipStream_t st) {
   constexpr int NW = 4, BM = 32 * IB, BN = 64 * NW;
   RbArgs a = a0;
@@ -43,7 +43,7 @@ int rb_launch(const RbArgs& a0, void* ws, int64_t wsb, hipStream_t st) {
   a.part = s > 1 ? (float*)ws : nullptr;
   if (T * s > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   const size_t lds = (size_t)3 * BM * RB_BK * 2;
-  auto kern = gemm_rb_kernel<BITS, SDT, ZDT, IB, NW>;
+  auto kern = gemm_rb_kernel<BITS, SDT, ZDT, IB, NW, 0, 2, false, TL>;
   if (lds > 65536) {
     static int attr_set = 0;   // benign race: every caller sets the same value
     if (!__atomic_load_n(&attr_set, __ATOMIC_ACQUIRE)) {
@@ -58,12 +58,12 @@ int rb_launch(const RbArgs& a0, void* ws, int64_t wsb, hipStream_t st) {
   return IMQ_OK;
 }
 
-template <int BITS, int SDT, int ZDT>
+template <int BITS, int SDT, int ZDT, bool TL = false>
 int rb_ib_dispatch(const RbArgs& a, void* ws, int64_t wsb, hipStream_t st) {
   int ib, s;
   rb_plan(a.M, a.N, a.K, device_info().cus, &ib, &s);
-  if (ib == 8) return rb_launch<BITS, SDT, ZDT, 8>(a, ws, wsb, st);
-  return rb_launch<BITS, SDT, ZDT, 4>(a, ws, wsb, st);
+  if (ib == 8) return rb_launch<BITS, SDT, ZDT, 8, TL>(a, ws, wsb, st);
+  return rb_launch<BITS, SDT, ZDT, 4, TL>(a, ws, wsb, st);
 }
 
 template <int BITS, int SDT>
@@ -114,8 +114,9 @@ int64_t rb_workspace_bytes(int bits, int64_t M, int64_t N, int64_t K, int cus) {
 // (misaligned operands, offsets beyond 32 bits); the caller then uses the LDS-dequant GEMM.
 int gemm_rb(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
             const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg, int zdt,
-            int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
+            int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st, bool tiled) {
   if (((uintptr_t)x & 15) || (sxm & 7) || ((uintptr_t)q & 15) || (sqn & 15)) return IMQ_ERR_UNSUPPORTED;
+  if (tiled && (bits != 4 || N % 16 != 0 || K % 256 != 0 || sqn != K / 2)) return IMQ_ERR_UNSUPPORTED;
   if (sxm < 0 || sqn < 0 || 256 * sxm > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   // the kernel's buffer offsets from a tile's first row (activations, weights, scale / zero)
   if ((256 * sxm + K) * 2 > 0x7fffffff || 256 * sqn + K > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
@@ -127,6 +128,15 @@ int gemm_rb(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, cons
     if ((256 * ssn + ng * ssg) * 4 > 0x7fffffff || (256 * szn + ng * szg) * 4 > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   }
   RbArgs a{x, sxm, (int)M, (int)K, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, gsh, y, sym, 0, 0, 1, 0, nullptr};
+  if (tiled) {   // line-tiled int4 weights: scale and zero of one dtype
+    if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
+    switch (sdt) {
+      case IMQ_DT_BF16: return rb_ib_dispatch<4, IMQ_DT_BF16, IMQ_DT_BF16, true>(a, ws, wsb, st);
+      case IMQ_DT_FP16: return rb_ib_dispatch<4, IMQ_DT_FP16, IMQ_DT_FP16, true>(a, ws, wsb, st);
+      case IMQ_DT_FP32: return rb_ib_dispatch<4, IMQ_DT_FP32, IMQ_DT_FP32, true>(a, ws, wsb, st);
+    }
+    return IMQ_ERR_INVALID;
+  }
   switch (sdt) {
     case IMQ_DT_BF16: return bits == 8 ? rb_z<8, IMQ_DT_BF16>(a, zdt, ws, wsb, st) : rb_z<4, IMQ_DT_BF16>(a, zdt, ws, wsb, st);
     case IMQ_DT_FP16: return bits == 8 ? rb_z<8, IMQ_DT_FP16>(a, zdt, ws, wsb, st) : rb_z<4, IMQ_DT_FP16>(a, zdt, ws, wsb, st);

@@ -46,6 +46,7 @@ struct SkinnyArgs {
   int chunk_steps;   // K-steps staged in LDS at once
   const int8_t* q8;  // int8 weights (the int8 kernel; q is unused there)
   float* part;       // split-K partials [splits][M][N] fp32 (the K-split kernel)
+  int tiled;         // int4 weights in the line-tiled layout (line, K-split and wave-split kernels)
 };
 
 constexpr int kStep = 128;          // codes per K-step
@@ -446,6 +447,29 @@ IMQ_DEV float row_swap8(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
 }
 
+// Per-lane addresses of a 16-row tile's two full-line loads (rows 0-7 and rows 8-15 of the tile
+// at qt) for line-step 0, and the byte stride between line-steps. Row layout: lane (c, ar) reads
+// row c & 7 (+ 8 in the second load) at bytes 16 ar of the 128-byte line, + 64 (the line's second
+// group) for c >= 8 in the first load and c < 8 in the second; rows past N read the last row.
+// Line-tiled layout (a.tiled; N a multiple of 16, dense rows): those same pieces are stored in lane
+// order, one 1 KiB half per load of the tile's 2 KiB line-step block, so lane l reads bytes 16 l
+// and each 16-lane quarter of a load covers two whole 128-byte lines instead of eight partial ones.
+IMQ_DEV void line_bases(const SkinnyArgs& a, const uint8_t* qt, int lane, int rlast, const uint8_t*& q0,
+                        const uint8_t*& q1, int& lstride) {
+  if (a.tiled) {
+    q0 = qt + 16 * lane;
+    q1 = q0 + 1024;
+    lstride = 2048;
+    return;
+  }
+  const int c = lane & 15, ar = lane >> 4;
+  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
+  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
+  q0 = qt + rr0 * (int)a.sqn + 16 * ar + (c < 8 ? 0 : 64);
+  q1 = qt + rr1 * (int)a.sqn + 16 * ar + (c < 8 ? 64 : 0);
+  lstride = 128;
+}
+
 // LDS bytes of one wave's staging area / of a whole workgroup
 IMQ_HOST_DEV inline int line_wave_lds(int M, int S2, int vb) {
   return M * (S2 * kLine + 8) * 2 + 2 * S2 * 16 * 4 + 2 * 16 * S2 * vb / 2 * 4;
@@ -514,17 +538,17 @@ __global__ __launch_bounds__(64 * MAXW) void w4_line_kernel(SkinnyArgs a) {
   }
   // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
   const uint8_t* qt = a.q + (int64_t)row0 * a.sqn;
-  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
-  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
-  const uint8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
-  const uint8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  const uint8_t* q0;
+  const uint8_t* q1;
+  int lst;
+  line_bases(a, qt, lane, rlast, q0, q1, lst);
   u32x4_t wb[2 * S2];
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
     int l = ls0 + i;
     l = l < KL ? l : KL - 1;
-    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
-    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + lst * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + lst * l));
   }
   // 4) stage x (permuted to the unpack order) with its per-group sums, and scale/zero
 #pragma unroll
@@ -752,17 +776,17 @@ __global__ __launch_bounds__(64 * NW) void w4_ksplit_kernel(SkinnyArgs a) {
   }
   // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
   const uint8_t* qt = a.q + (int64_t)rowa * a.sqn;
-  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
-  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
-  const uint8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
-  const uint8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  const uint8_t* q0;
+  const uint8_t* q1;
+  int lst;
+  line_bases(a, qt, lane, rlast, q0, q1, lst);
   u32x4_t wb[2 * S2];
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
     int l = ls0 + i;
     l = l < KL ? l : KL - 1;
-    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
-    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + lst * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + lst * l));
   }
   // 4) stage x (permuted) with per-group row sums, and this wave's scale / zero words
 #pragma unroll
@@ -897,7 +921,9 @@ IMQ_HOST_DEV inline int wsplit_lds(int R, int NW) {
   return NW * (16 * (R * kLine + 8) * 2 + 2 * R * 16 * 4) + 2 * NW * 256 * 4 + kWsYB * 256 * 2;
 }
 
-template <int R, int SDT, int NW, int PD>
+// TL: weights in the line-tiled layout (a separate instantiation: the address selection sits in
+// the per-tile prefetch of the persistent loop)
+template <int R, int SDT, int NW, int PD, bool TL>
 __global__ __launch_bounds__(64 * NW) void w4_wsplit_kernel(SkinnyArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int XROW = R * kLine + 8;                // staged row stride (bf16 elements)
@@ -937,12 +963,22 @@ __global__ __launch_bounds__(64 * NW) void w4_wsplit_kernel(SkinnyArgs a) {
     const bool live = t <= tlast;
     const int row0 = t * 16;
     const int rlast = a.N - 1 - row0;
-    const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
-    const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
-    const int64_t qo = (int64_t)row0 * a.sqn + ls0 * 128 + 16 * ar;
-    const uint8_t* q0 = a.q + (live ? qo + rr0 * a.sqn + (lo8 ? 0 : 64) : 0);
-    const uint8_t* q1 = a.q + (live ? qo + rr1 * a.sqn + (lo8 ? 64 : 0) : 0);
-    const int ist = live ? 128 : 0;
+    const uint8_t* q0;
+    const uint8_t* q1;
+    int ist;
+    if constexpr (TL) {   // line-tiled: lane l reads bytes 16 l of each half of the 2 KiB block
+      const int64_t qo = (int64_t)row0 * a.sqn + ls0 * 2048 + 16 * lane;
+      q0 = a.q + (live ? qo : 0);
+      q1 = a.q + (live ? qo + 1024 : 0);
+      ist = live ? 2048 : 0;
+    } else {
+      const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
+      const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
+      const int64_t qo = (int64_t)row0 * a.sqn + ls0 * 128 + 16 * ar;
+      q0 = a.q + (live ? qo + rr0 * a.sqn + (lo8 ? 0 : 64) : 0);
+      q1 = a.q + (live ? qo + rr1 * a.sqn + (lo8 ? 64 : 0) : 0);
+      ist = live ? 128 : 0;
+    }
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       tl.w[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + ist * i));
@@ -2445,19 +2481,33 @@ int wsplit_launch(const SkinnyArgs& a, int R, const DevInfo& di, hipStream_t st)
   const int64_t T = (a.N + 15) / 16;
   const dim3 g((unsigned)(T < di.cus ? T : di.cus)), b(64 * kWsNW);
   const size_t lds = (size_t)wsplit_lds(R, kWsNW);
-  auto kern = R == 1 ? w4_wsplit_kernel<1, SDT, kWsNW, IMQ_WS_PD> : w4_wsplit_kernel<2, SDT, kWsNW, IMQ_WS_PD>;
-  static int attr_set[2] = {0, 0};   // benign race: every caller sets the same value
-  if (lds > 65536 && !__atomic_load_n(&attr_set[R - 1], __ATOMIC_ACQUIRE)) {
+  auto kern = a.tiled ? (R == 1 ? w4_wsplit_kernel<1, SDT, kWsNW, IMQ_WS_PD, true>
+                                 : w4_wsplit_kernel<2, SDT, kWsNW, IMQ_WS_PD, true>)
+                      : (R == 1 ? w4_wsplit_kernel<1, SDT, kWsNW, IMQ_WS_PD, false>
+                                : w4_wsplit_kernel<2, SDT, kWsNW, IMQ_WS_PD, false>);
+  static int attr_set[4] = {0, 0, 0, 0};   // benign race: every caller sets the same value
+  const int ai = 2 * a.tiled + R - 1;
+  if (lds > 65536 && !__atomic_load_n(&attr_set[ai], __ATOMIC_ACQUIRE)) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
-    __atomic_store_n(&attr_set[R - 1], 1, __ATOMIC_RELEASE);
+    __atomic_store_n(&attr_set[ai], 1, __ATOMIC_RELEASE);
   }
   kern<<<g, b, lds, st>>>(a);
   IMQ_LAUNCH_CHECK();
   return IMQ_OK;
 }
 
+// On line-tiled weights the wave-split kernel takes only grids of IMQ_WS_TILED_MIN_TILES row
+// tiles per CU and more; below that the K-split kernel is faster on them (measured, M = 8 / 16,
+// µs per linear: qkv 4096 -> 6144 8.1 / 9.1 against 9.3 / 9.9, o 4096 -> 4096 7.1 / 7.7 against
+// 7.9 / 8.3), while gate_up's 7 tiles per CU keep the wave-split kernel (16.6 / 17.3 against
+// 19.0 / 22.3).
+#ifndef IMQ_WS_TILED_MIN_TILES
+#define IMQ_WS_TILED_MIN_TILES 4
+#endif
+
 int wsplit_w4(const SkinnyArgs& a, int sdt, const DevInfo& di, hipStream_t st) {
+  if (a.tiled && (a.N + 15) / 16 < (int64_t)IMQ_WS_TILED_MIN_TILES * di.cus) return IMQ_ERR_UNSUPPORTED;
   const int R = wsplit_plan(a.M, a.Kpad, a.G, a.N, a.sqn, a.sxm, a.ssn, a.ssg, a.szn, a.szg, sdt, sdt, di.max_lds, di.cus);
   if (!R) return IMQ_ERR_UNSUPPORTED;
   switch (sdt) {
@@ -2491,9 +2541,14 @@ int64_t w4_decode_workspace_bytes(int64_t M, int64_t Kpad, int64_t G, int64_t N,
 
 // Fast path eligibility + launch. Returns IMQ_ERR_UNSUPPORTED when the caller must fall back.
 // ws / wsb: the caller's optional workspace (the K-split path of 4 < M <= 16 needs one).
+//
+// tiled: qweight is in the line-tiled layout (see line_bases); only the line, wave-split and K-split
+// kernels read it, so a call none of them takes returns IMQ_ERR_UNSUPPORTED and the caller must not
+// fall back to a row-layout kernel.
 int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st,
+              bool tiled) {
   if (M < 1 || M > 16 || G % kStep != 0 || Kpad % G != 0 || Kpad <= 0) return IMQ_ERR_UNSUPPORTED;
   if (((G / kStep) & (G / kStep - 1)) != 0) return IMQ_ERR_UNSUPPORTED;   // groups of 2^k steps
   if (((uintptr_t)q & 15) || (sqn & 15) || ((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
@@ -2501,6 +2556,7 @@ int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
   if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
   const DevInfo di = device_info();
   SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, 0};
+  a.tiled = tiled ? 1 : 0;
   if (((uintptr_t)sc & 3) == 0 && ((uintptr_t)zr & 3) == 0) {
     int rc = line_w4(a, sdt, di, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
@@ -2509,6 +2565,7 @@ int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
     rc = ksplit_w4(a, sdt, ws, wsb, di, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }
+  if (tiled) return IMQ_ERR_UNSUPPORTED;
   switch (sdt) {
     case IMQ_DT_BF16: return skinny_dispatch<IMQ_DT_BF16, IMQ_DT_BF16>(a, di, st);
     case IMQ_DT_FP16: return skinny_dispatch<IMQ_DT_FP16, IMQ_DT_FP16>(a, di, st);

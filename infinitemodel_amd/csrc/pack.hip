@@ -12,6 +12,8 @@
 // so that, as in torch, a -0.0 zero point (min exactly 0) keeps its sign.
 // Per-row symmetric (int8), in W's own dtype: scale = max(dt(amax|w| / 127), dt(1e-8)),
 // q = clamp(rint(dt(w / scale)), -127, 127) -- the quotient is rounded to dt before rint.
+#include <algorithm>
+
 #include "imq_common.h"
 
 namespace {
@@ -142,7 +144,73 @@ int pack_g(const void* W, int64_t sw, int wdt, int64_t N, int64_t in_f, int64_t 
   return IMQ_ERR_INVALID;
 }
 
+// Line-tiled int4 layout: in 16-row tile t, the 2 KiB block of line-step l (bytes [128 l, 128 l +
+// 128) of each row) lies at 2048 (KL t + l) (KL = K_pad / 256 line-steps per row); its half h
+// holds rows 8 h .. 8 h + 7 of the tile, and its 16-byte slot s (0..63) piece
+// 4 (((s >> 3) & 1) ^ h) + (s >> 4) of row 8 h + (s & 7). Slot (h, s) of a block <-> (row, piece):
+IMQ_DEV void tiled_slot_src(int h, int s, int& r, int& piece) {
+  r = 8 * h + (s & 7);
+  piece = 4 * (((s >> 3) & 1) ^ h) + (s >> 4);
+}
+
+// One thread per 16-byte piece of the tiled array (tile) or of the row array (untile); the write
+// side is the contiguous one. Pieces are 64-bit indexed.
+__global__ __launch_bounds__(256) void w4_tile_kernel(const uint8_t* __restrict__ src, int64_t srs, int64_t KL,
+                                                      int64_t pieces, uint8_t* __restrict__ dst) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * 256) {
+    const int s = (int)(i & 63), h = (int)((i >> 6) & 1);
+    const int64_t blk = i >> 7, t = blk / KL, l = blk - t * KL;
+    int r, piece;
+    tiled_slot_src(h, s, r, piece);
+    const u32x4_t v = *(const u32x4_t*)(src + (16 * t + r) * srs + 128 * l + 16 * piece);
+    *(u32x4_t*)(dst + 16 * i) = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void w4_untile_kernel(const uint8_t* __restrict__ src, int64_t KL, int64_t pieces,
+                                                        uint8_t* __restrict__ dst, int64_t drs) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * 256) {
+    // row-order piece i: row n, line-step l, piece p (8 per line)
+    const int p = (int)(i & 7);
+    const int64_t rl = i >> 3, n = rl / KL, l = rl - n * KL;
+    const int r = (int)(n & 15), h = r >> 3;
+    const int s = (r & 7) + 8 * ((p >> 2) ^ h) + 16 * (p & 3);
+    const int64_t j = (((n >> 4) * KL + l) * 2 + h) * 64 + s;
+    *(u32x4_t*)(dst + n * drs + 128 * l + 16 * p) = *(const u32x4_t*)(src + 16 * j);
+  }
+}
+
+int tile_args_ok(const void* a, const void* b, int64_t rs, int64_t N, int64_t K_pad) {
+  if (!a || !b || N < 0 || K_pad <= 0 || N % 16 != 0 || K_pad % 256 != 0 || rs < K_pad / 2) return IMQ_ERR_INVALID;
+  if (((uintptr_t)a & 15) || ((uintptr_t)b & 15) || (rs & 15)) return IMQ_ERR_ALIGN;
+  return IMQ_OK;
+}
+
 }  // namespace
+
+extern "C" int imq_w4_line_tile(const void* q_rows, int64_t q_row_stride, int64_t N, int64_t K_pad, void* q_tiled,
+                                void* stream) {
+  const int rc = tile_args_ok(q_rows, q_tiled, q_row_stride, N, K_pad);
+  if (rc != IMQ_OK || N == 0) return rc;
+  const int64_t pieces = N * (K_pad / 32);
+  const unsigned grid = (unsigned)std::min<int64_t>((pieces + 255) / 256, 65536);
+  w4_tile_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)q_rows, q_row_stride, K_pad / 256, pieces,
+                                                         (uint8_t*)q_tiled);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
+
+extern "C" int imq_w4_line_untile(const void* q_tiled, int64_t N, int64_t K_pad, void* q_rows, int64_t q_row_stride,
+                                  void* stream) {
+  const int rc = tile_args_ok(q_tiled, q_rows, q_row_stride, N, K_pad);
+  if (rc != IMQ_OK || N == 0) return rc;
+  const int64_t pieces = N * (K_pad / 32);
+  const unsigned grid = (unsigned)std::min<int64_t>((pieces + 255) / 256, 65536);
+  w4_untile_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)q_tiled, K_pad / 256, pieces,
+                                                           (uint8_t*)q_rows, q_row_stride);
+  IMQ_LAUNCH_CHECK();
+  return IMQ_OK;
+}
 
 extern "C" int imq_pack_w4(const void* W, int64_t w_row_stride, int w_dtype, int64_t N, int64_t in_features,
                            int64_t group_size, void* qweight, int64_t q_row_stride, void* scale, void* zero,

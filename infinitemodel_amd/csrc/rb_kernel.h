@@ -183,9 +183,12 @@ IMQ_DEV u32x4_t rb_convert8(uint32_t lo, uint32_t hi) {
 // 8-element chunk is permuted to the order the magic unpack produces. Every product is exact
 // and no weight is rounded to bf16, so the sums are within fp32 accumulation error of the exact
 // (q - z) s products (the dequantizing form rounds each weight to bf16 first).
-template <int BITS, int SDT, int ZDT, int IB, int NW, int MOE = 0, int PD = 2, bool FOLD = false>
+// TL: the dense int4 form on weights in the line-tiled layout (16-byte pieces permuted within
+// 16-row tiles), a separate instantiation so the row-layout loop is unchanged.
+template <int BITS, int SDT, int ZDT, int IB, int NW, int MOE = 0, int PD = 2, bool FOLD = false, bool TL = false>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   static_assert(!FOLD || (MOE != 0 && BITS == 4 && PD % 2 == 0), "the folded form: int4 MoE, even pipeline depth");
+  static_assert(!TL || (MOE == 0 && BITS == 4), "line-tiled weights: the dense int4 form");
   constexpr int BM = 32 * IB, BN = 64 * NW, BK = RB_BK, NTHR = 64 * NW;
   constexpr int A_EL = BM * BK;                    // bf16 elements of one LDS buffer
   constexpr int XC = BM * 8 / NTHR;                // 16-byte activation chunks per thread per step
@@ -295,6 +298,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   const uint8_t* qb[2];
   int64_t sb[2], zb[2];
   uint32_t qvo[2], svo[2], zvo[2];                  // BUF: byte offsets from the tile's rows
+  uint32_t qto[2][2] = {{0u, 0u}, {0u, 0u}};        // line-tiled weights: lane offsets by (kt / 2) & 1
   constexpr int SES = SDT == IMQ_DT_FP32 ? 4 : 2, ZES = ZDT == IMQ_DT_FP32 ? 4 : 2;
   const int gh = (32 * h) >> a.gsh;                 // the lane half's group within a step (groups < 64)
 #pragma unroll
@@ -307,6 +311,16 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
     qvo[j] = (uint32_t)((n - n0) * (int)a.sqn + (BITS == 8 ? 32 : 16) * h);
     svo[j] = (uint32_t)(((n - n0) * (int)a.ssn + gh * (int)a.ssg) * SES);
     zvo[j] = (uint32_t)(((n - n0) * (int)a.szn + gh * (int)a.szg) * ZES);
+    if constexpr (TL) {
+      // line-tiled weights: the lane's 16 bytes at byte 32 kt + 16 h of row n (tile-relative rr)
+      // sit at tile (rr / 16), line-step kt / 4, half hr = (rr / 8) & 1, slot (rr & 7) + 8 ((kt / 2
+      // & 1) ^ hr) + 16 (2 (kt & 1) + h): a lane offset for each value of (kt / 2) & 1 plus the
+      // step's uniform 2048 (kt / 4) + 512 (kt & 1)
+      const int rr = n - n0, hr = (rr >> 3) & 1;
+      const uint32_t tb = (uint32_t)((rr >> 4) * 16 * (int)a.sqn + 1024 * hr + 16 * (rr & 7) + 256 * h);
+      qto[j][0] = tb + 128 * hr;
+      qto[j][1] = tb + 128 * (1 - hr);
+    }
   }
   // (built unconditionally; the forms that do not use them drop them)
   const __amdgpu_buffer_rsrc_t xrs = rb_rsrc(xtile);
@@ -466,8 +480,12 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
       const uint32_t gs = (uint32_t)((kt * BK) >> a.gsh);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
+        if constexpr (TL) {
+          qr[set][j][0] = rb_bload128(qrs, ((kt >> 1) & 1) ? qto[j][1] : qto[j][0], 2048 * (kt >> 2) + 512 * (kt & 1));
+        } else {
 #pragma unroll
-        for (int v = 0; v < QV; ++v) qr[set][j][v] = rb_bload128(qrs, qvo[j] + 16 * v, kt * (BK * BITS / 8));
+          for (int v = 0; v < QV; ++v) qr[set][j][v] = rb_bload128(qrs, qvo[j] + 16 * v, kt * (BK * BITS / 8));
+        }
         if constexpr (BITS != 8) {
           sr[set][j] = rb_bload_raw<SDT>(srs, svo[j], gs * (uint32_t)a.ssg * SES);
           zr[set][j] = rb_bload_raw<ZDT>(zrs, zvo[j], gs * (uint32_t)a.szg * ZES);
@@ -477,8 +495,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
+      if constexpr (TL) {
+        qr[set][j][0] = *(const u32x4_t*)(a.q + (int64_t)n0 * a.sqn + (((kt >> 1) & 1) ? qto[j][1] : qto[j][0]) +
+                                          2048 * (kt >> 2) + 512 * (kt & 1));
+      } else {
 #pragma unroll
-      for (int v = 0; v < QV; ++v) qr[set][j][v] = *(const u32x4_t*)(qb[j] + kt * (BK * BITS / 8) + 16 * v);
+        for (int v = 0; v < QV; ++v) qr[set][j][v] = *(const u32x4_t*)(qb[j] + kt * (BK * BITS / 8) + 16 * v);
+      }
       if constexpr (MOE == 0 && BITS != 8) {
         const int g = (kt * BK + 32 * h) >> a.gsh;
         sr[set][j] = load_raw_bits<SDT>(a.sc, sb[j] + (int64_t)g * a.ssg);

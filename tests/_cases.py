@@ -85,3 +85,19 @@ def u8(a, device):
 def t2np(t):
     import torch
     return t.detach().to(torch.float32).cpu().numpy()
+
+
+def line_tile_np(q):
+    """The line-tiled int4 layout of a row-layout qweight u8 [N, Kpad/2] (N % 16 == 0, Kpad % 256
+    == 0), restated from its definition: in 16-row tile t the 2 KiB block of line-step l holds in
+    16-byte slot 64 h + s piece 4 (((s >> 3) & 1) ^ h) + (s >> 4) of tile row 8 h + (s & 7)."""
+    q = np.ascontiguousarray(q)
+    N, KB = q.shape
+    assert N % 16 == 0 and KB % 128 == 0
+    KL = KB // 128
+    pieces = q.reshape(N // 16, 16, KL, 8, 16)            # tile, row, line-step, piece, byte
+    out = np.empty((N // 16, KL, 2, 64, 16), dtype=np.uint8)
+    for h in range(2):
+        for s in range(64):
+            out[:, :, h, s] = pieces[:, 8 * h + (s & 7), :, 4 * (((s >> 3) & 1) ^ h) + (s >> 4)]
+    return out.reshape(N, KB)

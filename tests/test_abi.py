@@ -81,7 +81,7 @@ def test_exports_are_c_linkage():
 
 
 def test_abi_version_and_strerror(L):
-    assert L.imq_abi_version() == 7
+    assert L.imq_abi_version() == 8
     assert L.imq_strerror(0) == b"ok"
     for rc in (_lib.IMQ_ERR_INVALID, _lib.IMQ_ERR_UNSUPPORTED, _lib.IMQ_ERR_ALIGN, _lib.IMQ_ERR_SCRATCH):
         assert len(L.imq_strerror(rc)) > 5

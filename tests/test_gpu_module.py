@@ -33,8 +33,9 @@ def test_quantlinear4_binds_hip_op_and_matches(dev):
     from infinitemodel_amd import ops
     m, c = _q4(dev, 512, 1000, 3, bias=True)
     m.prepare_fused()
-    assert m._fused is not None and m._fused[2] is ops.linear_w4 and m._fused[3] == 1024
-    assert m.qweight.stride(0) == 512 + 64          # de-aliased rows (512-byte rows -> 576)
+    assert m._fused is not None and m._fused[2] is ops.linear_w4_tiled and m._fused[3] == 1024
+    assert m._line_tiled and m.qweight.is_contiguous() and m._fused[0] is m.qweight
+    assert np.array_equal(m.qweight.cpu().numpy(), C.line_tile_np(c["q"]))
     bias = C.t2np(m.bias)
     for shape in [(1, 1000), (2, 3, 1000), (16, 1000), (40, 1000)]:
         x = C.bf16_normal(C.rng(len(shape)), shape)
@@ -42,6 +43,42 @@ def test_quantlinear4_binds_hip_op_and_matches(dev):
         assert y.dtype == torch.bfloat16 and y.shape[:-1] == shape[:-1]
         ref = oq.linear_ref(x.reshape(-1, 1000), c["Wd"]) + bias
         assert oq.max_rel(C.t2np(y).reshape(-1, 512), ref) <= MAX_REL
+
+
+def test_quantlinear4_row_layout_when_tiling_is_off_or_does_not_fit(dev, monkeypatch):
+    """Row layout with de-aliased rows: the switch off, or rows not a multiple of 16."""
+    from infinitemodel_amd import ops
+    from infinitemodel_amd import worker_quant as wq
+    monkeypatch.setattr(wq, "_W4_LINE_TILED", False)
+    m, c = _q4(dev, 512, 1000, 3, bias=False)
+    m.prepare_fused()
+    assert m._fused[2] is ops.linear_w4 and not m._line_tiled
+    assert m.qweight.stride(0) == 512 + 64          # de-aliased rows (512-byte rows -> 576)
+    monkeypatch.setattr(wq, "_W4_LINE_TILED", True)
+    m2, c2 = _q4(dev, 40, 512, 4, bias=False)
+    m2.prepare_fused()
+    assert m2._fused[2] is ops.linear_w4 and not m2._line_tiled
+    x = C.bf16_normal(C.rng(9), (3, 512))
+    assert oq.max_rel(C.t2np(m2(C.to_torch(x, "bf16", dev))), oq.linear_ref(x, c2["Wd"])) <= MAX_REL
+
+
+def test_quantlinear4_line_tiled_state_dict_round_trip(dev):
+    """A line-tiled module saves qweight in the row layout, dequantizes bit-exactly, and a
+    row-layout state dict loaded after binding serves the new weights."""
+    import torch
+    m, c = _q4(dev, 256, 512, 11, bias=False)
+    m.prepare_fused()
+    assert m._line_tiled
+    sd = m.state_dict()
+    assert np.array_equal(sd["qweight"].cpu().numpy(), c["q"])
+    assert np.array_equal(C.t2np(m._dequant(torch.bfloat16)), c["Wd"])
+    c2 = C.int4_case(256, 512, 128, 12)
+    m.load_state_dict({"qweight": C.u8(c2["q"], "cpu"), "scale": C.to_torch(c2["s"], "bf16", "cpu"),
+                       "zero": C.to_torch(c2["z"], "bf16", "cpu")}, strict=False)
+    assert np.array_equal(m.state_dict()["qweight"].cpu().numpy(), c2["q"])
+    x = C.bf16_normal(C.rng(13), (5, 512))
+    y = m(C.to_torch(x, "bf16", dev))
+    assert oq.max_rel(C.t2np(y), oq.linear_ref(x, c2["Wd"])) <= MAX_REL
 
 
 def test_quantlinear4_fp16_activations(dev):
@@ -87,7 +124,7 @@ def test_quantlinear4_prefill_threshold_falls_through(dev):
     m._naive_m_min = 64
     w = m._dequant(torch.bfloat16)
     qw, pair, op, in_pad = m._fused
-    assert op is ops.linear_w4
+    assert op is ops.linear_w4_tiled and qw is m.qweight      # line-tiled binding
     for rows in (1, 16, 32, 33, 64, 100):
         x = C.to_torch(C.bf16_normal(C.rng(rows), (rows, 1000)), "bf16", dev)
         y = m(x)
