@@ -105,18 +105,27 @@ def _mark():
     _lib.call("imq_probe_empty", 1, torch.cuda.current_stream().cuda_stream)
 
 
-def _w4_module_layout(lins):
-    """Give each int4 linear the packed layout the drop-in module binds (QuantLinear4 on ROCm:
-    line-tiled where the shape fits it, worker_quant._bind_group_rocm) and return the op that reads
-    it. The row-layout array is replaced, so the weights' footprint is unchanged."""
+def _packed_module_layout(qs, bits: int, N_of, G: int):
+    """The packed layout the drop-in module binds for these weights (QuantLinear4 / QuantLinear2 on
+    ROCm: line-tiled where the shape fits it, worker_quant._bind_group_rocm): the weights to pass
+    (row-layout arrays replaced by their tiled copies, so the footprint is unchanged), the op that
+    reads them and the layout's name."""
     from infinitemodel_amd import ops
     from infinitemodel_amd import worker_quant as wq
-    if not all(wq._W4_LINE_TILED and L.G == 128 and L.N % 16 == 0 and L.q.shape[1] % 128 == 0 and L.q.is_contiguous()
-               and L.s.dtype == L.z.dtype for L in lins):
-        return ops.linear_w4, "row"
-    for L in lins:
-        L.q = ops.w4_line_tile(L.q)
-    return ops.linear_w4_tiled, "line-tiled"
+    fits = all(wq._LINE_TILED and G == (128 if bits == 4 else 64) and N_of(i) % 16 == 0 and q.shape[1] % 128 == 0
+               and q.is_contiguous() for i, q in enumerate(qs))
+    row_op = ops.linear_w4 if bits == 4 else ops.linear_w2
+    if not fits:
+        return list(qs), row_op, "row"
+    return [ops.line_tile(q) for q in qs], (ops.linear_w4_tiled if bits == 4 else ops.linear_w2_tiled), "line-tiled"
+
+
+def _w4_module_layout(lins):
+    """_packed_module_layout over int4 Linear4 records, in place."""
+    qs, op, layout = _packed_module_layout([L.q for L in lins], 4, lambda i: lins[i].N, lins[0].G if lins else 128)
+    for L, q in zip(lins, qs):
+        L.q = q
+    return op, layout
 
 
 def _time_steps(step, steps: int, warmup: int) -> float:
@@ -367,22 +376,30 @@ def bench_c3(args, dev):
         for j, (N, K) in enumerate(shapes):
             q, s, z = wl.int2_random_linear(N, K, 2000 + 2 * i + j, dev)
             sets.append((N, K, q, s, z))
+    qs, op, layout = _packed_module_layout([t[2] for t in sets], 2, lambda i: sets[i][0], 64)
+    sets = [(N, K, q, s, z) for (N, K, _, s, z), q in zip(sets, qs)]
     xs = {K: wl.activations(M, K, 7, dev) for _, K in shapes}
     ys = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for N, _ in shapes}
 
     def step():
         for N, K, q, s, z in sets:
-            ops.linear_w2(xs[K], q, 64, (s, z), out=ys[N])
+            op(xs[K], q, 64, (s, z), out=ys[N])
 
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
     nbytes = sum(q.numel() + s.numel() * 2 + z.numel() * 2 + M * K * 2 + M * N * 2 for N, K, q, s, z in sets)
     us = ms * 1e3 / len(sets)
-    kern = ("w2_line_kernel" if M <= 2 else "w2_ksplit_kernel + splitk_rows_reduce_kernel" if M <= 16
-            else "gemm_wq_kernel<2>")
-    roof = _hbm_roofline(f"{kern} (imq_linear_w2, M={M})", nbytes / len(sets), us, _traffic(f"c3_m{M}"))
+    entry = "imq_linear_w2_tiled" if layout == "line-tiled" else "imq_linear_w2"
+    if M == 2:   # the line kernel's 16 waves hold K 8192 at M = 2, not 28672
+        kern = "w2_line_kernel (8192->28672) + " + ("w2_ksplit_kernel + splitk_rows_reduce_kernel (28672->8192)"
+                                                    if layout == "line-tiled" else "w2_skinny_kernel (28672->8192)")
+    else:
+        kern = ("w2_line_kernel" if M == 1 else
+                "w2_ksplit_kernel + splitk_rows_reduce_kernel" if M <= 16 and (M > 4 or layout == "line-tiled") else
+                "w2_skinny_kernel" if M <= 16 else "gemm_wq_kernel<2>")
+    roof = _hbm_roofline(f"{kern} ({entry}, M={M})", nbytes / len(sets), us, _traffic(f"c3_m{M}"))
     cfg = {"workload": f"C3 int2 g64 70B shapes 8192->28672 and 28672->8192, M={M}, 8 copies each", "M": M,
            "launches_per_step": len(sets), "distinct_bytes_per_step": nbytes,
-           "weights": "int2 g64, fp16 scale ~U(0.005,0.05), zero ~U(0,3)"}
+           "weights": "int2 g64, fp16 scale ~U(0.005,0.05), zero ~U(0,3)", "packed_layout": layout}
     cpu = None
     if not args.no_cpu:
         from oracle import cpu_path

@@ -100,7 +100,9 @@ int imq_pack_w8(const void* W, int64_t w_row_stride, int w_dtype, int64_t N, int
  * K_pad) bytes, 16-byte aligned, contents need not be initialised. With it, prefill shapes whose
  * tiles do not fill the CUs split K across workgroups; a second launch sums the fp32 partials in
  * split order (deterministic). Calls that share a workspace must be ordered on one stream.
- * Without it (or when too small) K is not split. */
+ * Without it (or when too small) K is not split. The bound covers the decode K-split kernels too
+ * (4 < M <= 16; on line-tiled int2 weights also M 3..4 and the M <= 2 shapes too long in K for
+ * the int2 line kernel). */
 int64_t imq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K_pad);
 
 /* Workspace bytes imq_linear_w4 uses for exactly this call (the same arguments as imq_linear_w4,
@@ -120,25 +122,32 @@ int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
                   int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
                   int64_t workspace_bytes, void* stream);
 
-/* ---- line-tiled int4 weights ---------------------------------------------------------------------
+/* ---- line-tiled packed weights ------------------------------------------------------------------
  * No counterpart in the reference: a device layout of the same bytes as a row-layout qweight
- * [N, K_pad/2] (N a multiple of 16, K_pad of 256), permuted in 16-byte pieces so that the decode
- * kernels' full-line weight loads read 256 contiguous bytes per 16 lanes instead of 8 partial
- * 128-byte lines. In 16-row tile t the 2 KiB block of line-step l (bytes [128 l, 128 l + 128) of
- * every row of the tile) sits at byte 2048 (t K_pad / 256 + l); its 16-byte slot 64 h + s (h 0..1,
- * s 0..63) holds piece 4 (((s >> 3) & 1) ^ h) + (s >> 4) of tile row 8 h + (s & 7).
- * imq_w4_line_tile / imq_w4_line_untile convert between the layouts, out of place (the tiled array
- * is dense: N * K_pad / 2 bytes). imq_linear_w4_tiled takes the arguments of imq_linear_w4 and
- * gives the same results bit for bit, with qweight tiled (q_row_stride = K_pad / 2, group_size
- * 128); the decode line / wave-split / K-split kernels and both prefill GEMMs read the layout, and
- * a call none of them takes returns IMQ_ERR_UNSUPPORTED. It serves the same reference operator as
- * imq_linear_w4 (_w4a16_triton_op, worker_quant.py:1079-1225) for modules whose weights were
- * tiled once at load. */
-int imq_w4_line_tile(const void* q_rows, int64_t q_row_stride, int64_t N, int64_t K_pad, void* q_tiled,
-                     void* stream);
-int imq_w4_line_untile(const void* q_tiled, int64_t N, int64_t K_pad, void* q_rows, int64_t q_row_stride,
-                       void* stream);
+ * [N, row_bytes] (int4: row_bytes = K_pad / 2, int2: K_pad / 4; N a multiple of 16, row_bytes of
+ * 128), permuted in 16-byte pieces so that the decode kernels' full-line weight loads read 256
+ * contiguous bytes per 16 lanes instead of 8 partial 128-byte lines. In 16-row tile t the 2 KiB
+ * block of line-step l (bytes [128 l, 128 l + 128) of every row of the tile) sits at byte
+ * 2048 (t row_bytes / 128 + l); its 16-byte slot 64 h + s (h 0..1, s 0..63) holds piece
+ * 4 (((s >> 3) & 1) ^ h) + (s >> 4) of tile row 8 h + (s & 7).
+ * imq_line_tile / imq_line_untile convert between the layouts, out of place (the tiled array is
+ * dense: N * row_bytes bytes). imq_linear_w4_tiled / imq_linear_w2_tiled take the arguments of
+ * imq_linear_w4 / imq_linear_w2 and give the same results, with qweight tiled (q_row_stride =
+ * row_bytes; int4 groups of 128, int2 groups of 64); the decode line / wave-split / K-split kernels
+ * and the prefill GEMMs read the layout, and a call none of them takes returns
+ * IMQ_ERR_UNSUPPORTED. They serve the reference operators of imq_linear_w4 / _w2
+ * (_w4a16_triton_op, worker_quant.py:1079-1225; _w2a16_triton_op, 1775-1918) for modules whose
+ * weights were tiled once at load. */
+int imq_line_tile(const void* q_rows, int64_t q_row_stride, int64_t N, int64_t row_bytes, void* q_tiled,
+                  void* stream);
+int imq_line_untile(const void* q_tiled, int64_t N, int64_t row_bytes, void* q_rows, int64_t q_row_stride,
+                    void* stream);
 int imq_linear_w4_tiled(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad, const void* qweight,
+                        int64_t q_row_stride, const void* scale, int64_t s_stride_n, int64_t s_stride_g,
+                        int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
+                        int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+int imq_linear_w2_tiled(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad, const void* qweight,
                         int64_t q_row_stride, const void* scale, int64_t s_stride_n, int64_t s_stride_g,
                         int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
                         int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* workspace,

@@ -48,9 +48,12 @@ SIGNATURES = {
     "imq_linear_w4": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_int,
                                _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
                                _c_vp]),
-    "imq_w4_line_tile": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
-    "imq_w4_line_untile": (_c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]),
+    "imq_line_tile": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
+    "imq_line_untile": (_c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]),
     "imq_linear_w4_tiled": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_int,
+                                     _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
+                                     _c_vp]),
+    "imq_linear_w2_tiled": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_int,
                                      _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
                                      _c_vp]),
     "imq_linear_w4_noalloc": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64,

@@ -46,7 +46,7 @@ struct SkinnyArgs {
   int chunk_steps;   // K-steps staged in LDS at once
   const int8_t* q8;  // int8 weights (the int8 kernel; q is unused there)
   float* part;       // split-K partials [splits][M][N] fp32 (the K-split kernel)
-  int tiled;         // int4 weights in the line-tiled layout (line, K-split and wave-split kernels)
+  int tiled;         // weights in the line-tiled layout (int4 line / K-split / wave-split, int2 line / K-split)
 };
 
 constexpr int kStep = 128;          // codes per K-step
@@ -1490,17 +1490,17 @@ __global__ __launch_bounds__(64 * MAXW) void w2_line_kernel(SkinnyArgs a) {
            ls0 * (GPL * VB / 4), a.Kpad / 64 * VB / 4);
   // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
   const uint8_t* qt = a.q + (int64_t)row0 * a.sqn;
-  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
-  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
-  const uint8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
-  const uint8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  const uint8_t* q0;
+  const uint8_t* q1;
+  int lst;
+  line_bases(a, qt, lane, rlast, q0, q1, lst);
   u32x4_t wb[2 * S2];
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
     int l = ls0 + i;
     l = l < KL ? l : KL - 1;
-    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
-    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + lst * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + lst * l));
   }
   // 4) stage x (permute_x16 per pair) with per-group sums, and scale / zero words
 #pragma unroll
@@ -1664,17 +1664,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(IMQ_W2K
            ls0 * (GPL * VB / 4), a.Kpad / 64 * VB / 4);
   // 3) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
   const uint8_t* qt = a.q + (int64_t)rowa * a.sqn;
-  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
-  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
-  const uint8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
-  const uint8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  const uint8_t* q0;
+  const uint8_t* q1;
+  int lst;
+  line_bases(a, qt, lane, rlast, q0, q1, lst);
   u32x4_t wb[2 * S2];
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
     int l = ls0 + i;
     l = l < KL ? l : KL - 1;
-    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + 128 * l));
-    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + 128 * l));
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + lst * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + lst * l));
   }
   // 4) stage x (permute_x16 per pair) with per-group sums, and this wave's scale / zero words
 #pragma unroll
@@ -2398,7 +2398,9 @@ bool ksplit_plan(int64_t M, int64_t Kpad, int64_t G, int64_t N, int64_t sqn, int
 // Workspace bytes of the K-split decode path for this shape on the current device (0: the shape
 // does not use it).
 int64_t ksplit_workspace_bytes(int64_t M, int64_t N, int64_t Kpad) {
-  if (M <= 4 || M > 16 || N <= 0 || Kpad <= 0 || Kpad % kLine != 0) return 0;
+  if (M < 1 || M > 16 || N <= 0 || Kpad <= 0 || Kpad % kLine != 0) return 0;
+  // below 5 rows only line-tiled weights whose K exceeds the line kernel's 16 waves of 4 line-steps
+  if (M <= 4 && Kpad / kLine <= 64) return 0;
   int s2, nw;
   ksplit_shape(Kpad, N, device_info().cus, &s2, &nw);
   return (Kpad / kLine + s2 - 1) / s2 * M * N * 4;
@@ -2429,7 +2431,10 @@ int ksplit_dispatch(const SkinnyArgs& a, int nw, int s2, int splits, size_t lds,
 int ksplit_w4(const SkinnyArgs& a0, int sdt, void* ws, int64_t wsb, const DevInfo& di, hipStream_t st) {
   int splits, nw, s2;
   size_t lds;
-  if (!ksplit_plan(a0.M, a0.Kpad, a0.G, a0.N, a0.sqn, a0.sxm, a0.ssn, a0.ssg, a0.szn, a0.szg, sdt, sdt,
+  // line-tiled weights below 5 rows whose K the line kernel declines (the skinny kernel reads
+  // rows): the plan of 5 rows, whose LDS covers the staging of fewer
+  const int64_t pm = a0.tiled && a0.M < 5 ? 5 : a0.M;
+  if (!ksplit_plan(pm, a0.Kpad, a0.G, a0.N, a0.sqn, a0.sxm, a0.ssn, a0.ssg, a0.szn, a0.szg, sdt, sdt,
                    di.max_lds, di.cus, &splits, &nw, &s2, &lds))
     return IMQ_ERR_UNSUPPORTED;
   const int64_t need = (int64_t)splits * a0.M * a0.N * 4;
@@ -2543,8 +2548,9 @@ int64_t w4_decode_workspace_bytes(int64_t M, int64_t Kpad, int64_t G, int64_t N,
 // ws / wsb: the caller's optional workspace (the K-split path of 4 < M <= 16 needs one).
 //
 // tiled: qweight is in the line-tiled layout (see line_bases); only the line, wave-split and K-split
-// kernels read it, so a call none of them takes returns IMQ_ERR_UNSUPPORTED and the caller must not
-// fall back to a row-layout kernel.
+// kernels read it (the K-split kernel then also takes the M <= 4 calls the line kernel declines), so
+// a call none of them takes returns IMQ_ERR_UNSUPPORTED and the caller must not fall back to a
+// row-layout kernel.
 int skinny_w4(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
               int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st,
@@ -2777,7 +2783,10 @@ int ksplit2_launch(const SkinnyArgs& a, int splits, size_t lds, hipStream_t st) 
 int ksplit_w2(const SkinnyArgs& a0, int sdt, void* ws, int64_t wsb, const DevInfo& di, hipStream_t st) {
   int splits, nw;
   size_t lds;
-  if (!ksplit2_plan(a0.M, a0.Kpad, a0.G, a0.N, a0.sqn, a0.sxm, a0.ssn, a0.ssg, a0.szn, a0.szg, sdt, sdt,
+  // line-tiled weights below 5 rows (the line kernel declined: M 3..4, or K too long for its 16
+  // waves; the skinny kernel reads rows): the plan of 5 rows, whose LDS covers the staging of fewer
+  const int64_t pm = a0.tiled && a0.M < 5 ? 5 : a0.M;
+  if (!ksplit2_plan(pm, a0.Kpad, a0.G, a0.N, a0.sqn, a0.sxm, a0.ssn, a0.ssg, a0.szn, a0.szg, sdt, sdt,
                     di.max_lds, di.cus, &splits, &nw, &lds))
     return IMQ_ERR_UNSUPPORTED;
   const int64_t need = (int64_t)splits * a0.M * a0.N * 4;
@@ -2793,10 +2802,24 @@ int ksplit_w2(const SkinnyArgs& a0, int sdt, void* ws, int64_t wsb, const DevInf
   return IMQ_ERR_UNSUPPORTED;
 }
 
+// The int2 K-split kernel's partials [splits][M][N] where it may run: 4 < M <= 16, and on
+// line-tiled weights also M 3..4 and the M <= 2 shapes whose K is too long for the line kernel
+// (more than 16 waves of its line-steps).
+int64_t ksplit2_workspace_bytes(int64_t M, int64_t N, int64_t Kpad) {
+  if (M < 1 || M > 16 || N <= 0 || Kpad <= 0 || Kpad % kLine2 != 0) return 0;
+  const int64_t KL = Kpad / kLine2;
+  if (M <= 2 && (KL + (M == 1 ? 4 : 2) - 1) / (M == 1 ? 4 : 2) <= 16) return 0;
+  return (KL + kKs2S2 - 1) / kKs2S2 * M * N * 4;
+}
+
 // ws / wsb: the caller's optional workspace (the K-split path of 4 < M <= 16 needs one).
+// tiled: qweight in the line-tiled layout; only the line and K-split kernels read it (the K-split
+// kernel then also takes every M the line kernel declines), so a call neither takes returns
+// IMQ_ERR_UNSUPPORTED.
 int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st,
+              bool tiled) {
   if (M < 1 || M > 16 || G % kStep2 != 0 || Kpad % G != 0 || Kpad <= 0) return IMQ_ERR_UNSUPPORTED;
   if (((G / kStep2) & (G / kStep2 - 1)) != 0) return IMQ_ERR_UNSUPPORTED;   // groups of 2^k steps
   if (((uintptr_t)q & 15) || (sqn & 15) || ((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
@@ -2805,12 +2828,14 @@ int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
   if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
   const DevInfo di = device_info();
   SkinnyArgs a{x, sxm, (int)M, (int)Kpad, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, (int)G, y, sym, 0};
+  a.tiled = tiled ? 1 : 0;
   if (((uintptr_t)sc & 3) == 0 && ((uintptr_t)zr & 3) == 0) {
     int rc = line_w2(a, sdt, di, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
     rc = ksplit_w2(a, sdt, ws, wsb, di, st);
     if (rc != IMQ_ERR_UNSUPPORTED) return rc;
   }
+  if (tiled) return IMQ_ERR_UNSUPPORTED;
   switch (sdt) {
     case IMQ_DT_BF16: return w2_dispatch<IMQ_DT_BF16, IMQ_DT_BF16>(a, di, st);
     case IMQ_DT_FP16: return w2_dispatch<IMQ_DT_FP16, IMQ_DT_FP16>(a, di, st);

@@ -20,13 +20,15 @@ int64_t w4_decode_workspace_bytes(int64_t M, int64_t Kpad, int64_t G, int64_t N,
                                   int64_t ssn, int64_t ssg, int64_t szn, int64_t szg, int sdt, int zdt);
 int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uint8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
-              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
+              int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st,
+              bool tiled);
+int64_t ksplit2_workspace_bytes(int64_t M, int64_t N, int64_t Kpad);
 int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t* q, int64_t sqn,
               const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st);
 int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
             const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
             int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
-int gemm_wq_tiled(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, const void* sc,
+int gemm_wq_tiled(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, const void* sc,
                   int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg, int zdt, int64_t N,
                   uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
 int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
@@ -63,7 +65,9 @@ extern "C" int64_t imq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K_pa
   if (M < 0 || N < 0 || K_pad <= 0) return -1;
   const int64_t g = imq::gemm_workspace_bytes(M, N, K_pad);
   const int64_t d = imq::ksplit_workspace_bytes(M, N, K_pad);
-  return g > d ? g : d;
+  const int64_t d2 = imq::ksplit2_workspace_bytes(M, N, K_pad);
+  const int64_t gd = g > d ? g : d;
+  return gd > d2 ? gd : d2;
 }
 
 extern "C" int64_t imq_linear_w4_workspace_bytes(int64_t M, int64_t K_pad, int64_t N, int64_t group_size,
@@ -163,7 +167,33 @@ extern "C" int imq_linear_w4_tiled(const void* x, int64_t x_row_stride, int64_t 
     return imq::skinny_w4(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g, s_dtype,
                           zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, workspace,
                           workspace_bytes, st, true);
-  return imq::gemm_wq_tiled(xb, x_row_stride, M, K_pad, q, scale, s_stride_n, s_stride_g, s_dtype, zero,
+  return imq::gemm_wq_tiled(4, xb, x_row_stride, M, K_pad, q, scale, s_stride_n, s_stride_g, s_dtype, zero,
+                            z_stride_n, z_stride_g, z_dtype, N, yb, y_row_stride, workspace, workspace_bytes, st);
+}
+
+// int2 weights in the line-tiled layout: the arguments and results of imq_linear_w2 (N a multiple of
+// 16, dense rows of K_pad / 4 bytes, K_pad a multiple of 512, groups of 64); the decode line and
+// K-split kernels and the LDS-dequant GEMM read it, other calls return IMQ_ERR_UNSUPPORTED.
+extern "C" int imq_linear_w2_tiled(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
+                                   const void* qweight, int64_t q_row_stride, const void* scale,
+                                   int64_t s_stride_n, int64_t s_stride_g, int s_dtype, const void* zero,
+                                   int64_t z_stride_n, int64_t z_stride_g, int z_dtype, int64_t N,
+                                   int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+  int rc = check_g(2, x, x_row_stride, M, K_pad, qweight, q_row_stride, scale, s_dtype, zero, z_dtype, N,
+                   group_size, y, y_row_stride);
+  if (rc != IMQ_OK) return rc;
+  if (N % 16 != 0 || K_pad % 512 != 0 || group_size != 64 || q_row_stride != K_pad / 4) return IMQ_ERR_INVALID;
+  if (M == 0 || N == 0) return IMQ_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xb = (const uint16_t*)x;
+  uint16_t* yb = (uint16_t*)y;
+  const uint8_t* q = (const uint8_t*)qweight;
+  if (M <= 16)
+    return imq::skinny_w2(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g, s_dtype,
+                          zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, workspace,
+                          workspace_bytes, st, true);
+  return imq::gemm_wq_tiled(2, xb, x_row_stride, M, K_pad, q, scale, s_stride_n, s_stride_g, s_dtype, zero,
                             z_stride_n, z_stride_g, z_dtype, N, yb, y_row_stride, workspace, workspace_bytes, st);
 }
 
@@ -245,7 +275,7 @@ extern "C" int imq_linear_w2(const void* x, int64_t x_row_stride, int64_t M, int
   if (M <= 16) {
     rc = imq::skinny_w2(xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g, s_dtype,
                         zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride, workspace,
-                        workspace_bytes, st);
+                        workspace_bytes, st, false);
   } else {
     rc = imq::gemm_wq(2, xb, x_row_stride, M, K_pad, q, q_row_stride, scale, s_stride_n, s_stride_g,
                       s_dtype, zero, z_stride_n, z_stride_g, z_dtype, N, group_size, yb, y_row_stride,

@@ -144,10 +144,10 @@ int pack_g(const void* W, int64_t sw, int wdt, int64_t N, int64_t in_f, int64_t 
   return IMQ_ERR_INVALID;
 }
 
-// Line-tiled int4 layout: in 16-row tile t, the 2 KiB block of line-step l (bytes [128 l, 128 l +
-// 128) of each row) lies at 2048 (KL t + l) (KL = K_pad / 256 line-steps per row); its half h
-// holds rows 8 h .. 8 h + 7 of the tile, and its 16-byte slot s (0..63) piece
-// 4 (((s >> 3) & 1) ^ h) + (s >> 4) of row 8 h + (s & 7). Slot (h, s) of a block <-> (row, piece):
+// Line-tiled layout of packed weight rows (int4 / int2 codes alike: it moves bytes): in 16-row tile
+// t, the 2 KiB block of line-step l (bytes [128 l, 128 l + 128) of each row) lies at 2048 (KL t + l)
+// (KL = row bytes / 128); its half h holds rows 8 h .. 8 h + 7 of the tile, and its 16-byte slot s
+// (0..63) piece 4 (((s >> 3) & 1) ^ h) + (s >> 4) of row 8 h + (s & 7).
 IMQ_DEV void tiled_slot_src(int h, int s, int& r, int& piece) {
   r = 8 * h + (s & 7);
   piece = 4 * (((s >> 3) & 1) ^ h) + (s >> 4);
@@ -155,8 +155,8 @@ IMQ_DEV void tiled_slot_src(int h, int s, int& r, int& piece) {
 
 // One thread per 16-byte piece of the tiled array (tile) or of the row array (untile); the write
 // side is the contiguous one. Pieces are 64-bit indexed.
-__global__ __launch_bounds__(256) void w4_tile_kernel(const uint8_t* __restrict__ src, int64_t srs, int64_t KL,
-                                                      int64_t pieces, uint8_t* __restrict__ dst) {
+__global__ __launch_bounds__(256) void line_tile_kernel(const uint8_t* __restrict__ src, int64_t srs, int64_t KL,
+                                                        int64_t pieces, uint8_t* __restrict__ dst) {
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * 256) {
     const int s = (int)(i & 63), h = (int)((i >> 6) & 1);
     const int64_t blk = i >> 7, t = blk / KL, l = blk - t * KL;
@@ -167,8 +167,8 @@ __global__ __launch_bounds__(256) void w4_tile_kernel(const uint8_t* __restrict_
   }
 }
 
-__global__ __launch_bounds__(256) void w4_untile_kernel(const uint8_t* __restrict__ src, int64_t KL, int64_t pieces,
-                                                        uint8_t* __restrict__ dst, int64_t drs) {
+__global__ __launch_bounds__(256) void line_untile_kernel(const uint8_t* __restrict__ src, int64_t KL, int64_t pieces,
+                                                          uint8_t* __restrict__ dst, int64_t drs) {
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * 256) {
     // row-order piece i: row n, line-step l, piece p (8 per line)
     const int p = (int)(i & 7);
@@ -180,34 +180,35 @@ __global__ __launch_bounds__(256) void w4_untile_kernel(const uint8_t* __restric
   }
 }
 
-int tile_args_ok(const void* a, const void* b, int64_t rs, int64_t N, int64_t K_pad) {
-  if (!a || !b || N < 0 || K_pad <= 0 || N % 16 != 0 || K_pad % 256 != 0 || rs < K_pad / 2) return IMQ_ERR_INVALID;
+int tile_args_ok(const void* a, const void* b, int64_t rs, int64_t N, int64_t row_bytes) {
+  if (!a || !b || N < 0 || row_bytes <= 0 || N % 16 != 0 || row_bytes % 128 != 0 || rs < row_bytes)
+    return IMQ_ERR_INVALID;
   if (((uintptr_t)a & 15) || ((uintptr_t)b & 15) || (rs & 15)) return IMQ_ERR_ALIGN;
   return IMQ_OK;
 }
 
 }  // namespace
 
-extern "C" int imq_w4_line_tile(const void* q_rows, int64_t q_row_stride, int64_t N, int64_t K_pad, void* q_tiled,
-                                void* stream) {
-  const int rc = tile_args_ok(q_rows, q_tiled, q_row_stride, N, K_pad);
+extern "C" int imq_line_tile(const void* q_rows, int64_t q_row_stride, int64_t N, int64_t row_bytes, void* q_tiled,
+                             void* stream) {
+  const int rc = tile_args_ok(q_rows, q_tiled, q_row_stride, N, row_bytes);
   if (rc != IMQ_OK || N == 0) return rc;
-  const int64_t pieces = N * (K_pad / 32);
+  const int64_t pieces = N * (row_bytes / 16);
   const unsigned grid = (unsigned)std::min<int64_t>((pieces + 255) / 256, 65536);
-  w4_tile_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)q_rows, q_row_stride, K_pad / 256, pieces,
-                                                         (uint8_t*)q_tiled);
+  line_tile_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)q_rows, q_row_stride, row_bytes / 128, pieces,
+                                                           (uint8_t*)q_tiled);
   IMQ_LAUNCH_CHECK();
   return IMQ_OK;
 }
 
-extern "C" int imq_w4_line_untile(const void* q_tiled, int64_t N, int64_t K_pad, void* q_rows, int64_t q_row_stride,
-                                  void* stream) {
-  const int rc = tile_args_ok(q_tiled, q_rows, q_row_stride, N, K_pad);
+extern "C" int imq_line_untile(const void* q_tiled, int64_t N, int64_t row_bytes, void* q_rows, int64_t q_row_stride,
+                               void* stream) {
+  const int rc = tile_args_ok(q_tiled, q_rows, q_row_stride, N, row_bytes);
   if (rc != IMQ_OK || N == 0) return rc;
-  const int64_t pieces = N * (K_pad / 32);
+  const int64_t pieces = N * (row_bytes / 16);
   const unsigned grid = (unsigned)std::min<int64_t>((pieces + 255) / 256, 65536);
-  w4_untile_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)q_tiled, K_pad / 256, pieces,
-                                                           (uint8_t*)q_rows, q_row_stride);
+  line_untile_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((const uint8_t*)q_tiled, row_bytes / 128, pieces,
+                                                             (uint8_t*)q_rows, q_row_stride);
   IMQ_LAUNCH_CHECK();
   return IMQ_OK;
 }

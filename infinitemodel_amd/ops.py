@@ -226,50 +226,62 @@ def linear_w4(x, qweight, group_size: int, sz, out=None):
 
 
 def linear_w4_tiled(x, qweight_tiled, group_size: int, sz, out=None):
-    """``linear_w4`` on int4 weights in the line-tiled layout (``w4_line_tile``): the same results
+    """``linear_w4`` on int4 weights in the line-tiled layout (``line_tile``): the same results
     bit for bit. ``qweight_tiled`` is the dense u8 [N, Kpad/2] tiled array (N a multiple of 16,
     Kpad of 256, groups of 128); shapes no tiled-layout kernel takes raise ImqError."""
     if group_size != 128:
-        raise ValueError("the line-tiled layout is defined for groups of 128")
+        raise ValueError("line-tiled int4 weights take groups of 128")
     if not qweight_tiled.is_contiguous():
         raise ValueError("the line-tiled weight array must be dense")
     return _linear_g("imq_linear_w4_tiled", 2, x, qweight_tiled, group_size, sz, out)
 
 
-def _tile_shape_check(N: int, Kpad: int):
-    if N % 16 or Kpad % 256:
-        raise ValueError(f"the line-tiled layout needs N % 16 == 0 and K_pad % 256 == 0, got N={N}, K_pad={Kpad}")
+def linear_w2_tiled(x, qweight_tiled, group_size: int, sz, out=None):
+    """``linear_w2`` on int2 weights in the line-tiled layout (``line_tile``): the dense u8
+    [N, Kpad/4] tiled array (N a multiple of 16, Kpad of 512, groups of 64)."""
+    if group_size != 64:
+        raise ValueError("line-tiled int2 weights take groups of 64")
+    if not qweight_tiled.is_contiguous():
+        raise ValueError("the line-tiled weight array must be dense")
+    return _linear_g("imq_linear_w2_tiled", 4, x, qweight_tiled, group_size, sz, out)
 
 
-def w4_line_tile(qweight, out=None):
-    """Row-layout int4 qweight u8 [N, Kpad/2] -> the line-tiled layout (a new dense array, or
-    ``out``): in 16-row tile t the 2 KiB block of line-step l holds, in slot 64 h + s, 16-byte piece
-    4 (((s >> 3) & 1) ^ h) + (s >> 4) of tile row 8 h + (s & 7). No counterpart in the reference."""
+def _tile_shape_check(N: int, row_bytes: int):
+    if N % 16 or row_bytes % 128:
+        raise ValueError(f"the line-tiled layout needs N % 16 == 0 and row bytes % 128 == 0, got N={N}, "
+                         f"row bytes={row_bytes}")
+
+
+def line_tile(qweight, out=None):
+    """Row-layout packed weight u8 [N, row_bytes] (int4 or int2 codes) -> the line-tiled layout (a
+    new dense array, or ``out``): in 16-row tile t the 2 KiB block of line-step l holds, in slot
+    64 h + s, 16-byte piece 4 (((s >> 3) & 1) ^ h) + (s >> 4) of tile row 8 h + (s & 7). No
+    counterpart in the reference."""
     dev = _check_dev(qweight)
     _check_packed(qweight)
     N, KB = qweight.shape
-    _tile_shape_check(N, 2 * KB)
+    _tile_shape_check(N, KB)
     t = out if out is not None else torch.empty((N, KB), dtype=torch.uint8, device=dev)
     if tuple(t.shape) != (N, KB) or t.dtype != torch.uint8 or not t.is_contiguous():
         raise ValueError("out must be a dense u8 array of qweight's shape")
     with torch.cuda.device(dev):
-        call("imq_w4_line_tile", _ptr(qweight), qweight.stride(0), N, 2 * KB, _ptr(t), _stream(dev))
+        call("imq_line_tile", _ptr(qweight), qweight.stride(0), N, KB, _ptr(t), _stream(dev))
     return t
 
 
-def w4_line_untile(qweight_tiled, out=None):
-    """Inverse of ``w4_line_tile``: the row-layout u8 [N, Kpad/2] array (new, or ``out``)."""
+def line_untile(qweight_tiled, out=None):
+    """Inverse of ``line_tile``: the row-layout u8 [N, row_bytes] array (new, or ``out``)."""
     dev = _check_dev(qweight_tiled)
     _check_packed(qweight_tiled)
     if not qweight_tiled.is_contiguous():
         raise ValueError("the line-tiled weight array must be dense")
     N, KB = qweight_tiled.shape
-    _tile_shape_check(N, 2 * KB)
+    _tile_shape_check(N, KB)
     r = out if out is not None else torch.empty((N, KB), dtype=torch.uint8, device=dev)
     if tuple(r.shape) != (N, KB) or r.dtype != torch.uint8 or r.stride(1) != 1:
         raise ValueError("out must be a u8 array of qweight's shape with unit column stride")
     with torch.cuda.device(dev):
-        call("imq_w4_line_untile", _ptr(qweight_tiled), N, 2 * KB, _ptr(r), r.stride(0), _stream(dev))
+        call("imq_line_untile", _ptr(qweight_tiled), N, KB, _ptr(r), r.stride(0), _stream(dev))
     return r
 
 

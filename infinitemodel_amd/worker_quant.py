@@ -41,9 +41,9 @@ _FUSED_INT4 = os.environ.get("IM_FUSED_INT4", "1") != "0"
 _FUSED_W8A16 = os.environ.get("IM_FUSED_W8A16", "1") != "0"
 _FUSED_INT2 = os.environ.get("IM_FUSED_INT2", "1") != "0"
 _LARGE_M_NAIVE = os.environ.get("IM_LARGE_M_NAIVE", "1") != "0"
-# int4 modules on ROCm hold their packed weight in the line-tiled layout once bound (this build's
-# own switch, no counterpart in the reference; "0" keeps the row layout with de-aliased rows)
-_W4_LINE_TILED = os.environ.get("IM_W4_LINE_TILED", "1") != "0"
+# int4 / int2 modules on ROCm hold their packed weight in the line-tiled layout once bound (this
+# build's own switch, no counterpart in the reference; "0" keeps the row layout, de-aliased rows)
+_LINE_TILED = os.environ.get("IM_LINE_TILED", "1") != "0"
 
 # CPU-resident matmuls upcast to fp32 from this many activation rows (fp32 GEMM beats the bf16
 # GEMV once compute-bound); tune_cpu_threads lowers it to 1 on CPUs whose bf16 GEMM is unusable.
@@ -248,8 +248,14 @@ def _w4a16_hip_op():
 
 def _w4a16_tiled_hip_op():
     """``op(x[M,Kpad] bf16, qweight_tiled u8[N,Kpad/2], 128, (scale, zero) [N,ng]) -> y[M,N] bf16``
-    on weights in the line-tiled layout (ops.w4_line_tile)."""
+    on weights in the line-tiled layout (ops.line_tile)."""
     return _build_op("w4a16_tiled", _ops_attr("linear_w4_tiled"))
+
+
+def _w2a16_tiled_hip_op():
+    """``op(x[M,Kpad] bf16, qweight_tiled u8[N,Kpad/4], 64, (scale, zero) [N,ng]) -> y[M,N] bf16``
+    on weights in the line-tiled layout (ops.line_tile)."""
+    return _build_op("w2a16_tiled", _ops_attr("linear_w2_tiled"))
 
 
 def _w2a16_hip_op():
@@ -329,29 +335,33 @@ def _dealias_rows(qw):
 
 
 # ---- group-wise int4 / int2 linear modules ---------------------------------------------------
-def _line_tiling_fits(mod, in_pad: int) -> bool:
-    """Whether an int4 module's packed weight can take the line-tiled layout: groups of 128, rows
-    a multiple of 16, K_pad a multiple of 256, scale and zero of one dtype."""
-    return (_W4_LINE_TILED and mod.group_size == 128 and mod.qweight.shape[0] % 16 == 0 and in_pad % 256 == 0
-            and mod.qweight.shape[1] * 2 == in_pad and mod.scale.dtype == mod.zero.dtype)
+def _line_tiling_fits(mod, bits: int, in_pad: int) -> bool:
+    """Whether a group-wise module's packed weight can take the line-tiled layout: rows a multiple
+    of 16, dense rows of whole 128-byte line-steps (K_pad a multiple of 256 codes for int4, 512
+    for int2), the kernels' groups (128 for int4, 64 for int2), scale and zero of one dtype."""
+    cpb = 8 // bits
+    return (_LINE_TILED and mod.group_size == (128 if bits == 4 else 64) and mod.qweight.shape[0] % 16 == 0
+            and mod.qweight.shape[1] * cpb == in_pad and mod.qweight.shape[1] % 128 == 0
+            and mod.scale.dtype == mod.zero.dtype)
 
 
-def _bind_w4_tiled(mod, in_pad: int, tag: str) -> bool:
-    """Bind QuantLinear4 to the line-tiled kernels: tile the packed weight (a dense copy), check
+def _bind_line_tiled(mod, bits: int, in_pad: int, tag: str) -> bool:
+    """Bind QuantLinear4/2 to the line-tiled kernels: tile the packed weight (a dense copy), check
     the tiled op against the bf16 dequant at M 1 and 8, then replace ``qweight`` with the tiled
     array (the row-layout buffer is released; ``_dequant`` and ``state_dict`` convert back).
     False (module unchanged) when the tiled op is unavailable or fails the check."""
     import torch
     from . import ops
-    op = _w4a16_tiled_hip_op()
+    op = _w4a16_tiled_hip_op() if bits == 4 else _w2a16_tiled_hip_op()
     if op is None:
         return False
-    tiled = ops.w4_line_tile(mod.qweight)
+    tiled = ops.line_tile(mod.qweight)
     pair = (mod.scale, mod.zero)
-    rel, bad_m = _selfcheck_rel(lambda xk: op(xk, tiled, 128, pair), mod._dequant(torch.bfloat16),
+    G = mod.group_size
+    rel, bad_m = _selfcheck_rel(lambda xk: op(xk, tiled, G, pair), mod._dequant(torch.bfloat16),
                                 mod.in_features, in_pad, tiled.device)
     if bad_m:
-        _log(f"[{tag}] hip w4a16 (line-tiled) self-check rel={rel:.3f} at M={bad_m} -> row layout")
+        _log(f"[{tag}] hip w{bits}a16 (line-tiled) self-check rel={rel:.3f} at M={bad_m} -> row layout")
         return False
     mod.qweight = tiled
     mod._line_tiled = True
@@ -360,8 +370,8 @@ def _bind_w4_tiled(mod, in_pad: int, tag: str) -> bool:
 
 
 def _bind_group_rocm(mod, bits: int, tag: str) -> None:
-    """ROCm binding of QuantLinear4/2 (worker_quant.py:668-724): int4 weights that fit it take
-    the line-tiled layout; otherwise de-alias the packed rows, check the HIP op against the bf16
+    """ROCm binding of QuantLinear4/2 (worker_quant.py:668-724): weights that fit it take the
+    line-tiled layout; otherwise de-alias the packed rows, check the HIP op against the bf16
     dequant at M 1 and 8 and bind ``_fused``; then measure the prefill dispatch threshold. Raises
     on errors; the caller keeps the naive path."""
     import torch
@@ -370,7 +380,7 @@ def _bind_group_rocm(mod, bits: int, tag: str) -> None:
         return
     G = mod.group_size
     in_pad = mod.scale.shape[1] * G
-    if bits == 4 and _line_tiling_fits(mod, in_pad) and _bind_w4_tiled(mod, in_pad, tag):
+    if _line_tiling_fits(mod, bits, in_pad) and _bind_line_tiled(mod, bits, in_pad, tag):
         mod._naive_m_min = _bench_large_m_naive(mod, tag)
         return
     mod.qweight = _dealias_rows(mod.qweight)
@@ -443,7 +453,7 @@ def _tile_on_load(module, state_dict, prefix, local_metadata, strict, missing_ke
     if getattr(module, "_line_tiled", False) and incoming is not None and module.qweight is not None:
         from . import ops
         if tuple(incoming.shape) == tuple(module.qweight.shape):
-            state_dict[key] = ops.w4_line_tile(incoming.to(module.qweight.device))
+            state_dict[key] = ops.line_tile(incoming.to(module.qweight.device))
 
 
 def _make_group_linear_cls(bits: int):
@@ -462,7 +472,7 @@ def _make_group_linear_cls(bits: int):
             self.bias = bias
             self.in_features = in_features
             self.group_size = group_size
-            # a bound int4 module may hold qweight line-tiled (_line_tiled); state_dict and
+            # a bound module may hold qweight line-tiled (_line_tiled); state_dict and
             # load_state_dict keep the reference's row layout
             self._line_tiled = False
             self.register_state_dict_post_hook(_untile_on_save)
@@ -474,7 +484,7 @@ def _make_group_linear_cls(bits: int):
                 return self.qweight
             if self.qweight.is_cuda:
                 from . import ops
-                return ops.w4_line_untile(self.qweight)
+                return ops.line_untile(self.qweight)
             return _line_untile_torch(self.qweight)   # a tiled module moved off the GPU
 
         def _dequant(self, dtype):

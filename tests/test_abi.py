@@ -97,11 +97,16 @@ def test_moe_workspace_bytes(L):
 
 
 def test_linear_workspace_bytes_host_rules(L):
-    """Decode rows M <= 4 never split K (no workspace); 4 < M <= 16 split K into 1024-code chunks
-    (512-code chunks for grids of at most two 4-tile workgroups per CU, at the host's default 256
-    CUs) with fp32 partials [splits][M][N]; negative sizes are rejected."""
+    """Decode rows M <= 2 split K only where the int2 line kernel declines a line-tiled weight (K
+    beyond its 16 waves), M 3..4 only on line-tiled int2 weights (1024-code chunks); 4 < M <= 16 split K into 1024-code chunks (512-code chunks for grids
+    of at most two 4-tile workgroups per CU, at the host's default 256 CUs) with fp32 partials
+    [splits][M][N]; negative sizes are rejected."""
     assert L.imq_linear_workspace_bytes(1, 4096, 4096) == 0
-    assert L.imq_linear_workspace_bytes(4, 4096, 14336) == 0
+    assert L.imq_linear_workspace_bytes(2, 4096, 14336) == 0
+    assert L.imq_linear_workspace_bytes(4, 4096, 14336) == 14 * 4 * 4096 * 4
+    assert L.imq_linear_workspace_bytes(3, 4096, 14592) == 0      # K_pad % 512: no int2 K-split
+    assert L.imq_linear_workspace_bytes(2, 8192, 28672) == 28 * 2 * 8192 * 4   # int2 line kernel declines
+    assert L.imq_linear_workspace_bytes(1, 256, 16640) > 0        # int4 line kernel declines (65 line-steps)
     assert L.imq_linear_workspace_bytes(16, 4096, 14336) == 14 * 16 * 4096 * 4
     assert L.imq_linear_workspace_bytes(5, 6144, 4096) == 8 * 5 * 6144 * 4    # short grid: 512-code splits
     assert L.imq_linear_workspace_bytes(8, 96, 384) == 0          # K_pad % 256: skinny kernel

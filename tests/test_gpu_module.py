@@ -49,12 +49,12 @@ def test_quantlinear4_row_layout_when_tiling_is_off_or_does_not_fit(dev, monkeyp
     """Row layout with de-aliased rows: the switch off, or rows not a multiple of 16."""
     from infinitemodel_amd import ops
     from infinitemodel_amd import worker_quant as wq
-    monkeypatch.setattr(wq, "_W4_LINE_TILED", False)
+    monkeypatch.setattr(wq, "_LINE_TILED", False)
     m, c = _q4(dev, 512, 1000, 3, bias=False)
     m.prepare_fused()
     assert m._fused[2] is ops.linear_w4 and not m._line_tiled
     assert m.qweight.stride(0) == 512 + 64          # de-aliased rows (512-byte rows -> 576)
-    monkeypatch.setattr(wq, "_W4_LINE_TILED", True)
+    monkeypatch.setattr(wq, "_LINE_TILED", True)
     m2, c2 = _q4(dev, 40, 512, 4, bias=False)
     m2.prepare_fused()
     assert m2._fused[2] is ops.linear_w4 and not m2._line_tiled
@@ -151,8 +151,9 @@ def test_quantlinear2_module(dev):
     m = wq._quant2_linear_cls()(C.u8(c["q"], dev), C.to_torch(c["s"], "fp16", dev),
                                 C.to_torch(c["z"], "fp16", dev), None, 512, 64)
     m.prepare_fused()
-    assert m._fused is not None and m._fused[2] is ops.linear_w2
-    for M in (1, 8, 32):
+    assert m._fused is not None and m._fused[2] is ops.linear_w2_tiled and m._line_tiled   # line-tiled
+    assert np.array_equal(m.state_dict()["qweight"].cpu().numpy(), c["q"])
+    for M in (1, 3, 8, 32):
         x = C.bf16_normal(C.rng(M), (M, 512))
         y = m(C.to_torch(x, "bf16", dev))
         assert oq.max_rel(C.t2np(y), oq.linear_ref(x, c["Wd"])) <= MAX_REL

@@ -1,12 +1,16 @@
-"""GPU: the line-tiled int4 layout.
+"""GPU: the line-tiled layout of packed int4 / int2 weights.
 
-* imq_w4_line_tile / _untile against the layout's definition (tests/_cases.line_tile_np);
+* imq_line_tile / imq_line_untile against the layout's definition (tests/_cases.line_tile_np);
 * imq_linear_w4_tiled bit-identical to imq_linear_w4 on the row layout, for every kernel that
   reads the tiled layout: the decode line kernel (M 1-4, 2 and 4 line-steps per wave), the
   wave-split and K-split kernels (4 < M <= 16), the LDS-dequant GEMM (16 < M <= 512) and the
   register-B GEMM (M > 512, with and without K splits, ragged N). The kernels read the same bytes
   into the same lanes in both layouts, so equality is exact, not within a tolerance; the row-layout
-  results themselves are pinned against the oracle by the other parity tests.
+  results themselves are pinned against the oracle by the other parity tests;
+* imq_linear_w2_tiled likewise for the int2 line kernel (M 1-2), K-split kernel (4 < M <= 16) and
+  LDS-dequant GEMM (M > 16); where the int2 line kernel declines below 5 rows (M 3-4, or K beyond
+  its 16 waves) the tiled call runs the K-split kernel and the row layout the skinny kernel, so
+  those calls are checked against the oracle instead.
 """
 import numpy as np
 import pytest
@@ -26,10 +30,10 @@ def test_tile_and_untile_match_the_definition(dev, N, K):
     import torch
     from infinitemodel_amd import ops
     c, q, _, _ = _weights(dev, N, K, seed=N)
-    t = ops.w4_line_tile(q)
+    t = ops.line_tile(q)
     torch.cuda.synchronize()
     assert np.array_equal(t.cpu().numpy(), C.line_tile_np(c["q"]))
-    assert torch.equal(ops.w4_line_untile(t), q)
+    assert torch.equal(ops.line_untile(t), q)
 
 
 def test_tile_reads_strided_rows_and_untile_writes_them(dev):
@@ -38,10 +42,10 @@ def test_tile_reads_strided_rows_and_untile_writes_them(dev):
     c, q, _, _ = _weights(dev, 32, 512, seed=7)
     wide = torch.zeros((32, 256 + 48), dtype=torch.uint8, device=dev)
     wide[:, :256] = q
-    t = ops.w4_line_tile(wide[:, :256])
+    t = ops.line_tile(wide[:, :256])
     assert np.array_equal(t.cpu().numpy(), C.line_tile_np(c["q"]))
     back = torch.full((32, 256 + 32), 7, dtype=torch.uint8, device=dev)
-    ops.w4_line_untile(t, out=back[:, :256])
+    ops.line_untile(t, out=back[:, :256])
     assert torch.equal(back[:, :256], q) and bool((back[:, 256:] == 7).all())
 
 
@@ -73,7 +77,7 @@ def test_tiled_linear_is_bit_identical_to_the_row_layout(dev, N, K, M, dt):
     from infinitemodel_amd import ops
     _, q, s, z = _weights(dev, N, K, dt=dt, seed=N + K)
     x = torch.randn(M, K, generator=torch.Generator(device=dev).manual_seed(M + N), device=dev).to(torch.bfloat16)
-    t = ops.w4_line_tile(q)
+    t = ops.line_tile(q)
     y_row = ops.linear_w4(x, q, 128, (s, z))
     y_t = ops.linear_w4_tiled(x, t, 128, (s, z))
     torch.cuda.synchronize()
@@ -81,12 +85,32 @@ def test_tiled_linear_is_bit_identical_to_the_row_layout(dev, N, K, M, dt):
     assert bool(torch.isfinite(y_t.float()).all())
 
 
+@pytest.mark.parametrize("M", [1, 4])
+def test_tiled_rows_beyond_the_line_kernel_match_the_oracle(dev, M):
+    """K beyond the line kernel's 16 waves (K_pad 16640): the K-split kernel on tiled weights,
+    the skinny kernel on the row layout -- both against the oracle."""
+    import torch
+    from oracle import quant as oq
+    from infinitemodel_amd import ops
+    K = 16640
+    c = C.int4_random_case(256, K, 128, seed=21)
+    q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev), C.to_torch(c["z"], "bf16", dev)
+    x = C.bf16_normal(C.rng(M), (M, K))
+    t = ops.line_tile(q)
+    y = ops.linear_w4_tiled(C.to_torch(x, "bf16", dev), t, 128, (s, z))
+    y_row = ops.linear_w4(C.to_torch(x, "bf16", dev), q, 128, (s, z))
+    torch.cuda.synchronize()
+    ref = oq.linear_ref(x, oq.dequant_int4(c["q"], c["s"], c["z"], K, 128, "bf16"))
+    assert oq.max_rel(C.t2np(y), ref) <= 1e-2
+    assert oq.max_rel(C.t2np(y), C.t2np(y_row)) <= 1e-2
+
+
 def test_tiled_linear_repeats_bit_identically(dev):
     """Two calls in a row (split-K partials and the persistent kernels' LDS reused) agree."""
     import torch
     from infinitemodel_amd import ops
     _, q, s, z = _weights(dev, 4096, 14336, seed=3)
-    t = ops.w4_line_tile(q)
+    t = ops.line_tile(q)
     for M in (16, 1, 700):
         x = torch.randn(M, 14336, device=dev).to(torch.bfloat16)
         a = ops.linear_w4_tiled(x, t, 128, (s, z))
@@ -100,11 +124,11 @@ def test_tiled_shapes_outside_the_layout_are_rejected(dev):
     from infinitemodel_amd import ops
     from infinitemodel_amd._lib import ImqError
     with pytest.raises(ValueError):
-        ops.w4_line_tile(torch.zeros((40, 128), dtype=torch.uint8, device=dev))    # N % 16
+        ops.line_tile(torch.zeros((40, 128), dtype=torch.uint8, device=dev))    # N % 16
     with pytest.raises(ValueError):
-        ops.w4_line_tile(torch.zeros((32, 192), dtype=torch.uint8, device=dev))    # K_pad % 256
+        ops.line_tile(torch.zeros((32, 192), dtype=torch.uint8, device=dev))    # K_pad % 256
     _, q, s, z = _weights(dev, 64, 512, seed=1)
-    t = ops.w4_line_tile(q)
+    t = ops.line_tile(q)
     x = torch.zeros((1, 512), dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError):
         ops.linear_w4_tiled(x, t, 64, (s, z))                                        # groups of 128 only
@@ -115,3 +139,50 @@ def test_tiled_shapes_outside_the_layout_are_rejected(dev):
         call("imq_linear_w4_tiled", x.data_ptr(), 512, 1, 512, t.data_ptr(), 512, s.data_ptr(), s.stride(0), 1,
              IMQ_DT_BF16, z.data_ptr(), z.stride(0), 1, IMQ_DT_BF16, 64, 128, y.data_ptr(), 64, None, 0,
              torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _w2(dev, N, K, seed):
+    c = C.int2_random_case(N, K, 64, seed=seed, dt="fp16")
+    return c, C.u8(c["q"], dev), C.to_torch(c["s"], "fp16", dev), C.to_torch(c["z"], "fp16", dev)
+
+
+W2_CASES = [
+    pytest.param(4096, 8192, 1, id="w2-line-M1"),
+    pytest.param(1008, 4096, 2, id="w2-line-M2-ragged-tiles"),
+    pytest.param(4096, 8192, 5, id="w2-ksplit-M5"),
+    pytest.param(8192, 4096, 8, id="w2-ksplit-M8"),
+    pytest.param(1008, 8192, 16, id="w2-ksplit-M16"),
+    pytest.param(4096, 4096, 17, id="w2-gemm-M17"),
+    pytest.param(1008, 8192, 300, id="w2-gemm-M300"),
+    pytest.param(4096, 4096, 700, id="w2-gemm-M700"),
+]
+
+
+@pytest.mark.parametrize("N,K,M", W2_CASES)
+def test_tiled_int2_linear_is_bit_identical_to_the_row_layout(dev, N, K, M):
+    import torch
+    from infinitemodel_amd import ops
+    _, q, s, z = _w2(dev, N, K, seed=N + K)
+    x = torch.randn(M, K, generator=torch.Generator(device=dev).manual_seed(M), device=dev).to(torch.bfloat16)
+    t = ops.line_tile(q)
+    y_row = ops.linear_w2(x, q, 64, (s, z))
+    y_t = ops.linear_w2_tiled(x, t, 64, (s, z))
+    torch.cuda.synchronize()
+    assert torch.equal(y_t, y_row)
+
+
+@pytest.mark.parametrize("M,K", [(3, 4096), (4, 4096), (2, 28672), (1, 33792)])
+def test_tiled_int2_rows_without_a_line_kernel_match_the_oracle(dev, M, K):
+    """M 3..4, and M 1..2 with K beyond the line kernel's 16 waves: the K-split kernel."""
+    import torch
+    from oracle import quant as oq
+    from infinitemodel_amd import ops
+    c, q, s, z = _w2(dev, 1024, K, seed=77)
+    x = C.bf16_normal(C.rng(M), (M, K))
+    t = ops.line_tile(q)
+    y = ops.linear_w2_tiled(C.to_torch(x, "bf16", dev), t, 64, (s, z))
+    y_row = ops.linear_w2(C.to_torch(x, "bf16", dev), q, 64, (s, z))
+    torch.cuda.synchronize()
+    ref = oq.linear_ref(x, c["Wd"])
+    assert oq.max_rel(C.t2np(y), ref) <= 1e-2
+    assert oq.max_rel(C.t2np(y), C.t2np(y_row)) <= 1e-2
