@@ -120,6 +120,24 @@ def _packed_module_layout(qs, bits: int, N_of, G: int):
     return [ops.line_tile(q) for q in qs], (ops.linear_w4_tiled if bits == 4 else ops.linear_w2_tiled), "line-tiled"
 
 
+def _w8_module_layout(pairs):
+    """The int8 weights as the drop-in QuantLinear binds them: each (q, scale) goes through the
+    module's own binding (worker_quant._w8_binding, then the line-tiled layout when its op serves
+    every M). Returns the (q, scale) pairs to pass, the op that reads them and the layout's name."""
+    from infinitemodel_amd import ops
+    from infinitemodel_amd import worker_quant as wq
+    out, tiled = [], []
+    for q, s in pairs:
+        mod = wq._quant_linear_cls()(q, s, None)
+        mod.prepare_fused()
+        tiled.append(bool(getattr(mod, "_line_tiled", False)))
+        out.append((mod.qweight, s))
+        del mod
+    if all(tiled):
+        return out, ops.linear_w8_tiled, "line-tiled"
+    return [(ops.line_untile(q) if t else q, s) for (q, s), t in zip(out, tiled)], ops.linear_w8, "row"
+
+
 def _w4_module_layout(lins):
     """_packed_module_layout over int4 Linear4 records, in place."""
     qs, op, layout = _packed_module_layout([L.q for L in lins], 4, lambda i: lins[i].N, lins[0].G if lins else 128)
@@ -456,6 +474,7 @@ def _c4_module_path(quant: str, shapes, dev) -> dict:
 
 
 C4_SHAPES = [(14336, 4096), (4096, 14336)]
+_c4_layout = "row"   # the packed layout of the last _c4_fused call's weights
 
 
 def _c4_fused(quant: str, M: int, dev, steps: int, warmup: int, use_graph: bool = True):
@@ -469,11 +488,12 @@ def _c4_fused(quant: str, M: int, dev, steps: int, warmup: int, use_graph: bool 
         for j, (N, K) in enumerate(C4_SHAPES):
             if quant == "int4":
                 L = wl.rtn_int4_linear(N, K, 5000 + 2 * i + j, dev)
-                op, _ = _w4_module_layout([L])
+                op, layout = _w4_module_layout([L])
                 sets.append((N, K, lambda x, y, L=L, op=op: op(x, L.q, 128, (L.s, L.z), out=y)))
             else:
-                q, s = wl.int8_linear(N, K, 5000 + 2 * i + j, dev)
-                sets.append((N, K, lambda x, y, q=q, s=s: ops.linear_w8(x, q, s, out=y)))
+                pairs, op8, layout = _w8_module_layout([wl.int8_linear(N, K, 5000 + 2 * i + j, dev)])
+                q, s = pairs[0]
+                sets.append((N, K, lambda x, y, q=q, s=s, op8=op8: op8(x, q, s, out=y)))
     xs = {K: wl.activations(M, K, 9, dev) for _, K in C4_SHAPES}
     ys = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for N, _ in C4_SHAPES}
 
@@ -483,6 +503,8 @@ def _c4_fused(quant: str, M: int, dev, steps: int, warmup: int, use_graph: bool 
 
     ms = _time_steps(_graph_or_eager(step, use_graph), steps, warmup)
     flops = sum(2.0 * M * N * K for N, K, _ in sets)
+    global _c4_layout
+    _c4_layout = layout
     return ms, flops / (ms * 1e-3), sets, xs, ys
 
 
@@ -561,6 +583,7 @@ def bench_c4(args, dev):
     wbytes = sum(N * K * (0.53125 if args.quant == "int4" else 1.0) for N, K, _ in sets)
     cfg = {"workload": f"C4 prefill {args.quant} 4096->14336 and 14336->4096, M={M}", "M": M,
            "quant": args.quant, "launches_per_step": len(sets), "distinct_bytes_per_step": int(wbytes),
+           "packed_layout": _c4_layout,
            "naive": {"value": round(tf_naive / 1e12, 3), "unit": "TFLOP/s",
                      "path": "imq dequant to bf16 + F.linear (hipBLASLt), both shapes, eager",
                      "fused_speedup": round(tf / tf_naive, 3)},
@@ -707,19 +730,21 @@ def bench_head(args, dev):
     from infinitemodel_amd import ops, workloads as wl
     M = args.m or 1
     N, K = 152064, 3584
-    heads = [wl.int8_linear(N, K, 17 + i, dev, dtype=torch.bfloat16) for i in range(2)]
+    heads, op, layout = _w8_module_layout([wl.int8_linear(N, K, 17 + i, dev, dtype=torch.bfloat16) for i in range(2)])
     x = wl.activations(M, K, 18, dev)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
 
     def step():
         for q, s in heads:
-            ops.linear_w8(x, q, s, out=y)
+            op(x, q, s, out=y)
 
     ms = _time_steps(_graph_or_eager(step, not args.no_graph), args.steps, args.warmup)
     nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
-    roof = _hbm_roofline("imq_linear_w8 decode kernel", nbytes, ms * 1e3 / len(heads), _traffic(f"head_m{M}"))
+    entry = "imq_linear_w8_tiled" if layout == "line-tiled" else "imq_linear_w8"
+    roof = _hbm_roofline(f"{'w8_line_kernel' if M <= 4 else 'w8_skinny_kernel'} ({entry}, M={M})", nbytes,
+                         ms * 1e3 / len(heads), _traffic(f"head_m{M}"))
     cfg = {"workload": f"int8 lm_head 3584 -> 152064 (Qwen2.5-7B), M={M}, {len(heads)} distinct copies per step",
-           "M": M, "launches_per_step": len(heads),
+           "M": M, "launches_per_step": len(heads), "packed_layout": layout,
            "weights": "int8 per-row symmetric, bf16 scale", "distinct_bytes_per_step": nbytes * len(heads)}
     cpu = None
     if not args.no_cpu:

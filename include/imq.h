@@ -124,8 +124,8 @@ int imq_linear_w4(const void* x, int64_t x_row_stride, int64_t M, int64_t K_pad,
 
 /* ---- line-tiled packed weights ------------------------------------------------------------------
  * No counterpart in the reference: a device layout of the same bytes as a row-layout qweight
- * [N, row_bytes] (int4: row_bytes = K_pad / 2, int2: K_pad / 4; N a multiple of 16, row_bytes of
- * 128), permuted in 16-byte pieces so that the decode kernels' full-line weight loads read 256
+ * [N, row_bytes] (int4: row_bytes = K_pad / 2, int2: K_pad / 4, int8: K; N a multiple of 16,
+ * row_bytes of 128), permuted in 16-byte pieces so that the decode kernels' full-line weight loads read 256
  * contiguous bytes per 16 lanes instead of 8 partial 128-byte lines. In 16-row tile t the 2 KiB
  * block of line-step l (bytes [128 l, 128 l + 128) of every row of the tile) sits at byte
  * 2048 (t row_bytes / 128 + l); its 16-byte slot 64 h + s (h 0..1, s 0..63) holds piece
@@ -152,6 +152,12 @@ int imq_linear_w2_tiled(const void* x, int64_t x_row_stride, int64_t M, int64_t 
                         int s_dtype, const void* zero, int64_t z_stride_n, int64_t z_stride_g, int z_dtype,
                         int64_t N, int64_t group_size, void* y, int64_t y_row_stride, void* workspace,
                         int64_t workspace_bytes, void* stream);
+/* int8 twin (imq_linear_w8's arguments; q_row_stride = K, K a multiple of 128): the decode line
+ * and skinny kernels and both prefill GEMMs read the layout. Serves _w8a16_triton_op
+ * (worker_quant.py:926-1057) for modules whose op serves every M. */
+int imq_linear_w8_tiled(const void* x, int64_t x_row_stride, int64_t M, int64_t K, const void* qweight,
+                        int64_t q_row_stride, const void* scale, int64_t s_stride_n, int s_dtype, int64_t N,
+                        void* y, int64_t y_row_stride, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* int2 twin: replaces _w2a16_triton_op() (worker_quant.py:1775-1918: `_ksk2`, `_k2`).
  * K_pad = 4 * qweight columns. */

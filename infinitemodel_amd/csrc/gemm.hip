@@ -192,7 +192,7 @@ IMQ_DEV u32x4_t weight_chunk(const WRegs<BITS, WC>& r, int c, float s, float nzs
 // row-layout loop is unchanged).
 template <class C, int BITS, int SDT, int ZDT, int MOE = 0, bool TL = false>
 __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
-  static_assert(!TL || (MOE == 0 && BITS != 8), "line-tiled weights: the dense int4 / int2 forms");
+  static_assert(!TL || MOE == 0, "line-tiled weights: the dense forms");
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, XC = C::XC, WC = C::WC;
   constexpr int BK = C::BK, CH = C::CH, KS = C::KS;
   constexpr int PD = 2;   // register sets of loaded-but-not-yet-stored steps
@@ -263,23 +263,28 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
   constexpr int BYTES_STEP = BK * BITS / 8;
   const uint8_t* wtile = MOE == 0 ? a.q + (int64_t)n0 * a.sqn : a.q + (int64_t)e * a.sqe;
   const int wo = (int)((gn - (MOE == 0 ? n0 : 0)) * a.sqn) + part * (WC * BITS / 8);
-  // line-tiled weights (K steps of 64 codes: 32 bytes of an int4 row, 16 of an int2 row): the
-  // thread's bytes at SB kt + o of tile-relative row rr sit at tile rr / 16, line-step
-  // SB kt / 128, half hr, slot (rr & 7) + 8 ((p / 4) ^ hr) + 16 (p & 3) for piece p = (SB kt + o)
-  // / 16 of the line, byte o & 15 of the piece. int4: p = 2 (kt & 3) + o / 16, line-step kt / 4;
-  // int2: p = kt & 7, line-step kt / 8. p / 4 is uniform per step, so a thread offset for each of
-  // its values plus the step's uniform part (tl_step) address every step.
+  // line-tiled weights (K steps of 64 codes: 64 bytes of an int8 row, 32 of an int4 row, 16 of an
+  // int2 row): the thread's bytes at SB kt + o of tile-relative row rr sit at tile rr / 16,
+  // line-step SB kt / 128, half hr, slot (rr & 7) + 8 ((p / 4) ^ hr) + 16 (p & 3) for piece
+  // p = (SB kt + o) / 16 of the line, byte o & 15 of the piece. int8: p = 4 (kt & 1) + o / 16,
+  // line-step kt / 2; int4: p = 2 (kt & 3) + o / 16, line-step kt / 4; int2: p = kt & 7,
+  // line-step kt / 8. p / 4 is uniform per step, so a thread offset for each of its values plus
+  // the step's uniform part (tl_step) address every step; a 32-byte int8 load is two pieces 256
+  // bytes apart.
   int wta = 0, wtb = 0;
   if constexpr (TL) {
-    static_assert(BK == 64 && WC * BITS / 8 <= 16, "a step's bytes of a thread lie in one 16-byte piece");
+    static_assert(BK == 64 && (WC * BITS / 8 <= 16 || (BITS == 8 && WC == 32)),
+                  "a thread's bytes of a step: one 16-byte piece, or two of an int8 row");
     const int rr = gn - n0, hr = (rr >> 3) & 1, o = part * (WC * BITS / 8);
     const int tb = (rr >> 4) * 16 * (int)a.sqn + 1024 * hr + 16 * (rr & 7) + 256 * (o >> 4) + (o & 15);
     wta = tb + 128 * hr;
     wtb = tb + 128 * (1 - hr);
   }
   // uniform part of a step's tiled offset, and the step's (p / 4) bit
-  auto tl_step = [&](int kt) { return BITS == 4 ? 2048 * (kt >> 2) + 512 * (kt & 1) : 2048 * (kt >> 3) + 256 * (kt & 3); };
-  auto tl_sel = [&](int kt) { return BITS == 4 ? ((kt >> 1) & 1) : ((kt >> 2) & 1); };
+  auto tl_step = [&](int kt) {
+    return BITS == 8 ? 2048 * (kt >> 1) : BITS == 4 ? 2048 * (kt >> 2) + 512 * (kt & 1) : 2048 * (kt >> 3) + 256 * (kt & 3);
+  };
+  auto tl_sel = [&](int kt) { return BITS == 8 ? (kt & 1) : BITS == 4 ? ((kt >> 1) & 1) : ((kt >> 2) & 1); };
   int bl[WC / 8];
 #pragma unroll
   for (int c = 0; c < WC / 8; ++c) bl[c] = swz<C>(wrow, (WC / 8) * part + c);
@@ -295,7 +300,15 @@ __global__ __launch_bounds__(C::NTHR, C::MINB) void gemm_wq_kernel(GemmArgs a) {
     const int kt = kt0 + ktl;
 #pragma unroll
     for (int j = 0; j < XC; ++j) xr[set][j] = *(const u32x4_t*)(xtile + kt * BK + xo[j]);
-    if constexpr (TL)
+    if constexpr (TL && WRegs<BITS, WC>::BYTES == 32) {   // int8, two pieces
+      const uint8_t* p = wtile + (tl_sel(kt) ? wtb : wta) + tl_step(kt);
+      const u32x4_t v0 = *(const u32x4_t*)p, v1 = *(const u32x4_t*)(p + 256);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wr[set].d[i] = v0[i];
+        wr[set].d[4 + i] = v1[i];
+      }
+    } else if constexpr (TL)
       load_w(wr[set], wtile + (tl_sel(kt) ? wtb : wta) + tl_step(kt));
     else
       load_w(wr[set], wtile + kt * BYTES_STEP + wo);
@@ -765,9 +778,15 @@ int gemm_wq_any(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, 
   }
   GemmArgs a{x, sxm, (int)M, (int)K, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, gsh, y, sym, 0, 0, 1, 0,
              nullptr};
-  if (tiled) {   // line-tiled int4 / int2 weights: scale and zero of one dtype
-    if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
-    if (bits == 4) {
+  if (tiled) {   // line-tiled weights: scale and zero of one dtype (int8: the scale's)
+    if (sdt != zdt && bits != 8) return IMQ_ERR_UNSUPPORTED;
+    if (bits == 8) {
+      switch (sdt) {
+        case IMQ_DT_BF16: return launch_gemm<8, IMQ_DT_BF16, IMQ_DT_BF16, true>(a, ws, wsb, st);
+        case IMQ_DT_FP16: return launch_gemm<8, IMQ_DT_FP16, IMQ_DT_FP16, true>(a, ws, wsb, st);
+        case IMQ_DT_FP32: return launch_gemm<8, IMQ_DT_FP32, IMQ_DT_FP32, true>(a, ws, wsb, st);
+      }
+    } else if (bits == 4) {
       switch (sdt) {
         case IMQ_DT_BF16: return launch_gemm<4, IMQ_DT_BF16, IMQ_DT_BF16, true>(a, ws, wsb, st);
         case IMQ_DT_FP16: return launch_gemm<4, IMQ_DT_FP16, IMQ_DT_FP16, true>(a, ws, wsb, st);
@@ -804,9 +823,9 @@ int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, cons
 int gemm_wq_tiled(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, const void* sc,
                   int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg, int zdt, int64_t N,
                   uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st) {
-  if ((bits != 4 && bits != 2) || N % 16 != 0 || (K * bits / 8) % 128 != 0) return IMQ_ERR_UNSUPPORTED;
-  return gemm_wq_any(bits, x, sxm, M, K, q, K * bits / 8, sc, ssn, ssg, sdt, zr, szn, szg, zdt, N, bits == 4 ? 128 : 64,
-                     y, sym, ws, wsb, st, true);
+  if ((bits != 8 && bits != 4 && bits != 2) || N % 16 != 0 || (K * bits / 8) % 128 != 0) return IMQ_ERR_UNSUPPORTED;
+  return gemm_wq_any(bits, x, sxm, M, K, q, K * bits / 8, sc, ssn, ssg, sdt, zr, szn, szg, zdt, N,
+                     bits == 8 ? 0 : bits == 4 ? 128 : 64, y, sym, ws, wsb, st, true);
 }
 
 }  // namespace imq

@@ -116,7 +116,7 @@ int gemm_rb(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, cons
             const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg, int zdt,
             int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st, bool tiled) {
   if (((uintptr_t)x & 15) || (sxm & 7) || ((uintptr_t)q & 15) || (sqn & 15)) return IMQ_ERR_UNSUPPORTED;
-  if (tiled && (bits != 4 || N % 16 != 0 || K % 256 != 0 || sqn != K / 2)) return IMQ_ERR_UNSUPPORTED;
+  if (tiled && (N % 16 != 0 || (K * bits / 8) % 128 != 0 || sqn != K * bits / 8)) return IMQ_ERR_UNSUPPORTED;
   if (sxm < 0 || sqn < 0 || 256 * sxm > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   // the kernel's buffer offsets from a tile's first row (activations, weights, scale / zero)
   if ((256 * sxm + K) * 2 > 0x7fffffff || 256 * sqn + K > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
@@ -128,12 +128,18 @@ int gemm_rb(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, cons
     if ((256 * ssn + ng * ssg) * 4 > 0x7fffffff || (256 * szn + ng * szg) * 4 > 0x7fffffff) return IMQ_ERR_UNSUPPORTED;
   }
   RbArgs a{x, sxm, (int)M, (int)K, q, sqn, sc, ssn, ssg, zr, szn, szg, (int)N, gsh, y, sym, 0, 0, 1, 0, nullptr};
-  if (tiled) {   // line-tiled int4 weights: scale and zero of one dtype
-    if (sdt != zdt) return IMQ_ERR_UNSUPPORTED;
+  if (tiled) {   // line-tiled weights: int4 with scale and zero of one dtype, or int8
+    if (bits == 4 && sdt != zdt) return IMQ_ERR_UNSUPPORTED;
     switch (sdt) {
-      case IMQ_DT_BF16: return rb_ib_dispatch<4, IMQ_DT_BF16, IMQ_DT_BF16, true>(a, ws, wsb, st);
-      case IMQ_DT_FP16: return rb_ib_dispatch<4, IMQ_DT_FP16, IMQ_DT_FP16, true>(a, ws, wsb, st);
-      case IMQ_DT_FP32: return rb_ib_dispatch<4, IMQ_DT_FP32, IMQ_DT_FP32, true>(a, ws, wsb, st);
+      case IMQ_DT_BF16:
+        return bits == 8 ? rb_ib_dispatch<8, IMQ_DT_BF16, IMQ_DT_BF16, true>(a, ws, wsb, st)
+                         : rb_ib_dispatch<4, IMQ_DT_BF16, IMQ_DT_BF16, true>(a, ws, wsb, st);
+      case IMQ_DT_FP16:
+        return bits == 8 ? rb_ib_dispatch<8, IMQ_DT_FP16, IMQ_DT_FP16, true>(a, ws, wsb, st)
+                         : rb_ib_dispatch<4, IMQ_DT_FP16, IMQ_DT_FP16, true>(a, ws, wsb, st);
+      case IMQ_DT_FP32:
+        return bits == 8 ? rb_ib_dispatch<8, IMQ_DT_FP32, IMQ_DT_FP32, true>(a, ws, wsb, st)
+                         : rb_ib_dispatch<4, IMQ_DT_FP32, IMQ_DT_FP32, true>(a, ws, wsb, st);
     }
     return IMQ_ERR_INVALID;
   }

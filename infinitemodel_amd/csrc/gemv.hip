@@ -46,7 +46,8 @@ struct SkinnyArgs {
   int chunk_steps;   // K-steps staged in LDS at once
   const int8_t* q8;  // int8 weights (the int8 kernel; q is unused there)
   float* part;       // split-K partials [splits][M][N] fp32 (the K-split kernel)
-  int tiled;         // weights in the line-tiled layout (int4 line / K-split / wave-split, int2 line / K-split)
+  int tiled;         // weights in the line-tiled layout (int4 line / K-split / wave-split, int2 line /
+                     // K-split, int8 line / skinny)
 };
 
 constexpr int kStep = 128;          // codes per K-step
@@ -454,8 +455,9 @@ IMQ_DEV float row_swap8(float v) {
 // Line-tiled layout (a.tiled; N a multiple of 16, dense rows): those same pieces are stored in lane
 // order, one 1 KiB half per load of the tile's 2 KiB line-step block, so lane l reads bytes 16 l
 // and each 16-lane quarter of a load covers two whole 128-byte lines instead of eight partial ones.
-IMQ_DEV void line_bases(const SkinnyArgs& a, const uint8_t* qt, int lane, int rlast, const uint8_t*& q0,
-                        const uint8_t*& q1, int& lstride) {
+template <class T>
+IMQ_DEV void line_bases(const SkinnyArgs& a, const T* qt, int lane, int rlast, const T*& q0, const T*& q1,
+                        int& lstride) {
   if (a.tiled) {
     q0 = qt + 16 * lane;
     q1 = q0 + 1024;
@@ -1839,7 +1841,8 @@ IMQ_DEV bf16x8_t biased_i8x8_bf16(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
-template <int S, int MC, int SDT, int MAXW>
+// TL: weights in the line-tiled layout (a separate instantiation: the per-load address).
+template <int S, int MC, int SDT, int MAXW, bool TL = false>
 __global__ __launch_bounds__(64 * MAXW) void w8_skinny_kernel(SkinnyArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x & 63;
@@ -1895,6 +1898,12 @@ __global__ __launch_bounds__(64 * MAXW) void w8_skinny_kernel(SkinnyArgs a) {
     int row = tile * 16 + nl;
     row = row < a.N ? row : a.N - 1;
     const int8_t* qrow = a.q8 + (int64_t)row * a.sqn + 16 * jl;
+    // line-tiled (N a multiple of 16): the 16 bytes at byte 64 st + 16 jl of tile row nl sit at
+    // tile line-step st / 2, half h = nl / 8, slot (nl & 7) + 8 ((st & 1) ^ h) + 16 jl
+    const int th = nl >> 3;
+    const int8_t* qtile = a.q8 + (int64_t)tile * 16 * a.sqn + 1024 * th + 16 * (nl & 7) + 256 * jl;
+    const int8_t* qte = qtile + 128 * th;
+    const int8_t* qto = qtile + 128 * (1 - th);
     f32x4_t acc[4];                          // four independent MFMA chains
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc[k] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -1919,7 +1928,10 @@ __global__ __launch_bounds__(64 * MAXW) void w8_skinny_kernel(SkinnyArgs a) {
         for (int i = 0; i < S; ++i) {
           int st = sbase + i;
           st = st < c1 ? st : c1 - 1;
-          wv[i] = __builtin_nontemporal_load((const u32x4_t*)(qrow + (int64_t)st * kStep8));
+          if constexpr (TL)
+            wv[i] = __builtin_nontemporal_load((const u32x4_t*)(((st & 1) ? qto : qte) + 2048 * (st >> 1)));
+          else
+            wv[i] = __builtin_nontemporal_load((const u32x4_t*)(qrow + (int64_t)st * kStep8));
         }
 #pragma unroll
         for (int i = 0; i < S; ++i) {
@@ -2011,17 +2023,17 @@ __global__ __launch_bounds__(64 * MAXW) void w8_line_kernel(SkinnyArgs a) {
   }
   // 2) weights: per line-step one full-line load for rows 0-7 and one for rows 8-15
   const int8_t* qt = a.q8 + (int64_t)row0 * a.sqn;
-  const int rr0 = (c & 7) < rlast ? (c & 7) : rlast;
-  const int rr1 = 8 + (c & 7) < rlast ? 8 + (c & 7) : rlast;
-  const int8_t* q0 = qt + rr0 * (int)a.sqn + 16 * ar + (lo8 ? 0 : 64);
-  const int8_t* q1 = qt + rr1 * (int)a.sqn + 16 * ar + (lo8 ? 64 : 0);
+  const int8_t* q0;
+  const int8_t* q1;
+  int lst;
+  line_bases(a, qt, lane, rlast, q0, q1, lst);
   u32x4_t wb[2 * S2];
 #pragma unroll
   for (int i = 0; i < S2; ++i) {
     int l = ls0 + i;
     l = l < KL ? l : KL - 1;
-    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + kLine8 * l));
-    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + kLine8 * l));
+    wb[2 * i] = __builtin_nontemporal_load((const u32x4_t*)(q0 + lst * l));
+    wb[2 * i + 1] = __builtin_nontemporal_load((const u32x4_t*)(q1 + lst * l));
   }
   // 3) stage x with its per-64-code row sums
 #pragma unroll
@@ -2843,13 +2855,19 @@ int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
   }
   return IMQ_ERR_INVALID;
 }
-template <int SDT, int MAXW>
-int w8_launch_mw(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
+template <int SDT, int MAXW, bool TL>
+int w8_launch_tl(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
   constexpr int S = 8;
   const dim3 g(grid), b(64 * W);
-  if (a.M == 1) return launch_with_lds(w8_skinny_kernel<S, 1, SDT, MAXW>, g, b, lds, st, a);
-  if (a.M <= 4) return launch_with_lds(w8_skinny_kernel<S, 4, SDT, MAXW>, g, b, lds, st, a);
-  return launch_with_lds(w8_skinny_kernel<S, 16, SDT, MAXW>, g, b, lds, st, a);
+  if (a.M == 1) return launch_with_lds(w8_skinny_kernel<S, 1, SDT, MAXW, TL>, g, b, lds, st, a);
+  if (a.M <= 4) return launch_with_lds(w8_skinny_kernel<S, 4, SDT, MAXW, TL>, g, b, lds, st, a);
+  return launch_with_lds(w8_skinny_kernel<S, 16, SDT, MAXW, TL>, g, b, lds, st, a);
+}
+
+template <int SDT, int MAXW>
+int w8_launch_mw(const SkinnyArgs& a, size_t lds, int grid, int W, hipStream_t st) {
+  if (a.tiled) return w8_launch_tl<SDT, MAXW, true>(a, lds, grid, W, st);
+  return w8_launch_tl<SDT, MAXW, false>(a, lds, grid, W, st);
 }
 
 template <int SDT>
@@ -2912,14 +2930,19 @@ int line8_dispatch(const SkinnyArgs& a, int S2, int W, size_t lds, hipStream_t s
   return line8_launch<4, SDT>(a, W, lds, st);
 }
 
+// tiled: q in the line-tiled layout (N a multiple of 16, dense rows of K a multiple of 128 bytes):
+// the line kernel and the skinny kernel's tiled form read it.
 int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t* q, int64_t sqn,
-              const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st) {
+              const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st,
+              bool tiled) {
   if (M < 1 || M > 16 || K <= 0 || K % kStep8 != 0) return IMQ_ERR_UNSUPPORTED;
   if (((uintptr_t)q & 15) || (sqn & 15) || ((uintptr_t)x & 15) || (sxm & 7)) return IMQ_ERR_UNSUPPORTED;
   if (N > (1 << 30) || K > (1 << 28)) return IMQ_ERR_UNSUPPORTED;
+  if (tiled && (N % 16 != 0 || K % kLine8 != 0 || sqn != K)) return IMQ_ERR_UNSUPPORTED;
   const DevInfo di = device_info();
   SkinnyArgs a{x, sxm, (int)M, (int)K, nullptr, sqn, sc, ssn, 0, nullptr, 0, 0, (int)N, 0, y, sym, 0};
   a.q8 = q;
+  a.tiled = tiled ? 1 : 0;
   {
     int S2, W;
     size_t lds;

@@ -24,7 +24,8 @@ int skinny_w2(const uint16_t* x, int64_t sxm, int64_t M, int64_t Kpad, const uin
               bool tiled);
 int64_t ksplit2_workspace_bytes(int64_t M, int64_t N, int64_t Kpad);
 int skinny_w8(const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const int8_t* q, int64_t sqn,
-              const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st);
+              const void* sc, int64_t ssn, int sdt, int64_t N, uint16_t* y, int64_t sym, hipStream_t st,
+              bool tiled);
 int gemm_wq(int bits, const uint16_t* x, int64_t sxm, int64_t M, int64_t K, const uint8_t* q, int64_t sqn,
             const void* sc, int64_t ssn, int64_t ssg, int sdt, const void* zr, int64_t szn, int64_t szg,
             int zdt, int64_t N, int64_t G, uint16_t* y, int64_t sym, void* ws, int64_t wsb, hipStream_t st);
@@ -197,6 +198,27 @@ extern "C" int imq_linear_w2_tiled(const void* x, int64_t x_row_stride, int64_t 
                             z_stride_n, z_stride_g, z_dtype, N, yb, y_row_stride, workspace, workspace_bytes, st);
 }
 
+// int8 weights in the line-tiled layout: the arguments and results of imq_linear_w8 (N a multiple of
+// 16, dense rows of K bytes, K a multiple of 128); the decode line and skinny kernels and both
+// prefill GEMMs read it, other calls return IMQ_ERR_UNSUPPORTED.
+extern "C" int imq_linear_w8_tiled(const void* x, int64_t x_row_stride, int64_t M, int64_t K,
+                                   const void* qweight, int64_t q_row_stride, const void* scale,
+                                   int64_t s_stride_n, int s_dtype, int64_t N, void* y, int64_t y_row_stride,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!x || !qweight || !scale || !y || M < 0 || N < 0 || K <= 0) return IMQ_ERR_INVALID;
+  if (q_row_stride < K || x_row_stride < K || y_row_stride < N || !dt_ok(s_dtype)) return IMQ_ERR_INVALID;
+  if (N % 16 != 0 || K % 128 != 0 || q_row_stride != K) return IMQ_ERR_INVALID;
+  if (M == 0 || N == 0) return IMQ_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xb = (const uint16_t*)x;
+  uint16_t* yb = (uint16_t*)y;
+  if (M <= 16)
+    return imq::skinny_w8(xb, x_row_stride, M, K, (const int8_t*)qweight, q_row_stride, scale, s_stride_n, s_dtype,
+                          N, yb, y_row_stride, st, true);
+  return imq::gemm_wq_tiled(8, xb, x_row_stride, M, K, (const uint8_t*)qweight, scale, s_stride_n, 0, s_dtype,
+                            nullptr, 0, 0, s_dtype, N, yb, y_row_stride, workspace, workspace_bytes, st);
+}
+
 // ---- allocation-free variant of imq_linear_w4 ----------------------------------------------------
 // The scratch array: each device the library runs on holds its own copy until the process ends.
 // Host code never uses the name `scratch` as an address (on the host it is only a stand-in for
@@ -300,7 +322,7 @@ extern "C" int imq_linear_w8(const void* x, int64_t x_row_stride, int64_t M, int
   int rc;
   if (M <= 16) {
     rc = imq::skinny_w8(xb, x_row_stride, M, K, (const int8_t*)qweight, q_row_stride, scale, s_stride_n,
-                        s_dtype, N, yb, y_row_stride, st);
+                        s_dtype, N, yb, y_row_stride, st, false);
   } else {
     rc = imq::gemm_wq(8, xb, x_row_stride, M, K, (const uint8_t*)qweight, q_row_stride, scale, s_stride_n,
                       0, s_dtype, nullptr, 0, 0, s_dtype, N, 0, yb, y_row_stride, workspace, workspace_bytes, st);

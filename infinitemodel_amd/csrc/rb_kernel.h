@@ -188,7 +188,7 @@ IMQ_DEV u32x4_t rb_convert8(uint32_t lo, uint32_t hi) {
 template <int BITS, int SDT, int ZDT, int IB, int NW, int MOE = 0, int PD = 2, bool FOLD = false, bool TL = false>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
   static_assert(!FOLD || (MOE != 0 && BITS == 4 && PD % 2 == 0), "the folded form: int4 MoE, even pipeline depth");
-  static_assert(!TL || (MOE == 0 && BITS == 4), "line-tiled weights: the dense int4 form");
+  static_assert(!TL || MOE == 0, "line-tiled weights: the dense forms");
   constexpr int BM = 32 * IB, BN = 64 * NW, BK = RB_BK, NTHR = 64 * NW;
   constexpr int A_EL = BM * BK;                    // bf16 elements of one LDS buffer
   constexpr int XC = BM * 8 / NTHR;                // 16-byte activation chunks per thread per step
@@ -312,12 +312,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
     svo[j] = (uint32_t)(((n - n0) * (int)a.ssn + gh * (int)a.ssg) * SES);
     zvo[j] = (uint32_t)(((n - n0) * (int)a.szn + gh * (int)a.szg) * ZES);
     if constexpr (TL) {
-      // line-tiled weights: the lane's 16 bytes at byte 32 kt + 16 h of row n (tile-relative rr)
-      // sit at tile (rr / 16), line-step kt / 4, half hr = (rr / 8) & 1, slot (rr & 7) + 8 ((kt / 2
-      // & 1) ^ hr) + 16 (2 (kt & 1) + h): a lane offset for each value of (kt / 2) & 1 plus the
-      // step's uniform 2048 (kt / 4) + 512 (kt & 1)
+      // line-tiled weights: the lane's bytes of a K step of row n (tile-relative rr) sit at tile
+      // rr / 16, half hr = (rr / 8) & 1, slot (rr & 7) + 8 (sel ^ hr) + 16 (piece & 3) of the
+      // step's line-step. int4 (16 bytes at 32 kt + 16 h): line-step kt / 4, piece 2 (kt & 1) + h,
+      // sel = (kt / 2) & 1; int8 (two pieces at 64 kt + 32 h + 16 v): line-step kt / 2, piece 2 h
+      // + v, sel = kt & 1. A lane offset per value of sel plus the step's uniform part (rb_tl_step).
       const int rr = n - n0, hr = (rr >> 3) & 1;
-      const uint32_t tb = (uint32_t)((rr >> 4) * 16 * (int)a.sqn + 1024 * hr + 16 * (rr & 7) + 256 * h);
+      const uint32_t tb = (uint32_t)((rr >> 4) * 16 * (int)a.sqn + 1024 * hr + 16 * (rr & 7) + (BITS == 8 ? 512 : 256) * h);
       qto[j][0] = tb + 128 * hr;
       qto[j][1] = tb + 128 * (1 - hr);
     }
@@ -481,7 +482,10 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         if constexpr (TL) {
-          qr[set][j][0] = rb_bload128(qrs, ((kt >> 1) & 1) ? qto[j][1] : qto[j][0], 2048 * (kt >> 2) + 512 * (kt & 1));
+          const int sel = BITS == 8 ? (kt & 1) : ((kt >> 1) & 1);
+          const uint32_t so = BITS == 8 ? 2048 * (kt >> 1) : 2048 * (kt >> 2) + 512 * (kt & 1);
+#pragma unroll
+          for (int v = 0; v < QV; ++v) qr[set][j][v] = rb_bload128(qrs, (sel ? qto[j][1] : qto[j][0]) + 256 * v, so);
         } else {
 #pragma unroll
           for (int v = 0; v < QV; ++v) qr[set][j][v] = rb_bload128(qrs, qvo[j] + 16 * v, kt * (BK * BITS / 8));
@@ -496,8 +500,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_rb_kernel(RbArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       if constexpr (TL) {
-        qr[set][j][0] = *(const u32x4_t*)(a.q + (int64_t)n0 * a.sqn + (((kt >> 1) & 1) ? qto[j][1] : qto[j][0]) +
-                                          2048 * (kt >> 2) + 512 * (kt & 1));
+        const int sel = BITS == 8 ? (kt & 1) : ((kt >> 1) & 1);
+        const uint32_t so = BITS == 8 ? 2048 * (kt >> 1) : 2048 * (kt >> 2) + 512 * (kt & 1);
+#pragma unroll
+        for (int v = 0; v < QV; ++v)
+          qr[set][j][v] = *(const u32x4_t*)(a.q + (int64_t)n0 * a.sqn + (sel ? qto[j][1] : qto[j][0]) + 256 * v + so);
       } else {
 #pragma unroll
         for (int v = 0; v < QV; ++v) qr[set][j][v] = *(const u32x4_t*)(qb[j] + kt * (BK * BITS / 8) + 16 * v);

@@ -253,10 +253,12 @@ def _tile_shape_check(N: int, row_bytes: int):
 
 
 def line_tile(qweight, out=None):
-    """Row-layout packed weight u8 [N, row_bytes] (int4 or int2 codes) -> the line-tiled layout (a
-    new dense array, or ``out``): in 16-row tile t the 2 KiB block of line-step l holds, in slot
-    64 h + s, 16-byte piece 4 (((s >> 3) & 1) ^ h) + (s >> 4) of tile row 8 h + (s & 7). No
-    counterpart in the reference."""
+    """Row-layout packed weight [N, row_bytes] (u8 int4 / int2 codes, or int8) -> the line-tiled
+    layout of the same dtype (a new dense array, or ``out``): in 16-row tile t the 2 KiB block of
+    line-step l holds, in slot 64 h + s, 16-byte piece 4 (((s >> 3) & 1) ^ h) + (s >> 4) of tile
+    row 8 h + (s & 7). No counterpart in the reference."""
+    if qweight.dtype == torch.int8:
+        return line_tile(qweight.view(torch.uint8), None if out is None else out.view(torch.uint8)).view(torch.int8)
     dev = _check_dev(qweight)
     _check_packed(qweight)
     N, KB = qweight.shape
@@ -270,7 +272,10 @@ def line_tile(qweight, out=None):
 
 
 def line_untile(qweight_tiled, out=None):
-    """Inverse of ``line_tile``: the row-layout u8 [N, row_bytes] array (new, or ``out``)."""
+    """Inverse of ``line_tile``: the row-layout [N, row_bytes] array (new, or ``out``)."""
+    if qweight_tiled.dtype == torch.int8:
+        return line_untile(qweight_tiled.view(torch.uint8),
+                           None if out is None else out.view(torch.uint8)).view(torch.int8)
     dev = _check_dev(qweight_tiled)
     _check_packed(qweight_tiled)
     if not qweight_tiled.is_contiguous():
@@ -283,6 +288,26 @@ def line_untile(qweight_tiled, out=None):
     with torch.cuda.device(dev):
         call("imq_line_untile", _ptr(qweight_tiled), N, KB, _ptr(r), r.stride(0), _stream(dev))
     return r
+
+
+def linear_w8_tiled(x, qweight_tiled, scale, out=None):
+    """``linear_w8`` on int8 weights in the line-tiled layout (``line_tile``): the dense int8 [N, K]
+    tiled array (N a multiple of 16, K of 128); the same results bit for bit."""
+    dev = _check_dev(x, qweight_tiled, scale)
+    _check_packed(qweight_tiled, torch.int8)
+    if not qweight_tiled.is_contiguous():
+        raise ValueError("the line-tiled weight array must be dense")
+    x = _rows2d(x)
+    M, K = x.shape
+    N = qweight_tiled.shape[0]
+    if qweight_tiled.shape[1] != K:
+        raise ValueError(f"x has {K} columns, qweight {qweight_tiled.shape[1]}")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        ws, wsb = _workspace(dev, M, N, K)
+        call("imq_linear_w8_tiled", _ptr(x), x.stride(0), M, K, _ptr(qweight_tiled), qweight_tiled.stride(0),
+             _ptr(scale), scale.stride(0), dtype_code(scale.dtype), N, _ptr(y), y.stride(0), ws, wsb, _stream(dev))
+    return y
 
 
 def linear_w2(x, qweight, group_size: int, sz, out=None):

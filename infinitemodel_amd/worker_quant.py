@@ -268,6 +268,12 @@ def _w8a16_hip_op():
     return _build_op("w8a16", _ops_attr("linear_w8"))
 
 
+def _w8a16_tiled_hip_op():
+    """``op(x[M,K] bf16, qweight_tiled int8[N,K], scale[N,1]) -> y[M,N] bf16`` on weights in the
+    line-tiled layout (ops.line_tile)."""
+    return _build_op("w8a16_tiled", _ops_attr("linear_w8_tiled"))
+
+
 def _w4a16_moe_hip_op():
     """``op(x[B,Kin] bf16, eid[B], q u8[E,N,Kpad/2], scale, zero [E,N,ng], group, in_features)
     -> y[B,N] bf16``: each row b against expert eid[b]."""
@@ -616,9 +622,23 @@ def _make_int8_linear_cls():
             self.register_buffer("qweight", qweight)   # int8 [out, in]
             self.register_buffer("scale", scale)        # [out, 1]
             self.bias = bias
+            # bound to the HIP op for every M, the packed weight may be line-tiled (_line_tiled);
+            # state_dict and load_state_dict keep the reference's row layout
+            self._line_tiled = False
+            self.register_state_dict_post_hook(_untile_on_save)
+            self.register_load_state_dict_pre_hook(_tile_on_load)
+
+        def _row_qweight(self):
+            """The packed weight in the row layout (a converted copy while line-tiled)."""
+            if not self._line_tiled:
+                return self.qweight
+            if self.qweight.is_cuda:
+                from . import ops
+                return ops.line_untile(self.qweight)
+            return _line_untile_torch(self.qweight)
 
         def _dequant(self, dtype):
-            return _dequant8(self.qweight, self.scale, dtype)
+            return _dequant8(self._row_qweight(), self.scale, dtype)
 
         def _kernel_serves(self, x) -> bool:
             if getattr(self, "_w8", None) is None or x.dtype is not torch.bfloat16:
@@ -652,8 +672,39 @@ def _make_int8_linear_cls():
                 bound = None
             if bound is not None:
                 self._w8, self._w8_m_max = bound
+                if self._w8_m_max == 0:
+                    try:
+                        _tile_w8(self)
+                    except Exception as exc:
+                        _log(f"[int8] line-tiled bind failed ({exc!r}) -> row layout")
 
     return QuantLinear
+
+
+def _tile_w8(mod) -> None:
+    """A QuantLinear whose HIP op serves every M takes the line-tiled layout (rows a multiple of
+    16, dense rows of a multiple of 128 bytes): the tiled op is checked against the bf16 dequant at
+    M 1 and 4 (and 32, a prefill row count), then ``qweight`` is replaced by the tiled copy. A module
+    that serves prefill through the naive path keeps the row layout, which that path reads."""
+    import torch
+    from . import ops
+    q = mod.qweight
+    if not (_LINE_TILED and q.shape[0] % 16 == 0 and q.shape[1] % 128 == 0 and q.is_contiguous()):
+        return
+    op = _w8a16_tiled_hip_op()
+    if op is None:
+        return
+    tiled = ops.line_tile(q.view(torch.uint8)).view(torch.int8)
+    ref_w = _dequant8(q, mod.scale.to(torch.bfloat16), torch.bfloat16)
+    for m in (1, 4, 32):
+        x = _bf16_rows(m, q.shape[1], q.device)
+        rel, _ = _rel_err(op(x, tiled, mod.scale), torch.nn.functional.linear(x, ref_w))
+        if not rel < _LINEAR_CHECK_REL:
+            _log(f"[int8] hip w8a16 (line-tiled) self-check rel={rel:.3f} at M={m} -> row layout")
+            return
+    mod.qweight = tiled
+    mod._line_tiled = True
+    mod._w8 = op
 
 
 def _quant_linear_cls():

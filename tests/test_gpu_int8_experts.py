@@ -97,5 +97,6 @@ def test_int8_head_quant_on_gpu(dev):
     x = C.bf16_normal(C.rng(32), (2, 1024))
     with torch.no_grad():
         y = C.t2np(head(C.to_torch(x, "bf16", dev)))
-    ref = oq.int8_gemm_ref(x, head.qweight.cpu().numpy(), head.scale.float().cpu().numpy())
+    # the packed weight in the reference's row layout (the bound module may hold it line-tiled)
+    ref = oq.int8_gemm_ref(x, head.state_dict()["qweight"].cpu().numpy(), head.scale.float().cpu().numpy())
     assert oq.max_rel(y, ref) <= MAX_REL and oq.mean_rel(y, ref) <= MEAN_REL

@@ -168,7 +168,9 @@ def test_quantlinear_int8_module(dev):
     m.prepare_fused()
     assert m._fused_tried
     if getattr(m, "_w8", None) is not None:
-        assert m._w8 is ops.linear_w8
+        # the op serves every M -> line-tiled weights; decode only -> the row layout
+        assert (m._w8 is ops.linear_w8_tiled) == (m._w8_m_max == 0 and m._line_tiled)
+        assert np.array_equal(m.state_dict()["qweight"].cpu().numpy().astype(np.int8), c["q"].astype(np.int8))
     for M in (1, 4, 64):
         x = C.bf16_normal(C.rng(M), (M, 1024))
         y = m(C.to_torch(x, "bf16", dev))

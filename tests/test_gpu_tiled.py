@@ -1,4 +1,4 @@
-"""GPU: the line-tiled layout of packed int4 / int2 weights.
+"""GPU: the line-tiled layout of packed int4 / int2 / int8 weights.
 
 * imq_line_tile / imq_line_untile against the layout's definition (tests/_cases.line_tile_np);
 * imq_linear_w4_tiled bit-identical to imq_linear_w4 on the row layout, for every kernel that
@@ -10,7 +10,9 @@
 * imq_linear_w2_tiled likewise for the int2 line kernel (M 1-2), K-split kernel (4 < M <= 16) and
   LDS-dequant GEMM (M > 16); where the int2 line kernel declines below 5 rows (M 3-4, or K beyond
   its 16 waves) the tiled call runs the K-split kernel and the row layout the skinny kernel, so
-  those calls are checked against the oracle instead.
+  those calls are checked against the oracle instead;
+* imq_linear_w8_tiled bit-identical to imq_linear_w8 for the int8 line kernel (M 1-4), the skinny
+  kernel (4 < M <= 16) and both prefill GEMMs.
 """
 import numpy as np
 import pytest
@@ -186,3 +188,33 @@ def test_tiled_int2_rows_without_a_line_kernel_match_the_oracle(dev, M, K):
     ref = oq.linear_ref(x, c["Wd"])
     assert oq.max_rel(C.t2np(y), ref) <= 1e-2
     assert oq.max_rel(C.t2np(y), C.t2np(y_row)) <= 1e-2
+
+
+W8_CASES = [
+    pytest.param(4096, 3584, 1, "bf16", id="w8-line-M1"),
+    pytest.param(1008, 4096, 2, "fp16", id="w8-line-M2"),
+    pytest.param(4096, 3584, 4, "bf16", id="w8-line-M4"),
+    pytest.param(4096, 4096, 5, "bf16", id="w8-skinny-M5"),
+    pytest.param(1008, 3584, 16, "fp16", id="w8-skinny-M16"),
+    pytest.param(4096, 4096, 17, "bf16", id="w8-gemm-M17"),
+    pytest.param(1008, 4096, 100, "fp16", id="w8-gemm-M100-small-tiles"),
+    pytest.param(4096, 14336, 512, "bf16", id="w8-gemm-M512"),
+    pytest.param(14336, 4096, 1024, "fp16", id="w8-rb-M1024"),
+    pytest.param(1008, 14336, 600, "bf16", id="w8-rb-M600-ragged-N-split"),
+]
+
+
+@pytest.mark.parametrize("N,K,M,dt", W8_CASES)
+def test_tiled_int8_linear_is_bit_identical_to_the_row_layout(dev, N, K, M, dt):
+    import torch
+    from infinitemodel_amd import ops
+    c = C.int8_case(N, K, seed=N + K, dt=dt)
+    q = torch.from_numpy(c["q"].astype(np.int8)).to(dev)
+    s = C.to_torch(c["s"], dt, dev)
+    x = torch.randn(M, K, generator=torch.Generator(device=dev).manual_seed(M), device=dev).to(torch.bfloat16)
+    t = ops.line_tile(q)
+    assert t.dtype == torch.int8 and torch.equal(ops.line_untile(t), q)
+    y_row = ops.linear_w8(x, q, s)
+    y_t = ops.linear_w8_tiled(x, t, s)
+    torch.cuda.synchronize()
+    assert torch.equal(y_t, y_row)
