@@ -1,7 +1,10 @@
-// Decode-regime (M <= 16) fused dequant GEMV kernels for gfx950.
+// Decode-regime (M <= 16) fused dequant GEMV kernels for gfx950: the int4 / int2 / int8 line
+// kernels (M <= 4), the wave-split and K-split kernels (4 < M <= 16) and the skinny kernels below
+// (the shapes those decline). The line, split and int8 skinny kernels also read weights in the
+// line-tiled layout (line_bases; the imq_linear_w*_tiled entry points).
 //
-// w4 skinny kernel (the hot path of the north-star metric)
-// -------------------------------------------------------
+// w4 skinny kernel
+// ----------------
 // Tile = 16 output rows (n) x all of K; a workgroup of W waves owns one tile at a time and
 // splits its K range across the waves; the tile loop is grid-strided.
 //
