@@ -72,6 +72,33 @@ def test_graph_linear_w8(dev, M):
     _replay_check(lambda: ops.linear_w8(x, q, s), lambda: (ops.linear_w8(x2, q, s), x2.float().sum()))
 
 
+@pytest.mark.parametrize("bits,M", [(4, 1), (4, 3), (4, 16), (4, 600), (2, 2), (2, 8), (8, 1), (8, 8), (8, 600)])
+def test_graph_linear_line_tiled(dev, bits, M):
+    """The line-tiled entry points under graph replay: line kernels, the K-split kernels with their
+    workspace and reduce launch (int4 M 16, int2 M 2..8 on tiled weights), the int8 skinny kernel and
+    the prefill GEMMs; each replay equal to the eager call."""
+    import torch
+    from infinitemodel_amd import ops
+    K = 4096
+    if bits == 4:
+        c = C.int4_case(1024, K, 128, seed=35)
+        q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "bf16", dev), C.to_torch(c["z"], "bf16", dev)
+        t = ops.line_tile(q)
+        fn = lambda x: ops.linear_w4_tiled(x, t, 128, (s, z))      # noqa: E731
+    elif bits == 2:
+        c = C.int2_case(1024, K, 64, seed=36, dt="fp16")
+        q, s, z = C.u8(c["q"], dev), C.to_torch(c["s"], "fp16", dev), C.to_torch(c["z"], "fp16", dev)
+        t = ops.line_tile(q)
+        fn = lambda x: ops.linear_w2_tiled(x, t, 64, (s, z))       # noqa: E731
+    else:
+        c = C.int8_case(1024, K, seed=37)
+        q, s = torch.from_numpy(c["q"].astype(np.int8)).to(dev), C.to_torch(c["s"], "bf16", dev)
+        t = ops.line_tile(q)
+        fn = lambda x: ops.linear_w8_tiled(x, t, s)                # noqa: E731
+    x, x2 = _x(dev, M, K, 7 + M), _x(dev, 5, K, 8)
+    _replay_check(lambda: fn(x), lambda: (fn(x2), x2.float().sum()))
+
+
 def test_graph_dequant_w4(dev):
     from infinitemodel_amd import ops
     c = C.int4_case(256, 1024, 128, seed=34)
