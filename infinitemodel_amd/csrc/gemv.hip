@@ -2306,10 +2306,10 @@ int skinny_dispatch(const SkinnyArgs& a0, const DevInfo& di, hipStream_t st) {
 }
 
 // Line kernel dispatch (M <= 4, G == 128, K_pad a multiple of 256 and at most 16384, unit group
-// strides, same scale / zero dtype). Line-steps per wave S2: 4 at M == 1, 2 otherwise (measured
-// on MI355X at Llama-8B shapes), raised to 4 when W = ceil(KL / S2) would exceed 16 waves. Deeper
-// S2 (larger K) would exceed the 128-VGPR budget of 16-wave workgroups; such K take the skinny
-// kernel.
+// strides, same scale / zero dtype). Line-steps per wave S2: 2 (measured on MI355X at Llama-8B
+// shapes), raised to 4 when W = ceil(KL / S2) would exceed 16 waves (line_plan). Deeper S2 (larger
+// K) would exceed the 128-VGPR budget of 16-wave workgroups; such K take the K-split or skinny
+// kernels.
 template <int S2, int SDT>
 int line_launch(const SkinnyArgs& a, int W, size_t lds, hipStream_t st) {
   const dim3 g((unsigned)((a.N + 15) / 16)), b(64 * W);
